@@ -1,0 +1,191 @@
+/*
+ * wsgpu.h — C ABI of the MI355X (gfx950) GPU partition of a physically
+ * partitioned decode KV cache.
+ *
+ * The library (scope_amd/lib/libwsgpu.so) holds the GPU side of a decode step
+ * whose KV tokens are split between host memory and HBM:
+ *
+ *   ws_kv_append / ws_latent_append   write the new token(s) of every sequence
+ *                                     into its HBM page (bit copies)
+ *   ws_gqa_decode_partial             split-KV GQA decode attention over the
+ *                                     HBM tokens -> (out, lse) per query head
+ *   ws_mla_decode_partial             the same for the absorbed MLA layout
+ *                                     (576-wide shared latent, 512-wide out)
+ *   ws_split_reduce                   LSE-combine per-split partials
+ *   ws_lse_merge                      combine the GPU partial with the host
+ *                                     partial (any of the reference's partial
+ *                                     formats) and normalise
+ *
+ * Conventions
+ *   - bf16 tensors are passed as uint16_t bit patterns; fp32 as float.
+ *   - A "partial" is (out, lse): out is the softmax-normalised attention
+ *     output over the partition's tokens, lse = max + log(sum) in natural log.
+ *     An empty partition is (0, -inf).  The reference triple
+ *     (o_unnormalised, max, sum) maps to it by out = o / sum,
+ *     lse = max + log(sum).
+ *   - Paged layout: a page holds page_size consecutive tokens of one sequence.
+ *       GQA pools  k_pages, v_pages : [num_pages][Hkv][page_size][D]  bf16
+ *       MLA pool   latent_pages     : [num_pages][page_size][576]     bf16
+ *                                     (512 latent c_kv followed by 64 rope k_pe)
+ *     page_table : [B][max_pages] int32 physical page ids,
+ *     gpu_len    : [B] int32 number of tokens of sequence b in the pool.
+ *     Token t of sequence b lives in page page_table[b][t / page_size] at
+ *     offset t % page_size.  A contiguous [N][S][D] buffer is the special
+ *     case Hkv = 1, page_size = S, num_pages = N, page_table[n][0] = n.
+ *   - Row order follows the reference: GQA query head h = kvh * G + g,
+ *     out index [b][h][d]; MLA row b * H + h.
+ *   - Every entry point is stream-ordered on `stream` (a hipStream_t; NULL is
+ *     the default stream), allocates nothing and keeps no global mutable state.
+ *     Device pointers are not dereferenced on the host.
+ *   - Return value: 0 on success, a negative WS_E* code on a bad argument or a
+ *     failed launch; ws_last_error() then describes it (thread-local string).
+ */
+#ifndef WSGPU_H
+#define WSGPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WS_OK 0
+#define WS_EINVAL (-1)   /* argument out of range / null pointer           */
+#define WS_ELAUNCH (-2)  /* kernel launch failed                            */
+#define WS_EWORKSPACE (-3) /* workspace too small                           */
+
+/* Formats of the second operand of ws_lse_merge (the host partial). */
+#define WS_PARTIAL_LSE_F32 0      /* (out normalised fp32, lse fp32)               */
+#define WS_TRIPLE_UNNORM_F32 1    /* (out unnormalised fp32, max fp32, sum fp32):
+                                     fused_cpu_attn_mla / _mla_compressed / the
+                                     fp32 path of fused_cpu_attn without normalise */
+#define WS_TRIPLE_NORM_BF16 2     /* (out normalised bf16, max bf16, sum bf16):
+                                     bf16 path of fused_cpu_attn                 */
+#define WS_TRIPLE_NORM_F32 3      /* (out normalised fp32, max fp32, sum fp32):
+                                     fp32 path of fused_cpu_attn                 */
+
+const char* ws_last_error(void);
+const char* ws_version(void);
+
+/*
+ * Append n_new tokens per sequence to the GQA pools at positions
+ * gpu_len[b] .. gpu_len[b] + n_new - 1, then (if update_len) gpu_len[b] += n_new.
+ * k_new, v_new: [B][Hkv][n_new][D] bf16 (the reference's k4d/v4d layout).
+ * Pages for the new positions must already be in page_table.
+ * Replaces InplaceKVCache.append_4d (system/qwenoffload.py:100-118,
+ * system/mixoffload.py:85-104) and the slot copy of _resident_layer
+ * (roofline/bench_resident_kv.py:268-269) for the HBM partition.
+ */
+int ws_kv_append(const uint16_t* k_new, const uint16_t* v_new,
+                 uint16_t* k_pages, uint16_t* v_pages,
+                 const int32_t* page_table, int32_t* gpu_len,
+                 int B, int Hkv, int D, int n_new,
+                 int page_size, int max_pages, int num_pages,
+                 int update_len, void* stream);
+
+/*
+ * Append n_new latent tokens per sequence to the MLA pool.
+ * c_new: [B][n_new][512] bf16 (row stride c_stride elements),
+ * pe_new: [B][n_new][64] bf16 (row stride pe_stride elements).
+ * Replaces the GPU-segment half of InplaceKVCacheCompressed.append
+ * (system/deepseek.py:171-192; boundary arithmetic 181-188 stays on the host).
+ */
+int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
+                     const uint16_t* pe_new, int64_t pe_stride,
+                     uint16_t* latent_pages,
+                     const int32_t* page_table, int32_t* gpu_len,
+                     int B, int n_new, int page_size, int max_pages,
+                     int num_pages, int update_len, void* stream);
+
+/*
+ * Workspace for the split-KV partials: max_splits * rows * (Dv + 1) * 4 bytes,
+ * rows = B * Hq (GQA) or B * H (MLA).
+ */
+size_t ws_decode_workspace_bytes(int rows, int Dv, int max_splits);
+
+/*
+ * Split plan of a decode call: for kind 0 (GQA, rows_kv = B * Hkv) or 1 (MLA,
+ * rows_kv = B), the tokens per split actually used (tokens_per_split, or the
+ * library's choice when it is 0) and the number of splits of the longest
+ * sequence.  Returns 0 or WS_EINVAL.  A call with n_splits > 1 needs
+ * ws_decode_workspace_bytes(rows, Dv, n_splits) bytes of workspace.
+ */
+int ws_decode_plan(int kind, int rows_kv, int max_len, int tokens_per_split,
+                   int* tps_out, int* n_splits_out);
+
+/*
+ * Split-KV GQA decode attention over the pooled tokens of every sequence.
+ * q: [B][Hq][D] bf16, Hq = Hkv * G, G in {1,2,4,8,16}, D = 128.
+ * tokens_per_split: multiple of 32 (0 = choose); max_len: upper bound of
+ * gpu_len[] (sets the grid; must be >= every gpu_len[b]).
+ * Outputs out: [B][Hq][D] fp32 normalised, lse: [B][Hq] fp32.
+ * Replaces _local_bmm_softmax / _resident_layer
+ * (roofline/bench_resident_kv.py:150-157, 261-271) and the GPU side of
+ * _compute_pipelined_attention (system/mixoffload.py:1389-1447).
+ */
+int ws_gqa_decode_partial(const uint16_t* q,
+                          const uint16_t* k_pages, const uint16_t* v_pages,
+                          const int32_t* page_table, const int32_t* gpu_len,
+                          int B, int Hq, int Hkv, int D,
+                          int page_size, int max_pages, int num_pages,
+                          int max_len, int tokens_per_split, float scale,
+                          float* out, float* lse,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/*
+ * Split-KV absorbed-MLA decode attention.
+ * q_nope: [B*H][512] bf16 (q_nope already multiplied by W_UK), q_pe: [B*H][64].
+ * score = (q_nope . c + q_pe . pe) * scale over the shared 576-wide latent,
+ * out = softmax . c (512-wide).  H = 16.
+ * Outputs out: [B*H][512] fp32 normalised, lse: [B*H] fp32.
+ * Replaces the GPU partial of _mla_compressed_forward
+ * (system/deepseek.py:364-392; also roofline/bench_rstar_revalidate_ds2.py:74-86).
+ */
+int ws_mla_decode_partial(const uint16_t* q_nope, const uint16_t* q_pe,
+                          const uint16_t* latent_pages,
+                          const int32_t* page_table, const int32_t* gpu_len,
+                          int B, int H, int page_size, int max_pages,
+                          int num_pages, int max_len, int tokens_per_split,
+                          float scale, float* out, float* lse,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/*
+ * LSE-combine per-split partials: part_out [n_splits][rows][Dv],
+ * part_lse [n_splits][rows] -> out [rows][Dv], lse [rows].  Split s of a row
+ * takes part in the merge iff s < n_valid[row / heads_per_len] where
+ * n_valid = ceil(len / tokens_per_split) for len = gpu_len[row / heads_per_len].
+ * Rows with n_valid <= 1 are left untouched unless n_valid == 0, which writes
+ * (0, -inf).  Used internally by the decode entry points; exported for callers
+ * that schedule their own splits.
+ * Replaces the running merge of _pingpong_stream
+ * (roofline/bench_resident_kv.py:188-201).
+ */
+int ws_split_reduce(const float* part_out, const float* part_lse,
+                    const int32_t* gpu_len, int rows, int heads_per_len,
+                    int Dv, int n_splits, int tokens_per_split,
+                    float* out, float* lse, void* stream);
+
+/*
+ * Merge the GPU partial (out_g, lse_g) with a second partial in format fmt_b
+ * (WS_PARTIAL_LSE_F32: b_out fp32, b_aux0 = lse fp32; WS_TRIPLE_*: b_aux0 =
+ * max, b_aux1 = sum, dtype per format), over rows x Dv.
+ * Writes any non-null of out_bf16 [rows][Dv], out_f32 [rows][Dv], lse_out
+ * [rows].  Empty + empty gives out 0, lse -inf.
+ * Replaces _pairwise_merge + the final normalise
+ * (roofline/bench_resident_kv.py:141-148, 345-350), the MLA merge
+ * (system/deepseek.py:394-403) and the GQA token-split merge with its CPU
+ * un-normalise (system/mixoffload.py:1334, 1452-1464).
+ */
+int ws_lse_merge(const float* out_g, const float* lse_g,
+                 const void* b_out, const void* b_aux0, const void* b_aux1,
+                 int fmt_b, uint16_t* out_bf16, float* out_f32,
+                 float* lse_out, int rows, int Dv, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WSGPU_H */

@@ -1,0 +1,23 @@
+"""Oracle for the GPU KV-partition path — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+anything from this package, and only as the checker (or, for bench.py, as the
+timed CPU baseline).  The product (scope_amd) never imports it.
+
+Contents
+  attn_np.py        numpy restatement of the reference's decode-attention math:
+                    fp64 closed forms (the mathematical pin), an fp32 blocked
+                    online softmax with tile merge, the pairwise LSE merge, the
+                    reference triple conventions, and the partition / page /
+                    boundary integer model.
+  cpu_attn_port.c   C restatement of the reference CPU partial kernels
+                    (kernel/cpu_attn.cpp: fused_cpu_attn, fused_cpu_attn_mla,
+                    fused_cpu_attn_mla_compressed) with OpenMP, used as the
+                    checker at full sizes and as the CPU baseline.
+  port.py           ctypes binding of the C restatement.
+  Makefile          builds oracle/_build/libwsoracle.so with gcc.
+
+The reference CPU kernel itself is not built here: it compiles only through
+torch.utils.cpp_extension against libtorch and pybind11 (kernel/build.py:13-25),
+i.e. it needs external libraries, so oracle/_ref stays empty.
+"""

@@ -1,0 +1,257 @@
+"""Paged HBM partitions of the decode KV cache, and host+GPU partitioned caches.
+
+GqaGpuPartition / MlaGpuPartition hold the GPU-affinity token range of every
+sequence in fixed-size HBM pages (default 64 tokens):
+  GQA  k, v       [num_layers, num_pages, Hkv, page_size, D] bf16
+  MLA  latent     [num_layers, num_pages, page_size, 576]    bf16
+  page_table      [B, max_pages] int32 (shared by all layers)
+  gpu_len         [num_layers, B] int32 (device) + a host mirror
+Pages come from a free list and are assigned on the host before an append
+needs them; the device page table is updated only when a sequence crosses a
+page boundary (once per 64 decode steps).
+
+PartitionedLatentCache mirrors the reference's token-range-partitioned MLA
+cache (system/deepseek.py:144-209): the leading `gs` tokens of each sequence
+in pinned host memory, the rest in an MlaGpuPartition.
+PartitionedKVCache is the GQA analogue (system/mixoffload.py:51-144 holds the
+whole cache on the host; here the trailing range lives in HBM).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import ops
+from .partition import boundary_split, pages_for
+
+
+class PagePool:
+    """Free list of physical page ids."""
+
+    def __init__(self, num_pages: int):
+        self.num_pages = num_pages
+        self._free = list(range(num_pages - 1, -1, -1))
+
+    def alloc(self) -> int:
+        if not self._free:
+            raise MemoryError("HBM page pool exhausted")
+        return self._free.pop()
+
+    def release(self, pid: int) -> None:
+        self._free.append(pid)
+
+    @property
+    def free(self) -> int:
+        return len(self._free)
+
+
+class _PagedBase:
+    def __init__(self, num_layers, batch, max_tokens, page_size, num_pages, device):
+        if page_size <= 0 or page_size % 32:
+            raise ValueError("page_size must be a positive multiple of 32")
+        self.device = torch.device(device)
+        self.num_layers = num_layers
+        self.batch = batch
+        self.page_size = page_size
+        self.max_pages = max(1, pages_for(max_tokens, page_size))
+        self.num_pages = num_pages if num_pages is not None else batch * self.max_pages
+        self.pool = PagePool(self.num_pages)
+        self.host_table = np.full((batch, self.max_pages), -1, np.int32)
+        self.page_table = torch.full((batch, self.max_pages), -1, dtype=torch.int32,
+                                     device=self.device)
+        self.lens = np.zeros((num_layers, batch), np.int64)  # host mirror
+        self.gpu_len = torch.zeros((num_layers, batch), dtype=torch.int32,
+                                   device=self.device)
+        self._pages_held = np.zeros(batch, np.int64)
+
+    def reserve(self, b: int, n_tokens: int) -> None:
+        """Make sure sequence b owns pages for its first n_tokens positions."""
+        need = pages_for(n_tokens, self.page_size)
+        if need > self.max_pages:
+            raise ValueError(f"sequence {b}: {n_tokens} tokens exceed capacity "
+                             f"{self.max_pages * self.page_size}")
+        have = int(self._pages_held[b])
+        if need <= have:
+            return
+        for p in range(have, need):
+            self.host_table[b, p] = self.pool.alloc()
+        self._pages_held[b] = need
+        self.page_table[b, have:need].copy_(
+            torch.from_numpy(self.host_table[b, have:need].copy()), non_blocking=False)
+
+    def reserve_all(self, n_tokens_per_seq) -> None:
+        for b, n in enumerate(n_tokens_per_seq):
+            self.reserve(b, int(n))
+
+    def max_len(self, layer: int) -> int:
+        return int(self.lens[layer].max()) if self.batch else 0
+
+    def reset(self) -> None:
+        """Drop all tokens and return every page to the pool."""
+        for b in range(self.batch):
+            for p in range(int(self._pages_held[b])):
+                self.pool.release(int(self.host_table[b, p]))
+        self.host_table[:] = -1
+        self.page_table.fill_(-1)
+        self._pages_held[:] = 0
+        self.lens[:] = 0
+        self.gpu_len.zero_()
+
+
+class GqaGpuPartition(_PagedBase):
+    """HBM pages of the GPU token range of a GQA KV cache."""
+
+    def __init__(self, num_layers, batch, num_kv_heads, head_dim, max_tokens,
+                 page_size=64, num_pages=None, device="cuda"):
+        super().__init__(num_layers, batch, max_tokens, page_size, num_pages, device)
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        shape = (num_layers, self.num_pages, num_kv_heads, page_size, head_dim)
+        self.k = torch.empty(shape, dtype=torch.bfloat16, device=self.device)
+        self.v = torch.empty(shape, dtype=torch.bfloat16, device=self.device)
+
+    def append_4d(self, layer: int, k4d: torch.Tensor, v4d: torch.Tensor) -> None:
+        """Append k4d/v4d [B, Hkv, n, D] to every sequence of `layer`
+        (InplaceKVCache.append_4d, system/qwenoffload.py:100-118)."""
+        n = k4d.shape[2]
+        for b in range(self.batch):
+            self.reserve(b, int(self.lens[layer, b]) + n)
+        ops.kv_append(k4d.contiguous(), v4d.contiguous(), self.k[layer], self.v[layer],
+                      self.page_table, self.gpu_len[layer])
+        self.lens[layer] += n
+
+    def load_sequence(self, layer: int, b: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Append k, v [Hkv, n, D] to sequence b only (prefill of one row)."""
+        n = k.shape[1]
+        self.reserve(b, int(self.lens[layer, b]) + n)
+        ops.kv_append(k.unsqueeze(0).contiguous(), v.unsqueeze(0).contiguous(),
+                      self.k[layer], self.v[layer], self.page_table[b:b + 1],
+                      self.gpu_len[layer, b:b + 1])
+        self.lens[layer, b] += n
+
+    def attend(self, layer: int, q: torch.Tensor, scale: float, tokens_per_split=0):
+        """GPU partial over the partition: q [B, Hq, D] -> (out fp32, lse fp32)."""
+        return ops.gqa_decode_partial(q, self.k[layer], self.v[layer], self.page_table,
+                                      self.gpu_len[layer], scale, self.max_len(layer),
+                                      tokens_per_split)
+
+
+class MlaGpuPartition(_PagedBase):
+    """HBM pages of the GPU token range of an absorbed-MLA latent cache."""
+
+    def __init__(self, num_layers, batch, max_tokens, page_size=64, num_pages=None,
+                 device="cuda"):
+        super().__init__(num_layers, batch, max_tokens, page_size, num_pages, device)
+        self.latent = torch.empty((num_layers, self.num_pages, page_size, ops.MLA_LATENT),
+                                  dtype=torch.bfloat16, device=self.device)
+
+    def append(self, layer: int, c_kv: torch.Tensor, k_pe: torch.Tensor) -> None:
+        """Append c_kv [B, n, 512], k_pe [B, n, 64] to every sequence."""
+        n = c_kv.shape[1]
+        for b in range(self.batch):
+            self.reserve(b, int(self.lens[layer, b]) + n)
+        ops.latent_append(c_kv, k_pe, self.latent[layer], self.page_table,
+                          self.gpu_len[layer])
+        self.lens[layer] += n
+
+    def load_sequence(self, layer: int, b: int, c_kv: torch.Tensor, k_pe: torch.Tensor) -> None:
+        """Append c_kv [n, 512], k_pe [n, 64] to sequence b only."""
+        n = c_kv.shape[0]
+        self.reserve(b, int(self.lens[layer, b]) + n)
+        ops.latent_append(c_kv.unsqueeze(0).contiguous(), k_pe.unsqueeze(0).contiguous(),
+                          self.latent[layer], self.page_table[b:b + 1],
+                          self.gpu_len[layer, b:b + 1])
+        self.lens[layer, b] += n
+
+    def attend(self, layer: int, q_nope: torch.Tensor, q_pe: torch.Tensor, scale: float,
+               tokens_per_split=0):
+        """GPU partial: q_nope [B*H, 512], q_pe [B*H, 64] -> (out, lse)."""
+        return ops.mla_decode_partial(q_nope, q_pe, self.latent[layer], self.page_table,
+                                      self.gpu_len[layer], scale, self.max_len(layer),
+                                      tokens_per_split)
+
+
+class PartitionedLatentCache:
+    """Token-range-partitioned MLA latent cache.
+
+    Same contract as InplaceKVCacheCompressed (system/deepseek.py:144-209):
+    the leading `gs` tokens of every sequence are the host segment (pinned
+    c [B, gs, 512] and pe [B, gs, 64] per layer), positions >= gs go to the
+    GPU partition.  append() splits new tokens at the boundary with the
+    reference's arithmetic; get() returns the host views and the GPU partition.
+    """
+
+    def __init__(self, num_layers, batch, max_seq, gs, page_size=64, device="cuda"):
+        if not 0 <= gs <= max_seq:
+            raise ValueError("boundary gs must lie in [0, max_seq]")
+        self.num_layers, self.batch, self.max_seq, self.gs = num_layers, batch, max_seq, gs
+        pin = torch.cuda.is_available()
+        self.host_c = [torch.empty((batch, gs, ops.MLA_C), dtype=torch.bfloat16,
+                                   pin_memory=pin) for _ in range(num_layers)]
+        self.host_pe = [torch.empty((batch, gs, ops.MLA_PE), dtype=torch.bfloat16,
+                                    pin_memory=pin) for _ in range(num_layers)]
+        self.gpu = MlaGpuPartition(num_layers, batch, max(max_seq - gs, 1), page_size,
+                                   device=device)
+        self._filled = [0] * num_layers
+
+    def append(self, layer: int, c_kv: torch.Tensor, k_pe: torch.Tensor) -> None:
+        """c_kv [B, n, 512], k_pe [B, n, 64] (host or device)."""
+        n = c_kv.shape[1]
+        t = self._filled[layer]
+        if t + n > self.max_seq:
+            raise ValueError("append beyond max_seq")
+        (h0, h1, hs), (g0, g1, gsrc) = boundary_split(t, n, self.gs)
+        if h1 > h0:
+            self.host_c[layer][:, h0:h1].copy_(c_kv[:, hs:hs + h1 - h0])
+            self.host_pe[layer][:, h0:h1].copy_(k_pe[:, hs:hs + h1 - h0])
+        if g1 > g0:
+            dev = self.gpu.device
+            c = c_kv[:, gsrc:gsrc + g1 - g0].to(dev).contiguous()
+            p = k_pe[:, gsrc:gsrc + g1 - g0].to(dev).contiguous()
+            self.gpu.append(layer, c, p)
+        self._filled[layer] = t + n
+
+    def get(self, layer: int):
+        """((host c, host pe) views of the filled host segment, GPU partition)."""
+        t = self._filled[layer]
+        n_host = min(t, self.gs)
+        return (self.host_c[layer][:, :n_host], self.host_pe[layer][:, :n_host]), self.gpu
+
+    def seq_len(self, layer: int) -> int:
+        return self._filled[layer]
+
+
+class PartitionedKVCache:
+    """Token-range-partitioned GQA KV cache: host rows [B*Hkv, S_host, D] for
+    the leading tokens of each sequence (pinned), GPU partition for the rest.
+
+    Host lengths may differ per sequence (variable-length batches), so the
+    host segment keeps its own per-sequence length.
+    """
+
+    def __init__(self, num_layers, batch, num_kv_heads, head_dim, max_host, max_gpu,
+                 page_size=64, device="cuda"):
+        pin = torch.cuda.is_available()
+        self.batch, self.num_kv_heads, self.head_dim = batch, num_kv_heads, head_dim
+        self.host_k = [torch.empty((batch * num_kv_heads, max_host, head_dim),
+                                   dtype=torch.bfloat16, pin_memory=pin)
+                       for _ in range(num_layers)]
+        self.host_v = [torch.empty_like(self.host_k[0], pin_memory=pin)
+                       for _ in range(num_layers)]
+        self.host_len = np.zeros((num_layers, batch), np.int64)
+        self.gpu = GqaGpuPartition(num_layers, batch, num_kv_heads, head_dim,
+                                   max(max_gpu, 1), page_size, device=device)
+
+    def load_host(self, layer: int, b: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Set sequence b's host segment to k, v [Hkv, n, D]."""
+        n = k.shape[1]
+        rows = slice(b * self.num_kv_heads, (b + 1) * self.num_kv_heads)
+        self.host_k[layer][rows, :n].copy_(k)
+        self.host_v[layer][rows, :n].copy_(v)
+        self.host_len[layer, b] = n
+
+    def host_rows(self, layer: int, b: int):
+        """(k, v) views [Hkv, n_host, D] of sequence b's host segment."""
+        n = int(self.host_len[layer, b])
+        rows = slice(b * self.num_kv_heads, (b + 1) * self.num_kv_heads)
+        return self.host_k[layer][rows, :n], self.host_v[layer][rows, :n]

@@ -1,0 +1,36 @@
+// Error reporting and version of the C ABI.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "ws_common.h"
+
+namespace ws {
+
+static thread_local char g_last_error[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(WS_ELAUNCH, "%s: launch failed: %s", what,
+                     hipGetErrorString(e));
+  return WS_OK;
+}
+
+}  // namespace ws
+
+extern "C" const char* ws_last_error(void) { return ws::g_last_error; }
+
+extern "C" const char* ws_version(void) { return "wsgpu 0.1 gfx950"; }
+
+extern "C" size_t ws_decode_workspace_bytes(int rows, int Dv, int max_splits) {
+  if (rows <= 0 || Dv <= 0 || max_splits <= 0) return 0;
+  return (size_t)max_splits * (size_t)rows * (size_t)(Dv + 1) * sizeof(float);
+}

@@ -1,0 +1,136 @@
+// Append kernels: copy each sequence's new token(s) into its HBM page slot.
+//
+// One workgroup per sequence.  Every thread moves 16-byte vectors, so a decode
+// step's append of a Mixtral layer (8 KV heads x 128 x bf16, K and V) is one
+// 256-thread pass.  The workgroup is the only reader of gpu_len[b], so it can
+// bump the length after a barrier without racing other workgroups.
+#include "ws_common.h"
+
+namespace ws {
+
+__global__ __launch_bounds__(256) void kv_append_kernel(
+    const u32x4* __restrict__ k_new, const u32x4* __restrict__ v_new,
+    u32x4* __restrict__ k_pages, u32x4* __restrict__ v_pages,
+    const int32_t* __restrict__ page_table, int32_t* __restrict__ gpu_len,
+    int Hkv, int dvec, int n_new, int page_size, int max_pages, int num_pages,
+    int update_len) {
+  const int b = blockIdx.x;
+  const int len = gpu_len[b];
+  const int per_token = Hkv * dvec;     // vectors of one token of one tensor
+  const int total = n_new * per_token;  // vectors of one tensor
+  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+    // source order [Hkv][n_new][dvec]
+    const int dv = idx % dvec;
+    const int rest = idx / dvec;
+    const int i = rest % n_new;
+    const int h = rest / n_new;
+    const int pos = len + i;
+    const int page = pos / page_size;
+    if (page >= max_pages) continue;
+    const int pid = page_table[(size_t)b * max_pages + page];
+    if (pid < 0 || pid >= num_pages) continue;
+    const size_t src = (((size_t)b * Hkv + h) * n_new + i) * dvec + dv;
+    const size_t dst =
+        (((size_t)pid * Hkv + h) * page_size + (pos % page_size)) * dvec + dv;
+    k_pages[dst] = k_new[src];
+    v_pages[dst] = v_new[src];
+  }
+  if (update_len) {
+    __syncthreads();
+    if (threadIdx.x == 0) gpu_len[b] = len + n_new;
+  }
+}
+
+constexpr int kLatent = 576;
+constexpr int kLatentC = 512;
+
+__global__ __launch_bounds__(256) void latent_append_kernel(
+    const u32x4* __restrict__ c_new, int64_t c_stride_vec,
+    const u32x4* __restrict__ pe_new, int64_t pe_stride_vec,
+    u32x4* __restrict__ latent_pages, const int32_t* __restrict__ page_table,
+    int32_t* __restrict__ gpu_len, int n_new, int page_size, int max_pages,
+    int num_pages, int update_len) {
+  const int b = blockIdx.x;
+  const int len = gpu_len[b];
+  constexpr int vec_row = kLatent / 8;    // 72 vectors per token
+  constexpr int vec_c = kLatentC / 8;     // 64 of them from c_kv
+  const int total = n_new * vec_row;
+  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+    const int v = idx % vec_row;
+    const int i = idx / vec_row;
+    const int pos = len + i;
+    const int page = pos / page_size;
+    if (page >= max_pages) continue;
+    const int pid = page_table[(size_t)b * max_pages + page];
+    if (pid < 0 || pid >= num_pages) continue;
+    const size_t row = (size_t)b * n_new + i;
+    const u32x4 val = (v < vec_c) ? c_new[row * c_stride_vec + v]
+                                  : pe_new[row * pe_stride_vec + (v - vec_c)];
+    latent_pages[((size_t)pid * page_size + (pos % page_size)) * vec_row + v] =
+        val;
+  }
+  if (update_len) {
+    __syncthreads();
+    if (threadIdx.x == 0) gpu_len[b] = len + n_new;
+  }
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace ws
+
+using namespace ws;
+
+extern "C" int ws_kv_append(const uint16_t* k_new, const uint16_t* v_new,
+                            uint16_t* k_pages, uint16_t* v_pages,
+                            const int32_t* page_table, int32_t* gpu_len, int B,
+                            int Hkv, int D, int n_new, int page_size,
+                            int max_pages, int num_pages, int update_len,
+                            void* stream) {
+  if (!k_new || !v_new || !k_pages || !v_pages || !page_table || !gpu_len)
+    return set_error(WS_EINVAL, "ws_kv_append: null pointer");
+  if (B < 0 || Hkv <= 0 || D <= 0 || D % 8 != 0 || n_new < 0 ||
+      page_size <= 0 || max_pages <= 0 || num_pages <= 0)
+    return set_error(WS_EINVAL,
+                     "ws_kv_append: bad sizes B=%d Hkv=%d D=%d n_new=%d "
+                     "page_size=%d max_pages=%d num_pages=%d",
+                     B, Hkv, D, n_new, page_size, max_pages, num_pages);
+  if (!aligned16(k_new) || !aligned16(v_new) || !aligned16(k_pages) ||
+      !aligned16(v_pages))
+    return set_error(WS_EINVAL, "ws_kv_append: bf16 buffers must be 16-byte aligned");
+  if (B == 0 || n_new == 0) return WS_OK;
+  hipLaunchKernelGGL(kv_append_kernel, dim3(B), dim3(256), 0,
+                     (hipStream_t)stream, (const u32x4*)k_new,
+                     (const u32x4*)v_new, (u32x4*)k_pages, (u32x4*)v_pages,
+                     page_table, gpu_len, Hkv, D / 8, n_new, page_size,
+                     max_pages, num_pages, update_len);
+  return check_launch("ws_kv_append");
+}
+
+extern "C" int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
+                                const uint16_t* pe_new, int64_t pe_stride,
+                                uint16_t* latent_pages,
+                                const int32_t* page_table, int32_t* gpu_len,
+                                int B, int n_new, int page_size, int max_pages,
+                                int num_pages, int update_len, void* stream) {
+  if (!c_new || !pe_new || !latent_pages || !page_table || !gpu_len)
+    return set_error(WS_EINVAL, "ws_latent_append: null pointer");
+  if (B < 0 || n_new < 0 || page_size <= 0 || max_pages <= 0 ||
+      num_pages <= 0 || c_stride < 512 || pe_stride < 64 || c_stride % 8 ||
+      pe_stride % 8)
+    return set_error(WS_EINVAL,
+                     "ws_latent_append: bad sizes B=%d n_new=%d page_size=%d "
+                     "max_pages=%d num_pages=%d c_stride=%lld pe_stride=%lld",
+                     B, n_new, page_size, max_pages, num_pages,
+                     (long long)c_stride, (long long)pe_stride);
+  if (!aligned16(c_new) || !aligned16(pe_new) || !aligned16(latent_pages))
+    return set_error(WS_EINVAL,
+                     "ws_latent_append: bf16 buffers must be 16-byte aligned");
+  if (B == 0 || n_new == 0) return WS_OK;
+  hipLaunchKernelGGL(latent_append_kernel, dim3(B), dim3(256), 0,
+                     (hipStream_t)stream, (const u32x4*)c_new, c_stride / 8,
+                     (const u32x4*)pe_new, pe_stride / 8, (u32x4*)latent_pages,
+                     page_table, gpu_len, n_new, page_size, max_pages,
+                     num_pages, update_len);
+  return check_launch("ws_latent_append");
+}

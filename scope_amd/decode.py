@@ -1,0 +1,144 @@
+"""Partitioned decode attention: GPU partial over HBM pages, host partial on a
+worker thread, LSE merge on the GPU.
+
+partitioned_gqa_decode mirrors the token-split flow of run_kvlen_resident
+(roofline/bench_resident_kv.py:314-352) and
+_compute_pipelined_attention (system/mixoffload.py:1201-1484);
+partitioned_mla_decode mirrors the decode branch of _mla_compressed_forward
+(system/deepseek.py:323-403).  The host partial is any callable with the
+contract of the reference CPU kernels (kernel/cpu_attn.cpp:1024-1054), which
+stay in place: fused_cpu_attn(q, k, v, scale) / fused_cpu_attn_mla_compressed(
+q_proj, q_pe, c_kv, k_pe, scale) on CPU tensors.
+"""
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import ops
+from .cache import PartitionedKVCache, PartitionedLatentCache
+
+# Host-partial output conventions -> merge format.
+CPU_FORMATS = {
+    "fused_cpu_attn_bf16": ops.TRIPLE_NORM_BF16,     # normalised bf16 triple
+    "fused_cpu_attn_fp32": ops.TRIPLE_NORM_F32,      # normalised fp32 triple
+    "fused_cpu_attn_mla": ops.TRIPLE_UNNORM_F32,     # unnormalised fp32 triple
+    "mla_compressed": ops.TRIPLE_UNNORM_F32,
+}
+
+
+class _CpuPartial(threading.Thread):
+    def __init__(self, fn):
+        super().__init__(daemon=True)
+        self._fn = fn
+        self.result = None
+        self.error = None
+
+    def run(self):
+        try:
+            self.result = self._fn()
+        except BaseException as e:  # surfaced by join_result
+            self.error = e
+
+    def join_result(self):
+        self.join()
+        if self.error is not None:
+            raise self.error
+        return self.result
+
+
+def _to_device_pinned(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    if t.is_cuda:
+        return t
+    if not t.is_pinned():
+        t = t.pin_memory()
+    return t.to(dev, non_blocking=True)
+
+
+def partitioned_gqa_decode(cache: PartitionedKVCache, layer: int, q: torch.Tensor,
+                           scale: float, cpu_attn=None, cpu_format="fused_cpu_attn_bf16",
+                           k_new=None, v_new=None, tokens_per_split=0):
+    """One decode step of GQA attention over a host/GPU partitioned cache.
+
+    q [B, Hq, D] bf16 on the GPU; k_new/v_new [B, Hkv, 1, D] (optional) are
+    appended to the GPU partition first.  cpu_attn(q [Hkv, G, D], k [Hkv, S, D],
+    v [Hkv, S, D], scale) -> (out, max, sum) is called once per sequence with
+    host tokens (the reference kernels take one S per call,
+    kernel/cpu_attn.cpp:590).  Returns out [B, Hq, 1, D] bf16.
+    """
+    gpu = cache.gpu
+    B, Hq, D = q.shape
+    Hkv = cache.num_kv_heads
+    G = Hq // Hkv
+    if k_new is not None:
+        gpu.append_4d(layer, k_new, v_new)
+    need_cpu = cpu_attn is not None and bool((cache.host_len[layer] > 0).any())
+    worker = None
+    if need_cpu:
+        q_host = q.view(B * Hkv, G, D).cpu()
+
+        def host_partial():
+            fmt = CPU_FORMATS[cpu_format]
+            odt = torch.bfloat16 if fmt == ops.TRIPLE_NORM_BF16 else torch.float32
+            o = torch.zeros((B * Hkv, G, D), dtype=odt)
+            m = torch.full((B * Hkv, G, 1), float("-inf"), dtype=odt)
+            s = torch.zeros((B * Hkv, G, 1), dtype=odt)
+            for b in range(B):
+                k, v = cache.host_rows(layer, b)
+                if k.shape[1] == 0:
+                    continue
+                rows = slice(b * Hkv, (b + 1) * Hkv)
+                ob, mb, sb = cpu_attn(q_host[rows].contiguous(), k, v, scale)
+                o[rows], m[rows], s[rows] = ob.to(odt), mb.reshape(Hkv, G, 1).to(odt), \
+                    sb.reshape(Hkv, G, 1).to(odt)
+            return o, m, s
+
+        worker = _CpuPartial(host_partial)
+        worker.start()
+    out_g, lse_g = gpu.attend(layer, q, scale, tokens_per_split)
+    if worker is None:
+        empty = torch.full_like(lse_g, float("-inf"))
+        out, _ = ops.lse_merge(out_g, lse_g, (out_g, empty), ops.PARTIAL_LSE_F32,
+                               want_lse=False)
+        return out.view(B, Hq, 1, D)
+    o, m, s = worker.join_result()
+    dev = q.device
+    triple = tuple(_to_device_pinned(x, dev) for x in (o, m, s))
+    out, _ = ops.lse_merge(out_g, lse_g, triple, CPU_FORMATS[cpu_format], want_lse=False)
+    return out.view(B, Hq, 1, D)
+
+
+def partitioned_mla_decode(cache: PartitionedLatentCache, layer: int,
+                           q_nope: torch.Tensor, q_pe: torch.Tensor, scale: float,
+                           cpu_attn_mla_compressed=None, c_new=None, pe_new=None,
+                           tokens_per_split=0):
+    """One decode step of absorbed-MLA attention over a partitioned latent cache.
+
+    q_nope [B*H, 512] (W_UK-absorbed) and q_pe [B*H, 64] bf16 on the GPU;
+    c_new [B, 1, 512] / pe_new [B, 1, 64] are appended first (split at the
+    boundary like system/deepseek.py:171-192).  The host partial runs
+    cpu_attn_mla_compressed(q_proj, q_pe, c, pe, scale) -> fp32 (o, max, sum)
+    over the host segment on a worker thread while the GPU partial runs.
+    Returns the merged latent output [B*H, 512] bf16 (before W_UV).
+    """
+    if c_new is not None:
+        cache.append(layer, c_new, pe_new)
+    (hc, hpe), gpu = cache.get(layer)
+    worker = None
+    if cpu_attn_mla_compressed is not None and hc.shape[1] > 0:
+        qn_host, qp_host = q_nope.cpu(), q_pe.cpu()
+        worker = _CpuPartial(lambda: cpu_attn_mla_compressed(
+            qn_host, qp_host, hc.contiguous(), hpe.contiguous(), scale))
+        worker.start()
+    out_g, lse_g = gpu.attend(layer, q_nope, q_pe, scale, tokens_per_split)
+    if worker is None:
+        empty = torch.full_like(lse_g, float("-inf"))
+        out, _ = ops.lse_merge(out_g, lse_g, (out_g, empty), ops.PARTIAL_LSE_F32,
+                               want_lse=False)
+        return out
+    o, m, s = worker.join_result()
+    dev = q_nope.device
+    triple = tuple(_to_device_pinned(x.float().contiguous(), dev) for x in (o, m, s))
+    out, _ = ops.lse_merge(out_g, lse_g, triple, ops.TRIPLE_UNNORM_F32, want_lse=False)
+    return out

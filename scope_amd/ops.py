@@ -1,0 +1,357 @@
+"""Operator surface of the GPU KV partition over the gfx950 C-ABI library.
+
+Thin ctypes layer: validates shapes/dtypes/devices, passes data pointers and
+the current HIP stream to scope_amd/lib/libwsgpu.so (include/wsgpu.h) and
+raises on any error.  There is no fallback: if the library is missing or a
+tensor is not on a GPU, the call fails.
+
+Tensor conventions (all CUDA/HIP tensors, contiguous):
+  GQA pools   k_pages, v_pages  [num_pages, Hkv, page_size, D] bfloat16
+  MLA pool    latent_pages      [num_pages, page_size, 576]    bfloat16
+  page_table  [B, max_pages] int32, gpu_len [B] int32
+  partials    (out fp32 normalised, lse fp32 natural log); empty = (0, -inf)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libwsgpu.so")
+
+# Entry points declared in include/wsgpu.h.
+EXPORTS = (
+    "ws_last_error",
+    "ws_version",
+    "ws_kv_append",
+    "ws_latent_append",
+    "ws_decode_workspace_bytes",
+    "ws_decode_plan",
+    "ws_gqa_decode_partial",
+    "ws_mla_decode_partial",
+    "ws_split_reduce",
+    "ws_lse_merge",
+)
+
+# Formats of the second operand of lse_merge (include/wsgpu.h).
+PARTIAL_LSE_F32 = 0
+TRIPLE_UNNORM_F32 = 1
+TRIPLE_NORM_BF16 = 2
+TRIPLE_NORM_F32 = 3
+
+MLA_LATENT = 576
+MLA_C = 512
+MLA_PE = 64
+
+
+class WsError(RuntimeError):
+    """A libwsgpu entry point returned an error."""
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libwsgpu.so (torch is imported first so that the process keeps a
+    single HIP runtime)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m scope_amd._build` "
+                "(or __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i32, i64, f32, sz = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64,
+                                 ctypes.c_float, ctypes.c_size_t)
+        L.ws_last_error.restype = ctypes.c_char_p
+        L.ws_last_error.argtypes = []
+        L.ws_version.restype = ctypes.c_char_p
+        L.ws_version.argtypes = []
+        L.ws_kv_append.restype = i32
+        L.ws_kv_append.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32,
+                                   i32, i32, i32, i32, vp]
+        L.ws_latent_append.restype = i32
+        L.ws_latent_append.argtypes = [vp, i64, vp, i64, vp, vp, vp, i32, i32,
+                                       i32, i32, i32, i32, vp]
+        L.ws_decode_workspace_bytes.restype = sz
+        L.ws_decode_workspace_bytes.argtypes = [i32, i32, i32]
+        L.ws_decode_plan.restype = i32
+        L.ws_decode_plan.argtypes = [i32, i32, i32, i32,
+                                     ctypes.POINTER(i32), ctypes.POINTER(i32)]
+        L.ws_gqa_decode_partial.restype = i32
+        L.ws_gqa_decode_partial.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32,
+                                            i32, i32, i32, i32, i32, i32, f32,
+                                            vp, vp, vp, sz, vp]
+        L.ws_mla_decode_partial.restype = i32
+        L.ws_mla_decode_partial.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32,
+                                            i32, i32, i32, i32, f32, vp, vp,
+                                            vp, sz, vp]
+        L.ws_split_reduce.restype = i32
+        L.ws_split_reduce.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp,
+                                      vp, vp]
+        L.ws_lse_merge.restype = i32
+        L.ws_lse_merge.argtypes = [vp, vp, vp, vp, vp, i32, vp, vp, vp, i32,
+                                   i32, vp]
+        _lib = L
+    return _lib
+
+
+def _check(rc: int, name: str) -> None:
+    if rc != 0:
+        raise WsError(f"{name}: {lib().ws_last_error().decode()} (rc={rc})")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require(t: torch.Tensor, name: str, dtype: torch.dtype, device=None,
+             ndim=None, contiguous=True) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be on a GPU (got {t.device})")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must have {ndim} dims (got {tuple(t.shape)})")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+# ---------------------------------------------------------------------------
+# workspace
+
+_workspaces: dict = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device scratch for split partials, grown on demand (stream-ordered
+    reuse is safe on the stream that launched the decode kernels)."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def decode_plan(kind: int, rows_kv: int, max_len: int, tokens_per_split: int = 0):
+    """(tokens_per_split, n_splits) the library uses for a decode call."""
+    tps, ns = ctypes.c_int(0), ctypes.c_int(0)
+    _check(lib().ws_decode_plan(kind, rows_kv, max_len, tokens_per_split,
+                                ctypes.byref(tps), ctypes.byref(ns)), "ws_decode_plan")
+    return tps.value, ns.value
+
+
+# ---------------------------------------------------------------------------
+# append
+
+
+def kv_append(k_new, v_new, k_pages, v_pages, page_table, gpu_len, update_len=True):
+    """Write k_new/v_new [B, Hkv, n_new, D] at slots gpu_len[b].. of each
+    sequence's pages (bit copies), then gpu_len += n_new if update_len."""
+    dev = k_pages.device
+    _require(k_new, "k_new", torch.bfloat16, dev, 4)
+    _require(v_new, "v_new", torch.bfloat16, dev, 4)
+    _require(k_pages, "k_pages", torch.bfloat16, dev, 4)
+    _require(v_pages, "v_pages", torch.bfloat16, dev, 4)
+    _require(page_table, "page_table", torch.int32, dev, 2)
+    _require(gpu_len, "gpu_len", torch.int32, dev, 1)
+    B, Hkv, n_new, D = k_new.shape
+    P, Hkv2, PS, D2 = k_pages.shape
+    if v_new.shape != k_new.shape or v_pages.shape != k_pages.shape:
+        raise ValueError("k/v shapes differ")
+    if Hkv2 != Hkv or D2 != D or page_table.shape[0] != B or gpu_len.shape[0] != B:
+        raise ValueError(
+            f"shape mismatch: new {tuple(k_new.shape)} pages {tuple(k_pages.shape)} "
+            f"page_table {tuple(page_table.shape)} gpu_len {tuple(gpu_len.shape)}")
+    _check(lib().ws_kv_append(_ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages),
+                              _ptr(page_table), _ptr(gpu_len), B, Hkv, D, n_new, PS,
+                              page_table.shape[1], P, int(bool(update_len)),
+                              _stream(dev)), "ws_kv_append")
+
+
+def latent_append(c_new, pe_new, latent_pages, page_table, gpu_len, update_len=True):
+    """Write c_new [B, n_new, 512] and pe_new [B, n_new, 64] as the 576-wide
+    latent at slots gpu_len[b].. of each sequence's pages."""
+    dev = latent_pages.device
+    for t, n in ((c_new, "c_new"), (pe_new, "pe_new")):
+        _require(t, n, torch.bfloat16, dev, 3, contiguous=False)
+        if t.stride(2) != 1 or t.stride(0) != t.shape[1] * t.stride(1):
+            raise ValueError(f"{n} must be [B, n, W] with unit last stride and "
+                             "batch stride n * row stride")
+    _require(latent_pages, "latent_pages", torch.bfloat16, dev, 3)
+    _require(page_table, "page_table", torch.int32, dev, 2)
+    _require(gpu_len, "gpu_len", torch.int32, dev, 1)
+    B, n_new, W = c_new.shape
+    P, PS, L = latent_pages.shape
+    if W != MLA_C or pe_new.shape != (B, n_new, MLA_PE) or L != MLA_LATENT:
+        raise ValueError("latent layout is 512 c_kv + 64 k_pe = 576")
+    if page_table.shape[0] != B or gpu_len.shape[0] != B:
+        raise ValueError("page_table/gpu_len batch mismatch")
+    _check(lib().ws_latent_append(_ptr(c_new), c_new.stride(1), _ptr(pe_new),
+                                  pe_new.stride(1), _ptr(latent_pages), _ptr(page_table),
+                                  _ptr(gpu_len), B, n_new, PS, page_table.shape[1], P,
+                                  int(bool(update_len)), _stream(dev)),
+           "ws_latent_append")
+
+
+# ---------------------------------------------------------------------------
+# decode partials
+
+
+def gqa_decode_partial(q, k_pages, v_pages, page_table, gpu_len, scale, max_len,
+                       tokens_per_split=0, out=None, lse=None):
+    """Split-KV GQA decode attention over the pooled tokens.
+
+    q [B, Hq, D] bf16 -> (out [B, Hq, D] fp32 normalised, lse [B, Hq] fp32).
+    max_len must bound every gpu_len[b] (the host's mirror of the lengths).
+    """
+    dev = k_pages.device
+    _require(q, "q", torch.bfloat16, dev, 3)
+    _require(k_pages, "k_pages", torch.bfloat16, dev, 4)
+    _require(v_pages, "v_pages", torch.bfloat16, dev, 4)
+    _require(page_table, "page_table", torch.int32, dev, 2)
+    _require(gpu_len, "gpu_len", torch.int32, dev, 1)
+    B, Hq, D = q.shape
+    P, Hkv, PS, D2 = k_pages.shape
+    if v_pages.shape != k_pages.shape or D2 != D:
+        raise ValueError("k/v page pools must match q's head_dim")
+    if page_table.shape[0] != B or gpu_len.shape[0] != B:
+        raise ValueError("page_table/gpu_len batch mismatch")
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device=dev)
+    if lse is None:
+        lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
+    _require(out, "out", torch.float32, dev, 3)
+    _require(lse, "lse", torch.float32, dev, 2)
+    tps, ns = decode_plan(0, B * Hkv, int(max_len), int(tokens_per_split))
+    ws, wsb = None, 0
+    if ns > 1:
+        wsb = lib().ws_decode_workspace_bytes(B * Hq, D, ns)
+        ws = _workspace(dev, wsb)
+    _check(lib().ws_gqa_decode_partial(
+        _ptr(q), _ptr(k_pages), _ptr(v_pages), _ptr(page_table), _ptr(gpu_len),
+        B, Hq, Hkv, D, PS, page_table.shape[1], P, int(max_len), tps, float(scale),
+        _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev)), "ws_gqa_decode_partial")
+    return out, lse
+
+
+def mla_decode_partial(q_nope, q_pe, latent_pages, page_table, gpu_len, scale, max_len,
+                       tokens_per_split=0, out=None, lse=None):
+    """Split-KV absorbed-MLA decode attention over the pooled latents.
+
+    q_nope [B*H, 512] bf16 (W_UK-absorbed), q_pe [B*H, 64] bf16 ->
+    (out [B*H, 512] fp32 normalised, lse [B*H] fp32).
+    """
+    dev = latent_pages.device
+    _require(q_nope, "q_nope", torch.bfloat16, dev, 2)
+    _require(q_pe, "q_pe", torch.bfloat16, dev, 2)
+    _require(latent_pages, "latent_pages", torch.bfloat16, dev, 3)
+    _require(page_table, "page_table", torch.int32, dev, 2)
+    _require(gpu_len, "gpu_len", torch.int32, dev, 1)
+    P, PS, L = latent_pages.shape
+    B = page_table.shape[0]
+    rows = q_nope.shape[0]
+    if L != MLA_LATENT or q_nope.shape[1] != MLA_C or q_pe.shape != (rows, MLA_PE):
+        raise ValueError("MLA layout is q_nope 512 + q_pe 64 over a 576 latent")
+    if B == 0 or rows % B or gpu_len.shape[0] != B:
+        raise ValueError("rows must be B * H with B = page_table.shape[0]")
+    H = rows // B
+    if out is None:
+        out = torch.empty((rows, MLA_C), dtype=torch.float32, device=dev)
+    if lse is None:
+        lse = torch.empty((rows,), dtype=torch.float32, device=dev)
+    _require(out, "out", torch.float32, dev, 2)
+    _require(lse, "lse", torch.float32, dev, 1)
+    tps, ns = decode_plan(1, B, int(max_len), int(tokens_per_split))
+    ws, wsb = None, 0
+    if ns > 1:
+        wsb = lib().ws_decode_workspace_bytes(rows, MLA_C, ns)
+        ws = _workspace(dev, wsb)
+    _check(lib().ws_mla_decode_partial(
+        _ptr(q_nope), _ptr(q_pe), _ptr(latent_pages), _ptr(page_table), _ptr(gpu_len),
+        B, H, PS, page_table.shape[1], P, int(max_len), tps, float(scale),
+        _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev)), "ws_mla_decode_partial")
+    return out, lse
+
+
+def split_reduce(part_out, part_lse, gpu_len, heads_per_len, tokens_per_split,
+                 out=None, lse=None):
+    """LSE-combine split partials part_out [n_splits, rows, Dv],
+    part_lse [n_splits, rows] (see ws_split_reduce)."""
+    dev = part_out.device
+    _require(part_out, "part_out", torch.float32, dev, 3)
+    _require(part_lse, "part_lse", torch.float32, dev, 2)
+    _require(gpu_len, "gpu_len", torch.int32, dev, 1)
+    ns, rows, Dv = part_out.shape
+    if out is None:
+        out = torch.empty((rows, Dv), dtype=torch.float32, device=dev)
+    if lse is None:
+        lse = torch.empty((rows,), dtype=torch.float32, device=dev)
+    _check(lib().ws_split_reduce(_ptr(part_out), _ptr(part_lse), _ptr(gpu_len), rows,
+                                 int(heads_per_len), Dv, ns, int(tokens_per_split),
+                                 _ptr(out), _ptr(lse), _stream(dev)), "ws_split_reduce")
+    return out, lse
+
+
+# ---------------------------------------------------------------------------
+# merge
+
+
+def lse_merge(out_g, lse_g, b, fmt=PARTIAL_LSE_F32, out_dtype=torch.bfloat16,
+              want_lse=True, out=None, lse_out=None):
+    """Merge the GPU partial (out_g [..., Dv] fp32, lse_g [...] fp32) with a
+    second partial `b`:
+      fmt PARTIAL_LSE_F32   b = (out fp32, lse fp32)
+      fmt TRIPLE_UNNORM_F32 b = (o unnormalised fp32, max fp32, sum fp32)
+      fmt TRIPLE_NORM_BF16  b = (out bf16 normalised, max bf16, sum bf16)
+      fmt TRIPLE_NORM_F32   b = (out fp32 normalised, max fp32, sum fp32)
+    Returns (merged out in out_dtype (bf16 or fp32), lse fp32 or None)."""
+    dev = out_g.device
+    _require(out_g, "out_g", torch.float32, dev)
+    _require(lse_g, "lse_g", torch.float32, dev)
+    Dv = out_g.shape[-1]
+    rows = out_g.numel() // Dv
+    if lse_g.numel() != rows:
+        raise ValueError("lse_g must have one value per output row")
+    if fmt == PARTIAL_LSE_F32:
+        b_out, b_aux0 = b
+        b_aux1 = None
+        _require(b_out, "b.out", torch.float32, dev)
+        _require(b_aux0, "b.lse", torch.float32, dev)
+    else:
+        b_out, b_aux0, b_aux1 = b
+        dt = torch.bfloat16 if fmt == TRIPLE_NORM_BF16 else torch.float32
+        _require(b_out, "b.out", dt, dev)
+        _require(b_aux0, "b.max", dt, dev)
+        _require(b_aux1, "b.sum", dt, dev)
+        if b_aux1.numel() != rows:
+            raise ValueError("b.sum must have one value per row")
+    if b_out.numel() != rows * Dv or b_aux0.numel() != rows:
+        raise ValueError("second partial does not match the GPU partial's shape")
+    if out is None:
+        out = torch.empty(out_g.shape, dtype=out_dtype, device=dev)
+    if want_lse and lse_out is None:
+        lse_out = torch.empty(lse_g.shape, dtype=torch.float32, device=dev)
+    if out.dtype == torch.bfloat16:
+        o16, o32 = out, None
+    elif out.dtype == torch.float32:
+        o16, o32 = None, out
+    else:
+        raise TypeError("merged output must be bfloat16 or float32")
+    _require(out, "out", out.dtype, dev)
+    _check(lib().ws_lse_merge(_ptr(out_g), _ptr(lse_g), _ptr(b_out), _ptr(b_aux0),
+                              _ptr(b_aux1), int(fmt), _ptr(o16), _ptr(o32),
+                              _ptr(lse_out if want_lse else None), rows, Dv,
+                              _stream(dev)), "ws_lse_merge")
+    return out, (lse_out if want_lse else None)

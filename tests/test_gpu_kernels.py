@@ -1,0 +1,289 @@
+"""GPU parity of the gfx950 kernels through the C-ABI (ops layer) against the
+oracle: fp64 closed forms and the C restatement of the reference CPU kernels.
+
+Bar: appends and page indexing bit-exact; outputs within 2e-2 abs/rel; fp32
+LSE within 1e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn_np as O
+from oracle import port
+from scope_amd import ops
+from tests.gpu_pool import gqa_pool, mla_pool, page_layout
+from tests.helpers import (LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, assert_close,
+                           bf16_randn, bits)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# append
+
+
+@pytest.mark.parametrize("n_new_seq", [[1, 1, 1, 1], [5, 70, 1], [64, 3]])
+def test_kv_append_bit_exact(n_new_seq):
+    _say(f"kv_append n_new_seq={n_new_seq}")
+    B, Hkv, D, PS = 3, 8, 128, 64
+    total = sum(n_new_seq)
+    table, num_pages = page_layout([total] * B, PS, seed=7)
+    k_pages = torch.zeros((num_pages, Hkv, PS, D), dtype=torch.bfloat16, device=DEV)
+    v_pages = torch.zeros_like(k_pages)
+    pt = torch.from_numpy(table).to(DEV)
+    gl = torch.zeros(B, dtype=torch.int32, device=DEV)
+    ks, vs = [], []
+    for i, n in enumerate(n_new_seq):
+        k = bf16_randn((B, Hkv, n, D), 100 + i)
+        v = bf16_randn((B, Hkv, n, D), 200 + i)
+        ops.kv_append(k.to(DEV), v.to(DEV), k_pages, v_pages, pt, gl)
+        ks.append(k); vs.append(v)
+    torch.cuda.synchronize()
+    assert gl.cpu().tolist() == [total] * B
+    want_k = torch.cat(ks, 2)
+    want_v = torch.cat(vs, 2)
+    kp, vp = bits(k_pages), bits(v_pages)
+    for b in range(B):
+        for h in range(Hkv):
+            got_k = O.gather_paged(kp, table, [total] * B, head=h)[b]
+            got_v = O.gather_paged(vp, table, [total] * B, head=h)[b]
+            assert np.array_equal(got_k, bits(want_k[b, h]))
+            assert np.array_equal(got_v, bits(want_v[b, h]))
+    # untouched pages stay zero
+    used = set(table[table >= 0].ravel().tolist())
+    for pid in range(num_pages):
+        if pid not in used:
+            assert not kp[pid].any()
+    # update_len=False leaves lengths alone
+    ops.kv_append(ks[0].to(DEV), vs[0].to(DEV), k_pages, v_pages, pt,
+                  torch.zeros(B, dtype=torch.int32, device=DEV), update_len=False)
+    torch.cuda.synchronize()
+
+
+def test_latent_append_bit_exact_strided():
+    _say("latent_append strided")
+    B, PS = 2, 64
+    steps = [1, 63, 2, 100]
+    total = sum(steps)
+    table, num_pages = page_layout([total] * B, PS, seed=9)
+    lat = torch.zeros((num_pages, PS, 576), dtype=torch.bfloat16, device=DEV)
+    pt = torch.from_numpy(table).to(DEV)
+    gl = torch.zeros(B, dtype=torch.int32, device=DEV)
+    full = []
+    for i, n in enumerate(steps):
+        kv = bf16_randn((B, n, 576), 300 + i).to(DEV)  # kv_a_proj-like [B, n, 576]
+        c, pe = kv[..., :512], kv[..., 512:]           # strided views (row stride 576)
+        ops.latent_append(c, pe, lat, pt, gl)
+        full.append(kv.cpu())
+    torch.cuda.synchronize()
+    assert gl.cpu().tolist() == [total] * B
+    want = torch.cat(full, 1)
+    got = O.gather_paged(bits(lat), table, [total] * B)
+    for b in range(B):
+        assert np.array_equal(got[b], bits(want[b]))
+
+
+# ---------------------------------------------------------------------------
+# GQA partial
+
+
+def _gqa_check(lens, Hkv, G, PS=64, tps=0, seed=1, sigma=1.0, port_check=True):
+    D = 128
+    B = len(lens)
+    _say(f"gqa lens={list(lens)[:8]}{'...' if B > 8 else ''} Hkv={Hkv} G={G} PS={PS} tps={tps}")
+    k_pages, v_pages, pt, gl, ks, vs = gqa_pool(lens, Hkv, D, PS, seed, DEV, sigma)
+    q = bf16_randn((B, Hkv * G, D), seed + 77, sigma)
+    scale = D ** -0.5
+    out, lse = ops.gqa_decode_partial(q.to(DEV), k_pages, v_pages, pt, gl, scale,
+                                      max(lens), tokens_per_split=tps)
+    torch.cuda.synchronize()
+    out, lse = out.cpu().numpy(), lse.cpu().numpy()
+    qb = bits(q).reshape(B, Hkv, G, D)
+    for b in range(B):
+        want, wl = O.gqa_attention_fp64(qb[b], bits(ks[b]), bits(vs[b]), scale)
+        assert_close(out[b].reshape(Hkv, G, D), want, OUT_ATOL, OUT_RTOL, f"out b={b}")
+        assert_close(lse[b].reshape(Hkv, G), wl, LSE_ATOL, LSE_RTOL, f"lse b={b}")
+        if port_check and lens[b] > 0:
+            po, pm, ps = port.cpu_attn(qb[b], bits(ks[b]), bits(vs[b]), scale,
+                                       normalize=True, n_threads=8)
+            assert_close(out[b].reshape(Hkv, G, D), po, OUT_ATOL, OUT_RTOL, f"port b={b}")
+            assert_close(lse[b].reshape(Hkv, G), (pm + np.log(ps))[..., 0],
+                         LSE_ATOL, LSE_RTOL, f"port lse b={b}")
+    return out, lse
+
+
+def test_gqa_config1_qwen3_single_partition():
+    # B=1, 32 q heads / 4 KV heads, D 128, L 4096 in one partition
+    _gqa_check([4096], Hkv=4, G=8, seed=1000)
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+def test_gqa_group_sizes(G):
+    _gqa_check([300, 64, 1], Hkv=2, G=G, seed=40 + G)
+
+
+@pytest.mark.parametrize("tps", [0, 32, 64, 96, 256])
+def test_gqa_ragged_lengths_and_splits(tps):
+    lens = [0, 1, 31, 32, 33, 63, 64, 65, 127, 1000]
+    _gqa_check(lens, Hkv=8, G=4, tps=tps, seed=5)
+
+
+def test_gqa_page_size_128_and_32():
+    _gqa_check([500, 129], Hkv=4, G=8, PS=128, seed=6)
+    _gqa_check([500, 129], Hkv=4, G=8, PS=32, seed=6)
+
+
+def test_gqa_large_scores_no_overflow():
+    # sigma 4 -> scores ~ N(0, 16^2 / ...) large; online rescale must hold
+    _gqa_check([700], Hkv=4, G=8, seed=8, sigma=4.0)
+
+
+def test_gqa_split_invariance_and_page_permutation():
+    lens = [3000, 2500]
+    k_pages, v_pages, pt, gl, ks, vs = gqa_pool(lens, 8, 128, 64, 11, DEV)
+    q = bf16_randn((2, 32, 128), 12).to(DEV)
+    res = [ops.gqa_decode_partial(q, k_pages, v_pages, pt, gl, 0.0884, 3000,
+                                  tokens_per_split=t) for t in (64, 512, 4096)]
+    # P is rounded to bf16 against each split's running max, so outputs of
+    # different split sizes differ at the bf16 level; the fp32 sums keep the
+    # LSE split-independent to fp32 rounding.
+    for o, l in res[1:]:
+        assert_close(o.cpu().numpy(), res[0][0].cpu().numpy(), 2e-3, 2e-3, "split inv")
+        assert_close(l.cpu().numpy(), res[0][1].cpu().numpy(), 1e-5, 1e-5, "split inv lse")
+    # moving pages to other physical ids changes nothing, bit for bit
+    perm = torch.randperm(k_pages.shape[0], generator=torch.Generator().manual_seed(3)).to(DEV)
+    inv = torch.empty_like(perm); inv[perm] = torch.arange(perm.numel(), device=DEV)
+    k2 = torch.empty_like(k_pages); v2 = torch.empty_like(v_pages)
+    k2[inv] = k_pages; v2[inv] = v_pages
+    pt2 = torch.where(pt >= 0, inv[pt.long().clamp(min=0)].int(), pt)
+    o2, l2 = ops.gqa_decode_partial(q, k2, v2, pt2, gl, 0.0884, 3000, tokens_per_split=512)
+    assert torch.equal(o2, res[1][0]) and torch.equal(l2, res[1][1])
+
+
+# ---------------------------------------------------------------------------
+# MLA partial
+
+
+def _mla_check(lens, tps=0, seed=3, sigma=0.5, PS=64):
+    B, H = len(lens), 16
+    _say(f"mla lens={lens} tps={tps} PS={PS}")
+    lat, pt, gl, cs, pes = mla_pool(lens, PS, seed, DEV, sigma)
+    qn = bf16_randn((B * H, 512), seed + 91, sigma)
+    qp = bf16_randn((B * H, 64), seed + 92, sigma)
+    scale = 192 ** -0.5
+    out, lse = ops.mla_decode_partial(qn.to(DEV), qp.to(DEV), lat, pt, gl, scale,
+                                      max(lens), tokens_per_split=tps)
+    torch.cuda.synchronize()
+    out, lse = out.cpu().numpy(), lse.cpu().numpy()
+    for b in range(B):
+        rows = slice(b * H, (b + 1) * H)
+        c, pe = bits(cs[b])[None], bits(pes[b])[None]
+        want, wl = O.mla_attention_fp64(bits(qn[rows]), bits(qp[rows]), c, pe, scale)
+        assert_close(out[rows], want, OUT_ATOL, OUT_RTOL, f"mla out b={b}")
+        assert_close(lse[rows], wl, LSE_ATOL, LSE_RTOL, f"mla lse b={b}")
+        if lens[b] > 0:
+            po, pm, ps = port.cpu_attn_mla_compressed(bits(qn[rows]), bits(qp[rows]), c, pe,
+                                                      scale, n_threads=8)
+            assert_close(out[rows], po / ps[:, None], OUT_ATOL, OUT_RTOL, f"port b={b}")
+            assert_close(lse[rows], pm + np.log(ps), LSE_ATOL, LSE_RTOL, f"port lse b={b}")
+
+
+@pytest.mark.parametrize("tps", [0, 32, 64, 256])
+def test_mla_ragged(tps):
+    _mla_check([0, 1, 37, 300, 1030], tps=tps)
+
+
+def test_mla_config3_shape_subset():
+    # DS-V2-Lite absorbed: H 16, latent 576, N(0, 0.5), L 16384 with r 0.5
+    _mla_check([8192, 8192], seed=3000)
+
+
+# ---------------------------------------------------------------------------
+# split reduce and merge
+
+
+def test_split_reduce_direct():
+    # 3 sequences x 3 heads: len 0 -> (0, -inf); len 64 with 64-token splits
+    # -> one split, row left untouched; len 200 -> 4 splits merged
+    rows, Dv, ns, tps, H = 9, 128, 4, 64, 3
+    lens = torch.tensor([0, 64, 200], dtype=torch.int32, device=DEV)
+    g = torch.Generator().manual_seed(4)
+    po = torch.randn((ns, rows, Dv), generator=g)
+    pl = torch.randn((ns, rows), generator=g) * 3
+    out = torch.full((rows, Dv), 7.0, device=DEV)
+    lse = torch.full((rows,), 7.0, device=DEV)
+    ops.split_reduce(po.to(DEV), pl.to(DEV), lens, H, tps, out, lse)
+    torch.cuda.synchronize()
+    o, l = out.cpu().numpy(), lse.cpu().numpy()
+    assert np.all(o[0:3] == 0) and np.all(np.isneginf(l[0:3]))
+    assert np.all(o[3:6] == 7.0) and np.all(l[3:6] == 7.0)
+    acc = (po[0, 6:9].numpy().astype(np.float64), pl[0, 6:9].numpy().astype(np.float64))
+    for s in range(1, 4):
+        acc = O.merge_fp64(*acc, po[s, 6:9].numpy(), pl[s, 6:9].numpy())
+    assert_close(o[6:9], acc[0], 1e-5, 1e-5, "reduce out")
+    assert_close(l[6:9], acc[1], 1e-5, 1e-5, "reduce lse")
+
+
+def test_split_reduce_merges_valid_splits():
+    rows, Dv, ns, tps, H = 2, 512, 5, 32, 2
+    lens = torch.tensor([100], dtype=torch.int32, device=DEV)  # 4 valid splits of 5
+    g = torch.Generator().manual_seed(5)
+    po = torch.randn((ns, rows, Dv), generator=g)
+    pl = torch.randn((ns, rows), generator=g) * 4
+    out, lse = ops.split_reduce(po.to(DEV), pl.to(DEV), lens, H, tps)
+    torch.cuda.synchronize()
+    acc = (po[0].numpy().astype(np.float64), pl[0].numpy().astype(np.float64))
+    for s in range(1, 4):
+        acc = O.merge_fp64(*acc, po[s].numpy(), pl[s].numpy())
+    assert_close(out.cpu().numpy(), acc[0], 1e-5, 1e-5, "reduce out")
+    assert_close(lse.cpu().numpy(), acc[1], 1e-5, 1e-5, "reduce lse")
+
+
+@pytest.mark.parametrize("fmt", [ops.PARTIAL_LSE_F32, ops.TRIPLE_UNNORM_F32,
+                                 ops.TRIPLE_NORM_BF16, ops.TRIPLE_NORM_F32])
+@pytest.mark.parametrize("Dv", [128, 512])
+def test_lse_merge_formats(fmt, Dv):
+    _say(f"lse_merge fmt={fmt} Dv={Dv}")
+    rows = 40
+    rng = np.random.default_rng(fmt * 10 + Dv)
+    oa = rng.standard_normal((rows, Dv)).astype(np.float32)
+    la = (rng.standard_normal(rows) * 3).astype(np.float32)
+    ob = rng.standard_normal((rows, Dv)).astype(np.float32)
+    mb = (rng.standard_normal(rows) * 3).astype(np.float32)
+    sb = rng.uniform(1, 50, rows).astype(np.float32)
+    # empties: row 0 GPU empty, row 1 host empty, row 2 both
+    la[0] = -np.inf; oa[0] = 0
+    sb[1] = 0.0; mb[1] = -np.inf
+    la[2] = -np.inf; oa[2] = 0; sb[2] = 0.0; mb[2] = -np.inf
+    if fmt == ops.PARTIAL_LSE_F32:
+        lb = np.where(sb > 0, mb + np.log(np.where(sb > 0, sb, 1)), -np.inf).astype(np.float32)
+        b = (torch.from_numpy(ob).to(DEV), torch.from_numpy(lb).to(DEV))
+        ob_n, lb_n = np.where(sb[:, None] > 0, ob, 0), lb
+    elif fmt == ops.TRIPLE_UNNORM_F32:
+        ou = np.where(sb[:, None] > 0, ob * sb[:, None], 0).astype(np.float32)
+        b = tuple(torch.from_numpy(x).to(DEV) for x in (ou, mb, sb))
+        ob_n, lb_n = O.triple_to_partial(ou, mb, sb, normalized=False)
+    elif fmt == ops.TRIPLE_NORM_F32:
+        b = tuple(torch.from_numpy(x).to(DEV) for x in (ob, mb, sb))
+        ob_n, lb_n = O.triple_to_partial(ob, mb, sb, normalized=True)
+    else:
+        ob16, mb16, sb16 = (torch.from_numpy(x).to(torch.bfloat16) for x in (ob, mb, sb))
+        b = tuple(x.to(DEV) for x in (ob16, mb16, sb16))
+        ob_n, lb_n = O.triple_to_partial(ob16.float().numpy(), mb16.float().numpy(),
+                                         sb16.float().numpy(), normalized=True)
+    want_o, want_l = O.merge_fp64(oa, la, ob_n, lb_n)
+    for odt in (torch.bfloat16, torch.float32):
+        out, lse = ops.lse_merge(torch.from_numpy(oa).to(DEV), torch.from_numpy(la).to(DEV),
+                                 b, fmt, out_dtype=odt)
+        torch.cuda.synchronize()
+        got = out.float().cpu().numpy()
+        assert np.isfinite(got).all()
+        assert_close(got, want_o, OUT_ATOL if odt == torch.bfloat16 else 1e-5,
+                     OUT_RTOL if odt == torch.bfloat16 else 1e-5, "merge out")
+        assert_close(lse.cpu().numpy(), want_l, 1e-5, 1e-5, "merge lse")
+    assert np.all(got[2] == 0) and np.isneginf(lse.cpu().numpy()[2])
