@@ -1,0 +1,545 @@
+"""Decode-step benchmark of the GPU KV partition on one MI355X.
+
+Headline workload (one "step" = one decode step of one attention layer):
+partitioned GQA decode at the Mixtral-8x7B layer shape: batch 16, 32 query
+heads, 8 KV heads, head_dim 128, bf16 N(0,1), per-sequence KV lengths uniform
+in [1024, 32768], the trailing floor(r*L) tokens of each sequence in 64-token
+HBM pages (r = 0.5 by default).  A step appends one token per sequence to the
+GPU partition, runs the split-KV GQA partial over the partition and LSE-merges
+it with the host partial (the bf16 (out, max, sum) triple of the CPU kernel,
+already resident in HBM) into the final bf16 output.
+
+Reported on one JSON line (stdout):
+  value      algorithmic HBM GB/s of the whole step (bytes below / step time)
+  ms_per_step, us_per_layer
+  roofline   the GQA partial kernel: algorithmic bytes per launch / its mean
+             duration from HIP events around every launch of the timed region,
+             against the 8 TB/s HBM peak; traffic from the committed rocprofv3
+             FETCH_SIZE / WRITE_SIZE summary when one exists for this workload
+  cpu_baseline  the oracle's C restatement of the reference CPU kernel over a
+             bounded sample of the same GPU-share tokens, on the host cores
+  by_share, kv_len_sweep, mla, single_partition
+             the other shares, the Qwen3 length sweep (batch 4, r = 1), the
+             absorbed-MLA layer (DeepSeek-V2-Lite, batch 8, L 16384, r 0.5)
+             and the batch-1 Qwen3 layer with all 4096 tokens on the GPU
+
+Algorithmic bytes of a step (each byte once): KV of every GPU token read,
+Q read, GPU partial (out fp32 + lse) written, host partial read, final bf16
+output written, appended token written, page-table entries read.
+
+Run: python bench.py [--gpus 1] [--steps K] [--warmup W] [--share r]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import re
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = ("GPU-partition decode attn µs/layer + HBM GB/s (% peak) vs KV len; "
+          "CPU ref alongside")
+PAGE = 64
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# paged pools
+
+
+def _page_table(gpu_tokens, capacity_extra, rng):
+    """Fragmented page assignment: every sequence gets the pages for its GPU
+    tokens plus room for the appends, page ids drawn from a random permutation."""
+    need = [-(-(int(g) + capacity_extra) // PAGE) for g in gpu_tokens]
+    max_pages = max(1, max(need))
+    num_pages = sum(need)
+    perm = rng.permutation(num_pages).astype(np.int32)
+    table = np.full((len(need), max_pages), -1, np.int32)
+    k = 0
+    for b, n in enumerate(need):
+        table[b, :n] = perm[k:k + n]
+        k += n
+    return table, num_pages
+
+
+def _randn_bf16(shape, gen, sigma, dev):
+    import torch
+
+    t = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    # fill in slabs to bound the fp32 temporary
+    flat = t.view(-1)
+    step = 1 << 27
+    for i in range(0, flat.numel(), step):
+        n = min(step, flat.numel() - i)
+        flat[i:i + n] = (torch.randn(n, generator=gen, device=dev) * sigma).to(torch.bfloat16)
+    return t
+
+
+class _Timer:
+    """Per-launch HIP events on the stream the kernels are launched on."""
+
+    def __init__(self, n):
+        import torch
+
+        self.a = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        self.b = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+    def mean_us(self, n):
+        return 1e3 * sum(self.a[i].elapsed_time(self.b[i]) for i in range(n)) / n
+
+
+# ---------------------------------------------------------------------------
+# GQA step
+
+
+def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_host,
+                   label):
+    """Times `steps` decode steps (append + GQA partial + merge) and returns a
+    dict of results.  lens: total KV lengths; the GPU holds floor(share*L)."""
+    import torch
+
+    from scope_amd import ops
+
+    D = 128
+    Hq = Hkv * G
+    L = ops.lib()
+    rng = np.random.default_rng(seed)
+    gpu_tokens = np.array([int(math.floor(share * int(x))) for x in lens], np.int64)
+    extra = warmup + steps + 1
+    table, num_pages = _page_table(gpu_tokens, extra, rng)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    k_pages = _randn_bf16((num_pages, Hkv, PAGE, D), gen, 1.0, dev)
+    v_pages = _randn_bf16((num_pages, Hkv, PAGE, D), gen, 1.0, dev)
+    page_table = torch.from_numpy(table).to(dev)
+    gpu_len = torch.from_numpy(gpu_tokens.astype(np.int32)).to(dev)
+    q = _randn_bf16((B, Hq, D), gen, 1.0, dev)
+    k_new = _randn_bf16((B, Hkv, 1, D), gen, 1.0, dev)
+    v_new = _randn_bf16((B, Hkv, 1, D), gen, 1.0, dev)
+    rows = B * Hq
+    # host partial: bf16 (normalised out, max, sum) as fused_cpu_attn returns it
+    h_out = _randn_bf16((rows, D), gen, 0.3, dev)
+    h_max = (torch.randn(rows, generator=gen, device=dev) + 4).to(torch.bfloat16)
+    h_sum = (torch.rand(rows, generator=gen, device=dev) * 50 + 1).to(torch.bfloat16)
+    if not with_host:  # r = 1: nothing on the host, merge with the empty partial
+        h_max.fill_(float("-inf"))
+        h_sum.zero_()
+    out_g = torch.empty((rows, D), dtype=torch.float32, device=dev)
+    lse_g = torch.empty((rows,), dtype=torch.float32, device=dev)
+    out = torch.empty((rows, D), dtype=torch.bfloat16, device=dev)
+
+    max_len0 = int(gpu_tokens.max())
+    max_len_end = max_len0 + extra
+    tps, _ = ops.decode_plan(0, B * Hkv, max_len0, 0)
+    n_splits_end = -(-max_len_end // tps)
+    wsb = L.ws_decode_workspace_bytes(rows, D, n_splits_end)
+    ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    max_pages = table.shape[1]
+    scale = ctypes.c_float(D ** -0.5)
+    a_append = (p(k_new), p(v_new), p(k_pages), p(v_pages), p(page_table), p(gpu_len),
+                B, Hkv, D, 1, PAGE, max_pages, num_pages, 1, stream)
+    a_part_head = (p(q), p(k_pages), p(v_pages), p(page_table), p(gpu_len),
+                   B, Hq, Hkv, D, PAGE, max_pages, num_pages)
+    a_part_tail = (tps, scale, p(out_g), p(lse_g), p(ws), ctypes.c_size_t(wsb), stream)
+    a_merge = (p(out_g), p(lse_g), p(h_out), p(h_max), p(h_sum), ops.TRIPLE_NORM_BF16,
+               p(out), None, None, rows, D, stream)
+    f_append, f_part, f_merge = L.ws_kv_append, L.ws_gqa_decode_partial, L.ws_lse_merge
+
+    def step(i, timer=None):
+        rc = f_append(*a_append)
+        if timer is not None:
+            timer.a[i].record()
+        rc |= f_part(*a_part_head, max_len0 + i + 1, *a_part_tail)
+        if timer is not None:
+            timer.b[i].record()
+        rc |= f_merge(*a_merge)
+        if rc:
+            raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    base = warmup
+    timer = _Timer(steps)
+    t_ev0 = torch.cuda.Event(enable_timing=True)
+    t_ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    t_ev0.record()
+    for i in range(steps):
+        a_i = base + i
+        rc = f_append(*a_append)
+        timer.a[i].record()
+        rc |= f_part(*a_part_head, max_len0 + a_i + 1, *a_part_tail)
+        timer.b[i].record()
+        rc |= f_merge(*a_merge)
+        if rc:
+            raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
+    t_ev1.record()
+    t_host = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t0
+    step_us = 1e3 * t_ev0.elapsed_time(t_ev1) / steps
+    part_us = timer.mean_us(steps)
+    # lengths during the timed region grow from g + warmup + 1 to g + warmup + steps
+    mean_tokens = float(gpu_tokens.sum()) + B * (warmup + (steps + 1) / 2.0)
+    kv_tok = Hkv * 2 * D * 2
+    pages_read = float(sum(-(-(int(g) + warmup + steps // 2) // PAGE) for g in gpu_tokens))
+    kernel_bytes = (mean_tokens * kv_tok + rows * D * 2 + rows * (D + 1) * 4
+                    + pages_read * 4)
+    step_bytes = (kernel_bytes + rows * (D * 2 + 4) + rows * D * 2 + B * kv_tok)
+    res = {
+        "label": label,
+        "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
+        "share": share,
+        "gpu_tokens": int(gpu_tokens.sum()),
+        "max_gpu_tokens": max_len0,
+        "tokens_per_split": tps,
+        "us_per_layer": round(step_us, 2),
+        "step_gbs": round(step_bytes / step_us / 1e3, 1),
+        "partial_us": round(part_us, 2),
+        "partial_gbs": round(kernel_bytes / part_us / 1e3, 1),
+        "partial_frac": round(kernel_bytes / part_us / 1e3 / HBM_PEAK_GBS, 4),
+        "step_bytes": int(step_bytes),
+        "partial_bytes": int(kernel_bytes),
+        "host_loop_us_per_step": round(1e6 * t_host / steps, 2),
+        "wall_us_per_step": round(1e6 * t_wall / steps, 2),
+    }
+    # keep the data for the CPU baseline of the headline case
+    res["_data"] = (k_pages, v_pages, table, gpu_tokens, q)
+    return res
+
+
+# ---------------------------------------------------------------------------
+# MLA step
+
+
+def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label):
+    import torch
+
+    from scope_amd import ops
+
+    L = ops.lib()
+    rng = np.random.default_rng(seed)
+    gpu_tokens = np.array([int(math.floor(share * int(x))) for x in lens], np.int64)
+    extra = warmup + steps + 1
+    table, num_pages = _page_table(gpu_tokens, extra, rng)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    latent = _randn_bf16((num_pages, PAGE, 576), gen, 0.5, dev)
+    page_table = torch.from_numpy(table).to(dev)
+    gpu_len = torch.from_numpy(gpu_tokens.astype(np.int32)).to(dev)
+    rows = B * H
+    qn = _randn_bf16((rows, 512), gen, 0.5, dev)
+    qp = _randn_bf16((rows, 64), gen, 0.5, dev)
+    kv_new = _randn_bf16((B, 1, 576), gen, 0.5, dev)
+    c_new, pe_new = kv_new[..., :512], kv_new[..., 512:]
+    # host partial: fp32 unnormalised (out, max, sum) of fused_cpu_attn_mla_compressed
+    h_out = torch.randn((rows, 512), generator=gen, device=dev) * 5
+    h_max = torch.randn(rows, generator=gen, device=dev) + 4
+    h_sum = torch.rand(rows, generator=gen, device=dev) * 50 + 1
+    out_g = torch.empty((rows, 512), dtype=torch.float32, device=dev)
+    lse_g = torch.empty((rows,), dtype=torch.float32, device=dev)
+    out = torch.empty((rows, 512), dtype=torch.bfloat16, device=dev)
+    max_len0 = int(gpu_tokens.max())
+    tps, _ = ops.decode_plan(1, B, max_len0, 0)
+    n_splits_end = -(-(max_len0 + extra) // tps)
+    wsb = L.ws_decode_workspace_bytes(rows, 512, n_splits_end)
+    ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    max_pages = table.shape[1]
+    a_app = (p(c_new), ctypes.c_int64(576), p(pe_new), ctypes.c_int64(576), p(latent),
+             p(page_table), p(gpu_len), B, 1, PAGE, max_pages, num_pages, 1, stream)
+    a_head = (p(qn), p(qp), p(latent), p(page_table), p(gpu_len), B, H, PAGE, max_pages,
+              num_pages)
+    a_tail = (tps, ctypes.c_float(192 ** -0.5), p(out_g), p(lse_g), p(ws),
+              ctypes.c_size_t(wsb), stream)
+    a_merge = (p(out_g), p(lse_g), p(h_out), p(h_max), p(h_sum), ops.TRIPLE_UNNORM_F32,
+               p(out), None, None, rows, 512, stream)
+    for i in range(warmup):
+        rc = L.ws_latent_append(*a_app) | L.ws_mla_decode_partial(
+            *a_head, max_len0 + i + 1, *a_tail) | L.ws_lse_merge(*a_merge)
+        if rc:
+            raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
+    timer = _Timer(steps)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(steps):
+        rc = L.ws_latent_append(*a_app)
+        timer.a[i].record()
+        rc |= L.ws_mla_decode_partial(*a_head, max_len0 + warmup + i + 1, *a_tail)
+        timer.b[i].record()
+        rc |= L.ws_lse_merge(*a_merge)
+        if rc:
+            raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
+    e1.record()
+    torch.cuda.synchronize()
+    step_us = 1e3 * e0.elapsed_time(e1) / steps
+    part_us = timer.mean_us(steps)
+    mean_tokens = float(gpu_tokens.sum()) + B * (warmup + (steps + 1) / 2.0)
+    pages_read = float(sum(-(-(int(g) + warmup + steps // 2) // PAGE) for g in gpu_tokens))
+    kernel_bytes = (mean_tokens * 1152 + rows * 576 * 2 + rows * 513 * 4 + pages_read * 4)
+    step_bytes = kernel_bytes + rows * 514 * 4 + rows * 512 * 2 + B * 1152
+    flops = mean_tokens * H * (2 * 576 + 2 * 512)
+    return {
+        "label": label, "batch": B, "heads": H, "share": share,
+        "gpu_tokens": int(gpu_tokens.sum()), "tokens_per_split": tps,
+        "us_per_layer": round(step_us, 2),
+        "step_gbs": round(step_bytes / step_us / 1e3, 1),
+        "partial_us": round(part_us, 2),
+        "partial_gbs": round(kernel_bytes / part_us / 1e3, 1),
+        "partial_frac": round(kernel_bytes / part_us / 1e3 / HBM_PEAK_GBS, 4),
+        "partial_tflops": round(flops / part_us / 1e6, 2),
+        "mfma_frac_bf16_dense": round(flops / part_us / 1e6 / 2500.0, 4),
+    }
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle's C restatement of the reference CPU kernel
+
+
+def _host_info():
+    info = {"affinity_cores": len(os.sched_getaffinity(0))}
+    try:
+        txt = open("/proc/cpuinfo").read()
+        m = re.search(r"model name\s*:\s*(.*)", txt)
+        info["cpu_model"] = m.group(1).strip() if m else "?"
+        flags = set(re.search(r"flags\s*:\s*(.*)", txt).group(1).split())
+        info["isa"] = [f for f in ("avx2", "avx512f", "avx512bw", "avx512_bf16",
+                                   "amx_bf16") if f in flags]
+    except Exception:  # pragma: no cover - informational only
+        pass
+    return info
+
+
+def cpu_baseline(data, Hkv, G, budget_s, threads):
+    """Times the C restatement (fused_cpu_attn contract, bf16, one call per
+    sequence as the reference kernels take one length per call) over the GPU
+    share of whole sequences of the headline workload, until budget_s of CPU
+    time has been spent.  Returns GB/s of KV streamed and the equivalent
+    microseconds for the whole GPU share of one layer."""
+    import torch
+
+    from oracle import port
+
+    k_pages, v_pages, table, gpu_tokens, q = data
+    D = 128
+    B = len(gpu_tokens)
+    port.lib()
+    qh = q.view(torch.int16).cpu().numpy().view(np.uint16).reshape(B, Hkv, G, D)
+    # host copies of the GPU share of the first few sequences (contiguous
+    # [Hkv, g, D] per sequence, the layout the CPU kernel takes)
+    sample = []
+    for b in range(min(B, 4)):
+        g = int(gpu_tokens[b])
+        if g <= 0:
+            continue
+        n_pages = -(-g // PAGE)
+        pids = torch.from_numpy(table[b, :n_pages].astype(np.int64)).to(k_pages.device)
+        k = k_pages[pids].permute(1, 0, 2, 3).reshape(Hkv, n_pages * PAGE, D)[:, :g]
+        v = v_pages[pids].permute(1, 0, 2, 3).reshape(Hkv, n_pages * PAGE, D)[:, :g]
+        sample.append((b, g, k.contiguous().view(torch.int16).cpu().numpy().view(np.uint16),
+                       v.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)))
+    done_bytes = 0.0
+    spent = 0.0
+    calls = 0
+    while sample and spent < budget_s:
+        b, g, kh, vh = sample[calls % len(sample)]
+        t0 = time.perf_counter()
+        port.cpu_attn(qh[b], kh, vh, D ** -0.5, normalize=True, n_threads=threads)
+        spent += time.perf_counter() - t0
+        done_bytes += g * Hkv * 2 * D * 2
+        calls += 1
+    if not calls:
+        return None
+    gbs = done_bytes / spent / 1e9
+    total = float(gpu_tokens.sum()) * Hkv * 2 * D * 2
+    return {
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{calls} calls over the GPU-share tokens of the first "
+                   f"{len(sample)} sequences ({done_bytes / 1e6:.0f} MB of bf16 K/V "
+                   f"streamed), one call per sequence ({Hkv} rows x {G} heads), "
+                   f"{spent:.1f} s of CPU time"),
+        "us_per_layer_equiv": round(total / (gbs * 1e3), 1),
+    }
+
+
+# ---------------------------------------------------------------------------
+# traffic from the committed rocprofv3 PMC summary
+
+
+def committed_traffic(workload_key):
+    """HBM bytes per launch of the GQA partial kernel from profiles/, if a
+    FETCH_SIZE/WRITE_SIZE summary for this workload is committed."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            doc = json.load(f)
+        ent = doc.get(workload_key)
+        return None if ent is None else ent.get("traffic_bytes_per_launch")
+    except Exception:
+        return None
+
+
+# ---------------------------------------------------------------------------
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--share", type=float, default=0.5)
+    ap.add_argument("--seed", type=int, default=2000)
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU time for the CPU baseline (0 = skip)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the headline workload (no sweep, MLA, other shares)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 256 MiB device copy (PMC scale factor)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the GPU "
+              "partition shards by (sequence, KV head) rows with no exchange, and no "
+              "multi-GPU figure is produced", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    from scope_amd import ops
+
+    ops.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # headline: Mixtral shape, B 16, L ~ U[1024, 32768], trailing floor(r L) on the GPU
+    B, Hkv, G = 16, 8, 4
+    lens = np.random.default_rng(args.seed).integers(1024, 32769, B)
+    log(f"headline: mixtral gqa B={B} share={args.share} lens={lens.tolist()}")
+    head = gqa_step_bench(B=B, Hkv=Hkv, G=G, lens=lens, share=args.share,
+                          steps=args.steps, warmup=args.warmup, seed=args.seed, dev=dev,
+                          with_host=args.share < 1.0, label="mixtral_b16")
+    data = head.pop("_data")
+    log(f"headline: {head['us_per_layer']} us/layer, partial {head['partial_us']} us "
+        f"= {head['partial_gbs']} GB/s")
+
+    extra = {}
+    if not args.headline_only:
+        by_share = []
+        for r in (0.25, 0.75):
+            res = gqa_step_bench(B=B, Hkv=Hkv, G=G, lens=lens, share=r, steps=args.steps,
+                                 warmup=args.warmup, seed=args.seed, dev=dev,
+                                 with_host=True, label=f"mixtral_b16_r{r}")
+            res.pop("_data")
+            by_share.append(res)
+            log(f"share {r}: {res['us_per_layer']} us/layer, partial {res['partial_gbs']} GB/s")
+        extra["by_share"] = by_share
+        sweep = []
+        for Lq in (8192, 32768, 65536, 131072):
+            res = gqa_step_bench(B=4, Hkv=4, G=8, lens=[Lq] * 4, share=1.0,
+                                 steps=max(10, args.steps // 2), warmup=args.warmup,
+                                 seed=args.seed + Lq, dev=dev, with_host=False,
+                                 label=f"qwen3_b4_L{Lq}")
+            res.pop("_data")
+            sweep.append(res)
+            log(f"qwen3 B4 L={Lq}: {res['us_per_layer']} us/layer, partial "
+                f"{res['partial_us']} us = {res['partial_gbs']} GB/s")
+        extra["kv_len_sweep"] = sweep
+        one = gqa_step_bench(B=1, Hkv=4, G=8, lens=[4096], share=1.0, steps=args.steps,
+                             warmup=args.warmup, seed=args.seed + 1, dev=dev,
+                             with_host=False, label="qwen3_b1_L4096")
+        one.pop("_data")
+        extra["single_partition"] = one
+        mla = mla_step_bench(B=8, H=16, lens=[16384] * 8, share=0.5, steps=args.steps,
+                             warmup=args.warmup, seed=args.seed + 3, dev=dev,
+                             label="dsv2lite_mla_b8_L16384")
+        extra["mla"] = mla
+        log(f"mla: {mla['us_per_layer']} us/layer, partial {mla['partial_us']} us = "
+            f"{mla['partial_gbs']} GB/s, {mla['partial_tflops']} TFLOP/s")
+
+    if args.copy_calibration:
+        n = 256 << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 5 x {n} bytes read + written")
+
+    cpu = None
+    if args.cpu_budget > 0:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+        cpu = cpu_baseline(data, Hkv, G, args.cpu_budget, threads)
+        cpu.update(_host_info())
+        log(f"cpu baseline: {cpu['value']} GB/s on {threads} threads")
+
+    wk = f"mixtral_b16_r{args.share}"
+    roofline = {
+        "bound": "hbm",
+        "achieved": head["partial_gbs"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(head["partial_gbs"] / HBM_PEAK_GBS, 4),
+        "traffic": committed_traffic(wk),
+        "kernel": "gqa_partial_kernel<4> (+ split_reduce_kernel), ws_gqa_decode_partial",
+        "algorithmic_bytes_per_launch": head["partial_bytes"],
+        "mean_launch_us": head["partial_us"],
+    }
+    line = {
+        "metric": METRIC,
+        "value": round(head["step_gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_layer"] / 1e3, 5),
+        "us_per_layer": head["us_per_layer"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"partitioned GQA decode step (append + split-KV partial + LSE "
+                         f"merge), Mixtral-8x7B layer: batch {B}, 32 q / 8 KV heads, "
+                         f"head_dim 128, L ~ U[1024, 32768], GPU share r={args.share} "
+                         f"in 64-token pages"),
+            "batch": B, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
+            "share": args.share, "page_size": PAGE,
+            "gpu_tokens": head["gpu_tokens"], "seed": args.seed,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "headline": head,
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
