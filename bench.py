@@ -5,15 +5,17 @@ partitioned GQA decode at the Mixtral-8x7B layer shape: batch 16, 32 query
 heads, 8 KV heads, head_dim 128, bf16 N(0,1), per-sequence KV lengths uniform
 in [1024, 32768], the trailing floor(r*L) tokens of each sequence in 64-token
 HBM pages (r = 0.5 by default).  A step appends one token per sequence to the
-GPU partition, runs the split-KV GQA partial over the partition and LSE-merges
-it with the host partial (the bf16 (out, max, sum) triple of the CPU kernel,
-already resident in HBM) into the final bf16 output.
+GPU partition and runs the split-KV GQA partial over the partition (one
+launch: ws_gqa_append_decode_partial), then LSE-merges it with the host
+partial (the bf16 (out, max, sum) triple of the CPU kernel, already resident
+in HBM) into the final bf16 output (ws_lse_merge).
 
 Reported on one JSON line (stdout):
   value      algorithmic HBM GB/s of the whole step (bytes below / step time)
   ms_per_step, us_per_layer
-  roofline   the GQA partial kernel: algorithmic bytes per launch / its mean
-             duration from HIP events around every launch of the timed region,
+  roofline   the fused append + GQA partial kernel: algorithmic bytes per
+             launch / its mean duration from HIP events around every launch of
+             the timed region,
              against the 8 TB/s HBM peak; traffic from the committed rocprofv3
              FETCH_SIZE / WRITE_SIZE summary when one exists for this workload
   cpu_baseline  the oracle's C restatement of the reference CPU kernel over a
@@ -60,13 +62,19 @@ def log(msg):
 # paged pools
 
 
+CONTIGUOUS_PAGES = False  # --contiguous-pages: pages in order (locality check)
+
+
 def _page_table(gpu_tokens, capacity_extra, rng):
     """Fragmented page assignment: every sequence gets the pages for its GPU
-    tokens plus room for the appends, page ids drawn from a random permutation."""
+    tokens plus room for the appends, page ids drawn from a random permutation
+    (in order with --contiguous-pages)."""
     need = [-(-(int(g) + capacity_extra) // PAGE) for g in gpu_tokens]
     max_pages = max(1, max(need))
     num_pages = sum(need)
     perm = rng.permutation(num_pages).astype(np.int32)
+    if CONTIGUOUS_PAGES:
+        perm = np.arange(num_pages, dtype=np.int32)
     table = np.full((len(need), max_pages), -1, np.int32)
     k = 0
     for b, n in enumerate(need):
@@ -106,9 +114,10 @@ class _Timer:
 
 
 def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_host,
-                   label):
-    """Times `steps` decode steps (append + GQA partial + merge) and returns a
-    dict of results.  lens: total KV lengths; the GPU holds floor(share*L)."""
+                   label, wg=0):
+    """Times `steps` decode steps (fused append + GQA partial, then the merge
+    with the host partial) and returns a dict of results.  lens: total KV
+    lengths; the GPU holds floor(share*L) of each."""
     import torch
 
     from scope_amd import ops
@@ -124,7 +133,9 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
     k_pages = _randn_bf16((num_pages, Hkv, PAGE, D), gen, 1.0, dev)
     v_pages = _randn_bf16((num_pages, Hkv, PAGE, D), gen, 1.0, dev)
     page_table = torch.from_numpy(table).to(dev)
-    gpu_len = torch.from_numpy(gpu_tokens.astype(np.int32)).to(dev)
+    # two length arrays, swapped every step (the fused step reads one, writes the other)
+    lens2 = torch.zeros((2, B), dtype=torch.int32, device=dev)
+    lens2[0] = torch.from_numpy(gpu_tokens.astype(np.int32)).to(dev)
     q = _randn_bf16((B, Hq, D), gen, 1.0, dev)
     k_new = _randn_bf16((B, Hkv, 1, D), gen, 1.0, dev)
     v_new = _randn_bf16((B, Hkv, 1, D), gen, 1.0, dev)
@@ -142,38 +153,26 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
 
     max_len0 = int(gpu_tokens.max())
     max_len_end = max_len0 + extra
-    tps, _ = ops.decode_plan(0, B * Hkv, max_len0, 0)
-    n_splits_end = -(-max_len_end // tps)
-    wsb = L.ws_decode_workspace_bytes(rows, D, n_splits_end)
-    ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+    nwg, wsb = ops.decode_plan(0, B * Hkv, G, max_len_end, wg)
+    ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     p = lambda t: ctypes.c_void_p(t.data_ptr())
     max_pages = table.shape[1]
     scale = ctypes.c_float(D ** -0.5)
-    a_append = (p(k_new), p(v_new), p(k_pages), p(v_pages), p(page_table), p(gpu_len),
-                B, Hkv, D, 1, PAGE, max_pages, num_pages, 1, stream)
-    a_part_head = (p(q), p(k_pages), p(v_pages), p(page_table), p(gpu_len),
-                   B, Hq, Hkv, D, PAGE, max_pages, num_pages)
-    a_part_tail = (tps, scale, p(out_g), p(lse_g), p(ws), ctypes.c_size_t(wsb), stream)
+    len_ptrs = (p(lens2[0]), p(lens2[1]))
+    a_head = (p(q), p(k_new), p(v_new), p(k_pages), p(v_pages), p(page_table))
+    a_mid = (B, Hq, Hkv, D, PAGE, max_pages, num_pages)
+    a_tail = (nwg, scale, p(out_g), p(lse_g), p(ws), ctypes.c_size_t(wsb), stream)
     a_merge = (p(out_g), p(lse_g), p(h_out), p(h_max), p(h_sum), ops.TRIPLE_NORM_BF16,
                p(out), None, None, rows, D, stream)
-    f_append, f_part, f_merge = L.ws_kv_append, L.ws_gqa_decode_partial, L.ws_lse_merge
+    f_step, f_merge = L.ws_gqa_append_decode_partial, L.ws_lse_merge
 
-    def step(i, timer=None):
-        rc = f_append(*a_append)
-        if timer is not None:
-            timer.a[i].record()
-        rc |= f_part(*a_part_head, max_len0 + i + 1, *a_part_tail)
-        if timer is not None:
-            timer.b[i].record()
+    for i in range(warmup):
+        rc = f_step(*a_head, len_ptrs[i % 2], len_ptrs[(i + 1) % 2], *a_mid,
+                    max_len0 + i + 1, *a_tail)
         rc |= f_merge(*a_merge)
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
-
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    base = warmup
     timer = _Timer(steps)
     t_ev0 = torch.cuda.Event(enable_timing=True)
     t_ev1 = torch.cuda.Event(enable_timing=True)
@@ -181,10 +180,10 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
     t0 = time.perf_counter()
     t_ev0.record()
     for i in range(steps):
-        a_i = base + i
-        rc = f_append(*a_append)
+        a_i = warmup + i
         timer.a[i].record()
-        rc |= f_part(*a_part_head, max_len0 + a_i + 1, *a_part_tail)
+        rc = f_step(*a_head, len_ptrs[a_i % 2], len_ptrs[(a_i + 1) % 2], *a_mid,
+                    max_len0 + a_i + 1, *a_tail)
         timer.b[i].record()
         rc |= f_merge(*a_merge)
         if rc:
@@ -193,22 +192,25 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
     t_host = time.perf_counter() - t0
     torch.cuda.synchronize()
     t_wall = time.perf_counter() - t0
+    final_len = lens2[(warmup + steps) % 2].cpu().numpy()
+    if not np.array_equal(final_len, gpu_tokens + warmup + steps):
+        raise RuntimeError(f"{label}: lengths did not advance by one per step")
     step_us = 1e3 * t_ev0.elapsed_time(t_ev1) / steps
     part_us = timer.mean_us(steps)
-    # lengths during the timed region grow from g + warmup + 1 to g + warmup + steps
+    # tokens attended during the timed region: g + warmup + 1 .. g + warmup + steps
     mean_tokens = float(gpu_tokens.sum()) + B * (warmup + (steps + 1) / 2.0)
     kv_tok = Hkv * 2 * D * 2
     pages_read = float(sum(-(-(int(g) + warmup + steps // 2) // PAGE) for g in gpu_tokens))
     kernel_bytes = (mean_tokens * kv_tok + rows * D * 2 + rows * (D + 1) * 4
-                    + pages_read * 4)
-    step_bytes = (kernel_bytes + rows * (D * 2 + 4) + rows * D * 2 + B * kv_tok)
-    res = {
+                    + pages_read * 4 + B * kv_tok)
+    step_bytes = kernel_bytes + rows * (D * 2 + 4) + rows * D * 2
+    return {
         "label": label,
         "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
         "share": share,
         "gpu_tokens": int(gpu_tokens.sum()),
         "max_gpu_tokens": max_len0,
-        "tokens_per_split": tps,
+        "workgroups": nwg,
         "us_per_layer": round(step_us, 2),
         "step_gbs": round(step_bytes / step_us / 1e3, 1),
         "partial_us": round(part_us, 2),
@@ -218,17 +220,17 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
         "partial_bytes": int(kernel_bytes),
         "host_loop_us_per_step": round(1e6 * t_host / steps, 2),
         "wall_us_per_step": round(1e6 * t_wall / steps, 2),
+        "_data": (k_pages, v_pages, table, gpu_tokens, q),
     }
-    # keep the data for the CPU baseline of the headline case
-    res["_data"] = (k_pages, v_pages, table, gpu_tokens, q)
-    return res
 
 
 # ---------------------------------------------------------------------------
 # MLA step
 
 
-def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label):
+def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label, wg=0):
+    """Times `steps` absorbed-MLA decode steps (fused latent append + partial,
+    then the merge with the host partial's fp32 (o, max, sum) triple)."""
     import torch
 
     from scope_amd import ops
@@ -241,13 +243,13 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label):
     gen = torch.Generator(device=dev).manual_seed(seed)
     latent = _randn_bf16((num_pages, PAGE, 576), gen, 0.5, dev)
     page_table = torch.from_numpy(table).to(dev)
-    gpu_len = torch.from_numpy(gpu_tokens.astype(np.int32)).to(dev)
+    lens2 = torch.zeros((2, B), dtype=torch.int32, device=dev)
+    lens2[0] = torch.from_numpy(gpu_tokens.astype(np.int32)).to(dev)
     rows = B * H
     qn = _randn_bf16((rows, 512), gen, 0.5, dev)
     qp = _randn_bf16((rows, 64), gen, 0.5, dev)
     kv_new = _randn_bf16((B, 1, 576), gen, 0.5, dev)
     c_new, pe_new = kv_new[..., :512], kv_new[..., 512:]
-    # host partial: fp32 unnormalised (out, max, sum) of fused_cpu_attn_mla_compressed
     h_out = torch.randn((rows, 512), generator=gen, device=dev) * 5
     h_max = torch.randn(rows, generator=gen, device=dev) + 4
     h_sum = torch.rand(rows, generator=gen, device=dev) * 50 + 1
@@ -255,24 +257,23 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label):
     lse_g = torch.empty((rows,), dtype=torch.float32, device=dev)
     out = torch.empty((rows, 512), dtype=torch.bfloat16, device=dev)
     max_len0 = int(gpu_tokens.max())
-    tps, _ = ops.decode_plan(1, B, max_len0, 0)
-    n_splits_end = -(-(max_len0 + extra) // tps)
-    wsb = L.ws_decode_workspace_bytes(rows, 512, n_splits_end)
-    ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+    nwg, wsb = ops.decode_plan(1, B, H, max_len0 + extra, wg)
+    ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     p = lambda t: ctypes.c_void_p(t.data_ptr())
     max_pages = table.shape[1]
-    a_app = (p(c_new), ctypes.c_int64(576), p(pe_new), ctypes.c_int64(576), p(latent),
-             p(page_table), p(gpu_len), B, 1, PAGE, max_pages, num_pages, 1, stream)
-    a_head = (p(qn), p(qp), p(latent), p(page_table), p(gpu_len), B, H, PAGE, max_pages,
-              num_pages)
-    a_tail = (tps, ctypes.c_float(192 ** -0.5), p(out_g), p(lse_g), p(ws),
+    len_ptrs = (p(lens2[0]), p(lens2[1]))
+    a_head = (p(qn), p(qp), p(c_new), ctypes.c_int64(576), p(pe_new), ctypes.c_int64(576),
+              p(latent), p(page_table))
+    a_mid = (B, H, PAGE, max_pages, num_pages)
+    a_tail = (nwg, ctypes.c_float(192 ** -0.5), p(out_g), p(lse_g), p(ws),
               ctypes.c_size_t(wsb), stream)
     a_merge = (p(out_g), p(lse_g), p(h_out), p(h_max), p(h_sum), ops.TRIPLE_UNNORM_F32,
                p(out), None, None, rows, 512, stream)
+    f_step = L.ws_mla_append_decode_partial
     for i in range(warmup):
-        rc = L.ws_latent_append(*a_app) | L.ws_mla_decode_partial(
-            *a_head, max_len0 + i + 1, *a_tail) | L.ws_lse_merge(*a_merge)
+        rc = f_step(*a_head, len_ptrs[i % 2], len_ptrs[(i + 1) % 2], *a_mid,
+                    max_len0 + i + 1, *a_tail) | L.ws_lse_merge(*a_merge)
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
     timer = _Timer(steps)
@@ -281,9 +282,10 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label):
     torch.cuda.synchronize()
     e0.record()
     for i in range(steps):
-        rc = L.ws_latent_append(*a_app)
+        a_i = warmup + i
         timer.a[i].record()
-        rc |= L.ws_mla_decode_partial(*a_head, max_len0 + warmup + i + 1, *a_tail)
+        rc = f_step(*a_head, len_ptrs[a_i % 2], len_ptrs[(a_i + 1) % 2], *a_mid,
+                    max_len0 + a_i + 1, *a_tail)
         timer.b[i].record()
         rc |= L.ws_lse_merge(*a_merge)
         if rc:
@@ -294,12 +296,13 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label):
     part_us = timer.mean_us(steps)
     mean_tokens = float(gpu_tokens.sum()) + B * (warmup + (steps + 1) / 2.0)
     pages_read = float(sum(-(-(int(g) + warmup + steps // 2) // PAGE) for g in gpu_tokens))
-    kernel_bytes = (mean_tokens * 1152 + rows * 576 * 2 + rows * 513 * 4 + pages_read * 4)
-    step_bytes = kernel_bytes + rows * 514 * 4 + rows * 512 * 2 + B * 1152
+    kernel_bytes = (mean_tokens * 1152 + rows * 576 * 2 + rows * 513 * 4 + pages_read * 4
+                    + B * 1152)
+    step_bytes = kernel_bytes + rows * 514 * 4 + rows * 512 * 2
     flops = mean_tokens * H * (2 * 576 + 2 * 512)
     return {
         "label": label, "batch": B, "heads": H, "share": share,
-        "gpu_tokens": int(gpu_tokens.sum()), "tokens_per_split": tps,
+        "gpu_tokens": int(gpu_tokens.sum()), "workgroups": nwg,
         "us_per_layer": round(step_us, 2),
         "step_gbs": round(step_bytes / step_us / 1e3, 1),
         "partial_us": round(part_us, 2),
@@ -416,9 +419,19 @@ def main():
                     help="seconds of CPU time for the CPU baseline (0 = skip)")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the headline workload (no sweep, MLA, other shares)")
+    ap.add_argument("--wg", type=int, default=0,
+                    help="workgroups of the headline GQA call (0 = library choice)")
+    ap.add_argument("--wg-sweep", type=str, default="",
+                    help="comma list of workgroup counts to time on the headline")
+    ap.add_argument("--mla-wg-sweep", type=str, default="",
+                    help="comma list of workgroup counts to time on the MLA layer")
+    ap.add_argument("--contiguous-pages", action="store_true",
+                    help="assign each sequence's pages in order instead of shuffled")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC scale factor)")
     args = ap.parse_args()
+    global CONTIGUOUS_PAGES
+    CONTIGUOUS_PAGES = args.contiguous_pages
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the GPU "
@@ -443,12 +456,35 @@ def main():
     log(f"headline: mixtral gqa B={B} share={args.share} lens={lens.tolist()}")
     head = gqa_step_bench(B=B, Hkv=Hkv, G=G, lens=lens, share=args.share,
                           steps=args.steps, warmup=args.warmup, seed=args.seed, dev=dev,
-                          with_host=args.share < 1.0, label="mixtral_b16")
+                          with_host=args.share < 1.0, label="mixtral_b16", wg=args.wg)
     data = head.pop("_data")
     log(f"headline: {head['us_per_layer']} us/layer, partial {head['partial_us']} us "
         f"= {head['partial_gbs']} GB/s")
 
     extra = {}
+    if args.wg_sweep:
+        sw = []
+        for w in [int(x) for x in args.wg_sweep.split(",")]:
+            res = gqa_step_bench(B=B, Hkv=Hkv, G=G, lens=lens, share=args.share,
+                                 steps=args.steps, warmup=args.warmup, seed=args.seed,
+                                 dev=dev, with_host=True, label=f"mixtral_b16_wg{w}", wg=w)
+            res.pop("_data")
+            sw.append({k: res[k] for k in ("workgroups", "us_per_layer", "partial_us",
+                                           "partial_gbs")})
+            log(f"wg {w}: {res['us_per_layer']} us/layer, partial {res['partial_us']} us "
+                f"= {res['partial_gbs']} GB/s")
+        extra["wg_sweep"] = sw
+    if args.mla_wg_sweep:
+        sw = []
+        for w in [int(x) for x in args.mla_wg_sweep.split(",")]:
+            res = mla_step_bench(B=8, H=16, lens=[16384] * 8, share=0.5, steps=args.steps,
+                                 warmup=args.warmup, seed=args.seed + 3, dev=dev,
+                                 label=f"mla_wg{w}", wg=w)
+            sw.append({k: res[k] for k in ("workgroups", "us_per_layer", "partial_us",
+                                           "partial_gbs")})
+            log(f"mla wg {w}: {res['us_per_layer']} us/layer, partial {res['partial_us']} "
+                f"us = {res['partial_gbs']} GB/s")
+        extra["mla_wg_sweep"] = sw
     if not args.headline_only:
         by_share = []
         for r in (0.25, 0.75):
@@ -506,7 +542,8 @@ def main():
         "unit": "GB/s",
         "frac": round(head["partial_gbs"] / HBM_PEAK_GBS, 4),
         "traffic": committed_traffic(wk),
-        "kernel": "gqa_partial_kernel<4> (+ split_reduce_kernel), ws_gqa_decode_partial",
+        "kernel": "gqa_decode_kernel<4, true> (ws_gqa_append_decode_partial: append + "
+                  "load-balanced split-KV partial + in-kernel combine, one launch)",
         "algorithmic_bytes_per_launch": head["partial_bytes"],
         "mean_launch_us": head["partial_us"],
     }

@@ -99,26 +99,38 @@ int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
                      int num_pages, int update_len, void* stream);
 
 /*
- * Workspace for the split-KV partials: max_splits * rows * (Dv + 1) * 4 bytes,
- * rows = B * Hq (GQA) or B * H (MLA).
+ * Plan of a decode call: kind 0 (GQA: rows_kv = B * Hkv, heads = the group
+ * size G) or 1 (MLA: rows_kv = B, heads = H = 16), over sequences of at most
+ * max_len tokens.  n_workgroups is the grid the call will use (0 = the
+ * library's choice for the current device: two 4-wave workgroups per CU for
+ * GQA, one per CU for MLA, fewer when the batch is small).  Writes the
+ * resolved workgroup count and the workspace bytes the call needs.
+ *
+ * Workgroups take equal shares of all 32-token blocks of all rows, so ragged
+ * batches stay balanced; a row shared by several workgroups is combined from
+ * their partials.  Workspace layout: [arrival counters int32 x 16384 (one per
+ * kv row; a call takes at most 16384 kv rows)][partial lse][partial out], one
+ * partial slot per (workgroup, row) pair.  The workspace must be 256-byte
+ * aligned and its counters zero before its first use (ws_workspace_clear, or
+ * memory that is zero); every completed call leaves them zero again.  Calls
+ * that share a workspace must be ordered on one stream.  At most 2048
+ * sequences per call.
  */
-size_t ws_decode_workspace_bytes(int rows, int Dv, int max_splits);
+int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
+                   int n_workgroups, int* n_workgroups_out,
+                   size_t* workspace_bytes_out);
 
-/*
- * Split plan of a decode call: for kind 0 (GQA, rows_kv = B * Hkv) or 1 (MLA,
- * rows_kv = B), the tokens per split actually used (tokens_per_split, or the
- * library's choice when it is 0) and the number of splits of the longest
- * sequence.  Returns 0 or WS_EINVAL.  A call with n_splits > 1 needs
- * ws_decode_workspace_bytes(rows, Dv, n_splits) bytes of workspace.
- */
-int ws_decode_plan(int kind, int rows_kv, int max_len, int tokens_per_split,
-                   int* tps_out, int* n_splits_out);
+/* Zero `bytes` bytes of device memory with a kernel on `stream` (no
+ * hipMemset node, so the call may be captured in a HIP graph). */
+int ws_workspace_clear(void* workspace, size_t bytes, void* stream);
 
 /*
  * Split-KV GQA decode attention over the pooled tokens of every sequence.
  * q: [B][Hq][D] bf16, Hq = Hkv * G, G in {1,2,4,8,16}, D = 128.
- * tokens_per_split: multiple of 32 (0 = choose); max_len: upper bound of
- * gpu_len[] (sets the grid; must be >= every gpu_len[b]).
+ * n_workgroups: grid size (0 = choose, see ws_decode_plan); max_len: upper
+ * bound of gpu_len[] (must be >= every gpu_len[b]).  One launch: when a row
+ * spans several workgroups, the last one to finish combines the partials
+ * (arrival counters in the workspace).
  * Outputs out: [B][Hq][D] fp32 normalised, lse: [B][Hq] fp32.
  * Replaces _local_bmm_softmax / _resident_layer
  * (roofline/bench_resident_kv.py:150-157, 261-271) and the GPU side of
@@ -129,10 +141,34 @@ int ws_gqa_decode_partial(const uint16_t* q,
                           const int32_t* page_table, const int32_t* gpu_len,
                           int B, int Hq, int Hkv, int D,
                           int page_size, int max_pages, int num_pages,
-                          int max_len, int tokens_per_split, float scale,
+                          int max_len, int n_workgroups, float scale,
                           float* out, float* lse,
                           void* workspace, size_t workspace_bytes,
                           void* stream);
+
+/*
+ * One decode step of the GPU partition in one launch: append the new token of
+ * every sequence and attend over the partition including it.
+ * k_new, v_new: [B][Hkv][1][D] bf16.  Token len_in[b] of sequence b is the new
+ * one: it is written into its page slot (page_table must already hold that
+ * page) and attended from k_new/v_new directly; len_out[b] = len_in[b] + 1
+ * when len_out is not NULL (len_out must not alias len_in: a cache keeps two
+ * length arrays and swaps them each step).  max_len must be >= every
+ * len_in[b] + 1.  Other arguments and outputs as ws_gqa_decode_partial.
+ * Replaces _resident_layer (roofline/bench_resident_kv.py:261-271): slot copy
+ * + attention over the resident buffer; equivalent to ws_kv_append followed by
+ * ws_gqa_decode_partial.
+ */
+int ws_gqa_append_decode_partial(const uint16_t* q, const uint16_t* k_new,
+                                 const uint16_t* v_new, uint16_t* k_pages,
+                                 uint16_t* v_pages, const int32_t* page_table,
+                                 const int32_t* len_in, int32_t* len_out,
+                                 int B, int Hq, int Hkv, int D,
+                                 int page_size, int max_pages, int num_pages,
+                                 int max_len, int n_workgroups, float scale,
+                                 float* out, float* lse,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* stream);
 
 /*
  * Split-KV absorbed-MLA decode attention.
@@ -147,10 +183,33 @@ int ws_mla_decode_partial(const uint16_t* q_nope, const uint16_t* q_pe,
                           const uint16_t* latent_pages,
                           const int32_t* page_table, const int32_t* gpu_len,
                           int B, int H, int page_size, int max_pages,
-                          int num_pages, int max_len, int tokens_per_split,
+                          int num_pages, int max_len, int n_workgroups,
                           float scale, float* out, float* lse,
                           void* workspace, size_t workspace_bytes,
                           void* stream);
+
+/*
+ * One absorbed-MLA decode step of the GPU partition in one call: append the
+ * new latent of every sequence (c_new [B] rows of 512, row stride c_stride;
+ * pe_new [B] rows of 64, row stride pe_stride; bf16) at position len_in[b]
+ * and attend over the partition including it; len_out[b] = len_in[b] + 1
+ * when len_out is not NULL (must not alias len_in).  max_len must be >= every
+ * len_in[b] + 1.  Replaces the GPU-segment append of
+ * InplaceKVCacheCompressed.append (system/deepseek.py:171-192) followed by
+ * the GPU partial of _mla_compressed_forward (system/deepseek.py:364-392).
+ */
+int ws_mla_append_decode_partial(const uint16_t* q_nope, const uint16_t* q_pe,
+                                 const uint16_t* c_new, int64_t c_stride,
+                                 const uint16_t* pe_new, int64_t pe_stride,
+                                 uint16_t* latent_pages,
+                                 const int32_t* page_table,
+                                 const int32_t* len_in, int32_t* len_out,
+                                 int B, int H, int page_size, int max_pages,
+                                 int num_pages, int max_len,
+                                 int n_workgroups, float scale,
+                                 float* out, float* lse,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* stream);
 
 /*
  * LSE-combine per-split partials: part_out [n_splits][rows][Dv],

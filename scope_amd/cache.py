@@ -5,7 +5,9 @@ sequence in fixed-size HBM pages (default 64 tokens):
   GQA  k, v       [num_layers, num_pages, Hkv, page_size, D] bf16
   MLA  latent     [num_layers, num_pages, page_size, 576]    bf16
   page_table      [B, max_pages] int32 (shared by all layers)
-  gpu_len         [num_layers, B] int32 (device) + a host mirror
+  lengths         two device arrays [2, num_layers, B] int32 + a host mirror:
+                  a fused decode step (step()) reads one array and writes the
+                  other, then the layer's current array flips
 Pages come from a free list and are assigned on the host before an append
 needs them; the device page table is updated only when a sequence crosses a
 page boundary (once per 64 decode steps).
@@ -60,9 +62,20 @@ class _PagedBase:
         self.page_table = torch.full((batch, self.max_pages), -1, dtype=torch.int32,
                                      device=self.device)
         self.lens = np.zeros((num_layers, batch), np.int64)  # host mirror
-        self.gpu_len = torch.zeros((num_layers, batch), dtype=torch.int32,
-                                   device=self.device)
+        self._len_bufs = torch.zeros((2, num_layers, batch), dtype=torch.int32,
+                                     device=self.device)
+        self._cur = np.zeros(num_layers, np.int64)
         self._pages_held = np.zeros(batch, np.int64)
+
+    def len_dev(self, layer: int) -> torch.Tensor:
+        """Device lengths [B] of `layer` (the current one of its two arrays)."""
+        return self._len_bufs[int(self._cur[layer]), layer]
+
+    def _len_next(self, layer: int) -> torch.Tensor:
+        return self._len_bufs[1 - int(self._cur[layer]), layer]
+
+    def _flip(self, layer: int) -> None:
+        self._cur[layer] = 1 - self._cur[layer]
 
     def reserve(self, b: int, n_tokens: int) -> None:
         """Make sure sequence b owns pages for its first n_tokens positions."""
@@ -95,7 +108,8 @@ class _PagedBase:
         self.page_table.fill_(-1)
         self._pages_held[:] = 0
         self.lens[:] = 0
-        self.gpu_len.zero_()
+        self._len_bufs.zero_()
+        self._cur[:] = 0
 
 
 class GqaGpuPartition(_PagedBase):
@@ -117,7 +131,7 @@ class GqaGpuPartition(_PagedBase):
         for b in range(self.batch):
             self.reserve(b, int(self.lens[layer, b]) + n)
         ops.kv_append(k4d.contiguous(), v4d.contiguous(), self.k[layer], self.v[layer],
-                      self.page_table, self.gpu_len[layer])
+                      self.page_table, self.len_dev(layer))
         self.lens[layer] += n
 
     def load_sequence(self, layer: int, b: int, k: torch.Tensor, v: torch.Tensor) -> None:
@@ -126,14 +140,30 @@ class GqaGpuPartition(_PagedBase):
         self.reserve(b, int(self.lens[layer, b]) + n)
         ops.kv_append(k.unsqueeze(0).contiguous(), v.unsqueeze(0).contiguous(),
                       self.k[layer], self.v[layer], self.page_table[b:b + 1],
-                      self.gpu_len[layer, b:b + 1])
+                      self.len_dev(layer)[b:b + 1])
         self.lens[layer, b] += n
 
-    def attend(self, layer: int, q: torch.Tensor, scale: float, tokens_per_split=0):
+    def attend(self, layer: int, q: torch.Tensor, scale: float, n_workgroups=0):
         """GPU partial over the partition: q [B, Hq, D] -> (out fp32, lse fp32)."""
         return ops.gqa_decode_partial(q, self.k[layer], self.v[layer], self.page_table,
-                                      self.gpu_len[layer], scale, self.max_len(layer),
-                                      tokens_per_split)
+                                      self.len_dev(layer), scale, self.max_len(layer),
+                                      n_workgroups)
+
+    def step(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+             scale: float, n_workgroups=0):
+        """One decode step in one launch: append k_new/v_new [B, Hkv, 1, D] and
+        attend over the partition including them (the slot copy + attention of
+        _resident_layer, roofline/bench_resident_kv.py:261-271).
+        Returns (out [B, Hq, D] fp32, lse [B, Hq] fp32)."""
+        for b in range(self.batch):
+            self.reserve(b, int(self.lens[layer, b]) + 1)
+        out = ops.gqa_append_decode_partial(
+            q, k_new.contiguous(), v_new.contiguous(), self.k[layer], self.v[layer],
+            self.page_table, self.len_dev(layer), self._len_next(layer), scale,
+            self.max_len(layer) + 1, n_workgroups)
+        self._flip(layer)
+        self.lens[layer] += 1
+        return out
 
 
 class MlaGpuPartition(_PagedBase):
@@ -151,7 +181,7 @@ class MlaGpuPartition(_PagedBase):
         for b in range(self.batch):
             self.reserve(b, int(self.lens[layer, b]) + n)
         ops.latent_append(c_kv, k_pe, self.latent[layer], self.page_table,
-                          self.gpu_len[layer])
+                          self.len_dev(layer))
         self.lens[layer] += n
 
     def load_sequence(self, layer: int, b: int, c_kv: torch.Tensor, k_pe: torch.Tensor) -> None:
@@ -160,15 +190,30 @@ class MlaGpuPartition(_PagedBase):
         self.reserve(b, int(self.lens[layer, b]) + n)
         ops.latent_append(c_kv.unsqueeze(0).contiguous(), k_pe.unsqueeze(0).contiguous(),
                           self.latent[layer], self.page_table[b:b + 1],
-                          self.gpu_len[layer, b:b + 1])
+                          self.len_dev(layer)[b:b + 1])
         self.lens[layer, b] += n
 
     def attend(self, layer: int, q_nope: torch.Tensor, q_pe: torch.Tensor, scale: float,
-               tokens_per_split=0):
+               n_workgroups=0):
         """GPU partial: q_nope [B*H, 512], q_pe [B*H, 64] -> (out, lse)."""
         return ops.mla_decode_partial(q_nope, q_pe, self.latent[layer], self.page_table,
-                                      self.gpu_len[layer], scale, self.max_len(layer),
-                                      tokens_per_split)
+                                      self.len_dev(layer), scale, self.max_len(layer),
+                                      n_workgroups)
+
+    def step(self, layer: int, q_nope: torch.Tensor, q_pe: torch.Tensor,
+             c_new: torch.Tensor, pe_new: torch.Tensor, scale: float, n_workgroups=0):
+        """One decode step in one call: append the new latent (c_new [B, 1, 512],
+        pe_new [B, 1, 64]) and attend over the partition including it.
+        Returns (out [B*H, 512] fp32, lse [B*H] fp32)."""
+        for b in range(self.batch):
+            self.reserve(b, int(self.lens[layer, b]) + 1)
+        out = ops.mla_append_decode_partial(
+            q_nope, q_pe, c_new, pe_new, self.latent[layer], self.page_table,
+            self.len_dev(layer), self._len_next(layer), scale, self.max_len(layer) + 1,
+            n_workgroups)
+        self._flip(layer)
+        self.lens[layer] += 1
+        return out
 
 
 class PartitionedLatentCache:

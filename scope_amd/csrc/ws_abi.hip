@@ -28,9 +28,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* ws_last_error(void) { return ws::g_last_error; }
 
-extern "C" const char* ws_version(void) { return "wsgpu 0.1 gfx950"; }
-
-extern "C" size_t ws_decode_workspace_bytes(int rows, int Dv, int max_splits) {
-  if (rows <= 0 || Dv <= 0 || max_splits <= 0) return 0;
-  return (size_t)max_splits * (size_t)rows * (size_t)(Dv + 1) * sizeof(float);
-}
+extern "C" const char* ws_version(void) { return "wsgpu 0.2 gfx950"; }

@@ -1,0 +1,399 @@
+// Split-KV absorbed-MLA decode attention over the HBM partition (gfx950),
+// optionally fused with the append of the decode step's new latent.
+//
+// Work decomposition (ws_plan.h): the grid's 256-thread workgroups take equal
+// shares of all 32-token blocks of all sequences; the 16 heads of sequence b
+// share each token's 576-wide latent (512 c_kv followed by 64 k_pe).  Per
+// 32-token block, wave w computes the QK partial of token tile (w & 1) over
+// latent half (w >> 1) (9 MFMA k-steps), the four partial score tiles meet in
+// LDS, every wave runs the same online softmax, and wave w accumulates output
+// columns [128w, 128w + 128).  Each wave requests the next block's operands
+// before the current block's MFMAs run.  A sequence held by one workgroup is
+// written final; otherwise each workgroup stores a partial (slot workgroup +
+// sequence) and mla_reduce_kernel combines them: a sequence carries 32 KB of
+// partial per workgroup, more than one workgroup combines quickly.
+//
+// With c_new != nullptr, token len_in[b] is the new latent: it is read from
+// c_new/pe_new, the workgroup whose segment holds it writes it into its page
+// slot, and len_out[b] = len_in[b] + 1.
+#include <math.h>
+
+#include <algorithm>
+
+#include "ws_attn.h"
+#include "ws_plan.h"
+#include "ws_reduce.h"
+
+namespace ws {
+
+constexpr int kMlaH = 16;
+constexpr int kMlaL = 576;
+constexpr int kMlaC = 512;
+
+struct MlaParams {
+  const uint16_t* q_nope;
+  const uint16_t* q_pe;
+  const uint16_t* latent;
+  uint16_t* latent_w;
+  const int32_t* page_table;
+  const int32_t* len_in;
+  int32_t* len_out;
+  const uint16_t* c_new;  // [B] rows of 512 (row stride c_stride) or nullptr
+  const uint16_t* pe_new;
+  long long c_stride, pe_stride;
+  float* out;
+  float* lse;
+  float* part_out;  // [slot][16][512]
+  float* part_lse;  // [slot][16]
+  int B, page_size, max_pages, num_pages, cap;
+  float scale_log2;
+};
+
+// Pointer to the 16-byte chunk q (0..71) of the new token's latent.
+__device__ __forceinline__ const u32x4* new_chunk(const MlaParams& p, int b, int q) {
+  return q < kMlaC / 8 ? (const u32x4*)(p.c_new + (size_t)b * p.c_stride) + q
+                       : (const u32x4*)(p.pe_new + (size_t)b * p.pe_stride) + (q - kMlaC / 8);
+}
+
+__device__ __forceinline__ void store_cols(float* __restrict__ dst, const f32x4 (&acc)[8],
+                                           int j, float inv_l) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float4* o = (float4*)(dst + 32 * j + 8 * i);
+    o[0] = make_float4(acc[0][i] * inv_l, acc[1][i] * inv_l, acc[2][i] * inv_l,
+                       acc[3][i] * inv_l);
+    o[1] = make_float4(acc[4][i] * inv_l, acc[5][i] * inv_l, acc[6][i] * inv_l,
+                       acc[7][i] * inv_l);
+  }
+}
+
+template <bool APPEND>
+__global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
+  constexpr int NT = 256;
+  constexpr int add = APPEND ? 1 : 0;
+  __shared__ f32x4 sbuf[2][2][2][64];  // [buffer][latent half][token tile][lane]
+  __shared__ int s_pref[kMaxSeqs + 1];
+  __shared__ int s_scan[NT / 64 + 1];
+  const int g = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int n16 = lane & 15;
+  const int j = lane >> 4;
+  const int tt = wave & 1;
+  const int kh = wave >> 1;
+  const int col0 = 128 * wave;
+
+  if (APPEND && p.len_out && g == 0)
+    for (int b = tid; b < p.B; b += NT) p.len_out[b] = plan_len(p.len_in, b, add, p.cap);
+  const Plan plan = plan_build<NT>(p.len_in, add, p.cap, p.B, 1, gridDim.x, s_pref, s_scan);
+  if (g == 0) {  // sequences without tokens: the empty partial (0, -inf)
+    for (int b = 0; b < p.B; ++b) {
+      if (s_pref[b + 1] != s_pref[b]) continue;
+      for (int idx = tid; idx < kMlaH * kMlaC; idx += NT)
+        p.out[(size_t)b * kMlaH * kMlaC + idx] = 0.f;
+      if (tid < kMlaH) p.lse[b * kMlaH + tid] = neg_inf();
+    }
+  }
+  if (g >= plan.n) return;
+  const int blk_end = plan_start(plan, g + 1);
+  int blk = plan_start(plan, g);
+
+  while (blk < blk_end) {
+    const int b = plan_seq(s_pref, p.B, blk);
+    const int len = uniform(plan_len(p.len_in, b, add, p.cap));
+    const int len_old = len - add;
+    const int row_start = uniform(s_pref[b]);
+    const int row_end = uniform(s_pref[b + 1]);
+    const int seg_end = min(blk_end, row_end);
+    const int t_begin = (blk - row_start) * 32;
+    const int t_end = min(len, (seg_end - row_start) * 32);
+    const int orow = b * kMlaH + n16;
+    const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
+
+    if (APPEND && tid < kMlaL / 8 && len_old >= t_begin && len_old < t_end) {
+      const int page = len_old / p.page_size;
+      const int pid = pt[page];
+      if (pid >= 0 && pid < p.num_pages)
+        ((u32x4*)(p.latent_w + ((size_t)pid * p.page_size + (len_old - page * p.page_size)) *
+                                   kMlaL))[tid] = *new_chunk(p, b, tid);
+    }
+
+    // Q^T for this wave's 9 k-steps: k = 32 * (9 * kh + u) + 8 * j .. + 8.
+    u32x4 qb[9];
+#pragma unroll
+    for (int u = 0; u < 9; ++u) {
+      const int k0 = 32 * (9 * kh + u) + 8 * j;
+      if (k0 < kMlaC)
+        qb[u] = ((const u32x4*)(p.q_nope + (size_t)orow * kMlaC))[k0 >> 3];
+      else
+        qb[u] = ((const u32x4*)(p.q_pe + (size_t)orow * 64))[(k0 - kMlaC) >> 3];
+    }
+
+    f32x4 acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = neg_inf();
+    float l_run = 0.f;
+
+    // Operands of the 32-token block at t0.  With valid == false (the
+    // prefetch past the last block) every lane reads the first 16 bytes of
+    // q_nope instead: same instructions and registers, a cache hit.  Plain
+    // (cached) loads: the QK waves and the PV waves read overlapping parts of
+    // each latent, and the second read is served from the cache.
+    auto load_block = [&](int t0, bool valid, u32x4 (&ka)[9], u32x4 (&vr)[8]) {
+      const int page = t0 / p.page_size;
+      const int pid = clamp_page(pt[page], p.num_pages);
+      const uint16_t* lb =
+          p.latent + ((size_t)pid * p.page_size + (t0 - page * p.page_size)) * (size_t)kMlaL;
+      const int last = min(32, t_end - t0) - 1;
+      const int new_r = (APPEND && valid) ? len_old - t0 : -1;
+      const int r = min(16 * tt + n16, last);
+      const u32x4* kr = (const u32x4*)(lb + (size_t)r * kMlaL);
+      const u32x4* dummy = (const u32x4*)p.q_nope;
+#pragma unroll
+      for (int u = 0; u < 9; ++u) {
+        const int q = 4 * (9 * kh + u) + j;
+        ka[u] = *(!valid ? dummy : (APPEND && r == new_r) ? new_chunk(p, b, q) : kr + q);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int ri = min(pv_token(i, j), last);
+        const int q = (col0 >> 3) + n16;
+        vr[i] = *(!valid ? dummy
+                  : (APPEND && ri == new_r) ? new_chunk(p, b, q)
+                                            : (const u32x4*)(lb + (size_t)ri * kMlaL) + q);
+      }
+    };
+    auto compute_block = [&](int t0, const u32x4 (&ka)[9], const u32x4 (&vr)[8], int buf) {
+      const int nt = min(32, t_end - t0);
+      f32x4 sp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 9; ++u) sp = mfma16x16x32(ka[u], qb[u], sp);
+      sbuf[buf][kh][tt][lane] = sp;
+      __syncthreads();
+      const f32x4 s0 = sbuf[buf][0][0][lane] + sbuf[buf][1][0][lane];
+      const f32x4 s1 = sbuf[buf][0][1][lane] + sbuf[buf][1][1][lane];
+      float alpha;
+      const u32x4 pb = softmax_block(s0, s1, j, nt, p.scale_log2, m_run, l_run, alpha);
+      pv_block(acc, vr, pb, alpha);
+    };
+
+    // Every wave walks the same blocks (they meet at one barrier per block);
+    // the score buffers alternate, so two barriers separate a buffer's reuse.
+    // sched_barrier keeps the next block's loads above the current math.
+    const int nblk = (t_end - t_begin + 31) / 32;
+    {
+      u32x4 kaA[9], vrA[8], kaB[9], vrB[8];
+      load_block(t_begin, true, kaA, vrA);
+      for (int i = 0; i < nblk; i += 2) {
+        load_block(t_begin + 32 * min(i + 1, nblk - 1), i + 1 < nblk, kaB, vrB);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_block(t_begin + 32 * i, kaA, vrA, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 >= nblk) break;
+        load_block(t_begin + 32 * min(i + 2, nblk - 1), i + 2 < nblk, kaA, vrA);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_block(t_begin + 32 * (i + 1), kaB, vrB, 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __syncthreads();  // the next segment starts with buffer 0 again
+
+    const float l_tot = wave_sum_xor16_32(l_run);
+    const float inv_l = 1.f / l_tot;
+    const float lse_v = (m_run + __log2f(l_tot)) * kLn2;
+    const int nseg = plan_owner(plan, row_end - 1) - plan_owner(plan, row_start) + 1;
+    if (nseg == 1) {
+      store_cols(p.out + (size_t)orow * kMlaC + col0, acc, j, inv_l);
+      if (wave == 0 && j == 0) p.lse[orow] = lse_v;
+    } else {
+      const size_t prow = (size_t)(g + b) * kMlaH + n16;
+      store_cols(p.part_out + prow * kMlaC + col0, acc, j, inv_l);
+      if (wave == 0 && j == 0) p.part_lse[prow] = lse_v;
+    }
+    blk = seg_end;
+  }
+}
+
+// Combines the partials of sequences held by several workgroups: one 64-lane
+// workgroup per (head row, 256-column chunk).  Recomputes the decode's plan
+// to find the sequence's workgroups (slots w + b for w in its owner range).
+// Runs after the decode kernel on the same stream, so plain loads see the
+// partials.
+__global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int grid) {
+  __shared__ int s_pref[kMaxSeqs + 1];
+  __shared__ int s_scan[2];
+  __shared__ float s_w[kReduceMaxWeights];
+  const int hrow = blockIdx.x;  // b * 16 + h
+  const int chunk = blockIdx.y;
+  const int t = threadIdx.x;
+  const int b = hrow / kMlaH;
+  const int h = hrow - b * kMlaH;
+  const int add = p.c_new ? 1 : 0;
+  const Plan plan = plan_build<64>(p.len_in, add, p.cap, p.B, 1, grid, s_pref, s_scan);
+  const int row_start = s_pref[b], row_end = s_pref[b + 1];
+  if (row_end == row_start) return;
+  const int w_first = plan_owner(plan, row_start);
+  const int n = plan_owner(plan, row_end - 1) - w_first + 1;
+  if (n == 1) return;
+  const size_t slot0 = (size_t)(w_first + b) * kMlaH + h;  // partial row of split 0
+  float mx = neg_inf();
+  for (int s = t; s < n; s += 64) {
+    const float v = p.part_lse[slot0 + (size_t)s * kMlaH];
+    s_w[s] = v;
+    mx = fmaxf(mx, v);
+  }
+  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  float sum = 0.f;
+  for (int s = t; s < n; s += 64) {
+    const float w = __expf(s_w[s] - mx);
+    s_w[s] = w;
+    sum += w;
+  }
+  for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
+  __syncthreads();
+  if (chunk == 0 && t == 0) p.lse[hrow] = mx + __logf(sum);
+  const int c = chunk * 64 + t;  // float4 column
+  const float4* src = (const float4*)(p.part_out + slot0 * kMlaC) + c;
+  const size_t sstride = (size_t)kMlaH * kMlaC / 4;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+  int s = 0;
+  for (; s + 8 <= n; s += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(s + u) * sstride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float w = s_w[s + u];
+      a.x += w * v[u].x; a.y += w * v[u].y; a.z += w * v[u].z; a.w += w * v[u].w;
+    }
+  }
+  for (; s < n; ++s) {
+    const float w = s_w[s];
+    const float4 v = src[(size_t)s * sstride];
+    a.x += w * v.x; a.y += w * v.y; a.z += w * v.z; a.w += w * v.w;
+  }
+  const float inv = 1.f / sum;
+  ((float4*)(p.out + (size_t)hrow * kMlaC))[c] =
+      make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Workgroups of an MLA call: n_workgroups when given, else one per CU (the
+// kernel's occupancy), at most what the blocks of the longest possible batch
+// can feed with 4 blocks each, and no more than the reduction's weights hold.
+int mla_workgroups(int n_workgroups, int B, int max_len) {
+  if (n_workgroups > 0) return n_workgroups;
+  const long long max_blocks = (long long)B * ((max_len + 31) / 32);
+  const int n = choose_workgroups(0, 1, max_blocks, 4);
+  return std::min(n, kReduceMaxWeights);
+}
+
+static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
+                      const uint16_t* c_new, long long c_stride, const uint16_t* pe_new,
+                      long long pe_stride, uint16_t* latent_pages,
+                      const int32_t* page_table, const int32_t* len_in,
+                      int32_t* len_out, int B, int H, int page_size, int max_pages,
+                      int num_pages, int max_len, int n_workgroups, float scale,
+                      float* out, float* lse, void* workspace, size_t workspace_bytes,
+                      void* stream, const char* name) {
+  if (!q_nope || !q_pe || !latent_pages || !page_table || !len_in || !out || !lse)
+    return set_error(WS_EINVAL, "%s: null pointer", name);
+  if (B < 0 || B > kMaxSeqs || H != kMlaH)
+    return set_error(WS_EINVAL, "%s: B=%d H=%d unsupported (H 16, B <= %d)", name, B, H,
+                     kMaxSeqs);
+  if (page_size <= 0 || max_pages <= 0 || num_pages <= 0 || max_len < 0 ||
+      (page_size % 32 && max_pages != 1) ||
+      (long long)max_len > (long long)page_size * max_pages)
+    return set_error(WS_EINVAL,
+                     "%s: bad paging page_size=%d max_pages=%d num_pages=%d max_len=%d",
+                     name, page_size, max_pages, num_pages, max_len);
+  if (n_workgroups < 0 || n_workgroups > kReduceMaxWeights)
+    return set_error(WS_EINVAL, "%s: n_workgroups %d outside [0, %d]", name, n_workgroups,
+                     kReduceMaxWeights);
+  if (!aligned16(q_nope) || !aligned16(q_pe) || !aligned16(latent_pages) ||
+      !aligned16(out))
+    return set_error(WS_EINVAL, "%s: buffers must be 16-byte aligned", name);
+  if (c_new && (!pe_new || !aligned16(c_new) || !aligned16(pe_new) || c_stride < 512 ||
+                pe_stride < 64 || c_stride % 8 || pe_stride % 8))
+    return set_error(WS_EINVAL, "%s: bad new-latent buffers", name);
+  if (len_out && len_out == len_in)
+    return set_error(WS_EINVAL, "%s: len_out must not alias len_in", name);
+  if (B == 0) return WS_OK;
+  if ((long long)B * ((max_len + 32) / 32) * 4096 >= (1LL << 31))
+    return set_error(WS_EINVAL, "%s: %d sequences of %d tokens exceed the block index range",
+                     name, B, max_len);
+  const int n = mla_workgroups(n_workgroups, B, max_len);
+  const size_t need = ws::workspace_bytes(B, kMlaH, kMlaC, n);
+  if (!workspace || workspace_bytes < need)
+    return set_error(WS_EWORKSPACE, "%s: workspace %zu < %zu bytes", name, workspace_bytes,
+                     need);
+  if (((uintptr_t)workspace & 255u) != 0)
+    return set_error(WS_EINVAL, "%s: workspace must be 256-byte aligned", name);
+  const SplitWorkspace w = carve_workspace(workspace, B, kMlaH, n);
+  MlaParams prm;
+  prm.q_nope = q_nope;
+  prm.q_pe = q_pe;
+  prm.latent = latent_pages;
+  prm.latent_w = latent_pages;
+  prm.page_table = page_table;
+  prm.len_in = len_in;
+  prm.len_out = len_out;
+  prm.c_new = c_new;
+  prm.pe_new = pe_new;
+  prm.c_stride = c_stride;
+  prm.pe_stride = pe_stride;
+  prm.out = out;
+  prm.lse = lse;
+  prm.part_out = w.part_out;
+  prm.part_lse = w.part_lse;
+  prm.B = B;
+  prm.page_size = page_size;
+  prm.max_pages = max_pages;
+  prm.num_pages = num_pages;
+  prm.cap = (int)std::min<long long>((long long)page_size * max_pages, 1LL << 30);
+  prm.scale_log2 = scale * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  if (c_new)
+    hipLaunchKernelGGL(mla_decode_kernel<true>, dim3(n), dim3(256), 0, s, prm);
+  else
+    hipLaunchKernelGGL(mla_decode_kernel<false>, dim3(n), dim3(256), 0, s, prm);
+  int rc = check_launch(name);
+  if (rc || n == 1) return rc;
+  hipLaunchKernelGGL(mla_reduce_kernel, dim3(B * kMlaH, kMlaC / 256), dim3(64), 0, s, prm,
+                     n);
+  return check_launch(name);
+}
+
+}  // namespace ws
+
+using namespace ws;
+
+extern "C" int ws_mla_decode_partial(const uint16_t* q_nope, const uint16_t* q_pe,
+                                     const uint16_t* latent_pages,
+                                     const int32_t* page_table, const int32_t* gpu_len,
+                                     int B, int H, int page_size, int max_pages,
+                                     int num_pages, int max_len, int n_workgroups,
+                                     float scale, float* out, float* lse, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  return mla_launch(q_nope, q_pe, nullptr, 0, nullptr, 0, (uint16_t*)latent_pages,
+                    page_table, gpu_len, nullptr, B, H, page_size, max_pages, num_pages,
+                    max_len, n_workgroups, scale, out, lse, workspace, workspace_bytes,
+                    stream, "ws_mla_decode_partial");
+}
+
+extern "C" int ws_mla_append_decode_partial(
+    const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_new,
+    int64_t c_stride, const uint16_t* pe_new, int64_t pe_stride, uint16_t* latent_pages,
+    const int32_t* page_table, const int32_t* len_in, int32_t* len_out, int B, int H,
+    int page_size, int max_pages, int num_pages, int max_len, int n_workgroups,
+    float scale, float* out, float* lse, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  if (!c_new) return set_error(WS_EINVAL, "ws_mla_append_decode_partial: c_new is null");
+  return mla_launch(q_nope, q_pe, c_new, c_stride, pe_new, pe_stride, latent_pages,
+                    page_table, len_in, len_out, B, H, page_size, max_pages, num_pages,
+                    max_len, n_workgroups, scale, out, lse, workspace, workspace_bytes,
+                    stream, "ws_mla_append_decode_partial");
+}

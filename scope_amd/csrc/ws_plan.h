@@ -1,0 +1,106 @@
+// Load-balanced work plan of the decode kernels, computed on the device.
+//
+// The work of a call is the list of 32-token blocks of every row (GQA row =
+// (sequence, kv head), MLA row = sequence), rows in order.  With
+// nb(b) = ceil(len_b / 32) blocks per row of sequence b and R rows per
+// sequence, T = sum_b R * nb(b).  A grid of n workgroups gives workgroup g
+// the blocks [floor(g T / n), floor((g + 1) T / n)), so every workgroup
+// streams the same amount of KV whatever the lengths (n is capped at T, so
+// no range is empty).  A workgroup walks its range as row segments; a row
+// covered by several workgroups gets one partial per workgroup, stored in
+// slot g + row: along the block order both g and row are non-decreasing, so
+// g + row is distinct for every (workgroup, row) pair and slots stay below
+// n + rows.
+#pragma once
+
+#include "ws_common.h"
+
+namespace ws {
+
+// Most sequences a call takes (the per-sequence prefix lives in LDS).
+constexpr int kMaxSeqs = 2048;
+
+struct Plan {
+  int T;  // total blocks (the host keeps it below 2^31 / grid)
+  int n;  // workgroups with work (min(grid, T))
+};
+
+// Workgroup-uniform value moved to a scalar register.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Sequence length used by the kernels: len_in[b] clamped to [0, cap - add],
+// plus `add` (1 when the call appends the step's new token).
+__device__ __forceinline__ int plan_len(const int32_t* len_in, int b, int add, int cap) {
+  int l = len_in[b];
+  l = max(0, min(l, cap - add));
+  return l + add;
+}
+
+// Builds s_pref[0..B] (exclusive prefix of blocks per sequence, R rows each)
+// with the NT threads of the workgroup and returns the plan.  s_scan holds
+// NT / 64 + 1 ints.  Every thread must call it (it synchronises).
+template <int NT>
+__device__ Plan plan_build(const int32_t* len_in, int add, int cap, int B, int R,
+                           int grid, int* s_pref, int* s_scan) {
+  constexpr int NW = NT / 64;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int chunk = (B + NT - 1) / NT;
+  const int b0 = min(B, t * chunk);
+  const int b1 = min(B, b0 + chunk);
+  int local = 0;
+  for (int b = b0; b < b1; ++b) local += R * ((plan_len(len_in, b, add, cap) + 31) >> 5);
+  // inclusive scan of `local` across the wave
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o);
+    if (lane >= o) incl += v;
+  }
+  if (lane == 63) s_scan[wave] = incl;
+  __syncthreads();
+  if (t == 0) {
+    int run = 0;
+    for (int w = 0; w < NW; ++w) {
+      const int v = s_scan[w];
+      s_scan[w] = run;
+      run += v;
+    }
+    s_scan[NW] = run;
+  }
+  __syncthreads();
+  int run = s_scan[wave] + incl - local;
+  for (int b = b0; b < b1; ++b) {
+    s_pref[b] = run;
+    run += R * ((plan_len(len_in, b, add, cap) + 31) >> 5);
+  }
+  if (t == 0) s_pref[B] = s_scan[NW];
+  __syncthreads();
+  Plan p;
+  p.T = uniform(s_scan[NW]);
+  p.n = min(grid, p.T);
+  return p;
+}
+
+__device__ __forceinline__ int plan_start(const Plan& p, int g) {
+  return (int)((long long)g * p.T / p.n);
+}
+
+// Workgroup whose range holds block blk.
+__device__ __forceinline__ int plan_owner(const Plan& p, int blk) {
+  return (int)(((long long)(blk + 1) * p.n + p.T - 1) / p.T) - 1;
+}
+
+// Sequence holding block blk: the last b with s_pref[b] <= blk (B >= 1).
+__device__ __forceinline__ int plan_seq(const int* s_pref, int B, int blk) {
+  int lo = 0, hi = B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (uniform(s_pref[mid]) <= blk) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+}  // namespace ws

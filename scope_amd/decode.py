@@ -58,11 +58,11 @@ def _to_device_pinned(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
 
 def partitioned_gqa_decode(cache: PartitionedKVCache, layer: int, q: torch.Tensor,
                            scale: float, cpu_attn=None, cpu_format="fused_cpu_attn_bf16",
-                           k_new=None, v_new=None, tokens_per_split=0):
+                           k_new=None, v_new=None, n_workgroups=0):
     """One decode step of GQA attention over a host/GPU partitioned cache.
 
     q [B, Hq, D] bf16 on the GPU; k_new/v_new [B, Hkv, 1, D] (optional) are
-    appended to the GPU partition first.  cpu_attn(q [Hkv, G, D], k [Hkv, S, D],
+    appended to the GPU partition in the same launch as its partial.  cpu_attn(q [Hkv, G, D], k [Hkv, S, D],
     v [Hkv, S, D], scale) -> (out, max, sum) is called once per sequence with
     host tokens (the reference kernels take one S per call,
     kernel/cpu_attn.cpp:590).  Returns out [B, Hq, 1, D] bf16.
@@ -71,8 +71,6 @@ def partitioned_gqa_decode(cache: PartitionedKVCache, layer: int, q: torch.Tenso
     B, Hq, D = q.shape
     Hkv = cache.num_kv_heads
     G = Hq // Hkv
-    if k_new is not None:
-        gpu.append_4d(layer, k_new, v_new)
     need_cpu = cpu_attn is not None and bool((cache.host_len[layer] > 0).any())
     worker = None
     if need_cpu:
@@ -96,7 +94,10 @@ def partitioned_gqa_decode(cache: PartitionedKVCache, layer: int, q: torch.Tenso
 
         worker = _CpuPartial(host_partial)
         worker.start()
-    out_g, lse_g = gpu.attend(layer, q, scale, tokens_per_split)
+    if k_new is not None:
+        out_g, lse_g = gpu.step(layer, q, k_new, v_new, scale, n_workgroups)
+    else:
+        out_g, lse_g = gpu.attend(layer, q, scale, n_workgroups)
     if worker is None:
         empty = torch.full_like(lse_g, float("-inf"))
         out, _ = ops.lse_merge(out_g, lse_g, (out_g, empty), ops.PARTIAL_LSE_F32,
@@ -112,7 +113,7 @@ def partitioned_gqa_decode(cache: PartitionedKVCache, layer: int, q: torch.Tenso
 def partitioned_mla_decode(cache: PartitionedLatentCache, layer: int,
                            q_nope: torch.Tensor, q_pe: torch.Tensor, scale: float,
                            cpu_attn_mla_compressed=None, c_new=None, pe_new=None,
-                           tokens_per_split=0):
+                           n_workgroups=0):
     """One decode step of absorbed-MLA attention over a partitioned latent cache.
 
     q_nope [B*H, 512] (W_UK-absorbed) and q_pe [B*H, 64] bf16 on the GPU;
@@ -131,7 +132,7 @@ def partitioned_mla_decode(cache: PartitionedLatentCache, layer: int,
         worker = _CpuPartial(lambda: cpu_attn_mla_compressed(
             qn_host, qp_host, hc.contiguous(), hpe.contiguous(), scale))
         worker.start()
-    out_g, lse_g = gpu.attend(layer, q_nope, q_pe, scale, tokens_per_split)
+    out_g, lse_g = gpu.attend(layer, q_nope, q_pe, scale, n_workgroups)
     if worker is None:
         empty = torch.full_like(lse_g, float("-inf"))
         out, _ = ops.lse_merge(out_g, lse_g, (out_g, empty), ops.PARTIAL_LSE_F32,

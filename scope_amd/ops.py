@@ -27,10 +27,12 @@ EXPORTS = (
     "ws_version",
     "ws_kv_append",
     "ws_latent_append",
-    "ws_decode_workspace_bytes",
+    "ws_workspace_clear",
     "ws_decode_plan",
     "ws_gqa_decode_partial",
+    "ws_gqa_append_decode_partial",
     "ws_mla_decode_partial",
+    "ws_mla_append_decode_partial",
     "ws_split_reduce",
     "ws_lse_merge",
 )
@@ -75,19 +77,27 @@ def lib() -> ctypes.CDLL:
         L.ws_latent_append.restype = i32
         L.ws_latent_append.argtypes = [vp, i64, vp, i64, vp, vp, vp, i32, i32,
                                        i32, i32, i32, i32, vp]
-        L.ws_decode_workspace_bytes.restype = sz
-        L.ws_decode_workspace_bytes.argtypes = [i32, i32, i32]
+        L.ws_workspace_clear.restype = i32
+        L.ws_workspace_clear.argtypes = [vp, sz, vp]
         L.ws_decode_plan.restype = i32
-        L.ws_decode_plan.argtypes = [i32, i32, i32, i32,
-                                     ctypes.POINTER(i32), ctypes.POINTER(i32)]
+        L.ws_decode_plan.argtypes = [i32, i32, i32, i32, i32,
+                                     ctypes.POINTER(i32), ctypes.POINTER(sz)]
         L.ws_gqa_decode_partial.restype = i32
         L.ws_gqa_decode_partial.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32,
                                             i32, i32, i32, i32, i32, i32, f32,
                                             vp, vp, vp, sz, vp]
+        L.ws_gqa_append_decode_partial.restype = i32
+        L.ws_gqa_append_decode_partial.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp,
+                                                   i32, i32, i32, i32, i32, i32, i32,
+                                                   i32, i32, f32, vp, vp, vp, sz, vp]
         L.ws_mla_decode_partial.restype = i32
         L.ws_mla_decode_partial.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32,
                                             i32, i32, i32, i32, f32, vp, vp,
                                             vp, sz, vp]
+        L.ws_mla_append_decode_partial.restype = i32
+        L.ws_mla_append_decode_partial.argtypes = [vp, vp, vp, i64, vp, i64, vp, vp,
+                                                   vp, vp, i32, i32, i32, i32, i32,
+                                                   i32, i32, f32, vp, vp, vp, sz, vp]
         L.ws_split_reduce.restype = i32
         L.ws_split_reduce.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp,
                                       vp, vp]
@@ -134,22 +144,33 @@ _workspaces: dict = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device scratch for split partials, grown on demand (stream-ordered
-    reuse is safe on the stream that launched the decode kernels)."""
+    """Per-device scratch for split partials and the split arrival counters,
+    grown on demand.  It starts zeroed (the counters must be zero before first
+    use; every completed decode call leaves them zero), and is reused in
+    stream order by calls on the stream that launches the decode kernels."""
     key = device.index if device.index is not None else torch.cuda.current_device()
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 
 
-def decode_plan(kind: int, rows_kv: int, max_len: int, tokens_per_split: int = 0):
-    """(tokens_per_split, n_splits) the library uses for a decode call."""
-    tps, ns = ctypes.c_int(0), ctypes.c_int(0)
-    _check(lib().ws_decode_plan(kind, rows_kv, max_len, tokens_per_split,
-                                ctypes.byref(tps), ctypes.byref(ns)), "ws_decode_plan")
-    return tps.value, ns.value
+def decode_plan(kind: int, rows_kv: int, heads: int, max_len: int,
+                n_workgroups: int = 0):
+    """(n_workgroups, workspace_bytes) of a decode call: kind 0 = GQA
+    (rows_kv = B * Hkv, heads = group size), 1 = MLA (rows_kv = B, heads = 16).
+    n_workgroups 0 lets the library choose for the current device."""
+    n, wsb = ctypes.c_int(0), ctypes.c_size_t(0)
+    _check(lib().ws_decode_plan(kind, rows_kv, heads, max_len, n_workgroups,
+                                ctypes.byref(n), ctypes.byref(wsb)), "ws_decode_plan")
+    return n.value, wsb.value
+
+
+def workspace_clear(ws: torch.Tensor) -> None:
+    """Zero a workspace tensor with the library's fill kernel."""
+    _check(lib().ws_workspace_clear(_ptr(ws), ws.numel() * ws.element_size(),
+                                    _stream(ws.device)), "ws_workspace_clear")
 
 
 # ---------------------------------------------------------------------------
@@ -210,7 +231,7 @@ def latent_append(c_new, pe_new, latent_pages, page_table, gpu_len, update_len=T
 
 
 def gqa_decode_partial(q, k_pages, v_pages, page_table, gpu_len, scale, max_len,
-                       tokens_per_split=0, out=None, lse=None):
+                       n_workgroups=0, out=None, lse=None):
     """Split-KV GQA decode attention over the pooled tokens.
 
     q [B, Hq, D] bf16 -> (out [B, Hq, D] fp32 normalised, lse [B, Hq] fp32).
@@ -234,20 +255,17 @@ def gqa_decode_partial(q, k_pages, v_pages, page_table, gpu_len, scale, max_len,
         lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
     _require(out, "out", torch.float32, dev, 3)
     _require(lse, "lse", torch.float32, dev, 2)
-    tps, ns = decode_plan(0, B * Hkv, int(max_len), int(tokens_per_split))
-    ws, wsb = None, 0
-    if ns > 1:
-        wsb = lib().ws_decode_workspace_bytes(B * Hq, D, ns)
-        ws = _workspace(dev, wsb)
+    nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
+    ws = _workspace(dev, wsb)
     _check(lib().ws_gqa_decode_partial(
         _ptr(q), _ptr(k_pages), _ptr(v_pages), _ptr(page_table), _ptr(gpu_len),
-        B, Hq, Hkv, D, PS, page_table.shape[1], P, int(max_len), tps, float(scale),
+        B, Hq, Hkv, D, PS, page_table.shape[1], P, int(max_len), nwg, float(scale),
         _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev)), "ws_gqa_decode_partial")
     return out, lse
 
 
 def mla_decode_partial(q_nope, q_pe, latent_pages, page_table, gpu_len, scale, max_len,
-                       tokens_per_split=0, out=None, lse=None):
+                       n_workgroups=0, out=None, lse=None):
     """Split-KV absorbed-MLA decode attention over the pooled latents.
 
     q_nope [B*H, 512] bf16 (W_UK-absorbed), q_pe [B*H, 64] bf16 ->
@@ -273,15 +291,97 @@ def mla_decode_partial(q_nope, q_pe, latent_pages, page_table, gpu_len, scale, m
         lse = torch.empty((rows,), dtype=torch.float32, device=dev)
     _require(out, "out", torch.float32, dev, 2)
     _require(lse, "lse", torch.float32, dev, 1)
-    tps, ns = decode_plan(1, B, int(max_len), int(tokens_per_split))
-    ws, wsb = None, 0
-    if ns > 1:
-        wsb = lib().ws_decode_workspace_bytes(rows, MLA_C, ns)
-        ws = _workspace(dev, wsb)
+    nwg, wsb = decode_plan(1, B, H, int(max_len), int(n_workgroups))
+    ws = _workspace(dev, wsb)
     _check(lib().ws_mla_decode_partial(
         _ptr(q_nope), _ptr(q_pe), _ptr(latent_pages), _ptr(page_table), _ptr(gpu_len),
-        B, H, PS, page_table.shape[1], P, int(max_len), tps, float(scale),
+        B, H, PS, page_table.shape[1], P, int(max_len), nwg, float(scale),
         _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev)), "ws_mla_decode_partial")
+    return out, lse
+
+
+def gqa_append_decode_partial(q, k_new, v_new, k_pages, v_pages, page_table, len_in,
+                              len_out, scale, max_len, n_workgroups=0, out=None,
+                              lse=None):
+    """Append k_new/v_new [B, Hkv, 1, D] at position len_in[b] of each sequence
+    and attend over the partition including it, in one launch.  len_out[b] =
+    len_in[b] + 1 (len_out may be None; it must not be len_in).  max_len must
+    bound every len_in[b] + 1.  Returns (out [B, Hq, D] fp32, lse [B, Hq])."""
+    dev = k_pages.device
+    _require(q, "q", torch.bfloat16, dev, 3)
+    _require(k_new, "k_new", torch.bfloat16, dev, 4)
+    _require(v_new, "v_new", torch.bfloat16, dev, 4)
+    _require(k_pages, "k_pages", torch.bfloat16, dev, 4)
+    _require(v_pages, "v_pages", torch.bfloat16, dev, 4)
+    _require(page_table, "page_table", torch.int32, dev, 2)
+    _require(len_in, "len_in", torch.int32, dev, 1)
+    B, Hq, D = q.shape
+    P, Hkv, PS, D2 = k_pages.shape
+    if v_pages.shape != k_pages.shape or D2 != D:
+        raise ValueError("k/v page pools must match q's head_dim")
+    if k_new.shape != (B, Hkv, 1, D) or v_new.shape != k_new.shape:
+        raise ValueError(f"k_new/v_new must be [B, Hkv, 1, D] = {(B, Hkv, 1, D)}")
+    if page_table.shape[0] != B or len_in.shape[0] != B:
+        raise ValueError("page_table/len_in batch mismatch")
+    if len_out is not None:
+        _require(len_out, "len_out", torch.int32, dev, 1)
+        if len_out.shape[0] != B or len_out.data_ptr() == len_in.data_ptr():
+            raise ValueError("len_out must be a separate [B] int32 tensor")
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device=dev)
+    if lse is None:
+        lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
+    _require(out, "out", torch.float32, dev, 3)
+    _require(lse, "lse", torch.float32, dev, 2)
+    nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
+    ws = _workspace(dev, wsb)
+    _check(lib().ws_gqa_append_decode_partial(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
+        _ptr(len_in), _ptr(len_out), B, Hq, Hkv, D, PS, page_table.shape[1], P,
+        int(max_len), nwg, float(scale), _ptr(out), _ptr(lse), _ptr(ws), wsb,
+        _stream(dev)), "ws_gqa_append_decode_partial")
+    return out, lse
+
+
+def mla_append_decode_partial(q_nope, q_pe, c_new, pe_new, latent_pages, page_table,
+                              len_in, len_out, scale, max_len, n_workgroups=0,
+                              out=None, lse=None):
+    """Append the new latent (c_new [B, 1, 512], pe_new [B, 1, 64], unit last
+    stride) at position len_in[b] and attend over the partition including it.
+    Returns (out [B*H, 512] fp32, lse [B*H])."""
+    dev = latent_pages.device
+    _require(q_nope, "q_nope", torch.bfloat16, dev, 2)
+    _require(q_pe, "q_pe", torch.bfloat16, dev, 2)
+    _require(latent_pages, "latent_pages", torch.bfloat16, dev, 3)
+    _require(page_table, "page_table", torch.int32, dev, 2)
+    _require(len_in, "len_in", torch.int32, dev, 1)
+    B = page_table.shape[0]
+    for t, n, w in ((c_new, "c_new", MLA_C), (pe_new, "pe_new", MLA_PE)):
+        _require(t, n, torch.bfloat16, dev, 3, contiguous=False)
+        if t.shape != (B, 1, w) or t.stride(2) != 1:
+            raise ValueError(f"{n} must be [B, 1, {w}] with unit last stride")
+    P, PS, L = latent_pages.shape
+    rows = q_nope.shape[0]
+    if L != MLA_LATENT or q_nope.shape[1] != MLA_C or q_pe.shape != (rows, MLA_PE):
+        raise ValueError("MLA layout is q_nope 512 + q_pe 64 over a 576 latent")
+    if B == 0 or rows % B or len_in.shape[0] != B:
+        raise ValueError("rows must be B * H with B = page_table.shape[0]")
+    if len_out is not None:
+        _require(len_out, "len_out", torch.int32, dev, 1)
+        if len_out.shape[0] != B or len_out.data_ptr() == len_in.data_ptr():
+            raise ValueError("len_out must be a separate [B] int32 tensor")
+    H = rows // B
+    if out is None:
+        out = torch.empty((rows, MLA_C), dtype=torch.float32, device=dev)
+    if lse is None:
+        lse = torch.empty((rows,), dtype=torch.float32, device=dev)
+    nwg, wsb = decode_plan(1, B, H, int(max_len), int(n_workgroups))
+    ws = _workspace(dev, wsb)
+    _check(lib().ws_mla_append_decode_partial(
+        _ptr(q_nope), _ptr(q_pe), _ptr(c_new), c_new.stride(0), _ptr(pe_new),
+        pe_new.stride(0), _ptr(latent_pages), _ptr(page_table), _ptr(len_in),
+        _ptr(len_out), B, H, PS, page_table.shape[1], P, int(max_len), nwg, float(scale),
+        _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev)), "ws_mla_append_decode_partial")
     return out, lse
 
 

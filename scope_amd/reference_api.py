@@ -24,7 +24,7 @@ def _dense_paging(n: int, s: int, device):
 
 
 def local_bmm_softmax(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
-                      tokens_per_split: int = 0):
+                      n_workgroups: int = 0):
     """_local_bmm_softmax (roofline/bench_resident_kv.py:150-157).
 
     q [N, G, D], k/v [N, S, D] bf16 contiguous on the GPU ->
@@ -39,7 +39,7 @@ def local_bmm_softmax(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: 
     pt, ln = _dense_paging(N, S, q.device)
     out, lse = ops.gqa_decode_partial(q.contiguous(), k.contiguous().view(N, 1, S, D),
                                       v.contiguous().view(N, 1, S, D), pt, ln, scale, S,
-                                      tokens_per_split)
+                                      n_workgroups)
     return out, lse.unsqueeze(-1), torch.ones_like(lse).unsqueeze(-1)
 
 
@@ -59,8 +59,9 @@ def pairwise_merge(o1, m1, s1, o2, m2, s2):
 
 def resident_layer(q, k_buf, v_buf, new_k, new_v, scale):
     """_resident_layer (roofline/bench_resident_kv.py:261-271): write the new
-    token into the last slot of the resident buffers, then attend over all of
-    them.  k_buf/v_buf [N, cap, D], new_k/new_v [N, 1, D], q [N, G, D]."""
+    token into the last slot of the resident buffers and attend over all of
+    them, in one launch.  k_buf/v_buf [N, cap, D], new_k/new_v [N, 1, D],
+    q [N, G, D]; returns the equivalent triple like local_bmm_softmax."""
     N, cap, D = k_buf.shape
     if N <= 0 or cap <= 0:
         G = q.shape[1]
@@ -69,7 +70,8 @@ def resident_layer(q, k_buf, v_buf, new_k, new_v, scale):
                            device=q.device),
                 torch.zeros((max(N, 0), G, 1), dtype=torch.float32, device=q.device))
     pt, ln = _dense_paging(N, cap - 1, q.device)
-    ops.kv_append(new_k.contiguous().view(N, 1, 1, D), new_v.contiguous().view(N, 1, 1, D),
-                  k_buf.view(N, 1, cap, D), v_buf.view(N, 1, cap, D), pt, ln,
-                  update_len=True)
-    return local_bmm_softmax(q, k_buf, v_buf, scale)
+    out, lse = ops.gqa_append_decode_partial(
+        q.contiguous(), new_k.contiguous().view(N, 1, 1, D),
+        new_v.contiguous().view(N, 1, 1, D), k_buf.view(N, 1, cap, D),
+        v_buf.view(N, 1, cap, D), pt, ln, None, scale, cap)
+    return out, lse.unsqueeze(-1), torch.ones_like(lse).unsqueeze(-1)

@@ -35,15 +35,24 @@ def test_every_declared_symbol_is_exported():
 def test_version_and_plan():
     L = ops.lib()
     assert L.ws_version().decode().startswith("wsgpu")
-    tps, ns = ops.decode_plan(0, 16, 32768, 256)
-    assert (tps, ns) == (256, 128)
-    tps, ns = ops.decode_plan(0, 16, 0, 0)
-    assert ns == 1 and tps % 32 == 0
-    tps, ns = ops.decode_plan(1, 8, 8192, 0)
-    assert tps % 32 == 0 and ns == -(-8192 // tps)
+    pad = lambda n: -(-n // 256) * 256
+    # explicit workgroup counts are kept; workspace = counters + slots
+    n, wsb = ops.decode_plan(0, 16, 8, 32768, 100)
+    assert n == 100 and wsb == 65536 + pad((100 + 16) * 8 * 4) + (100 + 16) * 8 * 128 * 4
+    n, wsb = ops.decode_plan(1, 8, 16, 16384, 64)
+    assert n == 64 and wsb == 65536 + pad((64 + 8) * 16 * 4) + (64 + 8) * 16 * 512 * 4
+    # the library's choice never exceeds the blocks available (8 per GQA
+    # workgroup, 4 per MLA workgroup) nor the combine's 4096 weights
+    for rows, G, L in ((128, 4, 15773), (16, 8, 131072), (4, 8, 4096), (1, 1, 1), (2, 16, 1 << 20)):
+        n, _ = ops.decode_plan(0, rows, G, L, 0)
+        assert 1 <= n <= max(1, -(-rows * -(-L // 32) // 8)) and n * G <= 4096
+    n, _ = ops.decode_plan(1, 8, 16, 8192, 0)
+    assert 1 <= n <= 8 * 256 // 4
     with pytest.raises(ops.WsError):
-        ops.decode_plan(0, 16, 100, 48)  # not a multiple of 32
-    assert L.ws_decode_workspace_bytes(10, 128, 3) == 3 * 10 * 129 * 4
+        ops.decode_plan(0, 16, 0, 100, 0)  # no heads
+    with pytest.raises(ops.WsError):
+        ops.decode_plan(0, 16, 8, 100, -1)
+
 
 
 def test_host_side_argument_checks():
@@ -60,13 +69,33 @@ def test_host_side_argument_checks():
     rc = L.ws_gqa_decode_partial(fake, fake, fake, fake, fake, 1, 32, 8, 128, 48, 4, 4,
                                  100, 0, 1.0, fake, fake, None, 0, None)
     assert rc == -1 and b"paging" in L.ws_last_error()
-    # workspace too small for a multi-split call
+    # workspace too small
     rc = L.ws_gqa_decode_partial(fake, fake, fake, fake, fake, 1, 32, 8, 128, 64, 64, 64,
-                                 4096, 256, 1.0, fake, fake, None, 0, None)
+                                 4096, 16, 1.0, fake, fake, None, 0, None)
     assert rc == -3 and b"workspace" in L.ws_last_error()
     rc = L.ws_mla_decode_partial(fake, fake, fake, fake, fake, 1, 8, 64, 4, 4, 100, 0, 1.0,
                                  fake, fake, None, 0, None)
     assert rc == -1 and b"H=8" in L.ws_last_error()
+    # fused append: len_out must not alias len_in; k_new required
+    rc = L.ws_gqa_append_decode_partial(fake, fake, fake, fake, fake, fake, fake, fake, 1, 32,
+                                        8, 128, 64, 4, 4, 100, 0, 1.0, fake, fake, None, 0,
+                                        None)
+    assert rc == -1 and b"alias" in L.ws_last_error()
+    rc = L.ws_gqa_append_decode_partial(fake, None, fake, fake, fake, fake, fake, None, 1, 32,
+                                        8, 128, 64, 4, 4, 100, 0, 1.0, fake, fake, None, 0,
+                                        None)
+    assert rc == -1 and b"k_new" in L.ws_last_error()
+    rc = L.ws_mla_append_decode_partial(fake, fake, fake, 100, fake, 576, fake, fake, fake,
+                                        None, 1, 16, 64, 4, 4, 100, 0, 1.0, fake, fake, None,
+                                        0, None)
+    assert rc == -1 and b"new-latent" in L.ws_last_error()
+    # misaligned workspace
+    rc = L.ws_gqa_decode_partial(fake, fake, fake, fake, fake, 1, 32, 8, 128, 64, 64, 64,
+                                 4096, 16, 1.0, fake, fake, ctypes.c_void_p(0x1010),
+                                 1 << 30, None)
+    assert rc == -1 and b"256-byte" in L.ws_last_error()
+    rc = L.ws_workspace_clear(None, 16, None)
+    assert rc == -1
     rc = L.ws_lse_merge(fake, fake, fake, fake, None, 1, None, fake, None, 4, 128, None)
     assert rc == -1 and b"b_aux1" in L.ws_last_error()
     rc = L.ws_lse_merge(fake, fake, fake, fake, None, 9, None, fake, None, 4, 128, None)

@@ -92,15 +92,15 @@ def test_latent_append_bit_exact_strided():
 # GQA partial
 
 
-def _gqa_check(lens, Hkv, G, PS=64, tps=0, seed=1, sigma=1.0, port_check=True):
+def _gqa_check(lens, Hkv, G, PS=64, wg=0, seed=1, sigma=1.0, port_check=True):
     D = 128
     B = len(lens)
-    _say(f"gqa lens={list(lens)[:8]}{'...' if B > 8 else ''} Hkv={Hkv} G={G} PS={PS} tps={tps}")
+    _say(f"gqa lens={list(lens)[:8]}{'...' if B > 8 else ''} Hkv={Hkv} G={G} PS={PS} wg={wg}")
     k_pages, v_pages, pt, gl, ks, vs = gqa_pool(lens, Hkv, D, PS, seed, DEV, sigma)
     q = bf16_randn((B, Hkv * G, D), seed + 77, sigma)
     scale = D ** -0.5
     out, lse = ops.gqa_decode_partial(q.to(DEV), k_pages, v_pages, pt, gl, scale,
-                                      max(lens), tokens_per_split=tps)
+                                      max(lens), n_workgroups=wg)
     torch.cuda.synchronize()
     out, lse = out.cpu().numpy(), lse.cpu().numpy()
     qb = bits(q).reshape(B, Hkv, G, D)
@@ -127,10 +127,12 @@ def test_gqa_group_sizes(G):
     _gqa_check([300, 64, 1], Hkv=2, G=G, seed=40 + G)
 
 
-@pytest.mark.parametrize("tps", [0, 32, 64, 96, 256])
-def test_gqa_ragged_lengths_and_splits(tps):
+@pytest.mark.parametrize("wg", [0, 1, 3, 7, 64, 1000])
+def test_gqa_ragged_lengths_and_workgroups(wg):
+    # 1 workgroup walks every row; 3 and 7 split rows across workgroups at
+    # odd block boundaries; 1000 exceeds the blocks (capped on the device)
     lens = [0, 1, 31, 32, 33, 63, 64, 65, 127, 1000]
-    _gqa_check(lens, Hkv=8, G=4, tps=tps, seed=5)
+    _gqa_check(lens, Hkv=8, G=4, wg=wg, seed=5)
 
 
 def test_gqa_page_size_128_and_32():
@@ -148,9 +150,9 @@ def test_gqa_split_invariance_and_page_permutation():
     k_pages, v_pages, pt, gl, ks, vs = gqa_pool(lens, 8, 128, 64, 11, DEV)
     q = bf16_randn((2, 32, 128), 12).to(DEV)
     res = [ops.gqa_decode_partial(q, k_pages, v_pages, pt, gl, 0.0884, 3000,
-                                  tokens_per_split=t) for t in (64, 512, 4096)]
+                                  n_workgroups=n) for n in (1, 8, 100)]
     # P is rounded to bf16 against each split's running max, so outputs of
-    # different split sizes differ at the bf16 level; the fp32 sums keep the
+    # different split counts differ at the bf16 level; the fp32 sums keep the
     # LSE split-independent to fp32 rounding.
     for o, l in res[1:]:
         assert_close(o.cpu().numpy(), res[0][0].cpu().numpy(), 2e-3, 2e-3, "split inv")
@@ -161,7 +163,7 @@ def test_gqa_split_invariance_and_page_permutation():
     k2 = torch.empty_like(k_pages); v2 = torch.empty_like(v_pages)
     k2[inv] = k_pages; v2[inv] = v_pages
     pt2 = torch.where(pt >= 0, inv[pt.long().clamp(min=0)].int(), pt)
-    o2, l2 = ops.gqa_decode_partial(q, k2, v2, pt2, gl, 0.0884, 3000, tokens_per_split=512)
+    o2, l2 = ops.gqa_decode_partial(q, k2, v2, pt2, gl, 0.0884, 3000, n_workgroups=8)
     assert torch.equal(o2, res[1][0]) and torch.equal(l2, res[1][1])
 
 
@@ -169,15 +171,15 @@ def test_gqa_split_invariance_and_page_permutation():
 # MLA partial
 
 
-def _mla_check(lens, tps=0, seed=3, sigma=0.5, PS=64):
+def _mla_check(lens, wg=0, seed=3, sigma=0.5, PS=64):
     B, H = len(lens), 16
-    _say(f"mla lens={lens} tps={tps} PS={PS}")
+    _say(f"mla lens={lens} wg={wg} PS={PS}")
     lat, pt, gl, cs, pes = mla_pool(lens, PS, seed, DEV, sigma)
     qn = bf16_randn((B * H, 512), seed + 91, sigma)
     qp = bf16_randn((B * H, 64), seed + 92, sigma)
     scale = 192 ** -0.5
     out, lse = ops.mla_decode_partial(qn.to(DEV), qp.to(DEV), lat, pt, gl, scale,
-                                      max(lens), tokens_per_split=tps)
+                                      max(lens), n_workgroups=wg)
     torch.cuda.synchronize()
     out, lse = out.cpu().numpy(), lse.cpu().numpy()
     for b in range(B):
@@ -193,9 +195,9 @@ def _mla_check(lens, tps=0, seed=3, sigma=0.5, PS=64):
             assert_close(lse[rows], pm + np.log(ps), LSE_ATOL, LSE_RTOL, f"port lse b={b}")
 
 
-@pytest.mark.parametrize("tps", [0, 32, 64, 256])
-def test_mla_ragged(tps):
-    _mla_check([0, 1, 37, 300, 1030], tps=tps)
+@pytest.mark.parametrize("wg", [0, 1, 3, 17, 500])
+def test_mla_ragged(wg):
+    _mla_check([0, 1, 37, 300, 1030], wg=wg)
 
 
 def test_mla_config3_shape_subset():
@@ -287,3 +289,148 @@ def test_lse_merge_formats(fmt, Dv):
                      OUT_RTOL if odt == torch.bfloat16 else 1e-5, "merge out")
         assert_close(lse.cpu().numpy(), want_l, 1e-5, 1e-5, "merge lse")
     assert np.all(got[2] == 0) and np.isneginf(lse.cpu().numpy()[2])
+
+
+# ---------------------------------------------------------------------------
+# fused append + partial (one launch per decode step)
+
+
+def _counters_zero():
+    """The fixed 16384-slot counter block of the ops layer's workspace is all
+    zero again after the calls completed."""
+    ws = next(iter(ops._workspaces.values()))
+    return not ws[: 16384 * 4].any().item()
+
+
+@pytest.mark.parametrize("Hkv,G,wg", [(8, 4, 0), (8, 4, 5), (4, 8, 64), (2, 16, 3)])
+def test_gqa_append_decode_fused_steps(Hkv, G, wg):
+    _say(f"gqa fused append+decode Hkv={Hkv} G={G} wg={wg}")
+    D, PS = 128, 64
+    lens = [0, 1, 63, 64, 200, 777]
+    B, steps = len(lens), 3
+    total = [L + steps for L in lens]
+    k_pages, v_pages, pt, gl, ks, vs = gqa_pool(total, Hkv, D, PS, seed=21)
+    # the pool holds all tokens; the partition starts with `lens` of them
+    lens2 = torch.zeros((2, B), dtype=torch.int32, device=DEV)
+    lens2[0] = torch.tensor(lens, dtype=torch.int32)
+    # zero the slots the steps will append into, so the writes are observable
+    for b, L in enumerate(lens):
+        for t in range(L, L + steps):
+            k_pages[pt[b, t // PS].long(), :, t % PS] = 0
+            v_pages[pt[b, t // PS].long(), :, t % PS] = 0
+    scale = D ** -0.5
+    for i in range(steps):
+        q = bf16_randn((B, Hkv * G, D), 900 + i)
+        k_new = torch.stack([k[:, L + i:L + i + 1] for k, L in zip(ks, lens)]).to(DEV)
+        v_new = torch.stack([v[:, L + i:L + i + 1] for v, L in zip(vs, lens)]).to(DEV)
+        len_in, len_out = lens2[i % 2], lens2[(i + 1) % 2]
+        out, lse = ops.gqa_append_decode_partial(q.to(DEV), k_new.contiguous(),
+                                                 v_new.contiguous(), k_pages, v_pages, pt,
+                                                 len_in, len_out, scale,
+                                                 max(lens) + i + 1, wg)
+        torch.cuda.synchronize()
+        assert len_out.cpu().tolist() == [L + i + 1 for L in lens]
+        assert len_in.cpu().tolist() == [L + i for L in lens]
+        o, l = out.cpu().numpy(), lse.cpu().numpy()
+        qb = bits(q).reshape(B, Hkv, G, D)
+        for b, L in enumerate(lens):
+            n = L + i + 1
+            want, wl = O.gqa_attention_fp64(qb[b], bits(ks[b][:, :n]), bits(vs[b][:, :n]),
+                                            scale)
+            assert_close(o[b].reshape(Hkv, G, D), want, OUT_ATOL, OUT_RTOL, f"b={b} i={i}")
+            assert_close(l[b].reshape(Hkv, G), wl, LSE_ATOL, LSE_RTOL, f"lse b={b} i={i}")
+        # the unfused pair over the pages the fused call wrote gives the same bits
+        o2, l2 = ops.gqa_decode_partial(q.to(DEV), k_pages, v_pages, pt, len_out, scale,
+                                        max(lens) + i + 1, wg)
+        torch.cuda.synchronize()
+        assert torch.equal(o2.cpu(), out.cpu()) and torch.equal(l2.cpu(), lse.cpu())
+    # pages now hold every appended token, bit for bit
+    kp, vp = bits(k_pages), bits(v_pages)
+    tab = pt.cpu().numpy()
+    for h in range(Hkv):
+        gk = O.gather_paged(kp, tab, total, head=h)
+        gv = O.gather_paged(vp, tab, total, head=h)
+        for b in range(B):
+            assert np.array_equal(gk[b], bits(ks[b][h])), (b, h)
+            assert np.array_equal(gv[b], bits(vs[b][h])), (b, h)
+    assert _counters_zero()
+
+
+def test_gqa_many_workgroups_in_kernel_reduce():
+    # one row spread over 512 workgroups (2 blocks each): the last workgroup
+    # to arrive combines 512 partials
+    _say("gqa one row over 512 workgroups")
+    _gqa_check([32768], Hkv=1, G=8, wg=512, seed=31, port_check=False)
+    assert _counters_zero()
+
+
+def test_gqa_combine_capacity_error():
+    # 1000 workgroups x 16 heads > 4096 weights of the in-kernel combine:
+    # rejected on the host before any launch
+    k_pages, v_pages, pt, gl, ks, vs = gqa_pool([64], 1, 128, 64, seed=2)
+    q = bf16_randn((1, 16, 128), 3).to(DEV)
+    with pytest.raises(ops.WsError, match="exceed"):
+        ops.gqa_decode_partial(q, k_pages, v_pages, pt, gl, 0.1, 64, n_workgroups=1000)
+
+
+def test_workspace_clear_kernel():
+    ws = torch.full((1000,), 7, dtype=torch.uint8, device=DEV)
+    ops.workspace_clear(ws)
+    torch.cuda.synchronize()
+    assert not ws.any().item()
+
+
+@pytest.mark.parametrize("wg", [0, 3])
+def test_mla_append_decode_fused_steps(wg):
+    _say(f"mla fused append+decode wg={wg}")
+    H, PS = 16, 64
+    lens = [0, 5, 64, 300]
+    B, steps = len(lens), 2
+    total = [L + steps for L in lens]
+    lat, pt, gl, cs, pes = mla_pool(total, PS, seed=44)
+    lens2 = torch.zeros((2, B), dtype=torch.int32, device=DEV)
+    lens2[0] = torch.tensor(lens, dtype=torch.int32)
+    for b, L in enumerate(lens):
+        for t in range(L, L + steps):
+            lat[pt[b, t // PS].long(), t % PS] = 0
+    scale = 192 ** -0.5
+    for i in range(steps):
+        qn = bf16_randn((B * H, 512), 600 + i, 0.5)
+        qp = bf16_randn((B * H, 64), 700 + i, 0.5)
+        kv = torch.stack([torch.cat([c[L + i:L + i + 1], pe[L + i:L + i + 1]], 1)
+                          for c, pe, L in zip(cs, pes, lens)]).to(DEV)  # [B, 1, 576]
+        c_new, pe_new = kv[..., :512], kv[..., 512:]
+        len_in, len_out = lens2[i % 2], lens2[(i + 1) % 2]
+        out, lse = ops.mla_append_decode_partial(qn.to(DEV), qp.to(DEV), c_new, pe_new, lat,
+                                                 pt, len_in, len_out, scale,
+                                                 max(lens) + i + 1, wg)
+        torch.cuda.synchronize()
+        assert len_out.cpu().tolist() == [L + i + 1 for L in lens]
+        o, l = out.cpu().numpy(), lse.cpu().numpy()
+        for b, L in enumerate(lens):
+            n = L + i + 1
+            rows = slice(b * H, (b + 1) * H)
+            want, wl = O.mla_attention_fp64(bits(qn[rows]), bits(qp[rows]),
+                                            bits(cs[b][:n])[None], bits(pes[b][:n])[None],
+                                            scale)
+            assert_close(o[rows], want, OUT_ATOL, OUT_RTOL, f"mla b={b} i={i}")
+            assert_close(l[rows], wl, LSE_ATOL, LSE_RTOL, f"mla lse b={b} i={i}")
+        o2, l2 = ops.mla_decode_partial(qn.to(DEV), qp.to(DEV), lat, pt, len_out, scale,
+                                        max(lens) + i + 1, wg)
+        torch.cuda.synchronize()
+        assert torch.equal(o2.cpu(), out.cpu()) and torch.equal(l2.cpu(), lse.cpu())
+    got = O.gather_paged(bits(lat), pt.cpu().numpy(), total)
+    for b in range(B):
+        assert np.array_equal(got[b], np.concatenate([bits(cs[b]), bits(pes[b])], 1)), b
+
+
+def test_workspace_shared_across_shapes():
+    # one workspace serves GQA and MLA calls of different row counts in turn;
+    # partials of one call never land on another call's arrival counters
+    _say("workspace shared across shapes")
+    _gqa_check([900, 700], Hkv=2, G=4, wg=9, seed=51, port_check=False)
+    _mla_check([700, 650, 600], wg=11, seed=52)
+    _gqa_check([800] * 12, Hkv=8, G=4, wg=300, seed=53, port_check=False)
+    _mla_check([300], wg=5, seed=54)
+    _gqa_check([1000] * 3, Hkv=8, G=8, wg=200, seed=55, port_check=False)
+    assert _counters_zero()
