@@ -5,10 +5,11 @@ partitioned GQA decode at the Mixtral-8x7B layer shape: batch 16, 32 query
 heads, 8 KV heads, head_dim 128, bf16 N(0,1), per-sequence KV lengths uniform
 in [1024, 32768], the trailing floor(r*L) tokens of each sequence in 64-token
 HBM pages (r = 0.5 by default).  A step appends one token per sequence to the
-GPU partition and runs the split-KV GQA partial over the partition (one
-launch: ws_gqa_append_decode_partial), then LSE-merges it with the host
-partial (the bf16 (out, max, sum) triple of the CPU kernel, already resident
-in HBM) into the final bf16 output (ws_lse_merge).
+GPU partition and runs the load-balanced split-KV GQA partial over the
+partition (one launch: ws_gqa_append_decode_split), then combines the split
+pieces and LSE-merges them with the host partial (the bf16 (out, max, sum)
+triple of the CPU kernel, already resident in HBM) into the final bf16 output
+(one launch: ws_merge_split).
 
 Reported on one JSON line (stdout):
   value      algorithmic HBM GB/s of the whole step (bytes below / step time)
@@ -163,14 +164,17 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
     a_head = (p(q), p(k_new), p(v_new), p(k_pages), p(v_pages), p(page_table))
     a_mid = (B, Hq, Hkv, D, PAGE, max_pages, num_pages)
     a_tail = (nwg, scale, p(out_g), p(lse_g), p(ws), ctypes.c_size_t(wsb), stream)
-    a_merge = (p(out_g), p(lse_g), p(h_out), p(h_max), p(h_sum), ops.TRIPLE_NORM_BF16,
-               p(out), None, None, rows, D, stream)
-    f_step, f_merge = L.ws_gqa_append_decode_partial, L.ws_lse_merge
+    cap = PAGE * max_pages
+    # the merge reads the lengths the step wrote (its len_out)
+    a_merge = [(len_ptrs[k], B, Hkv, G, D, cap, nwg, p(out_g), p(lse_g), p(ws),
+                ctypes.c_size_t(wsb), p(h_out), p(h_max), p(h_sum), ops.TRIPLE_NORM_BF16,
+                p(out), None, None, stream) for k in (0, 1)]
+    f_step, f_merge = L.ws_gqa_append_decode_split, L.ws_merge_split
 
     for i in range(warmup):
         rc = f_step(*a_head, len_ptrs[i % 2], len_ptrs[(i + 1) % 2], *a_mid,
                     max_len0 + i + 1, *a_tail)
-        rc |= f_merge(*a_merge)
+        rc |= f_merge(*a_merge[(i + 1) % 2])
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
     timer = _Timer(steps)
@@ -185,7 +189,7 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
         rc = f_step(*a_head, len_ptrs[a_i % 2], len_ptrs[(a_i + 1) % 2], *a_mid,
                     max_len0 + a_i + 1, *a_tail)
         timer.b[i].record()
-        rc |= f_merge(*a_merge)
+        rc |= f_merge(*a_merge[(a_i + 1) % 2])
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
     t_ev1.record()
@@ -268,12 +272,14 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label, wg=0):
     a_mid = (B, H, PAGE, max_pages, num_pages)
     a_tail = (nwg, ctypes.c_float(192 ** -0.5), p(out_g), p(lse_g), p(ws),
               ctypes.c_size_t(wsb), stream)
-    a_merge = (p(out_g), p(lse_g), p(h_out), p(h_max), p(h_sum), ops.TRIPLE_UNNORM_F32,
-               p(out), None, None, rows, 512, stream)
-    f_step = L.ws_mla_append_decode_partial
+    cap = PAGE * max_pages
+    a_merge = [(len_ptrs[k], B, 1, H, 512, cap, nwg, p(out_g), p(lse_g), p(ws),
+                ctypes.c_size_t(wsb), p(h_out), p(h_max), p(h_sum), ops.TRIPLE_UNNORM_F32,
+                p(out), None, None, stream) for k in (0, 1)]
+    f_step, f_merge = L.ws_mla_append_decode_split, L.ws_merge_split
     for i in range(warmup):
         rc = f_step(*a_head, len_ptrs[i % 2], len_ptrs[(i + 1) % 2], *a_mid,
-                    max_len0 + i + 1, *a_tail) | L.ws_lse_merge(*a_merge)
+                    max_len0 + i + 1, *a_tail) | f_merge(*a_merge[(i + 1) % 2])
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
     timer = _Timer(steps)
@@ -287,7 +293,7 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label, wg=0):
         rc = f_step(*a_head, len_ptrs[a_i % 2], len_ptrs[(a_i + 1) % 2], *a_mid,
                     max_len0 + a_i + 1, *a_tail)
         timer.b[i].record()
-        rc |= L.ws_lse_merge(*a_merge)
+        rc |= f_merge(*a_merge[(a_i + 1) % 2])
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
     e1.record()
@@ -425,13 +431,18 @@ def main():
                     help="comma list of workgroup counts to time on the headline")
     ap.add_argument("--mla-wg-sweep", type=str, default="",
                     help="comma list of workgroup counts to time on the MLA layer")
+    ap.add_argument("--page-size", type=int, default=64,
+                    help="tokens per HBM page (a multiple of 32)")
     ap.add_argument("--contiguous-pages", action="store_true",
                     help="assign each sequence's pages in order instead of shuffled")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC scale factor)")
     args = ap.parse_args()
-    global CONTIGUOUS_PAGES
+    global CONTIGUOUS_PAGES, PAGE
     CONTIGUOUS_PAGES = args.contiguous_pages
+    if args.page_size <= 0 or args.page_size % 32:
+        ap.error("--page-size must be a positive multiple of 32")
+    PAGE = args.page_size
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the GPU "
@@ -542,8 +553,8 @@ def main():
         "unit": "GB/s",
         "frac": round(head["partial_gbs"] / HBM_PEAK_GBS, 4),
         "traffic": committed_traffic(wk),
-        "kernel": "gqa_decode_kernel<4, true> (ws_gqa_append_decode_partial: append + "
-                  "load-balanced split-KV partial + in-kernel combine, one launch)",
+        "kernel": "gqa_decode_kernel<4, true, false> (ws_gqa_append_decode_split: append + "
+                  "load-balanced split-KV partial, one launch; combine in the merge launch)",
         "algorithmic_bytes_per_launch": head["partial_bytes"],
         "mean_launch_us": head["partial_us"],
     }

@@ -171,6 +171,27 @@ int ws_gqa_append_decode_partial(const uint16_t* q, const uint16_t* k_new,
                                  void* stream);
 
 /*
+ * Deferred-combine form of ws_gqa_append_decode_partial, for a step whose
+ * partial is merged with a host partial anyway: rows that one workgroup held
+ * are written final to out/lse as before, rows spread over several
+ * workgroups leave their partials in the workspace, and ws_merge_split
+ * combines them with the host partial in the merge launch.  This takes the
+ * cross-workgroup combine (a chain of dependent memory round trips) off the
+ * end of the streaming launch.  The workspace must not be reused until the
+ * matching ws_merge_split ran.
+ */
+int ws_gqa_append_decode_split(const uint16_t* q, const uint16_t* k_new,
+                               const uint16_t* v_new, uint16_t* k_pages,
+                               uint16_t* v_pages, const int32_t* page_table,
+                               const int32_t* len_in, int32_t* len_out,
+                               int B, int Hq, int Hkv, int D,
+                               int page_size, int max_pages, int num_pages,
+                               int max_len, int n_workgroups, float scale,
+                               float* out, float* lse,
+                               void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/*
  * Split-KV absorbed-MLA decode attention.
  * q_nope: [B*H][512] bf16 (q_nope already multiplied by W_UK), q_pe: [B*H][64].
  * score = (q_nope . c + q_pe . pe) * scale over the shared 576-wide latent,
@@ -210,6 +231,47 @@ int ws_mla_append_decode_partial(const uint16_t* q_nope, const uint16_t* q_pe,
                                  float* out, float* lse,
                                  void* workspace, size_t workspace_bytes,
                                  void* stream);
+
+/* Deferred-combine form of ws_mla_append_decode_partial (see
+ * ws_gqa_append_decode_split); finish with ws_merge_split. */
+int ws_mla_append_decode_split(const uint16_t* q_nope, const uint16_t* q_pe,
+                               const uint16_t* c_new, int64_t c_stride,
+                               const uint16_t* pe_new, int64_t pe_stride,
+                               uint16_t* latent_pages,
+                               const int32_t* page_table,
+                               const int32_t* len_in, int32_t* len_out,
+                               int B, int H, int page_size, int max_pages,
+                               int num_pages, int max_len,
+                               int n_workgroups, float scale,
+                               float* out, float* lse,
+                               void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/*
+ * Finish a deferred-combine step: for every output row, LSE-combine the GPU
+ * pieces the step left (its final out/lse, or the partials of the
+ * workgroups that shared the row) with the host partial, normalise, and
+ * write out_bf16 and/or out_f32 [rows][Dv] and lse_out [rows] (any may be
+ * NULL but not both outputs).
+ *   gpu_len          the lengths after the step (the step's len_out)
+ *   rows_per_seq     Hkv (GQA) or 1 (MLA); heads: G (GQA) or 16 (MLA)
+ *   Dv               128 (GQA) or 512 (MLA)
+ *   page_capacity    page_size * max_pages of the step
+ *   n_workgroups     the workgroup count the step ran with (ws_decode_plan)
+ *   out_g, lse_g     the step's out / lse; workspace as given to the step
+ *   b_*, fmt_b       host partial as in ws_lse_merge, or b_out = NULL for none
+ * rows = B * rows_per_seq * heads, ordered as the step's out.
+ * Replaces the merge of the CPU and GPU partials after a decode step
+ * (system/deepseek.py:394-403, system/mixoffload.py:1452-1464,
+ * roofline/bench_resident_kv.py:339-350) together with the split combine.
+ */
+int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, int heads,
+                   int Dv, int page_capacity, int n_workgroups,
+                   const float* out_g, const float* lse_g,
+                   const void* workspace, size_t workspace_bytes,
+                   const void* b_out, const void* b_aux0, const void* b_aux1,
+                   int fmt_b, uint16_t* out_bf16, float* out_f32,
+                   float* lse_out, void* stream);
 
 /*
  * LSE-combine per-split partials: part_out [n_splits][rows][Dv],

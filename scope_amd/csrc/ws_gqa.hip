@@ -29,6 +29,11 @@ namespace ws {
 
 constexpr int kGqaD = 128;
 constexpr int kGqaWaves = 4;
+#ifndef WS_GQA_STAGES
+#define WS_GQA_STAGES 2
+#endif
+// Register stages per wave: 2 fits two waves per SIMD; deeper rings take one.
+constexpr int kGqaStages = WS_GQA_STAGES;
 
 struct GqaParams {
   const uint16_t* q;
@@ -48,10 +53,15 @@ struct GqaParams {
   float scale_log2;
 };
 
-template <int G, bool APPEND>
-__global__ __launch_bounds__(64 * kGqaWaves, 2) void gqa_decode_kernel(const GqaParams p) {
+// COMBINE: rows held by several workgroups are combined in this launch by the
+// last one to arrive; without it their partials stay in the workspace for
+// ws_merge_split (the combine then rides on the merge launch of the step).
+template <int G, bool APPEND, bool COMBINE>
+__global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_decode_kernel(
+    const GqaParams p) {
   constexpr int D = kGqaD;
   constexpr int W = kGqaWaves;
+  constexpr int S = kGqaStages;
   constexpr int NT = 64 * W;
   constexpr int add = APPEND ? 1 : 0;
   __shared__ float s_m[W][16];
@@ -178,26 +188,30 @@ __global__ __launch_bounds__(64 * kGqaWaves, 2) void gqa_decode_kernel(const Gqa
       pv_block(acc, vr, pb, alpha);
     };
 
-    // Blocks of this wave: t_begin + 32 * (wave + W * i), i < nblk.  The next
-    // block is requested before the current one is consumed (past the last
-    // block the request is the q-row dummy of load_block).  sched_barrier
-    // keeps the compiler from sinking the next block's loads below the
-    // current block's math (which would serialise them again).
+    // Blocks of this wave: t_begin + 32 * (wave + W * i), i < nblk, through a
+    // ring of S register stages: while block i is consumed, blocks
+    // i + 1 .. i + S - 1 are in flight (past the last block the request is the
+    // q-row dummy of load_block).  sched_barrier keeps the compiler from
+    // sinking the loads below the math (which would serialise them again).
     const int first = t_begin + 32 * wave;
     const int nblk = first < t_end ? (t_end - first + 32 * W - 1) / (32 * W) : 0;
     if (nblk > 0) {
-      u32x4 kaA[2][4], vrA[8], kaB[2][4], vrB[8];
-      load_block(first, true, kaA, vrA);
-      for (int i = 0; i < nblk; i += 2) {
-        load_block(first + 32 * W * min(i + 1, nblk - 1), i + 1 < nblk, kaB, vrB);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_block(first + 32 * W * i, kaA, vrA);
-        __builtin_amdgcn_sched_barrier(0);
-        if (i + 1 >= nblk) break;
-        load_block(first + 32 * W * min(i + 2, nblk - 1), i + 2 < nblk, kaA, vrA);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_block(first + 32 * W * (i + 1), kaB, vrB);
-        __builtin_amdgcn_sched_barrier(0);
+      u32x4 ka[S][2][4], vr[S][8];
+#pragma unroll
+      for (int st = 0; st < S - 1; ++st)
+        load_block(first + 32 * W * min(st, nblk - 1), st < nblk, ka[st], vr[st]);
+      for (int i = 0; i < nblk; i += S) {
+#pragma unroll
+        for (int st = 0; st < S; ++st) {
+          const int blk = i + st;
+          if (blk >= nblk) break;
+          const int nxt = blk + S - 1;
+          load_block(first + 32 * W * min(nxt, nblk - 1), nxt < nblk, ka[(st + S - 1) % S],
+                     vr[(st + S - 1) % S]);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_block(first + 32 * W * blk, ka[st], vr[st]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
 
@@ -236,7 +250,7 @@ __global__ __launch_bounds__(64 * kGqaWaves, 2) void gqa_decode_kernel(const Gqa
       }
       const float ov = o / L;
       const float lv = (M + __log2f(L)) * kLn2;
-      if (final_write) {
+      if (final_write || !COMBINE) {
         dst_out[idx] = ov;
         if (d == 0) dst_lse[h] = lv;
       } else {  // read by the row's last workgroup, maybe on another XCD
@@ -244,7 +258,7 @@ __global__ __launch_bounds__(64 * kGqaWaves, 2) void gqa_decode_kernel(const Gqa
         if (d == 0) st_agent(dst_lse + h, lv);
       }
     }
-    if (!final_write && arrive_last(p.ws.counters + row, nseg, &s_flag)) {
+    if (COMBINE && !final_write && arrive_last(p.ws.counters + row, nseg, &s_flag)) {
       reduce_rows<NT>(p.ws.part_out + (size_t)(w_first + row) * G * D,
                       p.ws.part_lse + (size_t)(w_first + row) * G, G, G, D, nseg,
                       p.out + (size_t)q0 * D, p.lse + q0, s_w, s_red);
@@ -267,7 +281,7 @@ using namespace ws;
 static int gqa_workgroups(int n_workgroups, int rows_kv, int G, int max_len) {
   if (n_workgroups > 0) return n_workgroups;
   const long long max_blocks = (long long)rows_kv * ((max_len + 31) / 32);
-  const int n = choose_workgroups(0, 2, max_blocks, 8);
+  const int n = choose_workgroups(0, kGqaStages <= 2 ? 2 : 1, max_blocks, 8);
   return std::min(n, kReduceMaxWeights / G);
 }
 
@@ -277,7 +291,7 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
                       int D, int page_size, int max_pages, int num_pages, int max_len,
                       int n_workgroups, float scale, float* out, float* lse,
                       void* workspace, size_t workspace_bytes, void* stream,
-                      const char* name) {
+                      bool combine, const char* name) {
   if (!q || !k_pages || !v_pages || !page_table || !len_in || !out || !lse)
     return set_error(WS_EINVAL, "%s: null pointer", name);
   if (B < 0 || B > kMaxSeqs || Hkv <= 0 || Hq <= 0 || Hq % Hkv)
@@ -344,12 +358,16 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   prm.scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(n), block(64 * kGqaWaves);
-#define WS_GQA_CASE(GG)                                                              \
-  case GG:                                                                           \
-    if (k_new)                                                                       \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, true>), grid, block, 0, s, prm);     \
-    else                                                                             \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, false>), grid, block, 0, s, prm);    \
+#define WS_GQA_CASE(GG)                                                                 \
+  case GG:                                                                              \
+    if (k_new && combine)                                                               \
+      hipLaunchKernelGGL((gqa_decode_kernel<GG, true, true>), grid, block, 0, s, prm);  \
+    else if (k_new)                                                                     \
+      hipLaunchKernelGGL((gqa_decode_kernel<GG, true, false>), grid, block, 0, s, prm); \
+    else if (combine)                                                                   \
+      hipLaunchKernelGGL((gqa_decode_kernel<GG, false, true>), grid, block, 0, s, prm); \
+    else                                                                                \
+      hipLaunchKernelGGL((gqa_decode_kernel<GG, false, false>), grid, block, 0, s, prm); \
     break;
   switch (G) {
     WS_GQA_CASE(1)
@@ -391,7 +409,7 @@ extern "C" int ws_gqa_decode_partial(
   return gqa_launch(q, nullptr, nullptr, (uint16_t*)k_pages, (uint16_t*)v_pages,
                     page_table, gpu_len, nullptr, B, Hq, Hkv, D, page_size, max_pages,
                     num_pages, max_len, n_workgroups, scale, out, lse, workspace,
-                    workspace_bytes, stream, "ws_gqa_decode_partial");
+                    workspace_bytes, stream, true, "ws_gqa_decode_partial");
 }
 
 extern "C" int ws_gqa_append_decode_partial(
@@ -404,6 +422,20 @@ extern "C" int ws_gqa_append_decode_partial(
     return set_error(WS_EINVAL, "ws_gqa_append_decode_partial: k_new is null");
   return gqa_launch(q, k_new, v_new, k_pages, v_pages, page_table, len_in, len_out, B,
                     Hq, Hkv, D, page_size, max_pages, num_pages, max_len, n_workgroups,
-                    scale, out, lse, workspace, workspace_bytes, stream,
+                    scale, out, lse, workspace, workspace_bytes, stream, true,
                     "ws_gqa_append_decode_partial");
+}
+
+extern "C" int ws_gqa_append_decode_split(
+    const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new, uint16_t* k_pages,
+    uint16_t* v_pages, const int32_t* page_table, const int32_t* len_in,
+    int32_t* len_out, int B, int Hq, int Hkv, int D, int page_size, int max_pages,
+    int num_pages, int max_len, int n_workgroups, float scale, float* out,
+    float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!k_new)
+    return set_error(WS_EINVAL, "ws_gqa_append_decode_split: k_new is null");
+  return gqa_launch(q, k_new, v_new, k_pages, v_pages, page_table, len_in, len_out, B,
+                    Hq, Hkv, D, page_size, max_pages, num_pages, max_len, n_workgroups,
+                    scale, out, lse, workspace, workspace_bytes, stream, false,
+                    "ws_gqa_append_decode_split");
 }

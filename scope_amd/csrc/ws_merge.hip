@@ -5,7 +5,8 @@
 // needed after its host-to-device copy.
 #include <math.h>
 
-#include "ws_common.h"
+#include "ws_plan.h"
+#include "ws_reduce.h"
 
 namespace ws {
 
@@ -79,9 +80,200 @@ __global__ __launch_bounds__(128) void lse_merge_kernel(
   if (lse_out && c == 0) lse_out[row] = lse_r;
 }
 
+// ---------------------------------------------------------------------------
+// Split combine + host merge of a deferred-combine decode step.
+//
+// One 64-lane workgroup per output row (kv row * heads + head).  It rebuilds
+// the step's plan from the post-step lengths (ws_plan.h) to find the row's
+// GPU pieces: the final (out, lse) the step wrote when one workgroup held the
+// row, else the partials of the row's workgroups (slots w + kv row), then
+// LSE-combines them with the host partial (format FMT, or none when FMT < 0)
+// and writes the normalised result.  Runs after the step on the same stream,
+// so plain loads see its writes.
+struct MergeSplitParams {
+  const int32_t* gpu_len;
+  int B, R, heads, Dv, cap, grid;
+  const float* out_g;
+  const float* lse_g;
+  const float* part_out;
+  const float* part_lse;
+  const void* b_out;
+  const void* b_aux0;
+  const void* b_aux1;
+  uint16_t* out_bf16;
+  float* out_f32;
+  float* lse_out;
+};
+
+template <int FMT>
+__global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams p) {
+  __shared__ int s_pref[kMaxSeqs + 1];
+  __shared__ int s_scan[2];
+  __shared__ float s_w[kReduceMaxWeights];
+  const int qrow = blockIdx.x;
+  const int t = threadIdx.x;
+  const int krow = qrow / p.heads;
+  const int h = qrow - krow * p.heads;
+  const int b = krow / p.R;
+  const int r = krow - b * p.R;
+  const Plan plan = plan_build<64>(p.gpu_len, 0, p.cap, p.B, p.R, p.grid, s_pref, s_scan);
+  const int nbb = (plan_len(p.gpu_len, b, 0, p.cap) + 31) >> 5;
+  int n = 1;
+  const float* src = p.out_g + (size_t)qrow * p.Dv;  // piece s at src + s * sstride
+  const float* lsrc = p.lse_g + qrow;                // lse of piece s at lsrc[s * lstride]
+  size_t sstride = 0, lstride = 0;
+  if (nbb > 0 && plan.n > 0) {
+    const int row_start = s_pref[b] + r * nbb;
+    const int w_first = plan_owner(plan, row_start);
+    const int nseg = plan_owner(plan, row_start + nbb - 1) - w_first + 1;
+    if (nseg > 1) {
+      n = nseg;
+      const size_t slot0 = (size_t)(w_first + krow) * p.heads + h;
+      src = p.part_out + slot0 * p.Dv;
+      lsrc = p.part_lse + slot0;
+      sstride = (size_t)p.heads * p.Dv;
+      lstride = p.heads;
+    }
+  }
+  // weights: M over the GPU pieces and the host partial
+  float lb = neg_inf();
+  if (FMT >= 0) {
+    float4 dummy;
+    load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, 0, lb, dummy);
+  }
+  float mx = lb;
+  for (int s = t; s < n; s += 64) {
+    const float v = lsrc[(size_t)s * lstride];
+    s_w[s] = v;
+    mx = fmaxf(mx, v);
+  }
+  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  float sum = 0.f;
+  for (int s = t; s < n; s += 64) {
+    const float w = mx == neg_inf() ? 0.f : __expf(s_w[s] - mx);
+    s_w[s] = w;
+    sum += w;
+  }
+  for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
+  const float wb = (FMT >= 0 && mx != neg_inf()) ? __expf(lb - mx) : 0.f;
+  const float L = sum + wb;
+  __syncthreads();
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  if (t == 0 && p.lse_out) p.lse_out[qrow] = L > 0.f ? mx + __logf(L) : neg_inf();
+  const int c4 = p.Dv >> 2;
+  for (int c = t; c < c4; c += 64) {
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    int s = 0;
+    for (; s + 4 <= n; s += 4) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = ((const float4*)(src + (size_t)(s + u) * sstride))[c];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float w = s_w[s + u];
+        a.x += w * v[u].x; a.y += w * v[u].y; a.z += w * v[u].z; a.w += w * v[u].w;
+      }
+    }
+    for (; s < n; ++s) {
+      const float w = s_w[s];
+      const float4 v = ((const float4*)(src + (size_t)s * sstride))[c];
+      a.x += w * v.x; a.y += w * v.y; a.z += w * v.z; a.w += w * v.w;
+    }
+    if (FMT >= 0 && wb > 0.f) {
+      float lb2;
+      float4 ob;
+      load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, c, lb2, ob);
+      a.x += wb * ob.x; a.y += wb * ob.y; a.z += wb * ob.z; a.w += wb * ob.w;
+    }
+    const float4 o = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+    if (p.out_f32) ((float4*)(p.out_f32 + (size_t)qrow * p.Dv))[c] = o;
+    if (p.out_bf16) {
+      uint2 packed;
+      packed.x = pack_bf16x2(o.x, o.y);
+      packed.y = pack_bf16x2(o.z, o.w);
+      ((uint2*)(p.out_bf16 + (size_t)qrow * p.Dv))[c] = packed;
+    }
+  }
+}
+
 }  // namespace ws
 
 using namespace ws;
+
+extern "C" int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, int heads,
+                              int Dv, int page_capacity, int n_workgroups,
+                              const float* out_g, const float* lse_g,
+                              const void* workspace, size_t workspace_bytes,
+                              const void* b_out, const void* b_aux0, const void* b_aux1,
+                              int fmt_b, uint16_t* out_bf16, float* out_f32,
+                              float* lse_out, void* stream) {
+  if (!gpu_len || !out_g || !lse_g || !workspace)
+    return set_error(WS_EINVAL, "ws_merge_split: null input pointer");
+  if (!out_bf16 && !out_f32)
+    return set_error(WS_EINVAL, "ws_merge_split: no output");
+  if (B < 0 || B > kMaxSeqs || rows_per_seq <= 0 || heads <= 0 || heads > 16 || Dv <= 0 ||
+      Dv % 4 || Dv > 512 || page_capacity <= 0 || n_workgroups <= 0)
+    return set_error(WS_EINVAL, "ws_merge_split: bad sizes");
+  if (b_out && (!b_aux0 || (fmt_b != WS_PARTIAL_LSE_F32 && !b_aux1)))
+    return set_error(WS_EINVAL, "ws_merge_split: host partial without its lse / max / sum");
+  if (b_out && fmt_b != WS_PARTIAL_LSE_F32 && fmt_b != WS_TRIPLE_UNNORM_F32 &&
+      fmt_b != WS_TRIPLE_NORM_BF16 && fmt_b != WS_TRIPLE_NORM_F32)
+    return set_error(WS_EINVAL, "ws_merge_split: unknown format %d", fmt_b);
+  if (n_workgroups > kReduceMaxWeights)
+    return set_error(WS_EINVAL, "ws_merge_split: %d workgroups exceed %d", n_workgroups,
+                     kReduceMaxWeights);
+  if (((uintptr_t)workspace & 255u) || ((uintptr_t)out_g | (uintptr_t)out_f32 |
+                                         (uintptr_t)b_out) & 15u || ((uintptr_t)out_bf16 & 7u))
+    return set_error(WS_EINVAL, "ws_merge_split: misaligned buffer");
+  const long long rows_kv = (long long)B * rows_per_seq;
+  if (rows_kv > kCounterSlots)
+    return set_error(WS_EINVAL, "ws_merge_split: %lld rows exceed %d", rows_kv, kCounterSlots);
+  const size_t need = ws::workspace_bytes((int)rows_kv, heads, Dv, n_workgroups);
+  if (workspace_bytes < need)
+    return set_error(WS_EWORKSPACE, "ws_merge_split: workspace %zu < %zu bytes",
+                     workspace_bytes, need);
+  if (B == 0) return WS_OK;
+  const SplitWorkspace w = carve_workspace((void*)workspace, (int)rows_kv, heads, n_workgroups);
+  MergeSplitParams prm;
+  prm.gpu_len = gpu_len;
+  prm.B = B;
+  prm.R = rows_per_seq;
+  prm.heads = heads;
+  prm.Dv = Dv;
+  prm.cap = page_capacity;
+  prm.grid = n_workgroups;
+  prm.out_g = out_g;
+  prm.lse_g = lse_g;
+  prm.part_out = w.part_out;
+  prm.part_lse = w.part_lse;
+  prm.b_out = b_out;
+  prm.b_aux0 = b_aux0;
+  prm.b_aux1 = b_aux1;
+  prm.out_bf16 = out_bf16;
+  prm.out_f32 = out_f32;
+  prm.lse_out = lse_out;
+  const dim3 grid((unsigned)(rows_kv * heads)), block(64);
+  hipStream_t s = (hipStream_t)stream;
+  if (!b_out) {
+    hipLaunchKernelGGL(merge_split_kernel<-1>, grid, block, 0, s, prm);
+  } else {
+    switch (fmt_b) {
+      case WS_PARTIAL_LSE_F32:
+        hipLaunchKernelGGL(merge_split_kernel<WS_PARTIAL_LSE_F32>, grid, block, 0, s, prm);
+        break;
+      case WS_TRIPLE_UNNORM_F32:
+        hipLaunchKernelGGL(merge_split_kernel<WS_TRIPLE_UNNORM_F32>, grid, block, 0, s, prm);
+        break;
+      case WS_TRIPLE_NORM_BF16:
+        hipLaunchKernelGGL(merge_split_kernel<WS_TRIPLE_NORM_BF16>, grid, block, 0, s, prm);
+        break;
+      default:
+        hipLaunchKernelGGL(merge_split_kernel<WS_TRIPLE_NORM_F32>, grid, block, 0, s, prm);
+        break;
+    }
+  }
+  return check_launch("ws_merge_split");
+}
 
 extern "C" int ws_lse_merge(const float* out_g, const float* lse_g,
                             const void* b_out, const void* b_aux0,

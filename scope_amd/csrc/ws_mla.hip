@@ -298,7 +298,7 @@ static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
                       int32_t* len_out, int B, int H, int page_size, int max_pages,
                       int num_pages, int max_len, int n_workgroups, float scale,
                       float* out, float* lse, void* workspace, size_t workspace_bytes,
-                      void* stream, const char* name) {
+                      void* stream, bool combine, const char* name) {
   if (!q_nope || !q_pe || !latent_pages || !page_table || !len_in || !out || !lse)
     return set_error(WS_EINVAL, "%s: null pointer", name);
   if (B < 0 || B > kMaxSeqs || H != kMlaH)
@@ -361,7 +361,7 @@ static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
   else
     hipLaunchKernelGGL(mla_decode_kernel<false>, dim3(n), dim3(256), 0, s, prm);
   int rc = check_launch(name);
-  if (rc || n == 1) return rc;
+  if (rc || n == 1 || !combine) return rc;
   hipLaunchKernelGGL(mla_reduce_kernel, dim3(B * kMlaH, kMlaC / 256), dim3(64), 0, s, prm,
                      n);
   return check_launch(name);
@@ -381,7 +381,7 @@ extern "C" int ws_mla_decode_partial(const uint16_t* q_nope, const uint16_t* q_p
   return mla_launch(q_nope, q_pe, nullptr, 0, nullptr, 0, (uint16_t*)latent_pages,
                     page_table, gpu_len, nullptr, B, H, page_size, max_pages, num_pages,
                     max_len, n_workgroups, scale, out, lse, workspace, workspace_bytes,
-                    stream, "ws_mla_decode_partial");
+                    stream, true, "ws_mla_decode_partial");
 }
 
 extern "C" int ws_mla_append_decode_partial(
@@ -395,5 +395,19 @@ extern "C" int ws_mla_append_decode_partial(
   return mla_launch(q_nope, q_pe, c_new, c_stride, pe_new, pe_stride, latent_pages,
                     page_table, len_in, len_out, B, H, page_size, max_pages, num_pages,
                     max_len, n_workgroups, scale, out, lse, workspace, workspace_bytes,
-                    stream, "ws_mla_append_decode_partial");
+                    stream, true, "ws_mla_append_decode_partial");
+}
+
+extern "C" int ws_mla_append_decode_split(
+    const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_new,
+    int64_t c_stride, const uint16_t* pe_new, int64_t pe_stride, uint16_t* latent_pages,
+    const int32_t* page_table, const int32_t* len_in, int32_t* len_out, int B, int H,
+    int page_size, int max_pages, int num_pages, int max_len, int n_workgroups,
+    float scale, float* out, float* lse, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  if (!c_new) return set_error(WS_EINVAL, "ws_mla_append_decode_split: c_new is null");
+  return mla_launch(q_nope, q_pe, c_new, c_stride, pe_new, pe_stride, latent_pages,
+                    page_table, len_in, len_out, B, H, page_size, max_pages, num_pages,
+                    max_len, n_workgroups, scale, out, lse, workspace, workspace_bytes,
+                    stream, false, "ws_mla_append_decode_split");
 }

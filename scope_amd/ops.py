@@ -33,6 +33,9 @@ EXPORTS = (
     "ws_gqa_append_decode_partial",
     "ws_mla_decode_partial",
     "ws_mla_append_decode_partial",
+    "ws_gqa_append_decode_split",
+    "ws_mla_append_decode_split",
+    "ws_merge_split",
     "ws_split_reduce",
     "ws_lse_merge",
 )
@@ -98,6 +101,13 @@ def lib() -> ctypes.CDLL:
         L.ws_mla_append_decode_partial.argtypes = [vp, vp, vp, i64, vp, i64, vp, vp,
                                                    vp, vp, i32, i32, i32, i32, i32,
                                                    i32, i32, f32, vp, vp, vp, sz, vp]
+        L.ws_gqa_append_decode_split.restype = i32
+        L.ws_gqa_append_decode_split.argtypes = L.ws_gqa_append_decode_partial.argtypes
+        L.ws_mla_append_decode_split.restype = i32
+        L.ws_mla_append_decode_split.argtypes = L.ws_mla_append_decode_partial.argtypes
+        L.ws_merge_split.restype = i32
+        L.ws_merge_split.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, sz,
+                                     vp, vp, vp, i32, vp, vp, vp, vp]
         L.ws_split_reduce.restype = i32
         L.ws_split_reduce.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp,
                                       vp, vp]
@@ -383,6 +393,142 @@ def mla_append_decode_partial(q_nope, q_pe, c_new, pe_new, latent_pages, page_ta
         _ptr(len_out), B, H, PS, page_table.shape[1], P, int(max_len), nwg, float(scale),
         _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev)), "ws_mla_append_decode_partial")
     return out, lse
+
+
+class SplitStep:
+    """A deferred-combine decode step: its GPU pieces (out_g/lse_g finals and
+    the workgroup partials in `workspace`) wait for merge_split.  Holds every
+    buffer the merge reads, so the step's workspace is not reused early."""
+
+    def __init__(self, gpu_len, B, rows_per_seq, heads, Dv, cap, nwg, out_g, lse_g,
+                 workspace):
+        self.gpu_len, self.B, self.rows_per_seq, self.heads = gpu_len, B, rows_per_seq, heads
+        self.Dv, self.cap, self.nwg = Dv, cap, nwg
+        self.out_g, self.lse_g, self.workspace = out_g, lse_g, workspace
+
+
+def gqa_append_decode_split(q, k_new, v_new, k_pages, v_pages, page_table, len_in,
+                            len_out, scale, max_len, n_workgroups=0, workspace=None):
+    """Deferred-combine fused step (ws_gqa_append_decode_split): append and
+    attend like gqa_append_decode_partial, but rows spread over several
+    workgroups are combined later by merge_split.  len_out is required (the
+    merge reads the post-step lengths).  Returns a SplitStep."""
+    dev = k_pages.device
+    _require(q, "q", torch.bfloat16, dev, 3)
+    _require(k_new, "k_new", torch.bfloat16, dev, 4)
+    _require(v_new, "v_new", torch.bfloat16, dev, 4)
+    _require(k_pages, "k_pages", torch.bfloat16, dev, 4)
+    _require(v_pages, "v_pages", torch.bfloat16, dev, 4)
+    _require(page_table, "page_table", torch.int32, dev, 2)
+    _require(len_in, "len_in", torch.int32, dev, 1)
+    _require(len_out, "len_out", torch.int32, dev, 1)
+    B, Hq, D = q.shape
+    P, Hkv, PS, D2 = k_pages.shape
+    if v_pages.shape != k_pages.shape or D2 != D:
+        raise ValueError("k/v page pools must match q's head_dim")
+    if k_new.shape != (B, Hkv, 1, D) or v_new.shape != k_new.shape:
+        raise ValueError(f"k_new/v_new must be [B, Hkv, 1, D] = {(B, Hkv, 1, D)}")
+    if page_table.shape[0] != B or len_in.shape[0] != B or len_out.shape[0] != B:
+        raise ValueError("page_table/len_in/len_out batch mismatch")
+    if len_out.data_ptr() == len_in.data_ptr():
+        raise ValueError("len_out must be a separate [B] int32 tensor")
+    out = torch.empty((B, Hq, D), dtype=torch.float32, device=dev)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
+    nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
+    if workspace is None:
+        workspace = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+    elif workspace.numel() * workspace.element_size() < wsb:
+        raise ValueError(f"workspace needs {wsb} bytes")
+    _check(lib().ws_gqa_append_decode_split(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
+        _ptr(len_in), _ptr(len_out), B, Hq, Hkv, D, PS, page_table.shape[1], P,
+        int(max_len), nwg, float(scale), _ptr(out), _ptr(lse), _ptr(workspace),
+        workspace.numel() * workspace.element_size(), _stream(dev)),
+        "ws_gqa_append_decode_split")
+    return SplitStep(len_out, B, Hkv, Hq // Hkv, D, PS * page_table.shape[1], nwg, out, lse,
+                     workspace)
+
+
+def mla_append_decode_split(q_nope, q_pe, c_new, pe_new, latent_pages, page_table,
+                            len_in, len_out, scale, max_len, n_workgroups=0,
+                            workspace=None):
+    """Deferred-combine absorbed-MLA step (ws_mla_append_decode_split);
+    finish with merge_split.  Returns a SplitStep."""
+    dev = latent_pages.device
+    _require(q_nope, "q_nope", torch.bfloat16, dev, 2)
+    _require(q_pe, "q_pe", torch.bfloat16, dev, 2)
+    _require(latent_pages, "latent_pages", torch.bfloat16, dev, 3)
+    _require(page_table, "page_table", torch.int32, dev, 2)
+    _require(len_in, "len_in", torch.int32, dev, 1)
+    _require(len_out, "len_out", torch.int32, dev, 1)
+    B = page_table.shape[0]
+    for t, n, w in ((c_new, "c_new", MLA_C), (pe_new, "pe_new", MLA_PE)):
+        _require(t, n, torch.bfloat16, dev, 3, contiguous=False)
+        if t.shape != (B, 1, w) or t.stride(2) != 1:
+            raise ValueError(f"{n} must be [B, 1, {w}] with unit last stride")
+    P, PS, L = latent_pages.shape
+    rows = q_nope.shape[0]
+    if L != MLA_LATENT or q_nope.shape[1] != MLA_C or q_pe.shape != (rows, MLA_PE):
+        raise ValueError("MLA layout is q_nope 512 + q_pe 64 over a 576 latent")
+    if B == 0 or rows % B or len_in.shape[0] != B or len_out.shape[0] != B:
+        raise ValueError("rows must be B * H with B = page_table.shape[0]")
+    if len_out.data_ptr() == len_in.data_ptr():
+        raise ValueError("len_out must be a separate [B] int32 tensor")
+    H = rows // B
+    out = torch.empty((rows, MLA_C), dtype=torch.float32, device=dev)
+    lse = torch.empty((rows,), dtype=torch.float32, device=dev)
+    nwg, wsb = decode_plan(1, B, H, int(max_len), int(n_workgroups))
+    if workspace is None:
+        workspace = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+    elif workspace.numel() * workspace.element_size() < wsb:
+        raise ValueError(f"workspace needs {wsb} bytes")
+    _check(lib().ws_mla_append_decode_split(
+        _ptr(q_nope), _ptr(q_pe), _ptr(c_new), c_new.stride(0), _ptr(pe_new),
+        pe_new.stride(0), _ptr(latent_pages), _ptr(page_table), _ptr(len_in),
+        _ptr(len_out), B, H, PS, page_table.shape[1], P, int(max_len), nwg, float(scale),
+        _ptr(out), _ptr(lse), _ptr(workspace), workspace.numel() * workspace.element_size(),
+        _stream(dev)), "ws_mla_append_decode_split")
+    return SplitStep(len_out, B, 1, H, MLA_C, PS * page_table.shape[1], nwg, out, lse,
+                     workspace)
+
+
+def merge_split(step: SplitStep, b=None, fmt=PARTIAL_LSE_F32, out_dtype=torch.bfloat16,
+                want_lse=True, out=None, lse_out=None):
+    """Finish a deferred-combine step (ws_merge_split): combine its GPU pieces
+    with the host partial `b` (formats as lse_merge; None = no host partial),
+    normalise.  Returns (out [rows, Dv] in out_dtype, lse [rows] or None)."""
+    dev = step.out_g.device
+    rows = step.out_g.numel() // step.Dv
+    b_out = b_aux0 = b_aux1 = None
+    if b is not None:
+        if fmt == PARTIAL_LSE_F32:
+            b_out, b_aux0 = b
+            _require(b_out, "b.out", torch.float32, dev)
+            _require(b_aux0, "b.lse", torch.float32, dev)
+        else:
+            b_out, b_aux0, b_aux1 = b
+            dt = torch.bfloat16 if fmt == TRIPLE_NORM_BF16 else torch.float32
+            _require(b_out, "b.out", dt, dev)
+            _require(b_aux0, "b.max", dt, dev)
+            _require(b_aux1, "b.sum", dt, dev)
+            if b_aux1.numel() != rows:
+                raise ValueError("b.sum must have one value per row")
+        if b_out.numel() != rows * step.Dv or b_aux0.numel() != rows:
+            raise ValueError("host partial does not match the step's rows")
+    if out is None:
+        out = torch.empty((rows, step.Dv), dtype=out_dtype, device=dev)
+    if want_lse and lse_out is None:
+        lse_out = torch.empty((rows,), dtype=torch.float32, device=dev)
+    o16, o32 = (out, None) if out.dtype == torch.bfloat16 else (None, out)
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("merged output must be bfloat16 or float32")
+    ws = step.workspace
+    _check(lib().ws_merge_split(
+        _ptr(step.gpu_len), step.B, step.rows_per_seq, step.heads, step.Dv, step.cap,
+        step.nwg, _ptr(step.out_g), _ptr(step.lse_g), _ptr(ws), ws.numel() * ws.element_size(),
+        _ptr(b_out), _ptr(b_aux0), _ptr(b_aux1), int(fmt), _ptr(o16), _ptr(o32),
+        _ptr(lse_out if want_lse else None), _stream(dev)), "ws_merge_split")
+    return out, (lse_out if want_lse else None)
 
 
 def split_reduce(part_out, part_lse, gpu_len, heads_per_len, tokens_per_split,

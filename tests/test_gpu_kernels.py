@@ -434,3 +434,111 @@ def test_workspace_shared_across_shapes():
     _mla_check([300], wg=5, seed=54)
     _gqa_check([1000] * 3, Hkv=8, G=8, wg=200, seed=55, port_check=False)
     assert _counters_zero()
+
+
+# ---------------------------------------------------------------------------
+# deferred-combine step + merge_split
+
+
+def _host_partial(fmt, rows, Dv, seed):
+    """A host partial in format fmt plus its (out, lse) in float64."""
+    rng = np.random.default_rng(seed)
+    ob = rng.standard_normal((rows, Dv)).astype(np.float32)
+    mb = (rng.standard_normal(rows) * 2 + 3).astype(np.float32)
+    sb = rng.uniform(1, 40, rows).astype(np.float32)
+    sb[1] = 0.0
+    mb[1] = -np.inf  # one row without host tokens
+    if fmt == ops.PARTIAL_LSE_F32:
+        lb = np.where(sb > 0, mb + np.log(np.where(sb > 0, sb, 1)), -np.inf).astype(np.float32)
+        dev = (torch.from_numpy(ob).to(DEV), torch.from_numpy(lb).to(DEV))
+        return dev, np.where(sb[:, None] > 0, ob, 0), lb
+    if fmt == ops.TRIPLE_UNNORM_F32:
+        ou = np.where(sb[:, None] > 0, ob * sb[:, None], 0).astype(np.float32)
+        dev = tuple(torch.from_numpy(x).to(DEV) for x in (ou, mb, sb))
+        o, l = O.triple_to_partial(ou, mb, sb, normalized=False)
+        return dev, o, l
+    ob16, mb16, sb16 = (torch.from_numpy(x).to(torch.bfloat16) for x in (ob, mb, sb))
+    dev = tuple(x.to(DEV) for x in (ob16, mb16, sb16))
+    o, l = O.triple_to_partial(ob16.float().numpy(), mb16.float().numpy(),
+                               sb16.float().numpy(), normalized=True)
+    return dev, o, l
+
+
+@pytest.mark.parametrize("wg", [0, 3, 64])
+@pytest.mark.parametrize("fmt", [None, ops.PARTIAL_LSE_F32, ops.TRIPLE_UNNORM_F32,
+                                 ops.TRIPLE_NORM_BF16])
+def test_gqa_split_step_and_merge(wg, fmt):
+    _say(f"gqa split step wg={wg} fmt={fmt}")
+    Hkv, G, D, PS = 8, 4, 128, 64
+    lens = [1, 40, 700, 1500]
+    B = len(lens)
+    total = [L + 1 for L in lens]
+    k_pages, v_pages, pt, gl, ks, vs = gqa_pool(total, Hkv, D, PS, seed=61)
+    lens2 = torch.zeros((2, B), dtype=torch.int32, device=DEV)
+    lens2[0] = torch.tensor(lens, dtype=torch.int32)
+    q = bf16_randn((B, Hkv * G, D), 62)
+    k_new = torch.stack([k[:, L:L + 1] for k, L in zip(ks, lens)]).to(DEV).contiguous()
+    v_new = torch.stack([v[:, L:L + 1] for v, L in zip(vs, lens)]).to(DEV).contiguous()
+    scale = D ** -0.5
+    step = ops.gqa_append_decode_split(q.to(DEV), k_new, v_new, k_pages, v_pages, pt,
+                                       lens2[0], lens2[1], scale, max(lens) + 1, wg)
+    rows = B * Hkv * G
+    if fmt is None:
+        out, lse = ops.merge_split(step, None, out_dtype=torch.float32)
+        host_o, host_l = np.zeros((rows, D)), np.full(rows, -np.inf)
+    else:
+        hb, host_o, host_l = _host_partial(fmt, rows, D, 63)
+        out, lse = ops.merge_split(step, hb, fmt, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert lens2[1].cpu().tolist() == total
+    qb = bits(q).reshape(B, Hkv, G, D)
+    got, gl_ = out.cpu().numpy().reshape(B, Hkv, G, D), lse.cpu().numpy().reshape(B, Hkv, G)
+    ho, hl = host_o.reshape(B, Hkv, G, D), host_l.reshape(B, Hkv, G)
+    for b in range(B):
+        g_o, g_l = O.gqa_attention_fp64(qb[b], bits(ks[b]), bits(vs[b]), scale)
+        want, wl = O.merge_fp64(g_o, g_l, ho[b], hl[b])
+        assert_close(got[b], want, OUT_ATOL, OUT_RTOL, f"split merged b={b}")
+        assert_close(gl_[b], wl, LSE_ATOL, LSE_RTOL, f"split merged lse b={b}")
+    # same result as the one-launch step followed by ws_lse_merge (fp32 out)
+    lens3 = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    o1, l1 = ops.gqa_append_decode_partial(q.to(DEV), k_new, v_new, k_pages, v_pages, pt,
+                                           lens3, None, scale, max(lens) + 1, wg)
+    if fmt is None:
+        o2, l2 = o1.view(rows, D), l1.view(rows)
+    else:
+        o2, l2 = ops.lse_merge(o1.view(rows, D), l1.view(rows), hb, fmt,
+                               out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), o2.cpu().numpy(), 1e-5, 1e-5, "split vs one-launch")
+    assert_close(lse.cpu().numpy(), l2.cpu().numpy(), 1e-5, 1e-5, "split vs one-launch lse")
+
+
+@pytest.mark.parametrize("wg", [0, 5])
+def test_mla_split_step_and_merge(wg):
+    _say(f"mla split step wg={wg}")
+    H, PS = 16, 64
+    lens = [3, 300, 2000]
+    B = len(lens)
+    total = [L + 1 for L in lens]
+    lat, pt, gl, cs, pes = mla_pool(total, PS, seed=71)
+    lens2 = torch.zeros((2, B), dtype=torch.int32, device=DEV)
+    lens2[0] = torch.tensor(lens, dtype=torch.int32)
+    qn = bf16_randn((B * H, 512), 72, 0.5)
+    qp = bf16_randn((B * H, 64), 73, 0.5)
+    kv = torch.stack([torch.cat([c[L:L + 1], pe[L:L + 1]], 1)
+                      for c, pe, L in zip(cs, pes, lens)]).to(DEV)
+    scale = 192 ** -0.5
+    step = ops.mla_append_decode_split(qn.to(DEV), qp.to(DEV), kv[..., :512], kv[..., 512:],
+                                       lat, pt, lens2[0], lens2[1], scale, max(lens) + 1, wg)
+    rows = B * H
+    hb, host_o, host_l = _host_partial(ops.TRIPLE_UNNORM_F32, rows, 512, 74)
+    out, lse = ops.merge_split(step, hb, ops.TRIPLE_UNNORM_F32, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got, gl_ = out.cpu().numpy(), lse.cpu().numpy()
+    for b in range(B):
+        r = slice(b * H, (b + 1) * H)
+        g_o, g_l = O.mla_attention_fp64(bits(qn[r]), bits(qp[r]), bits(cs[b])[None],
+                                        bits(pes[b])[None], scale)
+        want, wl = O.merge_fp64(g_o, g_l, host_o[r], host_l[r])
+        assert_close(got[r], want, OUT_ATOL, OUT_RTOL, f"mla split merged b={b}")
+        assert_close(gl_[r], wl, LSE_ATOL, LSE_RTOL, f"mla split merged lse b={b}")
