@@ -21,10 +21,11 @@ Reported on one JSON line (stdout):
              FETCH_SIZE / WRITE_SIZE summary when one exists for this workload
   cpu_baseline  the oracle's C restatement of the reference CPU kernel over a
              bounded sample of the same GPU-share tokens, on the host cores
-  by_share, kv_len_sweep, mla, single_partition
+  by_share, kv_len_sweep, mla, mla_kv_len_sweep, single_partition
              the other shares, the Qwen3 length sweep (batch 4, r = 1), the
-             absorbed-MLA layer (DeepSeek-V2-Lite, batch 8, L 16384, r 0.5)
-             and the batch-1 Qwen3 layer with all 4096 tokens on the GPU
+             absorbed-MLA layer (DeepSeek-V2-Lite, batch 8, L 16384, r 0.5),
+             the MLA length sweep (batch 8, r = 1, 8k..128k tokens) and the
+             batch-1 Qwen3 layer with all 4096 tokens on the GPU
 
 Algorithmic bytes of a step (each byte once): KV of every GPU token read,
 Q read, GPU partial (out fp32 + lse) written, host partial read, final bf16
@@ -528,6 +529,15 @@ def main():
         extra["mla"] = mla
         log(f"mla: {mla['us_per_layer']} us/layer, partial {mla['partial_us']} us = "
             f"{mla['partial_gbs']} GB/s, {mla['partial_tflops']} TFLOP/s")
+        msweep = []
+        for Lm in (8192, 32768, 65536, 131072):
+            res = mla_step_bench(B=8, H=16, lens=[Lm] * 8, share=1.0,
+                                 steps=max(10, args.steps // 2), warmup=args.warmup,
+                                 seed=args.seed + 7 + Lm, dev=dev, label=f"dsv2lite_mla_b8_L{Lm}")
+            msweep.append(res)
+            log(f"mla B8 L={Lm}: {res['us_per_layer']} us/layer, partial {res['partial_us']} us "
+                f"= {res['partial_gbs']} GB/s")
+        extra["mla_kv_len_sweep"] = msweep
 
     if args.copy_calibration:
         n = 256 << 20

@@ -29,11 +29,9 @@ namespace ws {
 
 constexpr int kGqaD = 128;
 constexpr int kGqaWaves = 4;
-#ifndef WS_GQA_STAGES
-#define WS_GQA_STAGES 2
-#endif
-// Register stages per wave: 2 fits two waves per SIMD; deeper rings take one.
-constexpr int kGqaStages = WS_GQA_STAGES;
+// Register stages per wave.  Two keep two waves per SIMD (about 230 VGPRs);
+// measured on MI355X, deeper rings at one wave per SIMD stream no faster.
+constexpr int kGqaStages = 2;
 
 struct GqaParams {
   const uint16_t* q;

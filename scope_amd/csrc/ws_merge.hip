@@ -83,7 +83,8 @@ __global__ __launch_bounds__(128) void lse_merge_kernel(
 // ---------------------------------------------------------------------------
 // Split combine + host merge of a deferred-combine decode step.
 //
-// One 64-lane workgroup per output row (kv row * heads + head).  It rebuilds
+// One 64-lane workgroup per output row (kv row * heads + head) and 256-column
+// chunk.  It rebuilds
 // the step's plan from the post-step lengths (ws_plan.h) to find the row's
 // GPU pieces: the final (out, lse) the step wrote when one workgroup held the
 // row, else the partials of the row's workgroups (slots w + kv row), then
@@ -104,6 +105,11 @@ struct MergeSplitParams {
   float* out_f32;
   float* lse_out;
 };
+
+// One 64-lane workgroup per (output row, 256-column chunk): lane t owns float4
+// column chunk * 64 + t and accumulates it over the pieces with eight loads
+// in flight.
+constexpr int kMergeChunk4 = 64;
 
 template <int FMT>
 __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams p) {
@@ -136,11 +142,13 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
     }
   }
   // weights: M over the GPU pieces and the host partial
+  const int c = blockIdx.y * kMergeChunk4 + t;  // float4 column
+  const bool col_ok = c < (p.Dv >> 2);
   float lb = neg_inf();
-  if (FMT >= 0) {
-    float4 dummy;
-    load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, 0, lb, dummy);
-  }
+  float4 ob = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (FMT >= 0)
+    load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, col_ok ? c : 0, lb,
+                                 ob);
   float mx = lb;
   for (int s = t; s < n; s += 64) {
     const float v = lsrc[(size_t)s * lstride];
@@ -159,40 +167,37 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   const float L = sum + wb;
   __syncthreads();
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  if (t == 0 && p.lse_out) p.lse_out[qrow] = L > 0.f ? mx + __logf(L) : neg_inf();
-  const int c4 = p.Dv >> 2;
-  for (int c = t; c < c4; c += 64) {
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    int s = 0;
-    for (; s + 4 <= n; s += 4) {
-      float4 v[4];
+  if (blockIdx.y == 0 && t == 0 && p.lse_out)
+    p.lse_out[qrow] = L > 0.f ? mx + __logf(L) : neg_inf();
+  if (!col_ok) return;
+  const float4* src4 = (const float4*)src + c;
+  const size_t sstride4 = sstride / 4;
+  // an empty host side has weight 0 and must not turn its output into NaN
+  float4 a = wb > 0.f ? make_float4(wb * ob.x, wb * ob.y, wb * ob.z, wb * ob.w)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+  int s = 0;
+  for (; s + 8 <= n; s += 8) {
+    float4 v[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = ((const float4*)(src + (size_t)(s + u) * sstride))[c];
+    for (int u = 0; u < 8; ++u) v[u] = src4[(size_t)(s + u) * sstride4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float w = s_w[s + u];
-        a.x += w * v[u].x; a.y += w * v[u].y; a.z += w * v[u].z; a.w += w * v[u].w;
-      }
+    for (int u = 0; u < 8; ++u) {
+      const float w = s_w[s + u];
+      a.x += w * v[u].x; a.y += w * v[u].y; a.z += w * v[u].z; a.w += w * v[u].w;
     }
-    for (; s < n; ++s) {
-      const float w = s_w[s];
-      const float4 v = ((const float4*)(src + (size_t)s * sstride))[c];
-      a.x += w * v.x; a.y += w * v.y; a.z += w * v.z; a.w += w * v.w;
-    }
-    if (FMT >= 0 && wb > 0.f) {
-      float lb2;
-      float4 ob;
-      load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, c, lb2, ob);
-      a.x += wb * ob.x; a.y += wb * ob.y; a.z += wb * ob.z; a.w += wb * ob.w;
-    }
-    const float4 o = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
-    if (p.out_f32) ((float4*)(p.out_f32 + (size_t)qrow * p.Dv))[c] = o;
-    if (p.out_bf16) {
-      uint2 packed;
-      packed.x = pack_bf16x2(o.x, o.y);
-      packed.y = pack_bf16x2(o.z, o.w);
-      ((uint2*)(p.out_bf16 + (size_t)qrow * p.Dv))[c] = packed;
-    }
+  }
+  for (; s < n; ++s) {
+    const float w = s_w[s];
+    const float4 v = src4[(size_t)s * sstride4];
+    a.x += w * v.x; a.y += w * v.y; a.z += w * v.z; a.w += w * v.w;
+  }
+  const float4 o = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+  if (p.out_f32) ((float4*)(p.out_f32 + (size_t)qrow * p.Dv))[c] = o;
+  if (p.out_bf16) {
+    uint2 packed;
+    packed.x = pack_bf16x2(o.x, o.y);
+    packed.y = pack_bf16x2(o.z, o.w);
+    ((uint2*)(p.out_bf16 + (size_t)qrow * p.Dv))[c] = packed;
   }
 }
 
@@ -252,7 +257,8 @@ extern "C" int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, i
   prm.out_bf16 = out_bf16;
   prm.out_f32 = out_f32;
   prm.lse_out = lse_out;
-  const dim3 grid((unsigned)(rows_kv * heads)), block(64);
+  const dim3 grid((unsigned)(rows_kv * heads), (unsigned)((Dv / 4 + kMergeChunk4 - 1) / kMergeChunk4));
+  const dim3 block(64);
   hipStream_t s = (hipStream_t)stream;
   if (!b_out) {
     hipLaunchKernelGGL(merge_split_kernel<-1>, grid, block, 0, s, prm);

@@ -3,12 +3,14 @@
 //
 // Work decomposition (ws_plan.h): the grid's 256-thread workgroups take equal
 // shares of all 32-token blocks of all sequences; the 16 heads of sequence b
-// share each token's 576-wide latent (512 c_kv followed by 64 k_pe).  Per
-// 32-token block, wave w computes the QK partial of token tile (w & 1) over
-// latent half (w >> 1) (9 MFMA k-steps), the four partial score tiles meet in
-// LDS, every wave runs the same online softmax, and wave w accumulates output
-// columns [128w, 128w + 128).  Each wave requests the next block's operands
-// before the current block's MFMAs run.  A sequence held by one workgroup is
+// share each token's 576-wide latent (512 c_kv followed by 64 k_pe).  The
+// workgroup reads each 32-token block from HBM once, with coalesced 16-byte
+// loads, keeps three blocks in flight in registers and stages the block being
+// consumed in an LDS tile, from which all MFMA operands are read: wave w
+// computes the QK partial of token tile (w & 1) over latent half (w >> 1)
+// (9 k-steps), the four score tiles meet in LDS, every wave runs the same
+// online softmax, and wave w accumulates output columns [128w, 128w + 128).
+// A sequence held by one workgroup is
 // written final; otherwise each workgroup stores a partial (slot workgroup +
 // sequence) and mla_reduce_kernel combines them: a sequence carries 32 KB of
 // partial per workgroup, more than one workgroup combines quickly.
@@ -67,11 +69,22 @@ __device__ __forceinline__ void store_cols(float* __restrict__ dst, const f32x4 
   }
 }
 
+// LDS tile of one 32-token block: row-major latent rows of 72 16-byte chunks
+// plus one pad chunk, so the 16 rows a QK operand read touches start in
+// different banks.
+constexpr int kRowChunks = 73;
+constexpr int kTileChunks = 32 * kRowChunks;
+// Blocks in flight in registers while one is consumed from LDS.
+constexpr int kMlaDepth = 3;
+// 16-byte chunks of a block each thread moves (32 rows x 72 chunks / 256).
+constexpr int kChunksPerThread = 9;
+
 template <bool APPEND>
 __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
   constexpr int NT = 256;
   constexpr int add = APPEND ? 1 : 0;
-  __shared__ f32x4 sbuf[2][2][2][64];  // [buffer][latent half][token tile][lane]
+  __shared__ u32x4 s_lat[2][kTileChunks];  // the block being consumed and the next
+  __shared__ f32x4 sbuf[2][2][64];         // [latent half][token tile][lane] score partials
   __shared__ int s_pref[kMaxSeqs + 1];
   __shared__ int s_scan[NT / 64 + 1];
   const int g = blockIdx.x;
@@ -98,6 +111,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
   if (g >= plan.n) return;
   const int blk_end = plan_start(plan, g + 1);
   int blk = plan_start(plan, g);
+  const u32x4* dummy = (const u32x4*)p.q_nope;
 
   while (blk < blk_end) {
     const int b = plan_seq(s_pref, p.B, blk);
@@ -108,6 +122,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     const int seg_end = min(blk_end, row_end);
     const int t_begin = (blk - row_start) * 32;
     const int t_end = min(len, (seg_end - row_start) * 32);
+    const int nblk = seg_end - blk;
     const int orow = b * kMlaH + n16;
     const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
 
@@ -119,7 +134,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
                                    kMlaL))[tid] = *new_chunk(p, b, tid);
     }
 
-    // Q^T for this wave's 9 k-steps: k = 32 * (9 * kh + u) + 8 * j .. + 8.
+    // Q^T for this wave's 9 QK k-steps: k = 32 * (9 * kh + u) + 8 * j .. + 8.
     u32x4 qb[9];
 #pragma unroll
     for (int u = 0; u < 9; ++u) {
@@ -136,69 +151,81 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     float m_run = neg_inf();
     float l_run = 0.f;
 
-    // Operands of the 32-token block at t0.  With valid == false (the
-    // prefetch past the last block) every lane reads the first 16 bytes of
-    // q_nope instead: same instructions and registers, a cache hit.  Plain
-    // (cached) loads: the QK waves and the PV waves read overlapping parts of
-    // each latent, and the second read is served from the cache.
-    auto load_block = [&](int t0, bool valid, u32x4 (&ka)[9], u32x4 (&vr)[8]) {
+    // Block k of the segment, as this thread's 9 chunks (chunk c = tid + 256 u
+    // is row c / 72, 16-byte column c % 72): one fully coalesced 4 KB read per
+    // instruction across the workgroup.  Rows past t_end repeat the last
+    // valid row (masked in the softmax); past the segment's last block every
+    // lane reads the first 16 bytes of q_nope instead (a cache hit).
+    auto gload = [&](int k, u32x4 (&dst)[kChunksPerThread]) {
+      const bool valid = k < nblk;
+      const int t0 = t_begin + 32 * min(k, nblk - 1);
       const int page = t0 / p.page_size;
       const int pid = clamp_page(pt[page], p.num_pages);
       const uint16_t* lb =
           p.latent + ((size_t)pid * p.page_size + (t0 - page * p.page_size)) * (size_t)kMlaL;
       const int last = min(32, t_end - t0) - 1;
       const int new_r = (APPEND && valid) ? len_old - t0 : -1;
-      const int r = min(16 * tt + n16, last);
-      const u32x4* kr = (const u32x4*)(lb + (size_t)r * kMlaL);
-      const u32x4* dummy = (const u32x4*)p.q_nope;
 #pragma unroll
-      for (int u = 0; u < 9; ++u) {
-        const int q = 4 * (9 * kh + u) + j;
-        ka[u] = *(!valid ? dummy : (APPEND && r == new_r) ? new_chunk(p, b, q) : kr + q);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int ri = min(pv_token(i, j), last);
-        const int q = (col0 >> 3) + n16;
-        vr[i] = *(!valid ? dummy
-                  : (APPEND && ri == new_r) ? new_chunk(p, b, q)
-                                            : (const u32x4*)(lb + (size_t)ri * kMlaL) + q);
+      for (int u = 0; u < kChunksPerThread; ++u) {
+        const int c = tid + NT * u;
+        const int r = min(c / 72, last);
+        const int q = c - (c / 72) * 72;
+        const u32x4* src = !valid ? dummy
+                           : (APPEND && r == new_r) ? new_chunk(p, b, q)
+                                                    : (const u32x4*)(lb + (size_t)r * kMlaL) + q;
+        dst[u] = ld_stream(src);
       }
     };
-    auto compute_block = [&](int t0, const u32x4 (&ka)[9], const u32x4 (&vr)[8], int buf) {
-      const int nt = min(32, t_end - t0);
+    auto lwrite = [&](u32x4* tile, const u32x4 (&src)[kChunksPerThread]) {
+#pragma unroll
+      for (int u = 0; u < kChunksPerThread; ++u) {
+        const int c = tid + NT * u;
+        tile[(c / 72) * kRowChunks + (c - (c / 72) * 72)] = src[u];
+      }
+    };
+    // One block from its LDS tile: QK partial of token tile tt over latent
+    // half kh, score partials meet in LDS, shared softmax, PV of this wave's
+    // 128 output columns.
+    auto compute = [&](int k, const u32x4* tile) {
+      const int nt = min(32, t_end - (t_begin + 32 * k));
+      const u32x4* krow = tile + (16 * tt + n16) * kRowChunks + j;
       f32x4 sp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int u = 0; u < 9; ++u) sp = mfma16x16x32(ka[u], qb[u], sp);
-      sbuf[buf][kh][tt][lane] = sp;
+      for (int u = 0; u < 9; ++u) sp = mfma16x16x32(krow[4 * (9 * kh + u)], qb[u], sp);
+      sbuf[kh][tt][lane] = sp;
       __syncthreads();
-      const f32x4 s0 = sbuf[buf][0][0][lane] + sbuf[buf][1][0][lane];
-      const f32x4 s1 = sbuf[buf][0][1][lane] + sbuf[buf][1][1][lane];
+      const f32x4 s0 = sbuf[0][0][lane] + sbuf[1][0][lane];
+      const f32x4 s1 = sbuf[0][1][lane] + sbuf[1][1][lane];
       float alpha;
       const u32x4 pb = softmax_block(s0, s1, j, nt, p.scale_log2, m_run, l_run, alpha);
+      u32x4 vr[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vr[i] = tile[pv_token(i, j) * kRowChunks + (col0 >> 3) + n16];
       pv_block(acc, vr, pb, alpha);
     };
 
-    // Every wave walks the same blocks (they meet at one barrier per block);
-    // the score buffers alternate, so two barriers separate a buffer's reuse.
-    // sched_barrier keeps the next block's loads above the current math.
-    const int nblk = (t_end - t_begin + 31) / 32;
-    {
-      u32x4 kaA[9], vrA[8], kaB[9], vrB[8];
-      load_block(t_begin, true, kaA, vrA);
-      for (int i = 0; i < nblk; i += 2) {
-        load_block(t_begin + 32 * min(i + 1, nblk - 1), i + 1 < nblk, kaB, vrB);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_block(t_begin + 32 * i, kaA, vrA, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        if (i + 1 >= nblk) break;
-        load_block(t_begin + 32 * min(i + 2, nblk - 1), i + 2 < nblk, kaA, vrA);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_block(t_begin + 32 * (i + 1), kaB, vrB, 1);
-        __builtin_amdgcn_sched_barrier(0);
+    // Pipeline: registers hold blocks k + 1 .. k + kMlaDepth in flight while
+    // block k is consumed from one LDS tile and block k + 1 is written to the
+    // other.  Block m lives in register slot m % kMlaDepth; the loop is
+    // unrolled by kMlaDepth so every slot index is static.
+    u32x4 st[kMlaDepth][kChunksPerThread];
+#pragma unroll
+    for (int m = 0; m < kMlaDepth; ++m) gload(m, st[m]);
+    __syncthreads();  // the previous segment is done with the tiles and sbuf
+    lwrite(s_lat[0], st[0]);
+    gload(kMlaDepth, st[0]);
+    __syncthreads();
+    for (int k = 0; k < nblk; k += kMlaDepth) {
+#pragma unroll
+      for (int s = 0; s < kMlaDepth; ++s) {
+        const int kk = k + s;
+        if (kk >= nblk) break;
+        compute(kk, s_lat[kk & 1]);
+        if (kk + 1 < nblk) lwrite(s_lat[(kk + 1) & 1], st[(s + 1) % kMlaDepth]);
+        gload(kk + 1 + kMlaDepth, st[(s + 1) % kMlaDepth]);
+        __syncthreads();
       }
     }
-    __syncthreads();  // the next segment starts with buffer 0 again
 
     const float l_tot = wave_sum_xor16_32(l_run);
     const float inv_l = 1.f / l_tot;
