@@ -149,9 +149,11 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
     // masked in the softmax.  With valid == false (the prefetch past a wave's
     // last block) every lane reads the first row of q instead: same
     // instructions and registers, a cache hit, no HBM traffic.
-    auto load_block = [&](int t0, bool valid, u32x4 (&ka)[2][4], u32x4 (&vr)[8]) {
+    // Physical page of the block at t0 (a scalar load; the ring below issues
+    // it one block ahead, so its latency is not on the block's load path).
+    auto page_id = [&](int t0) { return clamp_page(pt[t0 / p.page_size], p.num_pages); };
+    auto load_block = [&](int t0, int pid, bool valid, u32x4 (&ka)[2][4], u32x4 (&vr)[8]) {
       const int page = t0 / p.page_size;
-      const int pid = clamp_page(pt[page], p.num_pages);
       const size_t tok0 =
           ((size_t)pid * p.Hkv + kvh) * p.page_size + (t0 - page * p.page_size);
       const uint16_t* kb = valid ? p.k_pages + tok0 * D : p.q;
@@ -194,18 +196,21 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
     const int first = t_begin + 32 * wave;
     const int nblk = first < t_end ? (t_end - first + 32 * W - 1) / (32 * W) : 0;
     if (nblk > 0) {
+      auto tblk = [&](int k) { return first + 32 * W * min(k, nblk - 1); };
       u32x4 ka[S][2][4], vr[S][8];
 #pragma unroll
       for (int st = 0; st < S - 1; ++st)
-        load_block(first + 32 * W * min(st, nblk - 1), st < nblk, ka[st], vr[st]);
+        load_block(tblk(st), page_id(tblk(st)), st < nblk, ka[st], vr[st]);
+      int pid_next = page_id(tblk(S - 1));
       for (int i = 0; i < nblk; i += S) {
 #pragma unroll
         for (int st = 0; st < S; ++st) {
           const int blk = i + st;
           if (blk >= nblk) break;
           const int nxt = blk + S - 1;
-          load_block(first + 32 * W * min(nxt, nblk - 1), nxt < nblk, ka[(st + S - 1) % S],
+          load_block(tblk(nxt), pid_next, nxt < nblk, ka[(st + S - 1) % S],
                      vr[(st + S - 1) % S]);
+          pid_next = page_id(tblk(nxt + 1));
           __builtin_amdgcn_sched_barrier(0);
           compute_block(first + 32 * W * blk, ka[st], vr[st]);
           __builtin_amdgcn_sched_barrier(0);
