@@ -397,9 +397,14 @@ def cpu_baseline(data, Hkv, G, budget_s, threads):
 # traffic from the committed rocprofv3 PMC summary
 
 
-def committed_traffic(workload_key):
+# The kernel the headline roofline is measured on (its rocprofv3 name).
+HEAD_KERNEL = "ws::gqa_decode_kernel<4, true, false>"
+
+
+def committed_traffic(workload_key, kernel=HEAD_KERNEL):
     """HBM bytes per launch of the GQA partial kernel from profiles/, if a
-    FETCH_SIZE/WRITE_SIZE summary for this workload is committed."""
+    FETCH_SIZE/WRITE_SIZE summary for this workload and this kernel is
+    committed (a summary of another kernel is not reported)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
@@ -407,8 +412,10 @@ def committed_traffic(workload_key):
         with open(path) as f:
             doc = json.load(f)
         ent = doc.get(workload_key)
-        return None if ent is None else ent.get("traffic_bytes_per_launch")
-    except Exception:
+        if ent is None or ent.get("kernel") != kernel:
+            return None
+        return ent.get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
         return None
 
 
@@ -563,8 +570,8 @@ def main():
         "unit": "GB/s",
         "frac": round(head["partial_gbs"] / HBM_PEAK_GBS, 4),
         "traffic": committed_traffic(wk),
-        "kernel": "gqa_decode_kernel<4, true, false> (ws_gqa_append_decode_split: append + "
-                  "load-balanced split-KV partial, one launch; combine in the merge launch)",
+        "kernel": f"{HEAD_KERNEL} (ws_gqa_append_decode_split: append + load-balanced "
+                  "split-KV partial, one launch; combine in the merge launch)",
         "algorithmic_bytes_per_launch": head["partial_bytes"],
         "mean_launch_us": head["partial_us"],
     }
