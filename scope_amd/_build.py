@@ -65,5 +65,48 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+# ---------------------------------------------------------------------------
+# Host partial: scope_amd/lib/libwshost.so (g++, OpenMP).  The kernels file is
+# built for AVX-512 BF16; the ABI file for the baseline ISA, so a CPU without
+# the kernels' instructions gets WH_ENOTSUP instead of an illegal instruction.
+
+HOST_LIB = os.path.join(LIBDIR, "libwshost.so")
+CXX = os.environ.get("CXX", "g++")
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-fopenmp", "-Wall", "-Wextra", "-fno-math-errno"]
+HOST_SOURCES = {
+    "wh_attn.cpp": [],
+    "wh_kernels.cpp": ["-mavx512f", "-mavx512bw", "-mavx512vl", "-mavx512dq", "-mavx512bf16",
+                       "-mfma"],
+}
+
+
+def build_host(verbose: bool = False) -> str:
+    """Compile the host partial and link libwshost.so; returns its path."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    os.makedirs(OBJDIR, exist_ok=True)
+
+    def one(item):
+        name, extra = item
+        obj = os.path.join(OBJDIR, name[:-4] + ".host.o")
+        cmd = [CXX, *HOST_FLAGS, *extra, "-c", os.path.join(CSRC, name), "-o", obj]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"{CXX} failed for {name}:\n{r.stdout}\n{r.stderr}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=len(HOST_SOURCES)) as ex:
+        objs = list(ex.map(one, HOST_SOURCES.items()))
+    tmp = HOST_LIB + ".tmp"
+    r = subprocess.run([CXX, "-shared", "-fopenmp", *objs, "-o", tmp], capture_output=True,
+                       text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, HOST_LIB)
+    if verbose:
+        print(f"built {HOST_LIB}", file=sys.stderr)
+    return HOST_LIB
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_host(verbose=True))

@@ -1,0 +1,333 @@
+// libwshost.so: the host partial of the partitioned decode KV cache.
+//
+// Work plan (the same one the GPU kernels build on the device): the rows of
+// a call (GQA row = (sequence, kv head), MLA row = sequence) are cut into
+// 32-token blocks, T blocks in all; thread i of n takes the blocks
+// [i*T/n, (i+1)*T/n) and walks them as row segments.  A segment that covers
+// its whole row writes the final (out, lse); one that does not leaves its
+// online-softmax state in slot i + row (distinct for every (thread, row)
+// pair, because both coordinates only grow along the block order).  After a
+// barrier, each split row is combined from the slots of its owner threads.
+//
+// This file is built for the baseline ISA; the kernels (wh_kernels.cpp) are
+// built for AVX-512 BF16 and only reached after wh_isa_supported().
+#include <omp.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <vector>
+
+#include "../../include/wshost.h"
+#include "wh_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+constexpr int kBlock = 32;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct Plan {
+  std::vector<int64_t> pref;  // R + 1 exclusive prefix of blocks per row
+  int64_t T = 0;
+  int64_t start(int i, int n) const { return (int64_t)i * T / n; }
+  int owner(int64_t blk, int n) const { return (int)(((blk + 1) * n + T - 1) / T) - 1; }
+};
+
+// State layout of one (row, heads) segment: m[H], l[H], o[H * Dv].
+struct StateView {
+  float* m;
+  float* l;
+  float* o;
+};
+inline StateView view(float* base, int H) { return {base, base + H, base + 2 * H}; }
+
+void state_init(float* base, int H, int Dv) {
+  for (int h = 0; h < H; ++h) base[h] = -INFINITY;
+  std::memset(base + H, 0, sizeof(float) * (size_t)H * (Dv + 1));
+}
+
+// Folds the states of `cnt` slots into dst (same layout); `oh(i)` is the head
+// of o element i.
+template <class HeadOf>
+void state_combine(const float* const* src, int cnt, int H, int Dv, float* dst, HeadOf oh) {
+  StateView d = view(dst, H);
+  std::vector<float> w((size_t)cnt * H);
+  for (int h = 0; h < H; ++h) {
+    float M = -INFINITY;
+    for (int s = 0; s < cnt; ++s) M = std::max(M, src[s][h]);
+    float L = 0.f;
+    for (int s = 0; s < cnt; ++s) {
+      const float ms = src[s][h];
+      const float ws = (M == -INFINITY || ms == -INFINITY) ? 0.f : std::exp2(ms - M);
+      w[(size_t)s * H + h] = ws;
+      L += ws * src[s][H + h];
+    }
+    d.m[h] = M;
+    d.l[h] = L;
+  }
+  const size_t no = (size_t)H * Dv;
+  for (size_t i = 0; i < no; ++i) {
+    const int h = oh(i);
+    float acc = 0.f;
+    for (int s = 0; s < cnt; ++s) acc += w[(size_t)s * H + h] * src[s][2 * H + i];
+    d.o[i] = acc;
+  }
+}
+
+bool isa_ok() {
+  static const bool ok = __builtin_cpu_supports("avx512f") &&
+                         __builtin_cpu_supports("avx512bw") &&
+                         __builtin_cpu_supports("avx512bf16");
+  return ok;
+}
+
+int resolve_threads(int n_threads, int64_t T) {
+  int n = n_threads > 0 ? n_threads : omp_get_max_threads();
+  n = std::min<int64_t>(n, 1024);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(n, T));
+}
+
+// Runs the plan.  seg(row, tok0, tok1, state) fills a state; fin(row, state)
+// writes a row's output; empty(row) writes the empty result.  Slots hold
+// states of rows split across threads.
+template <class Seg, class Fin, class Empty, class HeadOf>
+void run_plan(const Plan& P, int R, int H, int Dv, int n_req, const int32_t* row_len, Seg seg,
+              Fin fin, Empty empty, HeadOf oh) {
+  const size_t ssz = (size_t)H * (Dv + 2);
+  if (P.T == 0) {
+    for (int r = 0; r < R; ++r) empty(r);
+    return;
+  }
+  const int n_want = resolve_threads(n_req, P.T);
+  std::unique_ptr<float[]> slots(new float[(size_t)(n_want + R) * ssz]);
+#pragma omp parallel num_threads(n_want)
+  {
+    const int n = omp_get_num_threads();  // the runtime may give fewer
+    const int i = omp_get_thread_num();
+    std::unique_ptr<float[]> st(new float[ssz]);
+    int64_t b0 = P.start(i, n);
+    const int64_t b1 = P.start(i + 1, n);
+    int r = (int)(std::upper_bound(P.pref.begin(), P.pref.end(), b0) - P.pref.begin()) - 1;
+    while (b0 < b1) {
+      while (P.pref[r + 1] <= b0) ++r;  // rows without blocks
+      const int64_t e = std::min(b1, P.pref[r + 1]);
+      const int tk0 = (int)((b0 - P.pref[r]) * kBlock);
+      const int tk1 = (int)std::min<int64_t>(row_len[r], (e - P.pref[r]) * kBlock);
+      state_init(st.get(), H, Dv);
+      seg(r, tk0, tk1, st.get());
+      if (b0 == P.pref[r] && e == P.pref[r + 1])
+        fin(r, st.get());
+      else
+        std::memcpy(slots.get() + (size_t)(i + r) * ssz, st.get(), sizeof(float) * ssz);
+      b0 = e;
+    }
+#pragma omp barrier
+    std::vector<const float*> src;
+#pragma omp for schedule(static)
+    for (int row = 0; row < R; ++row) {
+      if (P.pref[row + 1] == P.pref[row]) {
+        empty(row);
+        continue;
+      }
+      const int o0 = P.owner(P.pref[row], n), o1 = P.owner(P.pref[row + 1] - 1, n);
+      if (o0 == o1) continue;  // written by its only thread
+      src.clear();
+      for (int o = o0; o <= o1; ++o) src.push_back(slots.get() + (size_t)(o + row) * ssz);
+      state_combine(src.data(), (int)src.size(), H, Dv, st.get(), oh);
+      fin(row, st.get());
+    }
+  }
+}
+
+Plan make_plan(const int32_t* row_len, int R) {
+  Plan P;
+  P.pref.resize((size_t)R + 1);
+  P.pref[0] = 0;
+  for (int r = 0; r < R; ++r) P.pref[r + 1] = P.pref[r] + (row_len[r] + kBlock - 1) / kBlock;
+  P.T = P.pref[R];
+  return P;
+}
+
+// Final (out, lse) of H heads from a state; o_at(h, s) reads o in staging
+// order, out_row(h) is head h's output row (Dv floats).
+template <class OAt, class OutRow>
+void write_final(const float* base, int H, int Dv, float* lse, OAt o_at, OutRow out_row) {
+  for (int h = 0; h < H; ++h) {
+    const float l = base[H + h];
+    float* dst = out_row(h);
+    if (!(l > 0.f)) {
+      std::memset(dst, 0, sizeof(float) * Dv);
+      lse[h] = -INFINITY;
+      continue;
+    }
+    const float inv = 1.f / l;
+    for (int s = 0; s < Dv; ++s) dst[wh::stage_col(s)] = o_at(h, s) * inv;
+    lse[h] = (base[h] + std::log2(l)) * kLn2;
+  }
+}
+
+// Validates the paging of a call: page size, lengths within the table, and
+// every page id a length reaches inside the pool.
+int check_pages(const char* fn, const int32_t* page_table, const int32_t* lens, int B,
+                int page_size, int max_pages, int num_pages) {
+  if (page_size < 1 || max_pages < 1 || num_pages < 1)
+    return fail(WH_EINVAL, "%s: bad paging page_size=%d max_pages=%d num_pages=%d", fn,
+                page_size, max_pages, num_pages);
+  if (page_size % kBlock != 0 && max_pages != 1)
+    return fail(WH_EINVAL, "%s: page_size %d is not a multiple of %d", fn, page_size, kBlock);
+  const int64_t cap = (int64_t)page_size * max_pages;
+  if (cap > (int64_t)1 << 30) return fail(WH_EINVAL, "%s: %lld tokens per sequence", fn,
+                                          (long long)cap);
+  for (int b = 0; b < B; ++b) {
+    if (lens[b] < 0 || lens[b] > cap)
+      return fail(WH_EINVAL, "%s: lens[%d] = %d outside [0, %lld]", fn, b, lens[b],
+                  (long long)cap);
+    const int np = (int)((lens[b] + (int64_t)page_size - 1) / page_size);
+    for (int p = 0; p < np; ++p) {
+      const int32_t pid = page_table[(size_t)b * max_pages + p];
+      if (pid < 0 || pid >= num_pages)
+        return fail(WH_EINVAL, "%s: page_table[%d][%d] = %d outside [0, %d)", fn, b, p, pid,
+                    num_pages);
+    }
+  }
+  return WH_OK;
+}
+
+// Calls f(page_id, a, e) for each page overlapping tokens [t0, t1) of a
+// sequence, with [a, e) the overlap in page-local token indices.
+template <class F>
+void for_pages(const int32_t* table_row, int page_size, int t0, int t1, F f) {
+  for (int t = t0; t < t1;) {
+    const int p = t / page_size;
+    const int e = std::min(t1, (p + 1) * page_size);
+    f(table_row[p], t - p * page_size, e - p * page_size);
+    t = e;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* wh_last_error(void) { return g_err; }
+
+const char* wh_version(void) { return "wshost 0.1 avx512bf16"; }
+
+int wh_isa_supported(void) { return isa_ok() ? 1 : 0; }
+
+int wh_gqa_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                   const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                   int D, int page_size, int max_pages, int num_pages, float scale,
+                   float* out, float* lse, int n_threads) {
+  g_err[0] = '\0';
+  if (!isa_ok()) return fail(WH_ENOTSUP, "wh_gqa_partial: this CPU lacks AVX-512 F/BW/BF16");
+  if (B < 0 || Hkv < 1 || Hq < 1 || Hq % Hkv != 0)
+    return fail(WH_EINVAL, "wh_gqa_partial: bad shape B=%d Hq=%d Hkv=%d", B, Hq, Hkv);
+  const int G = Hq / Hkv;
+  if (G > 16) return fail(WH_EINVAL, "wh_gqa_partial: group size %d > 16", G);
+  if (D < 32 || D > 256 || D % 32 != 0)
+    return fail(WH_EINVAL, "wh_gqa_partial: head_dim %d is not a multiple of 32 in [32, 256]", D);
+  if (B == 0) return WH_OK;
+  if (!q || !k_pages || !v_pages || !page_table || !lens || !out || !lse)
+    return fail(WH_EINVAL, "wh_gqa_partial: null pointer");
+  if (int rc = check_pages("wh_gqa_partial", page_table, lens, B, page_size, max_pages,
+                           num_pages))
+    return rc;
+  const int R = B * Hkv;
+  std::vector<int32_t> row_len((size_t)R);
+  for (int r = 0; r < R; ++r) row_len[r] = lens[r / Hkv];
+  const Plan P = make_plan(row_len.data(), R);
+  const float sl2 = scale * kLog2e;
+  const size_t head_elems = (size_t)page_size * D;  // one KV head of one page
+  auto seg = [&](int r, int t0, int t1, float* st) {
+    const int b = r / Hkv, kvh = r % Hkv;
+    StateView s = view(st, G);
+    for_pages(page_table + (size_t)b * max_pages, page_size, t0, t1,
+              [&](int pid, int a, int e) {
+                const size_t base = ((size_t)pid * Hkv + kvh) * head_elems;
+                wh::gqa_attend(q + (size_t)r * G * D, k_pages + base, v_pages + base, G, D, a,
+                               e, sl2, s.m, s.l, s.o);
+              });
+  };
+  auto fin = [&](int r, const float* st) {
+    write_final(
+        st, G, D, lse + (size_t)r * G, [&](int h, int s) { return st[2 * G + h * D + s]; },
+        [&](int h) { return out + ((size_t)r * G + h) * D; });
+  };
+  auto empty = [&](int r) {
+    std::memset(out + (size_t)r * G * D, 0, sizeof(float) * G * D);
+    for (int h = 0; h < G; ++h) lse[(size_t)r * G + h] = -INFINITY;
+  };
+  run_plan(P, R, G, D, n_threads, row_len.data(), seg, fin, empty,
+           [D](size_t i) { return (int)(i / D); });
+  return WH_OK;
+}
+
+int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
+                   int c_stride, const uint16_t* pe_pages, int pe_stride,
+                   const int32_t* page_table, const int32_t* lens, int B, int page_size,
+                   int max_pages, int num_pages, float scale, float* out, float* lse,
+                   int n_threads) {
+  using namespace wh;
+  g_err[0] = '\0';
+  if (!isa_ok()) return fail(WH_ENOTSUP, "wh_mla_partial: this CPU lacks AVX-512 F/BW/BF16");
+  if (B < 0) return fail(WH_EINVAL, "wh_mla_partial: bad batch %d", B);
+  if (c_stride < kMlaC || pe_stride < kMlaPe)
+    return fail(WH_EINVAL, "wh_mla_partial: token strides %d / %d below 512 / 64", c_stride,
+                pe_stride);
+  if (B == 0) return WH_OK;
+  if (!q_nope || !q_pe || !c_pages || !pe_pages || !page_table || !lens || !out || !lse)
+    return fail(WH_EINVAL, "wh_mla_partial: null pointer");
+  if (int rc = check_pages("wh_mla_partial", page_table, lens, B, page_size, max_pages,
+                           num_pages))
+    return rc;
+  const int H = kMlaHeads, Dv = kMlaC;
+  const Plan P = make_plan(lens, B);
+  const float sl2 = scale * kLog2e;
+  auto seg = [&](int b, int t0, int t1, float* st) {
+    // per-thread scratch: the pair-transposed query, then the staged value
+    // pairs (64-byte aligned: the kernel stores them with aligned stores)
+    thread_local std::vector<uint32_t> scratch;
+    scratch.resize(kMlaQtWords + kMlaScratchWords + 16);
+    uint32_t* qt = scratch.data();
+    qt += (64 - ((uintptr_t)qt & 63)) / 4 % 16;
+    uint32_t* vs = qt + kMlaQtWords;
+    mla_prepare_q(q_nope + (size_t)b * H * kMlaC, q_pe + (size_t)b * H * kMlaPe, qt);
+    StateView s = view(st, H);
+    for_pages(page_table + (size_t)b * max_pages, page_size, t0, t1,
+              [&](int pid, int a, int e) {
+                const size_t tok0 = (size_t)pid * page_size;
+                mla_attend(qt, c_pages + tok0 * c_stride, (size_t)c_stride,
+                           pe_pages + tok0 * pe_stride, (size_t)pe_stride, a, e, sl2, s.m, s.l,
+                           s.o, vs);
+              });
+  };
+  auto fin = [&](int b, const float* st) {
+    write_final(
+        st, H, Dv, lse + (size_t)b * H, [&](int h, int s) { return st[2 * H + s * H + h]; },
+        [&](int h) { return out + ((size_t)b * H + h) * Dv; });
+  };
+  auto empty = [&](int b) {
+    std::memset(out + (size_t)b * H * Dv, 0, sizeof(float) * H * Dv);
+    for (int h = 0; h < H; ++h) lse[(size_t)b * H + h] = -INFINITY;
+  };
+  run_plan(P, B, H, Dv, n_threads, lens, seg, fin, empty,
+           [](size_t i) { return (int)(i % kMlaHeads); });
+  return WH_OK;
+}
+
+}  // extern "C"

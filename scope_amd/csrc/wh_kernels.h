@@ -1,0 +1,52 @@
+// AVX-512 BF16 kernels of the host partial (libwshost.so).
+//
+// Each kernel attends the query heads of one row over a token range
+// [t0, t1) of that row and folds the result into an online-softmax state:
+//   m[h]  running max of the scaled scores, log2 domain (-inf when empty),
+//   l[h]  running sum of 2^(score - m),
+//   o     running sum of 2^(score - m) * v, fp32, in *staging order*.
+// Staging order: the value columns come out of the bf16 pair interleave
+// (vpunpck{l,h}wd of two tokens' rows) permuted inside each 32-column chunk;
+// column d of chunk c sits at slot stage_slot(d) below.  Callers keep o in
+// staging order until the final write, which un-permutes it.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+namespace wh {
+
+// Slot of value column d in staging order (and its inverse): inside a
+// 32-column chunk, slot 16*half + i holds column 8*(i/4) + 4*half + i%4.
+inline int stage_col(int s) {
+  const int c = s >> 5, half = (s >> 4) & 1, i = s & 15;
+  return 32 * c + 8 * (i >> 2) + 4 * half + (i & 3);
+}
+
+// Zero row used in place of tokens past the end of a range (no read past
+// the caller's buffers).  Wide enough for the 576-column MLA latent.
+extern const uint16_t kZeroRow[1024];
+
+// GQA: q holds G rows of D bf16 (the query heads sharing one KV head); token
+// t of the row is k + t*D / v + t*D.  D is a multiple of 32, at most 256;
+// G at most 16.  m, l: G floats; o: G*D floats (staging order).
+// scale_log2 = softmax scale * log2(e).
+void gqa_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G, int D,
+                int t0, int t1, float scale_log2, float* m, float* l, float* o);
+
+// MLA (absorbed, 16 heads): qt is the query in pair-transposed form
+// (mla_prepare_q); token t's latent is c + t*c_tok (512 bf16, also the value)
+// and pe + t*pe_tok (64 bf16).  m, l: 16 floats; o: 512*16 floats, slot-major
+// (o[s*16 + h]).  vst is scratch of kMlaScratchWords 32-bit words.
+constexpr int kMlaHeads = 16;
+constexpr int kMlaC = 512;
+constexpr int kMlaPe = 64;
+constexpr int kMlaPairs = (kMlaC + kMlaPe) / 2;          // 288
+constexpr size_t kMlaScratchWords = 16 * kMlaC;          // 16 token pairs x 512 columns
+constexpr size_t kMlaQtWords = (size_t)kMlaPairs * kMlaHeads;
+void mla_prepare_q(const uint16_t* q_nope, const uint16_t* q_pe, uint32_t* qt);
+void mla_attend(const uint32_t* qt, const uint16_t* c, size_t c_tok, const uint16_t* pe,
+                size_t pe_tok, int t0, int t1, float scale_log2, float* m, float* l, float* o,
+                uint32_t* vst);
+
+}  // namespace wh
