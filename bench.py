@@ -321,6 +321,240 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label, wg=0):
 
 
 # ---------------------------------------------------------------------------
+# Host partial (libwshost.so) and the multi-layer MLA decode with both partitions
+
+
+def _host_pages(tokens, rng):
+    """Exact page assignment of a host segment (no room for appends: decode
+    appends go to the GPU partition), page ids from a random permutation."""
+    need = [-(-int(t) // PAGE) for t in tokens]
+    max_pages = max(1, max(need))
+    num_pages = max(1, sum(need))
+    perm = rng.permutation(num_pages).astype(np.int32)
+    table = np.zeros((len(need), max_pages), np.int32)
+    k = 0
+    for b, n in enumerate(need):
+        table[b, :n] = perm[k:k + n]
+        k += n
+    return table, num_pages
+
+
+def _host_threads():
+    n = len(os.sched_getaffinity(0))
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return min(n, omp) if omp > 0 else n
+
+
+def host_gqa_bench(*, Hkv, G, host_tokens, reps, seed, dev, threads, label):
+    """Native host partial (wh_gqa_partial) over a paged host segment holding
+    host_tokens[b] tokens per sequence; median of `reps` calls."""
+    import torch
+
+    from scope_amd import host
+
+    D = 128
+    rng = np.random.default_rng(seed)
+    table, num_pages = _host_pages(host_tokens, rng)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    kp = _randn_bf16((num_pages, Hkv, PAGE, D), gen, 1.0, dev).cpu()
+    vp = _randn_bf16((num_pages, Hkv, PAGE, D), gen, 1.0, dev).cpu()
+    B = len(host_tokens)
+    q = _randn_bf16((B, Hkv * G, D), gen, 1.0, dev).cpu()
+    lens = torch.from_numpy(np.asarray(host_tokens, np.int32))
+    tab = torch.from_numpy(table)
+    out = torch.empty((B, Hkv * G, D), dtype=torch.float32)
+    lse = torch.empty((B, Hkv * G), dtype=torch.float32)
+    host.gqa_partial(q, kp, vp, tab, lens, D ** -0.5, threads, out, lse)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        host.gqa_partial(q, kp, vp, tab, lens, D ** -0.5, threads, out, lse)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    nbytes = float(np.sum(host_tokens)) * Hkv * 2 * D * 2
+    return {"label": label, "threads": threads, "host_tokens": int(np.sum(host_tokens)),
+            "us": round(t * 1e6, 1), "gbs": round(nbytes / t / 1e9, 2)}
+
+
+def host_mla_bench(*, host_tokens, reps, seed, dev, threads, label):
+    """Native host partial (wh_mla_partial) over a paged host latent pool."""
+    import torch
+
+    from scope_amd import host
+
+    rng = np.random.default_rng(seed)
+    table, num_pages = _host_pages(host_tokens, rng)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    pool = _randn_bf16((num_pages, PAGE, 576), gen, 0.5, dev).cpu()
+    B = len(host_tokens)
+    qn = _randn_bf16((B * 16, 512), gen, 0.5, dev).cpu()
+    qp = _randn_bf16((B * 16, 64), gen, 0.5, dev).cpu()
+    lens = torch.from_numpy(np.asarray(host_tokens, np.int32))
+    tab = torch.from_numpy(table)
+    out = torch.empty((B * 16, 512), dtype=torch.float32)
+    lse = torch.empty((B * 16,), dtype=torch.float32)
+    host.mla_partial(qn, qp, pool, tab, lens, 192 ** -0.5, threads, out, lse)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        host.mla_partial(qn, qp, pool, tab, lens, 192 ** -0.5, threads, out, lse)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    tok = float(np.sum(host_tokens))
+    return {"label": label, "threads": threads, "host_tokens": int(tok),
+            "us": round(t * 1e6, 1), "gbs": round(tok * 1152 / t / 1e9, 2),
+            "tflops": round(tok * 16 * (2 * 576 + 2 * 512) / t / 1e12, 3)}
+
+
+def host_read_gbs(threads, nbytes=1 << 30, reps=5):
+    """Host DRAM read bandwidth: a multi-threaded sum over an nbytes fp32
+    array (torch's CPU reduction on `threads` threads), best of `reps`."""
+    import torch
+
+    old = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        x = torch.ones(nbytes // 4, dtype=torch.float32)
+        x.sum()
+        best = float("inf")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            x.sum()
+            best = min(best, time.perf_counter() - t0)
+        return round(nbytes / best / 1e9, 1)
+    finally:
+        torch.set_num_threads(old)
+
+
+def lognormal_lens(B, seed, median=4096, sigma=1.0, lo=256, hi=65536):
+    """Sequence lengths ~ lognormal(ln median, sigma) clipped to [lo, hi]."""
+    rng = np.random.default_rng(seed)
+    x = rng.lognormal(mean=math.log(median), sigma=sigma, size=B)
+    return np.clip(np.floor(x), lo, hi).astype(np.int64)
+
+
+def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads, label):
+    """One decode step of a `layers`-layer absorbed-MLA model over a
+    token-range-partitioned latent cache, per layer in dependency order:
+    q -> host (pinned), GPU split step (append + partial over the HBM pages)
+    while the host partial (wh_mla_partial) attends the host pages, host
+    partial -> GPU, merge.  The q copy of layer l+1 is ordered after layer l's
+    merge on the stream, as the real model's next query would be.  Returns
+    the per-layer critical path and its parts."""
+    import torch
+
+    from scope_amd import host, ops
+
+    L = ops.lib()
+    H = 16
+    rows = B * H
+    lens = np.asarray(lens, np.int64)
+    g_tok = np.floor(share * lens).astype(np.int64)
+    h_tok = lens - g_tok
+    rng = np.random.default_rng(seed)
+    extra = warmup + steps + 1
+    g_table, g_pages = _page_table(g_tok, extra, rng)
+    h_table, h_pages = _host_pages(h_tok, rng)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    g_pools = [_randn_bf16((g_pages, PAGE, 576), gen, 0.5, dev) for _ in range(layers)]
+    h_pools = [_randn_bf16((h_pages, PAGE, 576), gen, 0.5, dev).cpu() for _ in range(layers)]
+    page_table = torch.from_numpy(g_table).to(dev)
+    lens_d = torch.zeros((layers, 2, B), dtype=torch.int32, device=dev)
+    lens_d[:, 0] = torch.from_numpy(g_tok.astype(np.int32)).to(dev)
+    qn = _randn_bf16((layers, rows, 512), gen, 0.5, dev)
+    qp = _randn_bf16((layers, rows, 64), gen, 0.5, dev)
+    kv_new = _randn_bf16((layers, B, 1, 576), gen, 0.5, dev)
+    out_g = torch.empty((rows, 512), dtype=torch.float32, device=dev)
+    lse_g = torch.empty((rows,), dtype=torch.float32, device=dev)
+    out = torch.empty((rows, 512), dtype=torch.bfloat16, device=dev)
+    qn_h = torch.empty((rows, 512), dtype=torch.bfloat16, pin_memory=True)
+    qp_h = torch.empty((rows, 64), dtype=torch.bfloat16, pin_memory=True)
+    oc_h = torch.empty((rows, 512), dtype=torch.float32, pin_memory=True)
+    lc_h = torch.empty((rows,), dtype=torch.float32, pin_memory=True)
+    oc_d = torch.empty((rows, 512), dtype=torch.float32, device=dev)
+    lc_d = torch.empty((rows,), dtype=torch.float32, device=dev)
+    h_lens = torch.from_numpy(h_tok.astype(np.int32))
+    h_tab = torch.from_numpy(h_table)
+    with_host = bool(h_tok.sum() > 0)
+    max_len0 = int(g_tok.max())
+    nwg, wsb = ops.decode_plan(1, B, H, max_len0 + extra, 0)
+    ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    scale = 192 ** -0.5
+    cap = PAGE * g_table.shape[1]
+    ev_q = torch.cuda.Event()
+    e_a = [torch.cuda.Event(enable_timing=True) for _ in range(layers)]
+    e_b = [torch.cuda.Event(enable_timing=True) for _ in range(layers)]
+    f_step, f_merge = L.ws_mla_append_decode_split, L.ws_merge_split
+
+    def one_step(i, timed):
+        cpu_s = 0.0
+        for l in range(layers):
+            if with_host:
+                qn_h.copy_(qn[l], non_blocking=True)
+                qp_h.copy_(qp[l], non_blocking=True)
+                ev_q.record()
+            li, lo = p(lens_d[l, i % 2]), p(lens_d[l, (i + 1) % 2])
+            if timed:
+                e_a[l].record()
+            rc = f_step(p(qn[l]), p(qp[l]), p(kv_new[l]), ctypes.c_int64(576),
+                        ctypes.c_void_p(kv_new[l].data_ptr() + 1024), ctypes.c_int64(576),
+                        p(g_pools[l]), p(page_table), li, lo, B, H, PAGE, g_table.shape[1],
+                        g_pages, max_len0 + i + 1, nwg, ctypes.c_float(scale), p(out_g),
+                        p(lse_g), p(ws), ctypes.c_size_t(wsb), stream)
+            if timed:
+                e_b[l].record()
+            if with_host:
+                ev_q.synchronize()
+                t0 = time.perf_counter()
+                host.mla_partial(qn_h, qp_h, h_pools[l], h_tab, h_lens, scale, threads,
+                                 oc_h, lc_h)
+                cpu_s += time.perf_counter() - t0
+                oc_d.copy_(oc_h, non_blocking=True)
+                lc_d.copy_(lc_h, non_blocking=True)
+                rc |= f_merge(lo, B, 1, H, 512, cap, nwg, p(out_g), p(lse_g), p(ws),
+                              ctypes.c_size_t(wsb), p(oc_d), p(lc_d), None,
+                              ops.PARTIAL_LSE_F32, p(out), None, None, stream)
+            else:
+                rc |= f_merge(lo, B, 1, H, 512, cap, nwg, p(out_g), p(lse_g), p(ws),
+                              ctypes.c_size_t(wsb), None, None, None, 0, p(out), None, None,
+                              stream)
+            if rc:
+                raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
+        return cpu_s
+
+    for i in range(warmup):
+        one_step(i, False)
+    torch.cuda.synchronize()
+    walls, cpus, gpus = [], [], []
+    for k in range(steps):
+        i = warmup + k
+        t0 = time.perf_counter()
+        cpus.append(one_step(i, True))
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+        gpus.append(sum(e_a[l].elapsed_time(e_b[l]) for l in range(layers)) * 1e-3)
+    wall = float(np.median(walls))
+    cpu = float(np.median(cpus))
+    gpu = float(np.median(gpus))
+    g_bytes = float(g_tok.sum()) * 1152
+    h_bytes = float(h_tok.sum()) * 1152
+    return {
+        "label": label, "batch": B, "layers": layers, "share": share,
+        "gpu_tokens": int(g_tok.sum()), "host_tokens": int(h_tok.sum()),
+        "host_threads": threads, "workgroups": nwg,
+        "us_per_layer": round(wall / layers * 1e6, 1),
+        "ms_per_step": round(wall * 1e3, 3),
+        "gpu_partial_us_per_layer": round(gpu / layers * 1e6, 1),
+        "gpu_partial_gbs": round(g_bytes / (gpu / layers) / 1e9, 1) if gpu > 0 else None,
+        "host_partial_us_per_layer": round(cpu / layers * 1e6, 1) if with_host else 0.0,
+        "host_partial_gbs": round(h_bytes / (cpu / layers) / 1e9, 2) if with_host else None,
+        "layer_bytes": int(g_bytes + h_bytes),
+    }
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: the oracle's C restatement of the reference CPU kernel
 
 
@@ -445,6 +679,10 @@ def main():
                     help="assign each sequence's pages in order instead of shuffled")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC scale factor)")
+    ap.add_argument("--model-layers", type=int, default=27,
+                    help="layers of the multi-layer MLA decode with host partials (0 = skip)")
+    ap.add_argument("--model-steps", type=int, default=5,
+                    help="timed decode steps of the multi-layer MLA run")
     args = ap.parse_args()
     global CONTIGUOUS_PAGES, PAGE
     CONTIGUOUS_PAGES = args.contiguous_pages
@@ -545,6 +783,39 @@ def main():
             log(f"mla B8 L={Lm}: {res['us_per_layer']} us/layer, partial {res['partial_us']} us "
                 f"= {res['partial_gbs']} GB/s")
         extra["mla_kv_len_sweep"] = msweep
+
+    if args.model_layers > 0 and not args.headline_only:
+        # native host partial rates (the other half of the partitioned step)
+        th = _host_threads()
+        h_mix = lens - np.floor(args.share * lens).astype(np.int64)
+        hp = [host_gqa_bench(Hkv=Hkv, G=G, host_tokens=h_mix, reps=5, seed=args.seed + 11,
+                             dev=dev, threads=th, label=f"mixtral_b16_r{args.share}_host"),
+              host_mla_bench(host_tokens=[8192] * 8, reps=5, seed=args.seed + 12, dev=dev,
+                             threads=th, label="dsv2lite_mla_b8_L16384_r0.5_host")]
+        bw = host_read_gbs(th)
+        for r in hp:
+            r["host_read_gbs"] = bw
+            r["frac_of_host_read"] = round(r["gbs"] / bw, 3)
+            log(f"host partial {r['label']}: {r['us']} us = {r['gbs']} GB/s on {th} threads "
+                f"({r['frac_of_host_read']:.0%} of the {bw} GB/s host read bandwidth)")
+        extra["host_partial"] = hp
+        # DeepSeek-V2-Lite decode step: B 32, lognormal lengths, every share
+        m_lens = lognormal_lens(32, args.seed + 5)
+        log(f"mla model: B=32 layers={args.model_layers} lens median "
+            f"{int(np.median(m_lens))} max {int(m_lens.max())} total {int(m_lens.sum())}")
+        rows = []
+        for r in (0.1, 0.3, 0.5, 0.7, 0.9, 1.0):
+            res = mla_model_bench(B=32, layers=args.model_layers, lens=m_lens, share=r,
+                                  steps=args.model_steps, warmup=2, seed=args.seed + 13,
+                                  dev=dev, threads=th, label=f"dsv2lite_mla_b32_r{r}")
+            rows.append(res)
+            log(f"mla model r={r}: {res['us_per_layer']} us/layer (gpu partial "
+                f"{res['gpu_partial_us_per_layer']} us, host partial "
+                f"{res['host_partial_us_per_layer']} us)")
+            torch.cuda.empty_cache()
+        extra["mla_model"] = {"lens_seed": args.seed + 5, "lens": m_lens.tolist(),
+                              "length_model": "lognormal(ln 4096, 1.0) clipped [256, 65536]",
+                              "by_share": rows}
 
     if args.copy_calibration:
         n = 256 << 20
