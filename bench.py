@@ -426,6 +426,40 @@ def host_read_gbs(threads, nbytes=1 << 30, reps=5):
         torch.set_num_threads(old)
 
 
+def share_model(rows):
+    """Calibrates the share scheduler's roofline model from a share sweep of
+    the multi-layer MLA run and compares its per-layer predictions with the
+    measured ones."""
+    from scope_amd.scheduler import ShareScheduler, fit_side
+
+    gpts = [(r["gpu_tokens"] * 1152.0, r["gpu_partial_us_per_layer"] * 1e-6) for r in rows]
+    hpts = [(r["host_tokens"] * 1152.0, r["host_partial_us_per_layer"] * 1e-6) for r in rows
+            if r["host_tokens"] > 0]
+    gpu, hst = fit_side(gpts), fit_side(hpts)
+    mixed = [r for r in rows if r["host_tokens"] > 0]
+    resid = [r["us_per_layer"] - max(r["gpu_partial_us_per_layer"],
+                                     r["host_partial_us_per_layer"]) for r in mixed]
+    only = [r for r in rows if r["host_tokens"] == 0]
+    gpu_only_resid = [r["us_per_layer"] - r["gpu_partial_us_per_layer"] for r in only]
+    sched = ShareScheduler(gpu=gpu, host=hst, xfer_s=float(np.median(resid)) * 1e-6,
+                           merge_s=0.0,
+                           merge_gpu_only_s=(float(np.median(gpu_only_resid)) * 1e-6
+                                             if only else 0.0))
+    W = rows[0]["layer_bytes"]
+    return {
+        "gpu_fit": {"fixed_us": round(gpu.fixed_s * 1e6, 1),
+                    "gbs": round(gpu.rate_bps / 1e9, 1)},
+        "host_fit": {"fixed_us": round(hst.fixed_s * 1e6, 1),
+                     "gbs": round(hst.rate_bps / 1e9, 1)},
+        "xfer_merge_us": round(sched.xfer_s * 1e6, 1),
+        "r_balance": round(sched.balance_share(W), 4),
+        "r_choice_unbounded": sched.choose(W),
+        "shares": [r["share"] for r in rows],
+        "predicted_us": [round(sched.predict(r["share"], W)["layer"] * 1e6, 1) for r in rows],
+        "measured_us": [r["us_per_layer"] for r in rows],
+    }
+
+
 def lognormal_lens(B, seed, median=4096, sigma=1.0, lo=256, hi=65536):
     """Sequence lengths ~ lognormal(ln median, sigma) clipped to [lo, hi]."""
     rng = np.random.default_rng(seed)
@@ -815,7 +849,12 @@ def main():
             torch.cuda.empty_cache()
         extra["mla_model"] = {"lens_seed": args.seed + 5, "lens": m_lens.tolist(),
                               "length_model": "lognormal(ln 4096, 1.0) clipped [256, 65536]",
-                              "by_share": rows}
+                              "by_share": rows,
+                              "scheduler": share_model(rows)}
+        sm = extra["mla_model"]["scheduler"]
+        log(f"share model: gpu {sm['gpu_fit']}, host {sm['host_fit']}, r_balance "
+            f"{sm['r_balance']}, predicted/measured us per layer "
+            f"{list(zip(sm['predicted_us'], sm['measured_us']))}")
 
     if args.copy_calibration:
         n = 256 << 20

@@ -1,0 +1,136 @@
+"""Share scheduler: which fraction r of every sequence's KV lives in HBM.
+
+The reference picks its split from calibrated tables (KV_LEN_GS_TABLE,
+system/deepseek.py:127-142; batch/length ladders, system/qwenoffload.py:
+1291-1327 and system/deepseek.py:846-864) and nudges it online with an EMA
+toward the point where GPU and CPU finish together (system/qwenoffload.py:
+1160-1165, system/mixoffload.py:1466-1474).  Here the choice comes from a
+roofline model of the two partials that the same measurements calibrate:
+
+  GPU partial   t_g(r) = a_g + r * W / bw_g        (HBM stream, W = KV bytes
+                                                    of one layer, all sequences)
+  host partial  t_h(r) = a_h + (1 - r) * W / bw_h  (host DRAM stream / AVX-512)
+  transfers     t_x    = q to the host + the host partial back (PCIe latency
+                         dominated; only when r < 1)
+  layer         T(r) = max(t_g(r), t_h(r) + t_x) + t_m   for r < 1
+                T(1) = t_g(1) + t_m1                      (no host partial)
+
+T is minimised where the two sides meet, r_bal = (a_h + t_x - a_g + W/bw_h) /
+(W/bw_g + W/bw_h), or at r = 1 when the whole cache fits, since the host side
+then disappears.  HBM capacity caps r: r <= hbm_budget / (layers * W).  With
+MI355X's HBM at ~6 TB/s against a host at ~0.1 TB/s, r_bal is above 0.97 for
+every realistic W, so in practice the choice is "as much as fits": the host
+partition exists for capacity, and its speed sets the step time once the
+cache outgrows HBM.
+
+Rates are tracked online with the reference's EMA form (new = (1 - w) * old
++ w * observed), per side, from (bytes, seconds) observations.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+
+@dataclass
+class Side:
+    """Affine time model of one partial: seconds = fixed + bytes / rate."""
+    fixed_s: float
+    rate_bps: float
+
+    def time(self, nbytes: float) -> float:
+        return self.fixed_s + nbytes / self.rate_bps
+
+
+@dataclass
+class ShareScheduler:
+    gpu: Side
+    host: Side
+    xfer_s: float = 30e-6        # q to the host + partial back, per layer
+    merge_s: float = 5e-6        # merge launch with a host partial
+    merge_gpu_only_s: float = 5e-6
+    hbm_budget_bytes: float | None = None
+    ema_weight: float = 0.2
+    history: list = field(default_factory=list)
+
+    # ------------------------------------------------------------------ model
+
+    def predict(self, r: float, layer_bytes: float) -> dict:
+        """Per-layer times (seconds) at share r for a layer of layer_bytes KV."""
+        if not 0.0 <= r <= 1.0:
+            raise ValueError(f"share {r} outside [0, 1]")
+        tg = self.gpu.time(r * layer_bytes)
+        if r >= 1.0:
+            return {"gpu": tg, "host": 0.0, "layer": tg + self.merge_gpu_only_s}
+        th = self.host.time((1.0 - r) * layer_bytes) + self.xfer_s
+        return {"gpu": tg, "host": th, "layer": max(tg, th) + self.merge_s}
+
+    def balance_share(self, layer_bytes: float) -> float:
+        """Share where the GPU partial and the host partial (+ transfers) take
+        equally long, clamped to [0, 1]."""
+        if layer_bytes <= 0:
+            return 1.0
+        wg = layer_bytes / self.gpu.rate_bps
+        wh = layer_bytes / self.host.rate_bps
+        r = (self.host.fixed_s + self.xfer_s - self.gpu.fixed_s + wh) / (wg + wh)
+        return min(1.0, max(0.0, r))
+
+    def capacity_share(self, layer_bytes: float, layers: int = 1) -> float:
+        """Largest share whose GPU pages fit the HBM budget."""
+        if self.hbm_budget_bytes is None or layer_bytes <= 0:
+            return 1.0
+        return min(1.0, max(0.0, self.hbm_budget_bytes / (layers * layer_bytes)))
+
+    def choose(self, layer_bytes: float, layers: int = 1, granularity: float = 0.0) -> float:
+        """The share minimising the per-layer time within the HBM budget.
+
+        Candidates: the balance point, the capacity limit and r = 1; T is
+        piecewise linear in r with its minimum at one of them.  granularity
+        > 0 rounds the result down to a multiple of it (a coarser policy
+        table), never above the capacity limit.
+        """
+        cap = self.capacity_share(layer_bytes, layers)
+        cands = {min(cap, self.balance_share(layer_bytes)), cap}
+        if cap >= 1.0:
+            cands.add(1.0)
+        best = min(cands, key=lambda r: (self.predict(r, layer_bytes)["layer"], -r))
+        if granularity > 0:
+            best = min(cap, math.floor(best / granularity + 1e-9) * granularity)
+        return best
+
+    def choose_for_lengths(self, lens, bytes_per_token: int, layers: int = 1,
+                           granularity: float = 0.0) -> float:
+        """choose() for a batch of sequence lengths (bytes of every token of one
+        layer: 1152 for the absorbed MLA latent, Hkv*2*D*2 for GQA)."""
+        return self.choose(float(sum(int(x) for x in lens)) * bytes_per_token, layers,
+                           granularity)
+
+    # ------------------------------------------------------------- calibration
+
+    def observe(self, side: str, nbytes: float, seconds: float) -> None:
+        """Folds one measured partial into that side's rate (EMA over the rate
+        implied by the current fixed cost)."""
+        s = self.gpu if side == "gpu" else self.host
+        eff = seconds - s.fixed_s
+        if nbytes <= 0 or eff <= 0:
+            return
+        w = self.ema_weight
+        s.rate_bps = (1.0 - w) * s.rate_bps + w * (nbytes / eff)
+        self.history.append((side, nbytes, seconds))
+
+
+def fit_side(points) -> Side:
+    """Least-squares affine fit seconds = fixed + bytes / rate over
+    (bytes, seconds) points (at least two distinct byte counts)."""
+    pts = [(float(b), float(t)) for b, t in points if b > 0]
+    if len(pts) < 2 or len({b for b, _ in pts}) < 2:
+        raise ValueError("need two or more distinct byte counts to fit a side")
+    n = len(pts)
+    mb = sum(b for b, _ in pts) / n
+    mt = sum(t for _, t in pts) / n
+    sbb = sum((b - mb) ** 2 for b, _ in pts)
+    sbt = sum((b - mb) * (t - mt) for b, t in pts)
+    slope = sbt / sbb
+    if slope <= 0:
+        raise ValueError("time does not grow with bytes; cannot fit a rate")
+    return Side(fixed_s=max(0.0, mt - slope * mb), rate_bps=1.0 / slope)

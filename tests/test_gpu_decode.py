@@ -1,6 +1,7 @@
 """End-to-end partitioned decode steps on the GPU (host partial from the
-oracle's C restatement of the reference CPU kernels) and the reference-API
-drop-ins, against fp64 attention over the whole sequence."""
+oracle's C restatement of the reference CPU kernels, or this package's native
+host partial) and the reference-API drop-ins, against fp64 attention over the
+whole sequence."""
 import numpy as np
 import pytest
 import torch
@@ -9,7 +10,7 @@ from oracle import attn_np as O
 from oracle import port
 from scope_amd import ops, reference_api
 from scope_amd.cache import GqaGpuPartition, PartitionedKVCache, PartitionedLatentCache
-from scope_amd.decode import partitioned_gqa_decode, partitioned_mla_decode
+from scope_amd.decode import NATIVE, partitioned_gqa_decode, partitioned_mla_decode
 from scope_amd.partition import gpu_share
 from tests.helpers import (LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, assert_close,
                            bf16_randn, bits)
@@ -42,7 +43,7 @@ def oracle_mla_compressed(q_proj, q_pe, c, pe, scale):
 
 
 @pytest.mark.parametrize("r", [0.25, 0.5, 0.75])
-@pytest.mark.parametrize("cpu", ["fused_cpu_attn_bf16", "fused_cpu_attn_mla"])
+@pytest.mark.parametrize("cpu", ["fused_cpu_attn_bf16", "fused_cpu_attn_mla", NATIVE])
 def test_partitioned_gqa_step_mixtral_shape(r, cpu):
     # Mixtral layer shape (32 q / 8 KV heads, D 128), variable lengths,
     # trailing floor(r*L) tokens on the GPU, one appended token per step.
@@ -63,9 +64,11 @@ def test_partitioned_gqa_step_mixtral_shape(r, cpu):
     k_new = torch.stack([k[:, -1:] for k in k_all]).to(DEV)
     v_new = torch.stack([v[:, -1:] for v in v_all]).to(DEV)
     q = bf16_randn((B, Hkv * G, D), 777)
-    fn = oracle_fused_cpu_attn_bf16 if cpu == "fused_cpu_attn_bf16" else oracle_fused_cpu_attn_mla
-    out = partitioned_gqa_decode(cache, 0, q.to(DEV), scale, fn, cpu_format=cpu,
-                                 k_new=k_new, v_new=v_new)
+    fn = {"fused_cpu_attn_bf16": oracle_fused_cpu_attn_bf16,
+          "fused_cpu_attn_mla": oracle_fused_cpu_attn_mla, NATIVE: NATIVE}[cpu]
+    fmt = cpu if cpu != NATIVE else "fused_cpu_attn_bf16"
+    out = partitioned_gqa_decode(cache, 0, q.to(DEV), scale, fn, cpu_format=fmt,
+                                 k_new=k_new, v_new=v_new, host_threads=3)
     torch.cuda.synchronize()
     assert out.shape == (B, Hkv * G, 1, D) and out.dtype == torch.bfloat16
     got = out.float().cpu().numpy()[:, :, 0]
@@ -76,12 +79,13 @@ def test_partitioned_gqa_step_mixtral_shape(r, cpu):
     assert cache.gpu.lens[0].tolist() == [gg + 1 for gg in g]
 
 
-def test_partitioned_mla_step_boundary_crossing():
+@pytest.mark.parametrize("host_fn", ["oracle", NATIVE])
+def test_partitioned_mla_step_boundary_crossing(host_fn):
     # DS-V2-Lite absorbed shape: 16 heads, 576 latent, host segment gs tokens;
     # the appended tokens cross the boundary (system/deepseek.py:181-188).
     B, H, gs, L0 = 2, 16, 96, 90
     scale = 192 ** -0.5
-    _say("partitioned mla boundary crossing")
+    _say(f"partitioned mla boundary crossing host={host_fn}")
     cache = PartitionedLatentCache(1, B, max_seq=400, gs=gs, device=DEV)
     c_all = bf16_randn((B, 300, 512), 901, 0.5)
     pe_all = bf16_randn((B, 300, 64), 902, 0.5)
@@ -92,8 +96,9 @@ def test_partitioned_mla_step_boundary_crossing():
     qn = bf16_randn((B * H, 512), 903, 0.5)
     qp = bf16_randn((B * H, 64), 904, 0.5)
     out = partitioned_mla_decode(cache, 0, qn.to(DEV), qp.to(DEV), scale,
-                                 oracle_mla_compressed,
-                                 c_new=c_all[:, 299:300].to(DEV), pe_new=pe_all[:, 299:300].to(DEV))
+                                 oracle_mla_compressed if host_fn == "oracle" else NATIVE,
+                                 c_new=c_all[:, 299:300].to(DEV), pe_new=pe_all[:, 299:300].to(DEV),
+                                 host_threads=4)
     torch.cuda.synchronize()
     assert cache.seq_len(0) == 300 and cache.gpu.lens[0].tolist() == [300 - gs] * B
     want, _ = O.mla_attention_fp64(bits(qn), bits(qp), bits(c_all), bits(pe_all), scale)
