@@ -495,27 +495,32 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
     page_table = torch.from_numpy(g_table).to(dev)
     lens_d = torch.zeros((layers, 2, B), dtype=torch.int32, device=dev)
     lens_d[:, 0] = torch.from_numpy(g_tok.astype(np.int32)).to(dev)
-    qn = _randn_bf16((layers, rows, 512), gen, 0.5, dev)
-    qp = _randn_bf16((layers, rows, 64), gen, 0.5, dev)
+    # q_nope and q_pe of a layer are adjacent (one copy to the host); the host
+    # partial's out and lse are adjacent (one copy back)
+    qbuf = _randn_bf16((layers, rows * 576), gen, 0.5, dev)
+    qn = [qbuf[l, :rows * 512].view(rows, 512) for l in range(layers)]
+    qp = [qbuf[l, rows * 512:].view(rows, 64) for l in range(layers)]
     kv_new = _randn_bf16((layers, B, 1, 576), gen, 0.5, dev)
     out_g = torch.empty((rows, 512), dtype=torch.float32, device=dev)
     lse_g = torch.empty((rows,), dtype=torch.float32, device=dev)
     out = torch.empty((rows, 512), dtype=torch.bfloat16, device=dev)
-    qn_h = torch.empty((rows, 512), dtype=torch.bfloat16, pin_memory=True)
-    qp_h = torch.empty((rows, 64), dtype=torch.bfloat16, pin_memory=True)
-    oc_h = torch.empty((rows, 512), dtype=torch.float32, pin_memory=True)
-    lc_h = torch.empty((rows,), dtype=torch.float32, pin_memory=True)
-    oc_d = torch.empty((rows, 512), dtype=torch.float32, device=dev)
-    lc_d = torch.empty((rows,), dtype=torch.float32, device=dev)
+    q_h = torch.empty((rows * 576,), dtype=torch.bfloat16, pin_memory=True)
+    qn_h, qp_h = q_h[:rows * 512].view(rows, 512), q_h[rows * 512:].view(rows, 64)
+    part_h = torch.empty((rows * 513,), dtype=torch.float32, pin_memory=True)
+    oc_h, lc_h = part_h[:rows * 512].view(rows, 512), part_h[rows * 512:]
+    part_d = torch.empty((rows * 513,), dtype=torch.float32, device=dev)
+    oc_d, lc_d = part_d[:rows * 512].view(rows, 512), part_d[rows * 512:]
     h_lens = torch.from_numpy(h_tok.astype(np.int32))
     h_tab = torch.from_numpy(h_table)
     with_host = bool(h_tok.sum() > 0)
+    scale = 192 ** -0.5
+    h_calls = [host.mla_partial(qn_h, qp_h, h_pools[l], h_tab, h_lens, scale, threads, oc_h,
+                                lc_h, prepare=True) for l in range(layers)]
     max_len0 = int(g_tok.max())
     nwg, wsb = ops.decode_plan(1, B, H, max_len0 + extra, 0)
     ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     p = lambda t: ctypes.c_void_p(t.data_ptr())
-    scale = 192 ** -0.5
     cap = PAGE * g_table.shape[1]
     ev_q = torch.cuda.Event()
     e_a = [torch.cuda.Event(enable_timing=True) for _ in range(layers)]
@@ -526,8 +531,7 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
         cpu_s = 0.0
         for l in range(layers):
             if with_host:
-                qn_h.copy_(qn[l], non_blocking=True)
-                qp_h.copy_(qp[l], non_blocking=True)
+                q_h.copy_(qbuf[l], non_blocking=True)
                 ev_q.record()
             li, lo = p(lens_d[l, i % 2]), p(lens_d[l, (i + 1) % 2])
             if timed:
@@ -542,11 +546,9 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
             if with_host:
                 ev_q.synchronize()
                 t0 = time.perf_counter()
-                host.mla_partial(qn_h, qp_h, h_pools[l], h_tab, h_lens, scale, threads,
-                                 oc_h, lc_h)
+                h_calls[l]()
                 cpu_s += time.perf_counter() - t0
-                oc_d.copy_(oc_h, non_blocking=True)
-                lc_d.copy_(lc_h, non_blocking=True)
+                part_d.copy_(part_h, non_blocking=True)
                 rc |= f_merge(lo, B, 1, H, 512, cap, nwg, p(out_g), p(lse_g), p(ws),
                               ctypes.c_size_t(wsb), p(oc_d), p(lc_d), None,
                               ops.PARTIAL_LSE_F32, p(out), None, None, stream)

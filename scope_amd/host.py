@@ -121,11 +121,30 @@ def _outputs(out, lse, out_shape, lse_shape):
     return out, lse
 
 
+class Prepared:
+    """A validated host-partial call bound to its buffers: calling it runs the
+    kernel again on whatever the buffers (queries, pools, page table, lengths)
+    hold now and overwrites its out / lse.  For decode loops that reuse their
+    buffers, it skips the per-call argument checks and marshalling (tens of
+    microseconds of Python per call)."""
+
+    def __init__(self, fn, args, keep):
+        self._fn = fn
+        self._args = args
+        self._keep = keep  # the bound tensors stay alive with the call
+        self.out, self.lse = keep[-2], keep[-1]
+
+    def __call__(self):
+        _check(self._fn(*self._args))
+        return self.out, self.lse
+
+
 def gqa_partial(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, page_table,
                 lens, scale: float, threads: int = 0, out: torch.Tensor | None = None,
-                lse: torch.Tensor | None = None):
+                lse: torch.Tensor | None = None, prepare: bool = False):
     """(out fp32 [B, Hq, D], lse fp32 [B, Hq]) over paged host KV pools
-    k_pages / v_pages [num_pages, Hkv, page_size, D] (the GPU pool layout)."""
+    k_pages / v_pages [num_pages, Hkv, page_size, D] (the GPU pool layout).
+    prepare=True returns a Prepared call instead of running it."""
     B, Hq, D = q.shape
     _cpu(q, torch.bfloat16, "q")
     _cpu(k_pages, torch.bfloat16, "k_pages")
@@ -137,9 +156,14 @@ def gqa_partial(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, p
     table = _table(page_table, B)
     lens = _lens(lens, B)
     out, lse = _outputs(out, lse, (B, Hq, D), (B, Hq))
-    _check(lib().wh_gqa_partial(_p(q), _p(k_pages), _p(v_pages), _p(table), _p(lens), B, Hq,
-                                Hkv, D, ps, table.shape[1], num_pages, float(scale), _p(out),
-                                _p(lse), int(threads)))
+    call = Prepared(lib().wh_gqa_partial,
+                    (_p(q), _p(k_pages), _p(v_pages), _p(table), _p(lens), B, Hq, Hkv, D, ps,
+                     table.shape[1], num_pages, ctypes.c_float(scale), _p(out), _p(lse),
+                     int(threads)),
+                    (q, k_pages, v_pages, table, lens, out, lse))
+    if prepare:
+        return call
+    call()
     return out, lse
 
 
@@ -159,10 +183,11 @@ def gqa_partial_dense(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens, s
 
 
 def mla_partial(q_nope: torch.Tensor, q_pe: torch.Tensor, latent_pages: torch.Tensor,
-                page_table, lens, scale: float, threads: int = 0, out=None, lse=None):
+                page_table, lens, scale: float, threads: int = 0, out=None, lse=None,
+                prepare: bool = False):
     """(out fp32 [B*16, 512], lse fp32 [B*16]) over a paged host latent pool
     latent_pages [num_pages, page_size, 576] (the GPU pool layout: 512 latent
-    then 64 rope per token)."""
+    then 64 rope per token).  prepare=True returns a Prepared call."""
     _cpu(latent_pages, torch.bfloat16, "latent_pages")
     if latent_pages.dim() != 3 or latent_pages.shape[2] != MLA_C + MLA_PE:
         raise ValueError(f"latent_pages must be [num_pages, page_size, 576], got "
@@ -170,7 +195,7 @@ def mla_partial(q_nope: torch.Tensor, q_pe: torch.Tensor, latent_pages: torch.Te
     num_pages, ps, W = latent_pages.shape
     pe_view = latent_pages.view(-1)[MLA_C:]
     return _mla_call(q_nope, q_pe, latent_pages, W, pe_view, W, page_table, lens, ps,
-                     num_pages, scale, threads, out, lse)
+                     num_pages, scale, threads, out, lse, prepare)
 
 
 def mla_partial_dense(q_nope: torch.Tensor, q_pe: torch.Tensor, c: torch.Tensor,
@@ -191,7 +216,7 @@ def mla_partial_dense(q_nope: torch.Tensor, q_pe: torch.Tensor, c: torch.Tensor,
 
 
 def _mla_call(q_nope, q_pe, c, c_stride, pe, pe_stride, page_table, lens, page_size,
-              num_pages, scale, threads, out, lse):
+              num_pages, scale, threads, out, lse, prepare=False):
     _cpu(q_nope, torch.bfloat16, "q_nope")
     _cpu(q_pe, torch.bfloat16, "q_pe")
     rows = q_nope.shape[0]
@@ -202,8 +227,12 @@ def _mla_call(q_nope, q_pe, c, c_stride, pe, pe_stride, page_table, lens, page_s
     table = _table(page_table, B)
     lens = _lens(lens, B)
     out, lse = _outputs(out, lse, (rows, MLA_C), (rows,))
-    _check(lib().wh_mla_partial(_p(q_nope), _p(q_pe), _p(c), int(c_stride), _p(pe),
-                                int(pe_stride), _p(table), _p(lens), B, int(page_size),
-                                table.shape[1], int(num_pages), float(scale), _p(out), _p(lse),
-                                int(threads)))
+    call = Prepared(lib().wh_mla_partial,
+                    (_p(q_nope), _p(q_pe), _p(c), int(c_stride), _p(pe), int(pe_stride),
+                     _p(table), _p(lens), B, int(page_size), table.shape[1], int(num_pages),
+                     ctypes.c_float(scale), _p(out), _p(lse), int(threads)),
+                    (q_nope, q_pe, c, pe, table, lens, out, lse))
+    if prepare:
+        return call
+    call()
     return out, lse

@@ -258,3 +258,26 @@ def test_mla_strided_rows_take_the_gather_path():
                                       r[None, :, 512:576], 192 ** -0.5)
         assert_close(out[h].numpy(), ow, OUT_ATOL, OUT_RTOL, f"mla out b={b}")
         assert_close(lse[h].numpy(), lw, LSE_ATOL, LSE_RTOL, f"mla lse b={b}")
+
+
+@needs_isa
+def test_prepared_call_reads_its_buffers_at_call_time():
+    rng = np.random.default_rng(5)
+    B, lens0 = 2, [200, 70]
+    table, num_pages = _paged(rng, [256, 128], 64)
+    qn = bf16_randn((B * 16, 512), 11, 0.5)
+    qp = bf16_randn((B * 16, 64), 12, 0.5)
+    pool = bf16_randn((num_pages, 64, 576), 13, 0.5)
+    lens = torch.tensor(lens0, dtype=torch.int32)
+    call = host.mla_partial(qn, qp, pool, table, lens, 0.07, 3, prepare=True)
+    o1, l1 = (x.clone() for x in call())
+    want_o, want_l = host.mla_partial(qn, qp, pool, table, lens0, 0.07, 3)
+    np.testing.assert_array_equal(o1.numpy(), want_o.numpy())
+    # new queries and lengths in place: the same call sees them
+    qn.copy_(bf16_randn((B * 16, 512), 14, 0.5))
+    lens[1] = 128
+    o2, l2 = call()
+    want_o, want_l = host.mla_partial(qn, qp, pool, table, [200, 128], 0.07, 3)
+    np.testing.assert_array_equal(o2.numpy(), want_o.numpy())
+    np.testing.assert_array_equal(l2.numpy(), want_l.numpy())
+    assert not np.array_equal(o1.numpy(), o2.numpy())
