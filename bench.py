@@ -667,6 +667,16 @@ def cpu_baseline(data, Hkv, G, budget_s, threads):
 # traffic from the committed rocprofv3 PMC summary
 
 
+# Workloads timed beside the headline (all by default; --workloads picks some):
+#   shares     headline shape at r = 0.25, 0.75
+#   qwen3      Qwen3 B4 length sweep 8k..128k (config 4)
+#   single     Qwen3 B1 L4096 in one partition (config 1)
+#   mla        DeepSeek-V2-Lite B8 L16384 r 0.5 (config 3)
+#   mla_sweep  DeepSeek-V2-Lite B8 length sweep 8k..128k
+#   host       native host partial rates and the host read bandwidth
+#   model      27-layer DeepSeek-V2-Lite decode, B32 lognormal, every share (config 5)
+WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "host", "model")
+
 # The kernel the headline roofline is measured on (its rocprofv3 name).
 HEAD_KERNEL = "ws::gqa_decode_kernel<4, true, false>"
 
@@ -715,6 +725,9 @@ def main():
                     help="assign each sequence's pages in order instead of shuffled")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC scale factor)")
+    ap.add_argument("--workloads", type=str, default=",".join(WORKLOADS),
+                    help="comma list of the workloads beside the headline: "
+                         + ", ".join(WORKLOADS))
     ap.add_argument("--model-layers", type=int, default=27,
                     help="layers of the multi-layer MLA decode with host partials (0 = skip)")
     ap.add_argument("--model-steps", type=int, default=5,
@@ -778,7 +791,11 @@ def main():
             log(f"mla wg {w}: {res['us_per_layer']} us/layer, partial {res['partial_us']} "
                 f"us = {res['partial_gbs']} GB/s")
         extra["mla_wg_sweep"] = sw
-    if not args.headline_only:
+    W = set() if args.headline_only else set(args.workloads.split(","))
+    unknown = W - set(WORKLOADS)
+    if unknown:
+        ap.error(f"unknown workloads {sorted(unknown)}; choose from {WORKLOADS}")
+    if "shares" in W:
         by_share = []
         for r in (0.25, 0.75):
             res = gqa_step_bench(B=B, Hkv=Hkv, G=G, lens=lens, share=r, steps=args.steps,
@@ -788,6 +805,7 @@ def main():
             by_share.append(res)
             log(f"share {r}: {res['us_per_layer']} us/layer, partial {res['partial_gbs']} GB/s")
         extra["by_share"] = by_share
+    if "qwen3" in W:
         sweep = []
         for Lq in (8192, 32768, 65536, 131072):
             res = gqa_step_bench(B=4, Hkv=4, G=8, lens=[Lq] * 4, share=1.0,
@@ -799,17 +817,20 @@ def main():
             log(f"qwen3 B4 L={Lq}: {res['us_per_layer']} us/layer, partial "
                 f"{res['partial_us']} us = {res['partial_gbs']} GB/s")
         extra["kv_len_sweep"] = sweep
+    if "single" in W:
         one = gqa_step_bench(B=1, Hkv=4, G=8, lens=[4096], share=1.0, steps=args.steps,
                              warmup=args.warmup, seed=args.seed + 1, dev=dev,
                              with_host=False, label="qwen3_b1_L4096")
         one.pop("_data")
         extra["single_partition"] = one
+    if "mla" in W:
         mla = mla_step_bench(B=8, H=16, lens=[16384] * 8, share=0.5, steps=args.steps,
                              warmup=args.warmup, seed=args.seed + 3, dev=dev,
                              label="dsv2lite_mla_b8_L16384")
         extra["mla"] = mla
         log(f"mla: {mla['us_per_layer']} us/layer, partial {mla['partial_us']} us = "
             f"{mla['partial_gbs']} GB/s, {mla['partial_tflops']} TFLOP/s")
+    if "mla_sweep" in W:
         msweep = []
         for Lm in (8192, 32768, 65536, 131072):
             res = mla_step_bench(B=8, H=16, lens=[Lm] * 8, share=1.0,
@@ -820,9 +841,9 @@ def main():
                 f"= {res['partial_gbs']} GB/s")
         extra["mla_kv_len_sweep"] = msweep
 
-    if args.model_layers > 0 and not args.headline_only:
+    th = _host_threads()
+    if "host" in W:
         # native host partial rates (the other half of the partitioned step)
-        th = _host_threads()
         h_mix = lens - np.floor(args.share * lens).astype(np.int64)
         hp = [host_gqa_bench(Hkv=Hkv, G=G, host_tokens=h_mix, reps=5, seed=args.seed + 11,
                              dev=dev, threads=th, label=f"mixtral_b16_r{args.share}_host"),
@@ -835,6 +856,7 @@ def main():
             log(f"host partial {r['label']}: {r['us']} us = {r['gbs']} GB/s on {th} threads "
                 f"({r['frac_of_host_read']:.0%} of the {bw} GB/s host read bandwidth)")
         extra["host_partial"] = hp
+    if "model" in W and args.model_layers > 0:
         # DeepSeek-V2-Lite decode step: B 32, lognormal lengths, every share
         m_lens = lognormal_lens(32, args.seed + 5)
         log(f"mla model: B=32 layers={args.model_layers} lens median "
