@@ -1,0 +1,146 @@
+"""Boundary movement of the two-sided paged caches (scope_amd/paged.py), on
+the CPU: both "sides" live in host memory here, the GPU pages are written
+directly, and only the bookkeeping and page copies run.  After every move
+the concatenation host tokens ++ GPU tokens must equal the original token
+sequence bit for bit, every page must be accounted for, and both sides'
+lengths and tables must agree."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_randn, bits
+from scope_amd.paged import PagedKVCache, PagedMlaCache
+
+PS = 32
+
+
+def _fill_gpu(part, layer, b, payloads):
+    """Write token rows into the GPU partition's pages of (layer, b) as the
+    append kernels would (payload token axis: -2 for GQA pools, 0 for MLA)."""
+    n = payloads[0].shape[-2] if payloads[0].dim() == 3 else payloads[0].shape[0]
+    part.reserve(b, int(part.lens[layer, b]) + n)
+    start = int(part.lens[layer, b])
+    pools = [part.k, part.v] if hasattr(part, "k") else [part.latent]
+    for t in range(n):
+        pos = start + t
+        pid = int(part.host_table[b, pos // part.page_size])
+        off = pos % part.page_size
+        for pool, pl in zip(pools, payloads):
+            if pl.dim() == 3:  # [Hkv, n, D]
+                pool[layer, pid, :, off] = pl[:, t]
+            else:              # [n, 576]
+                pool[layer, pid, off] = pl[t]
+    part.lens[layer, b] += n
+    part._len_bufs[:, layer, b] = int(part.lens[layer, b])
+
+
+def _gather(cache, layer, b):
+    """Token rows of sequence b in `layer`: host pages then GPU pages."""
+    ps = cache.page_size
+    h = int(cache.host.lens[b])
+    g = cache.gpu
+    gl = int(g.lens[layer, b])
+    out = []
+    for data_h, data_g in zip(cache.host.data, cache._gpu_payload()):
+        rows = []
+        for t in range(h):
+            pid = int(cache.host.table[b, t // ps])
+            rows.append(data_h[layer, pid, ..., t % ps, :] if data_h.dim() == 5
+                        else data_h[layer, pid, t % ps])
+        for t in range(gl):
+            pid = int(g.host_table[b, t // ps])
+            rows.append(data_g[layer, pid, ..., t % ps, :] if data_g.dim() == 5
+                        else data_g[layer, pid, t % ps])
+        out.append(torch.stack(rows, dim=-2) if rows[0].dim() == 2 else torch.stack(rows))
+    return out
+
+
+def _check_accounting(cache):
+    g = cache.gpu
+    used_g = sum(int(x) for x in g._pages_held)
+    assert g.pool.free + used_g == g.num_pages
+    used_h = sum(int(x) for x in cache.host.held)
+    assert cache.host.pool.free + used_h == cache.host.num_pages
+    for b in range(cache.batch):
+        assert int(cache.host.held[b]) * cache.page_size == int(cache.host.lens[b])
+        assert int(g._pages_held[b]) >= -(-int(g.lens[0, b]) // cache.page_size)
+        held = int(g._pages_held[b])
+        assert np.array_equal(g.page_table[b, :held].numpy(), g.host_table[b, :held])
+        assert (g.host_table[b, held:] == -1).all()
+        assert (g._len_bufs[:, :, b] == int(g.lens[0, b])).all()
+        ids = list(g.host_table[b, :held])
+        assert len(set(ids)) == len(ids)
+
+
+def test_mla_boundary_moves_keep_every_token():
+    layers, B = 2, 3
+    lens = [5 * PS + 7, 3 * PS, 2 * PS + 1]
+    hosts = [2 * PS, 1 * PS, 0]
+    cache = PagedMlaCache(layers, B, max_tokens=8 * PS, page_size=PS, device="cpu", pin=False)
+    data = {}
+    for layer in range(layers):
+        for b, (L, h) in enumerate(zip(lens, hosts)):
+            c = bf16_randn((L, 512), 100 * layer + b)
+            pe = bf16_randn((L, 64), 100 * layer + b + 50)
+            data[layer, b] = torch.cat([c, pe], dim=1)
+            # host part through load(); the GPU part written directly
+            cache.host.lens[b] = h if layer == 0 else cache.host.lens[b]
+            if layer == 0:
+                cache._host_reserve(b, h)
+            for p in range(h // PS):
+                cache.host.data[0][layer, int(cache.host.table[b, p])] = \
+                    data[layer, b][p * PS:(p + 1) * PS]
+            _fill_gpu(cache.gpu, layer, b, [data[layer, b][h:]])
+    _check_accounting(cache)
+    moves = [(0, 4 * PS), (0, 0), (1, 3 * PS), (2, 2 * PS), (0, 5 * PS), (2, 0), (1, 0)]
+    for b, h_new in moves:
+        cache.set_boundary(b, h_new)
+        assert cache.host_tokens(b) == h_new
+        _check_accounting(cache)
+        for layer in range(layers):
+            for bb in range(B):
+                (got,) = _gather(cache, layer, bb)
+                assert np.array_equal(bits(got), bits(data[layer, bb])), (b, h_new, layer, bb)
+    with pytest.raises(ValueError):
+        cache.set_boundary(0, PS + 1)          # not a page multiple
+    with pytest.raises(ValueError):
+        cache.set_boundary(1, 4 * PS)          # beyond the sequence
+    cache.set_share(0.5)
+    for b, L in enumerate(lens):
+        h = L - int(np.floor(0.5 * L))
+        assert cache.host_tokens(b) == (h // PS) * PS
+    _check_accounting(cache)
+
+
+def test_gqa_boundary_moves_keep_every_token():
+    layers, B, Hkv, D = 2, 2, 2, 64
+    lens = [4 * PS + 3, 2 * PS]
+    cache = PagedKVCache(layers, B, Hkv, D, max_tokens=6 * PS, page_size=PS, device="cpu",
+                         pin=False)
+    data = {}
+    for layer in range(layers):
+        for b, L in enumerate(lens):
+            k = bf16_randn((Hkv, L, D), 10 * layer + b)
+            v = bf16_randn((Hkv, L, D), 10 * layer + b + 5)
+            data[layer, b] = (k, v)
+            _fill_gpu(cache.gpu, layer, b, [k, v])
+    _check_accounting(cache)
+    for b, h_new in [(0, 3 * PS), (1, 2 * PS), (0, PS), (1, 0), (0, 4 * PS), (0, 0)]:
+        cache.set_boundary(b, h_new)
+        _check_accounting(cache)
+        for layer in range(layers):
+            for bb in range(B):
+                gk, gv = _gather(cache, layer, bb)
+                k, v = data[layer, bb]
+                assert np.array_equal(bits(gk), bits(k)) and np.array_equal(bits(gv), bits(v))
+
+
+def test_gpu_capacity_is_checked_before_moving():
+    cache = PagedMlaCache(1, 1, max_tokens=2 * PS, page_size=PS, device="cpu", pin=False)
+    lat = bf16_randn((2 * PS, 576), 1)
+    _fill_gpu(cache.gpu, 0, 0, [lat])
+    cache.set_boundary(0, 2 * PS)      # everything to the host
+    assert int(cache.gpu.lens[0, 0]) == 0 and cache.gpu.pool.free == cache.gpu.num_pages
+    cache.set_boundary(0, 0)           # and back
+    (got,) = _gather(cache, 0, 0)
+    assert np.array_equal(bits(got), bits(lat))
