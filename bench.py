@@ -406,6 +406,42 @@ def host_mla_bench(*, host_tokens, reps, seed, dev, threads, label):
             "tflops": round(tok * 16 * (2 * 576 + 2 * 512) / t / 1e12, 3)}
 
 
+def migration_bench(*, B, layers, lens, seed, dev, label):
+    """Boundary movement of a two-sided paged MLA cache (scope_amd.paged):
+    share 0.5 -> 0.75 moves host pages to HBM, 0.75 -> 0.5 moves them back,
+    every layer; wall time of each set_share, in GB/s of pages moved."""
+    import torch
+
+    from scope_amd.paged import PagedMlaCache
+
+    lens = np.asarray(lens, np.int64)
+    pages = int(sum(-(-int(L) // PAGE) for L in lens)) + B
+    cache = PagedMlaCache(layers, B, max_tokens=int(lens.max()) + PAGE, page_size=PAGE,
+                          host_pages=pages, gpu_pages=pages, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    src = _randn_bf16((int(lens.max()), 576), gen, 0.5, dev).cpu()
+    c, pe = src[:, :512].contiguous(), src[:, 512:].contiguous()
+    for layer in range(layers):
+        for b, L in enumerate(lens):
+            L = int(L)
+            h = L - int(math.floor(0.5 * L))
+            cache.load(layer, b, c[:L], pe[:L], (h // PAGE) * PAGE)
+    torch.cuda.synchronize()
+    page_bytes = PAGE * 576 * 2 * layers
+    res = {"label": label, "batch": B, "layers": layers, "page_size": PAGE}
+    for name, r in (("host_to_hbm", 0.75), ("hbm_to_host", 0.5), ("host_to_hbm_2", 0.75),
+                    ("hbm_to_host_2", 0.5)):
+        before = int(cache.host.held.sum())
+        t0 = time.perf_counter()
+        cache.set_share(r)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        moved = abs(before - int(cache.host.held.sum()))
+        res[name] = {"pages": moved, "bytes": moved * page_bytes, "ms": round(dt * 1e3, 2),
+                     "gbs": round(moved * page_bytes / dt / 1e9, 2)}
+    return res
+
+
 def host_read_gbs(threads, nbytes=1 << 30, reps=5):
     """Host DRAM read bandwidth: a multi-threaded sum over an nbytes fp32
     array (torch's CPU reduction on `threads` threads), best of `reps`."""
@@ -675,7 +711,8 @@ def cpu_baseline(data, Hkv, G, budget_s, threads):
 #   mla_sweep  DeepSeek-V2-Lite B8 length sweep 8k..128k
 #   host       native host partial rates and the host read bandwidth
 #   model      27-layer DeepSeek-V2-Lite decode, B32 lognormal, every share (config 5)
-WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "host", "model")
+#   migrate    boundary movement of a paged two-sided MLA cache (4 layers, B32)
+WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "host", "model", "migrate")
 
 # The kernel the headline roofline is measured on (its rocprofv3 name).
 HEAD_KERNEL = "ws::gqa_decode_kernel<4, true, false>"
@@ -879,6 +916,13 @@ def main():
         log(f"share model: gpu {sm['gpu_fit']}, host {sm['host_fit']}, r_balance "
             f"{sm['r_balance']}, predicted/measured us per layer "
             f"{list(zip(sm['predicted_us'], sm['measured_us']))}")
+
+    if "migrate" in W:
+        mig = migration_bench(B=32, layers=4, lens=lognormal_lens(32, args.seed + 5),
+                              seed=args.seed + 17, dev=dev, label="dsv2lite_mla_b32_4layers")
+        extra["migration"] = mig
+        log(f"migration: {mig}")
+        torch.cuda.empty_cache()
 
     if args.copy_calibration:
         n = 256 << 20

@@ -101,80 +101,173 @@ class _PagedTwoSided:
         g = self.gpu
         g.page_table[b].copy_(torch.from_numpy(g.host_table[b].copy()))
 
-    # -- filling -------------------------------------------------------------
-
-    def _load_host(self, layer: int, b: int, tensors) -> None:
-        """Host tokens [0, n) of sequence b in `layer` from CPU payload rows
-        shaped like a page with the token axis holding n (page axis -2 for GQA
-        K/V [Hkv, n, D], axis 0 for MLA [n, 576])."""
-        raise NotImplementedError
-
     # -- boundary movement ---------------------------------------------------
 
     def set_boundary(self, b: int, h_new: int) -> None:
         """Move sequence b's boundary to h_new host tokens (a multiple of the
         page size, at most its length), copying pages between the sides in
         every layer."""
-        ps = self.page_size
-        L = self.seq_len(b)
-        h = int(self.host.lens[b])
-        if h_new % ps or not 0 <= h_new <= L:
-            raise ValueError(f"boundary {h_new} must be a multiple of {ps} in [0, {L}]")
-        if h_new == h:
-            return
-        g = self.gpu
-        k = abs(h_new - h) // ps
-        gpu_tok = L - h
-        dev = g.device
-        if h_new > h:  # GPU's leading k pages -> host
-            held_g = int(g._pages_held[b])
-            pids_g = g.host_table[b, :k].copy()
-            hp0 = int(self.host.held[b])
-            self._host_reserve(b, h_new)
-            pids_h = self.host.table[b, hp0:hp0 + k].copy()
-            ig = torch.from_numpy(pids_g.astype(np.int64)).to(dev)
-            ih = torch.from_numpy(pids_h.astype(np.int64))
-            for gp, hp in zip(self._gpu_payload(), self.host.data):
-                for layer in range(self.num_layers):
-                    hp[layer].index_copy_(0, ih, gp[layer].index_select(0, ig).cpu())
-            g.host_table[b, :held_g - k] = g.host_table[b, k:held_g]
-            g.host_table[b, held_g - k:held_g] = -1
-            g._pages_held[b] = held_g - k
-            for pid in pids_g:
-                g.pool.release(int(pid))
-            self._set_gpu_lens(b, gpu_tok - k * ps)
-        else:  # host's trailing k pages -> GPU
-            held_g = int(g._pages_held[b])
-            if held_g + k > g.max_pages:
-                raise ValueError(f"sequence {b}: GPU partition capacity exceeded")
-            hp1 = h // ps
-            pids_h = self.host.table[b, hp1 - k:hp1].copy()
-            pids_g = np.array([g.pool.alloc() for _ in range(k)], np.int32)
-            ig = torch.from_numpy(pids_g.astype(np.int64)).to(dev)
-            ih = torch.from_numpy(pids_h.astype(np.int64))
-            for gp, hp in zip(self._gpu_payload(), self.host.data):
-                for layer in range(self.num_layers):
-                    gp[layer].index_copy_(0, ig, hp[layer].index_select(0, ih).to(dev))
-            g.host_table[b, k:held_g + k] = g.host_table[b, :held_g].copy()
-            g.host_table[b, :k] = pids_g
-            g._pages_held[b] = held_g + k
-            for pid in pids_h:
-                self.host.pool.release(int(pid))
-            self.host.table[b, hp1 - k:hp1] = 0
-            self.host.held[b] = hp1 - k
-            self._set_gpu_lens(b, gpu_tok + k * ps)
-        self.host.lens[b] = h_new
-        self._write_gpu_row(b)
+        targets = [int(x) for x in self.host.lens]
+        targets[b] = h_new
+        self.set_boundaries(targets)
 
     def set_share(self, r: float) -> None:
         """GPU share r for every sequence: host tokens L - floor(r L), rounded
         down to a page multiple (the GPU takes the remainder)."""
         if not 0.0 <= r <= 1.0:
             raise ValueError(f"share {r} outside [0, 1]")
+        targets = []
         for b in range(self.batch):
             L = self.seq_len(b)
             h = L - int(np.floor(r * L))
-            self.set_boundary(b, (h // self.page_size) * self.page_size)
+            targets.append((h // self.page_size) * self.page_size)
+        self.set_boundaries(targets)
+
+    def set_boundaries(self, targets) -> None:
+        """Move every sequence's boundary to targets[b] host tokens in one
+        batch: one gather, one transfer and one scatter per direction and
+        payload, all layers at once, through pinned staging.  New pages are
+        taken before any page is given back, so no page is both read and
+        written within a batch.  Returns when the copies are done."""
+        ps = self.page_size
+        g = self.gpu
+        if len(targets) != self.batch:
+            raise ValueError(f"need {self.batch} targets")
+        plan = []
+        for b, h_new in enumerate(targets):
+            h_new = int(h_new)
+            L = self.seq_len(b)
+            if h_new % ps or not 0 <= h_new <= L:
+                raise ValueError(f"sequence {b}: boundary {h_new} must be a multiple of {ps} "
+                                 f"in [0, {L}]")
+            h = int(self.host.lens[b])
+            if h_new != h:
+                plan.append((b, h, h_new, L))
+        if not plan:
+            return
+        need_g = sum((h - hn) // ps for _, h, hn, _ in plan if hn < h)
+        need_h = sum((hn - h) // ps for _, h, hn, _ in plan if hn > h)
+        if need_g > g.pool.free or need_h > self.host.pool.free:
+            raise MemoryError(f"boundary move needs {need_g} GPU / {need_h} host free pages, "
+                              f"{g.pool.free} / {self.host.pool.free} available")
+        for b, h, hn, _ in plan:
+            if hn < h and int(g._pages_held[b]) + (h - hn) // ps > g.max_pages:
+                raise ValueError(f"sequence {b}: GPU partition capacity exceeded")
+        down_g, down_h, up_h, up_g = [], [], [], []  # page ids, in move order
+        release_g, release_h = [], []
+        for b, h, h_new, L in plan:
+            k = abs(h_new - h) // ps
+            gpu_tok = L - h
+            held_g = int(g._pages_held[b])
+            if h_new > h:  # GPU's leading k pages -> new host pages
+                pids_g = g.host_table[b, :k].copy()
+                hp0 = int(self.host.held[b])
+                self._host_reserve(b, h_new)
+                down_g.extend(int(x) for x in pids_g)
+                down_h.extend(int(x) for x in self.host.table[b, hp0:hp0 + k])
+                g.host_table[b, :held_g - k] = g.host_table[b, k:held_g].copy()
+                g.host_table[b, held_g - k:held_g] = -1
+                g._pages_held[b] = held_g - k
+                release_g.extend(int(x) for x in pids_g)
+                self._set_gpu_lens(b, gpu_tok - k * ps)
+            else:  # host's trailing k pages -> new GPU pages
+                hp1 = h // ps
+                pids_h = self.host.table[b, hp1 - k:hp1].copy()
+                pids_g = [g.pool.alloc() for _ in range(k)]
+                up_h.extend(int(x) for x in pids_h)
+                up_g.extend(pids_g)
+                g.host_table[b, k:held_g + k] = g.host_table[b, :held_g].copy()
+                g.host_table[b, :k] = pids_g
+                g._pages_held[b] = held_g + k
+                self.host.table[b, hp1 - k:hp1] = 0
+                self.host.held[b] = hp1 - k
+                release_h.extend(int(x) for x in pids_h)
+                self._set_gpu_lens(b, gpu_tok + k * ps)
+            self.host.lens[b] = h_new
+        for gp, hp in zip(self._gpu_payload(), self.host.data):  # all layers at once
+            if down_g:
+                self._pages_to_host(gp, hp, down_g, down_h)
+            if up_g:
+                self._pages_to_gpu(gp, hp, up_g, up_h)
+        for pid in release_g:
+            g.pool.release(pid)
+        for pid in release_h:
+            self.host.pool.release(pid)
+        for b, _, _, _ in plan:
+            self._write_gpu_row(b)
+
+    # -- page copies through pinned staging ------------------------------------
+
+    STAGE_BYTES = 32 << 20  # per staging buffer (two of them, allocated once)
+
+    def _stages(self):
+        """Two pinned staging buffers (page copies alternate between them so the
+        host-side gather or scatter of one chunk overlaps the other's PCIe
+        transfer)."""
+        if getattr(self, "_stage", None) is None:
+            pin = self.gpu.device.type == "cuda"
+            self._stage = [torch.empty(self.STAGE_BYTES, dtype=torch.uint8, pin_memory=pin)
+                           for _ in range(2)]
+            self._stage_ev = [None, None]
+        return self._stage
+
+    def _chunks(self, hp, n):
+        per_page = hp.shape[0] * hp[0, 0].numel() * hp.element_size()
+        step = max(1, self.STAGE_BYTES // per_page)
+        return [(i, min(n, i + step)) for i in range(0, n, step)]
+
+    def _stage_view(self, k, hp, n):
+        return self._stage[k][:hp.shape[0] * n * hp[0, 0].numel() * hp.element_size()].view(
+            hp.dtype).view(hp.shape[0], n, *hp.shape[2:])
+
+    def _wait_stage(self, k):
+        ev = self._stage_ev[k]
+        if ev is not None:
+            ev.synchronize()
+            self._stage_ev[k] = None
+
+    def _record_stage(self, k):
+        if self.gpu.device.type == "cuda":
+            ev = torch.cuda.Event()
+            ev.record()
+            self._stage_ev[k] = ev
+
+    def _pages_to_gpu(self, gp, hp, pids_g, pids_h):
+        """gp[:, pids_g] = hp[:, pids_h] for every layer."""
+        dev = self.gpu.device
+        self._stages()
+        ig = torch.tensor(pids_g, dtype=torch.int64, device=dev)
+        ih = torch.tensor(pids_h, dtype=torch.int64)
+        for c, (lo, hi) in enumerate(self._chunks(hp, len(pids_g))):
+            k = c & 1
+            self._wait_stage(k)  # its previous transfer has been read
+            view = self._stage_view(k, hp, hi - lo)
+            torch.index_select(hp, 1, ih[lo:hi], out=view)
+            gp.index_copy_(1, ig[lo:hi], view.to(dev, non_blocking=True))
+            self._record_stage(k)
+        for k in (0, 1):
+            self._wait_stage(k)
+
+    def _pages_to_host(self, gp, hp, pids_g, pids_h):
+        """hp[:, pids_h] = gp[:, pids_g] for every layer."""
+        dev = self.gpu.device
+        self._stages()
+        ig = torch.tensor(pids_g, dtype=torch.int64, device=dev)
+        ih = torch.tensor(pids_h, dtype=torch.int64)
+        pending = None  # (stage index, lo, hi) copied but not yet scattered
+        for c, (lo, hi) in enumerate(self._chunks(hp, len(pids_g))):
+            k = c & 1
+            view = self._stage_view(k, hp, hi - lo)
+            view.copy_(gp.index_select(1, ig[lo:hi]), non_blocking=True)
+            self._record_stage(k)
+            if pending is not None:
+                pk, plo, phi = pending
+                self._wait_stage(pk)
+                hp.index_copy_(1, ih[plo:phi], self._stage_view(pk, hp, phi - plo))
+            pending = (k, lo, hi)
+        pk, plo, phi = pending
+        self._wait_stage(pk)
+        hp.index_copy_(1, ih[plo:phi], self._stage_view(pk, hp, phi - plo))
 
     # -- decode-step plumbing -----------------------------------------------
 

@@ -77,6 +77,7 @@ def test_mla_boundary_moves_keep_every_token():
     lens = [5 * PS + 7, 3 * PS, 2 * PS + 1]
     hosts = [2 * PS, 1 * PS, 0]
     cache = PagedMlaCache(layers, B, max_tokens=8 * PS, page_size=PS, device="cpu", pin=False)
+    cache.STAGE_BYTES = 2 * layers * PS * 576 * 2   # two pages per chunk: multi-chunk copies
     data = {}
     for layer in range(layers):
         for b, (L, h) in enumerate(zip(lens, hosts)):
@@ -117,6 +118,7 @@ def test_gqa_boundary_moves_keep_every_token():
     lens = [4 * PS + 3, 2 * PS]
     cache = PagedKVCache(layers, B, Hkv, D, max_tokens=6 * PS, page_size=PS, device="cpu",
                          pin=False)
+    cache.STAGE_BYTES = layers * Hkv * PS * D * 2    # one page per chunk
     data = {}
     for layer in range(layers):
         for b, L in enumerate(lens):
@@ -144,3 +146,35 @@ def test_gpu_capacity_is_checked_before_moving():
     cache.set_boundary(0, 0)           # and back
     (got,) = _gather(cache, 0, 0)
     assert np.array_equal(bits(got), bits(lat))
+
+
+def test_mixed_direction_batch_and_pool_exhaustion():
+    layers, B = 2, 3
+    lens = [4 * PS, 3 * PS + 5, 2 * PS]
+    hosts = [0, 3 * PS, PS]
+    # pools sized exactly: a move must find its free pages before releasing
+    cache = PagedMlaCache(layers, B, max_tokens=5 * PS, page_size=PS, host_pages=7,
+                          gpu_pages=9, device="cpu", pin=False)
+    data = {}
+    for layer in range(layers):
+        for b, (L, h) in enumerate(zip(lens, hosts)):
+            data[layer, b] = bf16_randn((L, 576), 70 + 10 * layer + b)
+            if layer == 0:
+                cache._host_reserve(b, h)
+                cache.host.lens[b] = h
+            for p in range(h // PS):
+                cache.host.data[0][layer, int(cache.host.table[b, p])] = \
+                    data[layer, b][p * PS:(p + 1) * PS]
+            _fill_gpu(cache.gpu, layer, b, [data[layer, b][h:]])
+    _check_accounting(cache)
+    cache.set_boundaries([2 * PS, PS, 0])   # seq 0 down, seqs 1 and 2 up, in one batch
+    assert [cache.host_tokens(b) for b in range(B)] == [2 * PS, PS, 0]
+    _check_accounting(cache)
+    for layer in range(layers):
+        for b in range(B):
+            (got,) = _gather(cache, layer, b)
+            assert np.array_equal(bits(got), bits(data[layer, b]))
+    with pytest.raises(MemoryError):          # 4 + 3 + 2 pages > 7 host pages
+        cache.set_boundaries([4 * PS, 3 * PS, 2 * PS])
+    _check_accounting(cache)                  # a refused move changes nothing
+    assert [cache.host_tokens(b) for b in range(B)] == [2 * PS, PS, 0]
