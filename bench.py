@@ -442,6 +442,56 @@ def migration_bench(*, B, layers, lens, seed, dev, label):
     return res
 
 
+def epilogue_bench(*, B, L, steps, seed, dev, label):
+    """The MLA step's finish with and without the fused W_UV epilogue: (a)
+    ws_merge_split to the bf16 latent, then the reference's per-head bmm with
+    W_UV^T (system/deepseek.py:405) through torch; (b) ws_mla_merge_split_uv.
+    Both after the same split step; event time per finish."""
+    import torch
+
+    from scope_amd import ops
+
+    H, Dout = 16, 128
+    rng = np.random.default_rng(seed)
+    lens = np.full(B, L, np.int64)
+    table, num_pages = _page_table(lens, 2, rng)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    latent = _randn_bf16((num_pages, PAGE, 576), gen, 0.5, dev)
+    pt = torch.from_numpy(table).to(dev)
+    lens2 = torch.zeros((2, B), dtype=torch.int32, device=dev)
+    lens2[0] = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    qn = _randn_bf16((B * H, 512), gen, 0.5, dev)
+    qp = _randn_bf16((B * H, 64), gen, 0.5, dev)
+    kv = _randn_bf16((B, 1, 576), gen, 0.5, dev)
+    w_uv = _randn_bf16((H, Dout, 512), gen, 0.05, dev)
+    w_uv_t = w_uv.transpose(1, 2).contiguous()  # [H, 512, Dout]
+    step = ops.mla_append_decode_split(qn, qp, kv[..., :512], kv[..., 512:], latent, pt,
+                                       lens2[0], lens2[1], 192 ** -0.5, L + 1)
+
+    def unfused():
+        lat, _ = ops.merge_split(step, None, want_lse=False)
+        o_v = torch.bmm(lat.view(B, H, 512).transpose(0, 1).contiguous(), w_uv_t)
+        return o_v.transpose(0, 1).reshape(B, H * Dout)  # the layout o_proj takes
+
+    def fused():
+        return ops.merge_split_uv(step, w_uv)[0]
+
+    res = {"label": label, "batch": B, "tokens": L}
+    for name, fn in (("merge_then_bmm_us", unfused), ("fused_uv_us", fused)):
+        for _ in range(5):
+            fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = round(1e3 * e0.elapsed_time(e1) / steps, 2)
+    return res
+
+
 def host_read_gbs(threads, nbytes=1 << 30, reps=5):
     """Host DRAM read bandwidth: a multi-threaded sum over an nbytes fp32
     array (torch's CPU reduction on `threads` threads), best of `reps`."""
@@ -712,7 +762,9 @@ def cpu_baseline(data, Hkv, G, budget_s, threads):
 #   host       native host partial rates and the host read bandwidth
 #   model      27-layer DeepSeek-V2-Lite decode, B32 lognormal, every share (config 5)
 #   migrate    boundary movement of a paged two-sided MLA cache (4 layers, B32)
-WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "host", "model", "migrate")
+#   epilogue   MLA merge + W_UV: fused kernel against merge then bmm
+WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "host", "model", "migrate",
+             "epilogue")
 
 # The kernel the headline roofline is measured on (its rocprofv3 name).
 HEAD_KERNEL = "ws::gqa_decode_kernel<4, true, false>"
@@ -916,6 +968,16 @@ def main():
         log(f"share model: gpu {sm['gpu_fit']}, host {sm['host_fit']}, r_balance "
             f"{sm['r_balance']}, predicted/measured us per layer "
             f"{list(zip(sm['predicted_us'], sm['measured_us']))}")
+
+    if "epilogue" in W:
+        ep = [epilogue_bench(B=8, L=8192, steps=args.steps, seed=args.seed + 19, dev=dev,
+                             label="dsv2lite_mla_b8_L8192"),
+              epilogue_bench(B=32, L=4096, steps=args.steps, seed=args.seed + 20, dev=dev,
+                             label="dsv2lite_mla_b32_L4096")]
+        for r in ep:
+            log(f"epilogue {r['label']}: merge + bmm {r['merge_then_bmm_us']} us, fused "
+                f"{r['fused_uv_us']} us")
+        extra["epilogue"] = ep
 
     if "migrate" in W:
         mig = migration_bench(B=32, layers=4, lens=lognormal_lens(32, args.seed + 5),

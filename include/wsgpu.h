@@ -274,6 +274,26 @@ int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, int heads,
                    float* lse_out, void* stream);
 
 /*
+ * ws_merge_split for an absorbed-MLA step (rows_per_seq 1, Dv 512) fused with
+ * the W_UV epilogue: each merged row (b, h) is normalised, rounded to bf16
+ * and multiplied by W_UV[h]^T, giving out_v [B][heads * Dout] bf16, the
+ * attention output in the layout o_proj takes.
+ *   w_uv       [heads][Dout][512] bf16 (the value half of kv_b_proj's weight,
+ *              system/deepseek.py:256-260); Dout a multiple of 32, <= 512
+ *   out_latent [B * heads][512] bf16 merged latent, or NULL
+ *   lse_out    [B * heads] or NULL
+ * Other arguments as ws_merge_split (rows_per_seq 1, Dv 512).
+ * Replaces the merge + normalise + bf16 cast + W_UV bmm of the MLA decode
+ * branch (system/deepseek.py:397-407) in one launch.
+ */
+int ws_mla_merge_split_uv(const int32_t* gpu_len, int B, int heads, int page_capacity,
+                          int n_workgroups, const float* out_g, const float* lse_g,
+                          const void* workspace, size_t workspace_bytes,
+                          const void* b_out, const void* b_aux0, const void* b_aux1,
+                          int fmt_b, const uint16_t* w_uv, int Dout, uint16_t* out_latent,
+                          uint16_t* out_v, float* lse_out, void* stream);
+
+/*
  * LSE-combine per-split partials: part_out [n_splits][rows][Dv],
  * part_lse [n_splits][rows] -> out [rows][Dv], lse [rows].  Split s of a row
  * takes part in the merge iff s < n_valid[row / heads_per_len] where

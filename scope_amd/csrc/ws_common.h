@@ -40,6 +40,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return (uint32_t)ua | ((uint32_t)ub << 16);
 }
 
+// Round-to-nearest-even fp32 -> bf16 bits.
+__device__ __forceinline__ uint16_t f32_to_bf16(float a) {
+  return __builtin_bit_cast(uint16_t, (__bf16)a);
+}
+
 // Streaming 16-byte load: the KV pages are read once per call, so the
 // non-temporal hint keeps them from displacing reused lines in the caches
 // (and measurably raises the HBM read rate on gfx950).

@@ -201,6 +201,143 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Split combine + host merge + the W_UV epilogue of absorbed MLA
+// (system/deepseek.py:397-407): the merged latent row of (sequence b, head h)
+// is normalised, rounded to bf16 as the reference rounds it before its bmm,
+// and projected onto W_UV[h] ([Dout][512] bf16), giving out_v[b][h * Dout + v].
+//
+// One 256-thread workgroup per (b, h) row: threads 0..127 merge one float4
+// column each (the same pieces, weights and accumulation order as
+// merge_split_kernel, so the optional latent output is bit-identical to it)
+// into an LDS row; then eight lanes per W_UV row read it 128 contiguous bytes
+// at a time and reduce by shuffles, 32 rows per pass.  W_UV[h] is shared by
+// the B rows of head h through L2.
+constexpr int kUvThreads = 256;
+
+template <int FMT>
+__global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
+    const MergeSplitParams p, const uint16_t* __restrict__ w_uv, int Dout,
+    uint16_t* __restrict__ out_v) {
+  __shared__ int s_pref[kMaxSeqs + 1];
+  __shared__ int s_scan[kUvThreads / 64 + 1];
+  __shared__ float s_w[kReduceMaxWeights];
+  __shared__ float s_row[512];
+  __shared__ float s_ml[2];  // M, 1 / L
+  const int qrow = blockIdx.x;  // b * heads + h
+  const int t = threadIdx.x;
+  const int b = qrow / p.heads;
+  const int h = qrow - b * p.heads;
+  const Plan plan =
+      plan_build<kUvThreads>(p.gpu_len, 0, p.cap, p.B, 1, p.grid, s_pref, s_scan);
+  const int nbb = (plan_len(p.gpu_len, b, 0, p.cap) + 31) >> 5;
+  int n = 1;
+  const float* src = p.out_g + (size_t)qrow * p.Dv;
+  const float* lsrc = p.lse_g + qrow;
+  size_t sstride = 0, lstride = 0;
+  if (nbb > 0 && plan.n > 0) {
+    const int row_start = s_pref[b];
+    const int w_first = plan_owner(plan, row_start);
+    const int nseg = plan_owner(plan, row_start + nbb - 1) - w_first + 1;
+    if (nseg > 1) {
+      n = nseg;
+      const size_t slot0 = (size_t)(w_first + b) * p.heads + h;
+      src = p.part_out + slot0 * p.Dv;
+      lsrc = p.part_lse + slot0;
+      sstride = (size_t)p.heads * p.Dv;
+      lstride = p.heads;
+    }
+  }
+  const int c = t;  // float4 column (threads < 128)
+  const bool merging = c < (p.Dv >> 2);
+  float lb = neg_inf();
+  float4 ob = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (FMT >= 0 && merging)
+    load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, c, lb, ob);
+  if (t < 64) {  // wave 0: the pieces' weights
+    float mx = lb;
+    for (int s = t; s < n; s += 64) {
+      const float v = lsrc[(size_t)s * lstride];
+      s_w[s] = v;
+      mx = fmaxf(mx, v);
+    }
+    for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float sum = 0.f;
+    for (int s = t; s < n; s += 64) {
+      const float w = mx == neg_inf() ? 0.f : __expf(s_w[s] - mx);
+      s_w[s] = w;
+      sum += w;
+    }
+    for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
+    const float wb = (FMT >= 0 && mx != neg_inf()) ? __expf(lb - mx) : 0.f;
+    const float L = sum + wb;
+    if (t == 0) {
+      s_ml[0] = mx;
+      s_ml[1] = L > 0.f ? 1.f / L : 0.f;
+      if (p.lse_out) p.lse_out[qrow] = L > 0.f ? mx + __logf(L) : neg_inf();
+    }
+  }
+  __syncthreads();
+  if (merging) {
+    const float mx = s_ml[0];
+    const float inv = s_ml[1];
+    const float wb = (FMT >= 0 && mx != neg_inf()) ? __expf(lb - mx) : 0.f;
+    const float4* src4 = (const float4*)src + c;
+    const size_t sstride4 = sstride / 4;
+    float4 a = wb > 0.f ? make_float4(wb * ob.x, wb * ob.y, wb * ob.z, wb * ob.w)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    int s = 0;
+    for (; s + 8 <= n; s += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = src4[(size_t)(s + u) * sstride4];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float w = s_w[s + u];
+        a.x += w * v[u].x; a.y += w * v[u].y; a.z += w * v[u].z; a.w += w * v[u].w;
+      }
+    }
+    for (; s < n; ++s) {
+      const float w = s_w[s];
+      const float4 v = src4[(size_t)s * sstride4];
+      a.x += w * v.x; a.y += w * v.y; a.z += w * v.z; a.w += w * v.w;
+    }
+    const float4 o = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+    uint2 packed;
+    packed.x = pack_bf16x2(o.x, o.y);
+    packed.y = pack_bf16x2(o.z, o.w);
+    if (p.out_bf16) ((uint2*)(p.out_bf16 + (size_t)qrow * p.Dv))[c] = packed;
+    s_row[4 * c + 0] = bf16_to_f32(packed.x & 0xffffu);
+    s_row[4 * c + 1] = bf16_to_f32(packed.x >> 16);
+    s_row[4 * c + 2] = bf16_to_f32(packed.y & 0xffffu);
+    s_row[4 * c + 3] = bf16_to_f32(packed.y >> 16);
+  }
+  __syncthreads();
+  // out_v[b][h * Dout + v] = sum_k s_row[k] * W_UV[h][v][k]
+  const int lane8 = t & 7;
+  const int rsub = t >> 3;  // 32 rows per pass
+  for (int v0 = 0; v0 < Dout; v0 += kUvThreads / 8) {
+    const int v = v0 + rsub;
+    const u32x4* wrow = (const u32x4*)(w_uv + ((size_t)h * Dout + v) * 512);
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k8 = j * 8 + lane8;  // 8-element chunk of the 512
+      const u32x4 wv = wrow[k8];
+      const float* r = s_row + 8 * k8;
+      acc += bf16_to_f32(wv.x & 0xffffu) * r[0] + bf16_to_f32(wv.x >> 16) * r[1];
+      acc += bf16_to_f32(wv.y & 0xffffu) * r[2] + bf16_to_f32(wv.y >> 16) * r[3];
+      acc += bf16_to_f32(wv.z & 0xffffu) * r[4] + bf16_to_f32(wv.z >> 16) * r[5];
+      acc += bf16_to_f32(wv.w & 0xffffu) * r[6] + bf16_to_f32(wv.w >> 16) * r[7];
+    }
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 4);
+    if (lane8 == 0)
+      out_v[(size_t)b * p.heads * Dout + (size_t)h * Dout + v] = f32_to_bf16(acc);
+  }
+}
+
 }  // namespace ws
 
 using namespace ws;
@@ -314,4 +451,82 @@ extern "C" int ws_lse_merge(const float* out_g, const float* lse_g,
       return set_error(WS_EINVAL, "ws_lse_merge: unknown format %d", fmt_b);
   }
   return check_launch("ws_lse_merge");
+}
+
+extern "C" int ws_mla_merge_split_uv(const int32_t* gpu_len, int B, int heads,
+                                     int page_capacity, int n_workgroups, const float* out_g,
+                                     const float* lse_g, const void* workspace,
+                                     size_t workspace_bytes, const void* b_out,
+                                     const void* b_aux0, const void* b_aux1, int fmt_b,
+                                     const uint16_t* w_uv, int Dout, uint16_t* out_latent,
+                                     uint16_t* out_v, float* lse_out, void* stream) {
+  constexpr int Dv = 512;
+  if (!gpu_len || !out_g || !lse_g || !workspace || !w_uv || !out_v)
+    return set_error(WS_EINVAL, "ws_mla_merge_split_uv: null pointer");
+  if (B < 0 || B > kMaxSeqs || heads <= 0 || heads > 16 || page_capacity <= 0 ||
+      n_workgroups <= 0 || Dout <= 0 || Dout % 32 || Dout > 512)
+    return set_error(WS_EINVAL, "ws_mla_merge_split_uv: bad sizes B=%d heads=%d Dout=%d", B,
+                     heads, Dout);
+  if (b_out && (!b_aux0 || (fmt_b != WS_PARTIAL_LSE_F32 && !b_aux1)))
+    return set_error(WS_EINVAL, "ws_mla_merge_split_uv: host partial without its lse / max / sum");
+  if (b_out && fmt_b != WS_PARTIAL_LSE_F32 && fmt_b != WS_TRIPLE_UNNORM_F32 &&
+      fmt_b != WS_TRIPLE_NORM_BF16 && fmt_b != WS_TRIPLE_NORM_F32)
+    return set_error(WS_EINVAL, "ws_mla_merge_split_uv: unknown format %d", fmt_b);
+  if (n_workgroups > kReduceMaxWeights)
+    return set_error(WS_EINVAL, "ws_mla_merge_split_uv: %d workgroups exceed %d", n_workgroups,
+                     kReduceMaxWeights);
+  if (((uintptr_t)workspace & 255u) || ((uintptr_t)out_g | (uintptr_t)b_out |
+                                         (uintptr_t)w_uv) & 15u ||
+      ((uintptr_t)out_latent & 7u) || ((uintptr_t)out_v & 1u))
+    return set_error(WS_EINVAL, "ws_mla_merge_split_uv: misaligned buffer");
+  const size_t need = ws::workspace_bytes(B, heads, Dv, n_workgroups);
+  if (workspace_bytes < need)
+    return set_error(WS_EWORKSPACE, "ws_mla_merge_split_uv: workspace %zu < %zu bytes",
+                     workspace_bytes, need);
+  if (B == 0) return WS_OK;
+  const SplitWorkspace w = carve_workspace((void*)workspace, B, heads, n_workgroups);
+  MergeSplitParams prm;
+  prm.gpu_len = gpu_len;
+  prm.B = B;
+  prm.R = 1;
+  prm.heads = heads;
+  prm.Dv = Dv;
+  prm.cap = page_capacity;
+  prm.grid = n_workgroups;
+  prm.out_g = out_g;
+  prm.lse_g = lse_g;
+  prm.part_out = w.part_out;
+  prm.part_lse = w.part_lse;
+  prm.b_out = b_out;
+  prm.b_aux0 = b_aux0;
+  prm.b_aux1 = b_aux1;
+  prm.out_bf16 = out_latent;
+  prm.out_f32 = nullptr;
+  prm.lse_out = lse_out;
+  const dim3 grid((unsigned)(B * heads));
+  const dim3 block(kUvThreads);
+  hipStream_t s = (hipStream_t)stream;
+  if (!b_out) {
+    hipLaunchKernelGGL(merge_split_uv_kernel<-1>, grid, block, 0, s, prm, w_uv, Dout, out_v);
+  } else {
+    switch (fmt_b) {
+      case WS_PARTIAL_LSE_F32:
+        hipLaunchKernelGGL(merge_split_uv_kernel<WS_PARTIAL_LSE_F32>, grid, block, 0, s, prm,
+                           w_uv, Dout, out_v);
+        break;
+      case WS_TRIPLE_UNNORM_F32:
+        hipLaunchKernelGGL(merge_split_uv_kernel<WS_TRIPLE_UNNORM_F32>, grid, block, 0, s, prm,
+                           w_uv, Dout, out_v);
+        break;
+      case WS_TRIPLE_NORM_BF16:
+        hipLaunchKernelGGL(merge_split_uv_kernel<WS_TRIPLE_NORM_BF16>, grid, block, 0, s, prm,
+                           w_uv, Dout, out_v);
+        break;
+      default:
+        hipLaunchKernelGGL(merge_split_uv_kernel<WS_TRIPLE_NORM_F32>, grid, block, 0, s, prm,
+                           w_uv, Dout, out_v);
+        break;
+    }
+  }
+  return check_launch("ws_mla_merge_split_uv");
 }

@@ -36,6 +36,7 @@ EXPORTS = (
     "ws_gqa_append_decode_split",
     "ws_mla_append_decode_split",
     "ws_merge_split",
+    "ws_mla_merge_split_uv",
     "ws_split_reduce",
     "ws_lse_merge",
 )
@@ -108,6 +109,9 @@ def lib() -> ctypes.CDLL:
         L.ws_merge_split.restype = i32
         L.ws_merge_split.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, sz,
                                      vp, vp, vp, i32, vp, vp, vp, vp]
+        L.ws_mla_merge_split_uv.restype = i32
+        L.ws_mla_merge_split_uv.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp, sz, vp, vp, vp,
+                                            i32, vp, i32, vp, vp, vp, vp]
         L.ws_split_reduce.restype = i32
         L.ws_split_reduce.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp,
                                       vp, vp]
@@ -529,6 +533,55 @@ def merge_split(step: SplitStep, b=None, fmt=PARTIAL_LSE_F32, out_dtype=torch.bf
         _ptr(b_out), _ptr(b_aux0), _ptr(b_aux1), int(fmt), _ptr(o16), _ptr(o32),
         _ptr(lse_out if want_lse else None), _stream(dev)), "ws_merge_split")
     return out, (lse_out if want_lse else None)
+
+
+def _host_operand(b, fmt, rows, Dv, dev):
+    b_out = b_aux0 = b_aux1 = None
+    if b is not None:
+        if fmt == PARTIAL_LSE_F32:
+            b_out, b_aux0 = b
+            _require(b_out, "b.out", torch.float32, dev)
+            _require(b_aux0, "b.lse", torch.float32, dev)
+        else:
+            b_out, b_aux0, b_aux1 = b
+            dt = torch.bfloat16 if fmt == TRIPLE_NORM_BF16 else torch.float32
+            _require(b_out, "b.out", dt, dev)
+            _require(b_aux0, "b.max", dt, dev)
+            _require(b_aux1, "b.sum", dt, dev)
+            if b_aux1.numel() != rows:
+                raise ValueError("b.sum must have one value per row")
+        if b_out.numel() != rows * Dv or b_aux0.numel() != rows:
+            raise ValueError("host partial does not match the step's rows")
+    return b_out, b_aux0, b_aux1
+
+
+def merge_split_uv(step: SplitStep, w_uv: torch.Tensor, b=None, fmt=PARTIAL_LSE_F32,
+                   want_latent=False, want_lse=False):
+    """Finish an absorbed-MLA split step with the W_UV epilogue
+    (ws_mla_merge_split_uv): w_uv [heads, Dout, 512] bf16.  Returns
+    (out_v [B, heads * Dout] bf16, latent [B * heads, 512] bf16 or None,
+    lse [B * heads] or None)."""
+    dev = step.out_g.device
+    if step.rows_per_seq != 1 or step.Dv != MLA_C:
+        raise ValueError("merge_split_uv finishes an MLA step")
+    H = step.heads
+    _require(w_uv, "w_uv", torch.bfloat16, dev, 3)
+    if w_uv.shape[0] != H or w_uv.shape[2] != MLA_C:
+        raise ValueError(f"w_uv must be [{H}, Dout, {MLA_C}]")
+    Dout = w_uv.shape[1]
+    rows = step.B * H
+    b_out, b_aux0, b_aux1 = _host_operand(b, fmt, rows, MLA_C, dev)
+    out_v = torch.empty((step.B, H * Dout), dtype=torch.bfloat16, device=dev)
+    latent = (torch.empty((rows, MLA_C), dtype=torch.bfloat16, device=dev)
+              if want_latent else None)
+    lse = torch.empty((rows,), dtype=torch.float32, device=dev) if want_lse else None
+    ws = step.workspace
+    _check(lib().ws_mla_merge_split_uv(
+        _ptr(step.gpu_len), step.B, H, step.cap, step.nwg, _ptr(step.out_g), _ptr(step.lse_g),
+        _ptr(ws), ws.numel() * ws.element_size(), _ptr(b_out), _ptr(b_aux0), _ptr(b_aux1),
+        int(fmt), _ptr(w_uv), Dout, _ptr(latent), _ptr(out_v), _ptr(lse), _stream(dev)),
+        "ws_mla_merge_split_uv")
+    return out_v, latent, lse
 
 
 def split_reduce(part_out, part_lse, gpu_len, heads_per_len, tokens_per_split,

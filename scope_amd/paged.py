@@ -282,11 +282,10 @@ class _PagedTwoSided:
         ev.record()
         return out, ev
 
-    def _merge(self, step, part, dev):
-        if part is None:
-            out, _ = ops.merge_split(step, None, want_lse=False)
-            return out
-        b = tuple(x.to(dev, non_blocking=True) for x in part)
+    def _merge(self, step, part, dev, w_uv=None):
+        b = None if part is None else tuple(x.to(dev, non_blocking=True) for x in part)
+        if w_uv is not None:
+            return ops.merge_split_uv(step, w_uv, b, ops.PARTIAL_LSE_F32)[0]
         out, _ = ops.merge_split(step, b, ops.PARTIAL_LSE_F32, want_lse=False)
         return out
 
@@ -331,10 +330,13 @@ class PagedMlaCache(_PagedTwoSided):
 
     def step(self, layer: int, q_nope: torch.Tensor, q_pe: torch.Tensor,
              c_new: torch.Tensor, pe_new: torch.Tensor, scale: float, host_threads: int = 0,
-             n_workgroups: int = 0) -> torch.Tensor:
+             n_workgroups: int = 0, w_uv: torch.Tensor | None = None) -> torch.Tensor:
         """One decode step of `layer`: append c_new [B, 1, 512] / pe_new
         [B, 1, 64] to the GPU side and attend over both sides.  q_nope
-        [B*16, 512], q_pe [B*16, 64] on the GPU.  Returns [B*16, 512] bf16."""
+        [B*16, 512] (W_UK-absorbed), q_pe [B*16, 64] on the GPU.  Returns the
+        merged latent [B*16, 512] bf16, or with w_uv [16, Dout, 512] the
+        projected attention output [B, 16 * Dout] bf16 (the merge and the
+        W_UV epilogue in one launch), ready for o_proj."""
         g = self.gpu
         dev = q_nope.device
         with_host = bool(self.host.lens.any())
@@ -356,7 +358,7 @@ class PagedMlaCache(_PagedTwoSided):
                 scale, host_threads,
                 torch.empty((rows, ops.MLA_C), dtype=torch.float32, pin_memory=True),
                 torch.empty((rows,), dtype=torch.float32, pin_memory=True))
-        return self._merge(step, part, dev)
+        return self._merge(step, part, dev, w_uv)
 
 
 class PagedKVCache(_PagedTwoSided):
@@ -428,3 +430,15 @@ class PagedKVCache(_PagedTwoSided):
                 torch.empty((B, Hq, D), dtype=torch.float32, pin_memory=True),
                 torch.empty((B, Hq), dtype=torch.float32, pin_memory=True))
         return self._merge(step, part, dev).view(q.shape)
+
+
+def absorb_q(q_nope: torch.Tensor, w_uk: torch.Tensor) -> torch.Tensor:
+    """The q-side W_UK absorption of the MLA decode (system/deepseek.py:256-263):
+    q_nope [B, H, 128] times W_UK[h] [128, 512] per head -> [B*H, 512] bf16,
+    the q_nope the MLA step takes.  A plain batched GEMM (torch, per head with
+    contiguous operands), not a hand-written kernel."""
+    B, H, D = q_nope.shape
+    if w_uk.shape[:2] != (H, D):
+        raise ValueError(f"w_uk must be [{H}, {D}, latent]")
+    q = torch.bmm(q_nope.transpose(0, 1).contiguous(), w_uk.contiguous())  # [H, B, latent]
+    return q.transpose(0, 1).reshape(B * H, w_uk.shape[2]).contiguous()

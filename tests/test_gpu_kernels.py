@@ -542,3 +542,55 @@ def test_mla_split_step_and_merge(wg):
         want, wl = O.merge_fp64(g_o, g_l, host_o[r], host_l[r])
         assert_close(got[r], want, OUT_ATOL, OUT_RTOL, f"mla split merged b={b}")
         assert_close(gl_[r], wl, LSE_ATOL, LSE_RTOL, f"mla split merged lse b={b}")
+
+
+@pytest.mark.parametrize("wg", [0, 5, 40])
+@pytest.mark.parametrize("fmt", [None, ops.PARTIAL_LSE_F32, ops.TRIPLE_UNNORM_F32,
+                                 ops.TRIPLE_NORM_BF16])
+def test_mla_merge_split_uv_epilogue(wg, fmt):
+    """Merge + W_UV in one launch: its latent equals ws_merge_split's bit for
+    bit; out_v equals that latent times W_UV^T (fp64) within bf16 rounding,
+    and the fp64 merged attention times W_UV^T within the parity bar."""
+    _say(f"mla merge_split_uv wg={wg} fmt={fmt}")
+    H, PS, Dout = 16, 64, 128
+    lens = [0, 37, 700, 1500]
+    B = len(lens)
+    total = [L + 1 for L in lens]
+    lat, pt, gl, cs, pes = mla_pool(total, PS, seed=81)
+    lens2 = torch.zeros((2, B), dtype=torch.int32, device=DEV)
+    lens2[0] = torch.tensor(lens, dtype=torch.int32)
+    qn = bf16_randn((B * H, 512), 82, 0.5)
+    qp = bf16_randn((B * H, 64), 83, 0.5)
+    kv = torch.stack([torch.cat([c[L:L + 1], pe[L:L + 1]], 1)
+                      for c, pe, L in zip(cs, pes, lens)]).to(DEV)
+    w_uv = bf16_randn((H, Dout, 512), 84, 0.05)
+    scale = 192 ** -0.5
+    step = ops.mla_append_decode_split(qn.to(DEV), qp.to(DEV), kv[..., :512], kv[..., 512:],
+                                       lat, pt, lens2[0], lens2[1], scale, max(lens) + 1, wg)
+    rows = B * H
+    if fmt is None:
+        hb, host_o, host_l = None, np.zeros((rows, 512)), np.full(rows, -np.inf)
+        f = ops.PARTIAL_LSE_F32
+    else:
+        hb, host_o, host_l = _host_partial(fmt, rows, 512, 85)
+        f = fmt
+    ref_lat, ref_lse = ops.merge_split(step, hb, f)
+    out_v, latent, lse = ops.merge_split_uv(step, w_uv.to(DEV), hb, f, want_latent=True,
+                                            want_lse=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(latent), bits(ref_lat)), "latent differs from ws_merge_split"
+    assert np.array_equal(lse.cpu().numpy(), ref_lse.cpu().numpy())
+    wv = bits(w_uv).view(np.uint16)
+    w64 = O.as_f64(wv)                                         # [H, Dout, 512]
+    lat64 = O.as_f64(bits(ref_lat)).reshape(B, H, 512)
+    want_from_latent = np.einsum("bhk,hvk->bhv", lat64, w64).reshape(B, H * Dout)
+    got = out_v.float().cpu().numpy()
+    # fp32 accumulation of 512 products, then one bf16 rounding
+    assert_close(got, want_from_latent, 2e-3, 8e-3, "out_v vs latent @ W_UV^T")
+    for b in range(B):
+        r = slice(b * H, (b + 1) * H)
+        g_o, g_l = O.mla_attention_fp64(bits(qn[r]), bits(qp[r]), bits(cs[b])[None],
+                                        bits(pes[b])[None], scale)
+        m_o, _ = O.merge_fp64(g_o, g_l, host_o[r], host_l[r])
+        want = np.einsum("hk,hvk->hv", m_o, w64).reshape(H * Dout)
+        assert_close(got[b], want, OUT_ATOL, OUT_RTOL, f"out_v b={b} vs fp64 attention")

@@ -86,3 +86,39 @@ def test_paged_gqa_steps_across_boundary_moves():
             want, _ = O.gqa_attention_fp64(qb[b], bits(ks[b][:, :pos[b] + 1]),
                                            bits(vs[b][:, :pos[b] + 1]), scale)
             assert_close(got[b].reshape(Hkv, G, D), want, OUT_ATOL, OUT_RTOL, f"step {s} b={b}")
+
+
+def test_paged_mla_step_with_uv_epilogue_and_absorbed_query():
+    """The full MLA attention block of a decode step: W_UK absorption of the
+    raw query, the two-sided step, merge + W_UV in one launch; against fp64
+    attention over the whole sequence with the same weights."""
+    from scope_amd.paged import absorb_q
+    B, H, Dout = 2, 16, 128
+    lens, hosts = [300, 90], [128, 64]
+    scale = 192 ** -0.5
+    cache = PagedMlaCache(1, B, max_tokens=max(lens) + PS + 1, page_size=PS, device=DEV)
+    lat = [torch.cat([bf16_randn((L + 1, 512), 40 + b, 0.5), bf16_randn((L + 1, 64), 45 + b, 0.5)],
+                     dim=1) for b, L in enumerate(lens)]
+    for b, (L, h) in enumerate(zip(lens, hosts)):
+        cache.load(0, b, lat[b][:L, :512].contiguous(), lat[b][:L, 512:].contiguous(), h)
+    w_uk = bf16_randn((H, 128, 512), 50, 0.05)
+    w_uv = bf16_randn((H, Dout, 512), 51, 0.05)
+    q_raw = bf16_randn((B, H, 128), 52, 1.0)
+    qn = absorb_q(q_raw.to(DEV), w_uk.to(DEV))
+    qp = bf16_randn((B * H, 64), 53, 0.5).to(DEV)
+    new = torch.stack([lat[b][lens[b]] for b in range(B)]).view(B, 1, 576).to(DEV)
+    out_v = cache.step(0, qn, qp, new[..., :512].contiguous(), new[..., 512:].contiguous(),
+                       scale, host_threads=2, w_uv=w_uv.to(DEV))
+    torch.cuda.synchronize()
+    assert out_v.shape == (B, H * Dout) and out_v.dtype == torch.bfloat16
+    got = out_v.float().cpu().numpy()
+    qn_bits = bits(qn)   # the absorbed query as the step saw it (bf16)
+    want_qn = np.einsum("bhd,hdk->bhk", O.as_f64(bits(q_raw)), O.as_f64(bits(w_uk)))
+    assert_close(O.as_f64(qn_bits).reshape(B, H, 512), want_qn, 2e-2, 2e-2, "absorbed q")
+    for b in range(B):
+        full = bits(lat[b][:lens[b] + 1])
+        hh = slice(b * H, (b + 1) * H)
+        m_o, _ = O.mla_attention_fp64(qn_bits[hh], bits(qp.cpu())[hh], full[None, :, :512],
+                                      full[None, :, 512:], scale)
+        want = np.einsum("hk,hvk->hv", m_o, O.as_f64(bits(w_uv))).reshape(H * Dout)
+        assert_close(got[b], want, OUT_ATOL, OUT_RTOL, f"out_v b={b}")
