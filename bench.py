@@ -686,6 +686,10 @@ def _host_info():
         txt = open("/proc/cpuinfo").read()
         m = re.search(r"model name\s*:\s*(.*)", txt)
         info["cpu_model"] = m.group(1).strip() if m else "?"
+        fam = re.search(r"cpu family\s*:\s*(\d+)", txt)
+        mod = re.search(r"model\s*:\s*(\d+)", txt)
+        if fam and mod:  # e.g. family 25 = Zen 3/4, 26 = Zen 5 on AMD
+            info["cpu_family_model"] = f"{fam.group(1)}/{mod.group(1)}"
         flags = set(re.search(r"flags\s*:\s*(.*)", txt).group(1).split())
         info["isa"] = [f for f in ("avx2", "avx512f", "avx512bw", "avx512_bf16",
                                    "amx_bf16") if f in flags]
@@ -939,7 +943,9 @@ def main():
               host_mla_bench(host_tokens=[8192] * 8, reps=5, seed=args.seed + 12, dev=dev,
                              threads=th, label="dsv2lite_mla_b8_L16384_r0.5_host")]
         bw = host_read_gbs(th)
+        hinfo = _host_info()
         for r in hp:
+            r.update(hinfo)
             r["host_read_gbs"] = bw
             r["frac_of_host_read"] = round(r["gbs"] / bw, 3)
             log(f"host partial {r['label']}: {r['us']} us = {r['gbs']} GB/s on {th} threads "

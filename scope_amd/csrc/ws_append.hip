@@ -1,12 +1,22 @@
 // Append kernels: copy each sequence's new token(s) into its HBM page slot.
 //
-// One workgroup per sequence.  Every thread moves 16-byte vectors, so a decode
-// step's append of a Mixtral layer (8 KV heads x 128 x bf16, K and V) is one
-// 256-thread pass.  The workgroup is the only reader of gpu_len[b], so it can
-// bump the length after a barrier without racing other workgroups.
+// Grid (sequence, chunk of kChunkVecs 16-byte vectors).  A decode step's
+// append (one token) is one chunk per sequence: that workgroup is the only
+// reader of gpu_len[b], so it bumps the length after a barrier.  A longer
+// append (prefill into the partition) spreads over many chunks, which all
+// read the old length, and len_add_kernel bumps it afterwards on the same
+// stream.
 #include "ws_common.h"
 
 namespace ws {
+
+constexpr int kChunkVecs = 256 * 8;  // 32 KB of each tensor per workgroup
+
+__global__ __launch_bounds__(256) void len_add_kernel(int32_t* __restrict__ gpu_len, int B,
+                                                      int n_new) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B) gpu_len[b] += n_new;
+}
 
 __global__ __launch_bounds__(256) void kv_append_kernel(
     const u32x4* __restrict__ k_new, const u32x4* __restrict__ v_new,
@@ -18,7 +28,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
   const int len = gpu_len[b];
   const int per_token = Hkv * dvec;     // vectors of one token of one tensor
   const int total = n_new * per_token;  // vectors of one tensor
-  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+  const int end = min(total, (int)(blockIdx.y + 1) * kChunkVecs);
+  for (int idx = blockIdx.y * kChunkVecs + threadIdx.x; idx < end; idx += blockDim.x) {
     // source order [Hkv][n_new][dvec]
     const int dv = idx % dvec;
     const int rest = idx / dvec;
@@ -55,7 +66,8 @@ __global__ __launch_bounds__(256) void latent_append_kernel(
   constexpr int vec_row = kLatent / 8;    // 72 vectors per token
   constexpr int vec_c = kLatentC / 8;     // 64 of them from c_kv
   const int total = n_new * vec_row;
-  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+  const int end = min(total, (int)(blockIdx.y + 1) * kChunkVecs);
+  for (int idx = blockIdx.y * kChunkVecs + threadIdx.x; idx < end; idx += blockDim.x) {
     const int v = idx % vec_row;
     const int i = idx / vec_row;
     const int pos = len + i;
@@ -76,6 +88,13 @@ __global__ __launch_bounds__(256) void latent_append_kernel(
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Chunks per sequence of an append moving `vecs` vectors per sequence; 0 if
+// the grid would be too tall.
+static int append_chunks(long long vecs) {
+  const long long c = (vecs + kChunkVecs - 1) / kChunkVecs;
+  return c > 65535 ? 0 : (int)c;
+}
 
 }  // namespace ws
 
@@ -99,11 +118,16 @@ extern "C" int ws_kv_append(const uint16_t* k_new, const uint16_t* v_new,
       !aligned16(v_pages))
     return set_error(WS_EINVAL, "ws_kv_append: bf16 buffers must be 16-byte aligned");
   if (B == 0 || n_new == 0) return WS_OK;
-  hipLaunchKernelGGL(kv_append_kernel, dim3(B), dim3(256), 0,
-                     (hipStream_t)stream, (const u32x4*)k_new,
-                     (const u32x4*)v_new, (u32x4*)k_pages, (u32x4*)v_pages,
-                     page_table, gpu_len, Hkv, D / 8, n_new, page_size,
-                     max_pages, num_pages, update_len);
+  const int chunks = append_chunks((long long)n_new * Hkv * (D / 8));
+  if (chunks == 0) return set_error(WS_EINVAL, "ws_kv_append: %d tokens in one call", n_new);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(kv_append_kernel, dim3(B, chunks), dim3(256), 0, s, (const u32x4*)k_new,
+                     (const u32x4*)v_new, (u32x4*)k_pages, (u32x4*)v_pages, page_table,
+                     gpu_len, Hkv, D / 8, n_new, page_size, max_pages, num_pages,
+                     chunks == 1 ? update_len : 0);
+  if (update_len && chunks > 1)
+    hipLaunchKernelGGL(len_add_kernel, dim3((B + 255) / 256), dim3(256), 0, s, gpu_len, B,
+                       n_new);
   return check_launch("ws_kv_append");
 }
 
@@ -127,10 +151,15 @@ extern "C" int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
     return set_error(WS_EINVAL,
                      "ws_latent_append: bf16 buffers must be 16-byte aligned");
   if (B == 0 || n_new == 0) return WS_OK;
-  hipLaunchKernelGGL(latent_append_kernel, dim3(B), dim3(256), 0,
-                     (hipStream_t)stream, (const u32x4*)c_new, c_stride / 8,
-                     (const u32x4*)pe_new, pe_stride / 8, (u32x4*)latent_pages,
-                     page_table, gpu_len, n_new, page_size, max_pages,
-                     num_pages, update_len);
+  const int chunks = append_chunks((long long)n_new * (kLatent / 8));
+  if (chunks == 0) return set_error(WS_EINVAL, "ws_latent_append: %d tokens in one call", n_new);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(latent_append_kernel, dim3(B, chunks), dim3(256), 0, s,
+                     (const u32x4*)c_new, c_stride / 8, (const u32x4*)pe_new, pe_stride / 8,
+                     (u32x4*)latent_pages, page_table, gpu_len, n_new, page_size, max_pages,
+                     num_pages, chunks == 1 ? update_len : 0);
+  if (update_len && chunks > 1)
+    hipLaunchKernelGGL(len_add_kernel, dim3((B + 255) / 256), dim3(256), 0, s, gpu_len, B,
+                       n_new);
   return check_launch("ws_latent_append");
 }
