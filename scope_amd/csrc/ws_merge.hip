@@ -214,6 +214,7 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
 // at a time and reduce by shuffles, 32 rows per pass.  W_UV[h] is shared by
 // the B rows of head h through L2.
 constexpr int kUvThreads = 256;
+constexpr int kUvGroup = 2;  // passes of 32 W_UV rows whose loads are in flight together
 
 template <int FMT>
 __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
@@ -228,6 +229,18 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
   const int t = threadIdx.x;
   const int b = qrow / p.heads;
   const int h = qrow - b * p.heads;
+  // The W_UV rows of the first kUvGroup passes do not depend on the merge:
+  // their loads go out first and land while the plan and the merge run.
+  const int lane8 = t & 7;
+  const int rsub = t >> 3;  // 32 rows per pass
+  u32x4 wv[kUvGroup][8];
+#pragma unroll
+  for (int g = 0; g < kUvGroup; ++g) {
+    const int v = min(g * (kUvThreads / 8) + rsub, Dout - 1);
+    const u32x4* wrow = (const u32x4*)(w_uv + ((size_t)h * Dout + v) * 512);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wv[g][j] = wrow[j * 8 + lane8];
+  }
   const Plan plan =
       plan_build<kUvThreads>(p.gpu_len, 0, p.cap, p.B, 1, p.grid, s_pref, s_scan);
   const int nbb = (plan_len(p.gpu_len, b, 0, p.cap) + 31) >> 5;
@@ -313,28 +326,37 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     s_row[4 * c + 3] = bf16_to_f32(packed.y >> 16);
   }
   __syncthreads();
-  // out_v[b][h * Dout + v] = sum_k s_row[k] * W_UV[h][v][k]
-  const int lane8 = t & 7;
-  const int rsub = t >> 3;  // 32 rows per pass
-  for (int v0 = 0; v0 < Dout; v0 += kUvThreads / 8) {
-    const int v = v0 + rsub;
-    const u32x4* wrow = (const u32x4*)(w_uv + ((size_t)h * Dout + v) * 512);
-    float acc = 0.f;
+  // out_v[b][h * Dout + v] = sum_k s_row[k] * W_UV[h][v][k]: eight lanes per
+  // W_UV row, 32 rows per pass, kUvGroup passes per group of loads
+  for (int v0 = 0; v0 < Dout; v0 += kUvGroup * (kUvThreads / 8)) {
+    if (v0 > 0) {  // groups after the first load here
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int k8 = j * 8 + lane8;  // 8-element chunk of the 512
-      const u32x4 wv = wrow[k8];
-      const float* r = s_row + 8 * k8;
-      acc += bf16_to_f32(wv.x & 0xffffu) * r[0] + bf16_to_f32(wv.x >> 16) * r[1];
-      acc += bf16_to_f32(wv.y & 0xffffu) * r[2] + bf16_to_f32(wv.y >> 16) * r[3];
-      acc += bf16_to_f32(wv.z & 0xffffu) * r[4] + bf16_to_f32(wv.z >> 16) * r[5];
-      acc += bf16_to_f32(wv.w & 0xffffu) * r[6] + bf16_to_f32(wv.w >> 16) * r[7];
+      for (int g = 0; g < kUvGroup; ++g) {
+        const int v = min(v0 + g * (kUvThreads / 8) + rsub, Dout - 1);
+        const u32x4* wrow = (const u32x4*)(w_uv + ((size_t)h * Dout + v) * 512);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wv[g][j] = wrow[j * 8 + lane8];
+      }
     }
-    acc += __shfl_xor(acc, 1);
-    acc += __shfl_xor(acc, 2);
-    acc += __shfl_xor(acc, 4);
-    if (lane8 == 0)
-      out_v[(size_t)b * p.heads * Dout + (size_t)h * Dout + v] = f32_to_bf16(acc);
+#pragma unroll
+    for (int g = 0; g < kUvGroup; ++g) {
+      const int v = v0 + g * (kUvThreads / 8) + rsub;
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const u32x4 w = wv[g][j];
+        const float* r = s_row + 8 * (j * 8 + lane8);
+        acc += bf16_to_f32(w.x & 0xffffu) * r[0] + bf16_to_f32(w.x >> 16) * r[1];
+        acc += bf16_to_f32(w.y & 0xffffu) * r[2] + bf16_to_f32(w.y >> 16) * r[3];
+        acc += bf16_to_f32(w.z & 0xffffu) * r[4] + bf16_to_f32(w.z >> 16) * r[5];
+        acc += bf16_to_f32(w.w & 0xffffu) * r[6] + bf16_to_f32(w.w >> 16) * r[7];
+      }
+      acc += __shfl_xor(acc, 1);
+      acc += __shfl_xor(acc, 2);
+      acc += __shfl_xor(acc, 4);
+      if (lane8 == 0 && v < Dout)
+        out_v[(size_t)b * p.heads * Dout + (size_t)h * Dout + v] = f32_to_bf16(acc);
+    }
   }
 }
 
