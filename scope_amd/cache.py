@@ -99,6 +99,28 @@ class _PagedBase:
     def max_len(self, layer: int) -> int:
         return int(self.lens[layer].max()) if self.batch else 0
 
+    def workspace(self, nbytes: int) -> torch.Tensor:
+        """The partition's decode workspace, zeroed once and grown on demand.
+        Calls that share it are ordered on the device's stream, and every
+        completed call leaves its arrival counters zero."""
+        ws = getattr(self, "_ws", None)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self._ws = ws
+        return ws
+
+    def _split_workspace(self, kind: int, rows_kv: int, heads: int, max_len: int,
+                         n_workgroups: int) -> torch.Tensor:
+        _, wsb = ops.decode_plan(kind, rows_kv, heads, max_len, n_workgroups)
+        self._ws_gen = getattr(self, "_ws_gen", 0) + 1
+        return self.workspace(wsb)
+
+    def _own(self, st: "ops.SplitStep") -> "ops.SplitStep":
+        """Tie a split step to the current workspace generation: its merge
+        refuses to run once a later step has reused the workspace."""
+        st.guard = lambda gen=self._ws_gen: self._ws_gen == gen
+        return st
+
     def reset(self) -> None:
         """Drop all tokens and return every page to the pool."""
         for b in range(self.batch):
@@ -165,6 +187,24 @@ class GqaGpuPartition(_PagedBase):
         self.lens[layer] += 1
         return out
 
+    def step_split(self, layer: int, q: torch.Tensor, k_new: torch.Tensor,
+                   v_new: torch.Tensor, scale: float, n_workgroups=0) -> "ops.SplitStep":
+        """step() with the combine of rows shared by several workgroups left to
+        ops.merge_split, which does it in the same launch as the merge with the
+        host partial.  Returns the ops.SplitStep to finish."""
+        for b in range(self.batch):
+            self.reserve(b, int(self.lens[layer, b]) + 1)
+        max_len = self.max_len(layer) + 1
+        G = q.shape[1] // self.num_kv_heads
+        ws = self._split_workspace(0, self.batch * self.num_kv_heads, G, max_len, n_workgroups)
+        st = ops.gqa_append_decode_split(
+            q, k_new.contiguous(), v_new.contiguous(), self.k[layer], self.v[layer],
+            self.page_table, self.len_dev(layer), self._len_next(layer), scale, max_len,
+            n_workgroups, ws)
+        self._flip(layer)
+        self.lens[layer] += 1
+        return self._own(st)
+
 
 class MlaGpuPartition(_PagedBase):
     """HBM pages of the GPU token range of an absorbed-MLA latent cache."""
@@ -214,6 +254,23 @@ class MlaGpuPartition(_PagedBase):
         self._flip(layer)
         self.lens[layer] += 1
         return out
+
+    def step_split(self, layer: int, q_nope: torch.Tensor, q_pe: torch.Tensor,
+                   c_new: torch.Tensor, pe_new: torch.Tensor, scale: float,
+                   n_workgroups=0) -> "ops.SplitStep":
+        """step() with the combine of sequences held by several workgroups left
+        to ops.merge_split / ops.merge_split_uv.  Returns the ops.SplitStep."""
+        for b in range(self.batch):
+            self.reserve(b, int(self.lens[layer, b]) + 1)
+        max_len = self.max_len(layer) + 1
+        H = q_nope.shape[0] // self.batch
+        ws = self._split_workspace(1, self.batch, H, max_len, n_workgroups)
+        st = ops.mla_append_decode_split(
+            q_nope, q_pe, c_new, pe_new, self.latent[layer], self.page_table,
+            self.len_dev(layer), self._len_next(layer), scale, max_len, n_workgroups, ws)
+        self._flip(layer)
+        self.lens[layer] += 1
+        return self._own(st)
 
 
 class PartitionedLatentCache:

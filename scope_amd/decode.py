@@ -84,9 +84,24 @@ def _pinned_out(out_shape, lse_shape):
 
 
 def _gqa_gpu(gpu, layer, q, scale, k_new, v_new, n_workgroups):
+    """The GPU side: a split step when the call appends (its combine then runs
+    inside the merge), else the one-launch partial."""
     if k_new is not None:
-        return gpu.step(layer, q, k_new, v_new, scale, n_workgroups)
+        return gpu.step_split(layer, q, k_new, v_new, scale, n_workgroups)
     return gpu.attend(layer, q, scale, n_workgroups)
+
+
+def _finish(gpu_part, b, fmt):
+    """Merge the GPU side (a SplitStep or an (out, lse) partial) with the host
+    partial b in format fmt (None: no host partial); bf16 [rows, Dv]."""
+    if isinstance(gpu_part, ops.SplitStep):
+        out, _ = ops.merge_split(gpu_part, b, fmt, want_lse=False)
+        return out
+    out_g, lse_g = gpu_part
+    if b is None:
+        b, fmt = (out_g, torch.full_like(lse_g, float("-inf"))), ops.PARTIAL_LSE_F32
+    out, _ = ops.lse_merge(out_g, lse_g, b, fmt, want_lse=False)
+    return out
 
 
 def partitioned_gqa_decode(cache: PartitionedKVCache, layer: int, q: torch.Tensor,
@@ -109,15 +124,14 @@ def partitioned_gqa_decode(cache: PartitionedKVCache, layer: int, q: torch.Tenso
     need_cpu = cpu_attn is not None and bool((cache.host_len[layer] > 0).any())
     if need_cpu and cpu_attn == NATIVE:
         q_host, ev = _query_to_host(q)
-        out_g, lse_g = _gqa_gpu(gpu, layer, q, scale, k_new, v_new, n_workgroups)
+        g = _gqa_gpu(gpu, layer, q, scale, k_new, v_new, n_workgroups)
         ev.synchronize()
         lens = torch.from_numpy(cache.host_len[layer].astype(np.int32))
         part = host.gqa_partial_dense(q_host, cache.host_k[layer], cache.host_v[layer], lens,
                                       scale, host_threads, *_pinned_out((B, Hq, D), (B, Hq)))
         dev = q.device
         b = tuple(x.to(dev, non_blocking=True) for x in part)
-        out, _ = ops.lse_merge(out_g, lse_g, b, ops.PARTIAL_LSE_F32, want_lse=False)
-        return out.view(B, Hq, 1, D)
+        return _finish(g, b, ops.PARTIAL_LSE_F32).view(B, Hq, 1, D)
     worker = None
     if need_cpu:
         q_host = q.view(B * Hkv, G, D).cpu()
@@ -140,17 +154,13 @@ def partitioned_gqa_decode(cache: PartitionedKVCache, layer: int, q: torch.Tenso
 
         worker = _CpuPartial(host_partial)
         worker.start()
-    out_g, lse_g = _gqa_gpu(gpu, layer, q, scale, k_new, v_new, n_workgroups)
+    g = _gqa_gpu(gpu, layer, q, scale, k_new, v_new, n_workgroups)
     if worker is None:
-        empty = torch.full_like(lse_g, float("-inf"))
-        out, _ = ops.lse_merge(out_g, lse_g, (out_g, empty), ops.PARTIAL_LSE_F32,
-                               want_lse=False)
-        return out.view(B, Hq, 1, D)
+        return _finish(g, None, None).view(B, Hq, 1, D)
     o, m, s = worker.join_result()
     dev = q.device
     triple = tuple(_to_device_pinned(x, dev) for x in (o, m, s))
-    out, _ = ops.lse_merge(out_g, lse_g, triple, CPU_FORMATS[cpu_format], want_lse=False)
-    return out.view(B, Hq, 1, D)
+    return _finish(g, triple, CPU_FORMATS[cpu_format]).view(B, Hq, 1, D)
 
 
 def partitioned_mla_decode(cache: PartitionedLatentCache, layer: int,

@@ -409,6 +409,12 @@ class SplitStep:
         self.gpu_len, self.B, self.rows_per_seq, self.heads = gpu_len, B, rows_per_seq, heads
         self.Dv, self.cap, self.nwg = Dv, cap, nwg
         self.out_g, self.lse_g, self.workspace = out_g, lse_g, workspace
+        self.guard = None  # set by an owner that reuses the workspace
+
+    def check_workspace(self):
+        if self.guard is not None and not self.guard():
+            raise RuntimeError("this step's workspace was reused by a later step before "
+                               "its merge")
 
 
 def gqa_append_decode_split(q, k_new, v_new, k_pages, v_pages, page_table, len_in,
@@ -501,6 +507,7 @@ def merge_split(step: SplitStep, b=None, fmt=PARTIAL_LSE_F32, out_dtype=torch.bf
     """Finish a deferred-combine step (ws_merge_split): combine its GPU pieces
     with the host partial `b` (formats as lse_merge; None = no host partial),
     normalise.  Returns (out [rows, Dv] in out_dtype, lse [rows] or None)."""
+    step.check_workspace()
     dev = step.out_g.device
     rows = step.out_g.numel() // step.Dv
     b_out = b_aux0 = b_aux1 = None
@@ -561,6 +568,7 @@ def merge_split_uv(step: SplitStep, w_uv: torch.Tensor, b=None, fmt=PARTIAL_LSE_
     (ws_mla_merge_split_uv): w_uv [heads, Dout, 512] bf16.  Returns
     (out_v [B, heads * Dout] bf16, latent [B * heads, 512] bf16 or None,
     lse [B * heads] or None)."""
+    step.check_workspace()
     dev = step.out_g.device
     if step.rows_per_seq != 1 or step.Dv != MLA_C:
         raise ValueError("merge_split_uv finishes an MLA step")

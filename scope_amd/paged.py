@@ -342,13 +342,7 @@ class PagedMlaCache(_PagedTwoSided):
         with_host = bool(self.host.lens.any())
         if with_host:
             (qn_h, qp_h), ev = self._to_host(q_nope, q_pe)
-        for b in range(self.batch):
-            g.reserve(b, int(g.lens[layer, b]) + 1)
-        step = ops.mla_append_decode_split(q_nope, q_pe, c_new, pe_new, g.latent[layer],
-                                           g.page_table, g.len_dev(layer), g._len_next(layer),
-                                           scale, g.max_len(layer) + 1, n_workgroups)
-        g._flip(layer)
-        g.lens[layer] += 1
+        step = g.step_split(layer, q_nope, q_pe, c_new, pe_new, scale, n_workgroups)
         part = None
         if with_host:
             ev.synchronize()
@@ -412,14 +406,7 @@ class PagedKVCache(_PagedTwoSided):
         with_host = bool(self.host.lens.any())
         if with_host:
             (q_h,), ev = self._to_host(q)
-        for b in range(self.batch):
-            g.reserve(b, int(g.lens[layer, b]) + 1)
-        step = ops.gqa_append_decode_split(q, k_new.contiguous(), v_new.contiguous(),
-                                           g.k[layer], g.v[layer], g.page_table,
-                                           g.len_dev(layer), g._len_next(layer), scale,
-                                           g.max_len(layer) + 1, n_workgroups)
-        g._flip(layer)
-        g.lens[layer] += 1
+        step = g.step_split(layer, q, k_new, v_new, scale, n_workgroups)
         part = None
         if with_host:
             ev.synchronize()

@@ -166,3 +166,37 @@ def test_reference_api_resident_layer():
     assert_close((o / s).cpu().numpy(), want, OUT_ATOL, OUT_RTOL, "resident")
     z = reference_api.resident_layer(q, k[:, :0], v[:, :0], nk, nv, 1.0)
     assert torch.all(z[0] == 0) and torch.all(torch.isinf(z[1]))
+
+
+def test_split_steps_share_the_partition_workspace_in_order():
+    """Two layers' split steps reuse the partition's workspace: merging each
+    step before the next is correct; merging a step after a later step has
+    reused the workspace is refused."""
+    B, Hkv, G, D = 2, 4, 8, 128
+    part = GqaGpuPartition(2, B, Hkv, D, max_tokens=600, device=DEV)
+    ks = [[bf16_randn((Hkv, 300 + 100 * b + 1, D), 70 + 10 * l + b) for b in range(B)]
+          for l in range(2)]
+    vs = [[bf16_randn((Hkv, 300 + 100 * b + 1, D), 80 + 10 * l + b) for b in range(B)]
+          for l in range(2)]
+    for l in range(2):
+        for b in range(B):
+            part.load_sequence(l, b, ks[l][b][:, :-1].to(DEV), vs[l][b][:, :-1].to(DEV))
+    q = bf16_randn((B, Hkv * G, D), 90)
+    outs = []
+    for l in range(2):
+        kn = torch.stack([ks[l][b][:, -1:] for b in range(B)]).to(DEV)
+        vn = torch.stack([vs[l][b][:, -1:] for b in range(B)]).to(DEV)
+        st = part.step_split(l, q.to(DEV), kn, vn, D ** -0.5, n_workgroups=13)
+        outs.append(ops.merge_split(st, None, out_dtype=torch.float32)[0])
+    torch.cuda.synchronize()
+    qb = bits(q).reshape(B, Hkv, G, D)
+    for l in range(2):
+        got = outs[l].cpu().numpy().reshape(B, Hkv, G, D)
+        for b in range(B):
+            want, _ = O.gqa_attention_fp64(qb[b], bits(ks[l][b]), bits(vs[l][b]), D ** -0.5)
+            assert_close(got[b], want, OUT_ATOL, OUT_RTOL, f"layer {l} b={b}")
+    kn = torch.stack([ks[0][b][:, -1:] for b in range(B)]).to(DEV)
+    st0 = part.step_split(0, q.to(DEV), kn, kn, D ** -0.5)
+    part.step_split(1, q.to(DEV), kn, kn, D ** -0.5)
+    with pytest.raises(RuntimeError, match="reused"):
+        ops.merge_split(st0)
