@@ -771,7 +771,7 @@ WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "host", "model", "
              "epilogue")
 
 # The kernel the headline roofline is measured on (its rocprofv3 name).
-HEAD_KERNEL = "ws::gqa_decode_kernel<4, true, false>"
+HEAD_KERNEL = "ws::gqa_decode_kernel<4, true>"
 
 
 def committed_traffic(workload_key, kernel=HEAD_KERNEL):

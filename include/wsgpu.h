@@ -101,23 +101,25 @@ int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
 /*
  * Plan of a decode call: kind 0 (GQA: rows_kv = B * Hkv, heads = the group
  * size G) or 1 (MLA: rows_kv = B, heads = H = 16), over sequences of at most
- * max_len tokens.  n_workgroups is the grid the call will use (0 = the
- * library's choice for the current device: two 4-wave workgroups per CU for
- * GQA, one per CU for MLA, fewer when the batch is small).  Writes the
- * resolved workgroup count and the workspace bytes the call needs.
+ * max_len tokens.  n_splits is the number of pieces the call cuts its work
+ * into: one per wave for GQA (two per workgroup, each streaming on its
+ * own), one per workgroup for MLA.  0 = the library's choice for the current
+ * device: two GQA waves (one workgroup) or one MLA workgroup per CU, fewer
+ * when the batch is small.  Writes the resolved split count and the
+ * workspace bytes the call needs; the same count goes to ws_merge_split.
  *
- * Workgroups take equal shares of all 32-token blocks of all rows, so ragged
- * batches stay balanced; a row shared by several workgroups is combined from
+ * Splits take equal shares of all 32-token blocks of all rows, so ragged
+ * batches stay balanced; a row shared by several splits is combined from
  * their partials.  Workspace layout: [arrival counters int32 x 16384 (one per
  * kv row; a call takes at most 16384 kv rows)][partial lse][partial out], one
- * partial slot per (workgroup, row) pair.  The workspace must be 256-byte
+ * partial slot per (split, row) pair.  The workspace must be 256-byte
  * aligned and its counters zero before its first use (ws_workspace_clear, or
  * memory that is zero); every completed call leaves them zero again.  Calls
  * that share a workspace must be ordered on one stream.  At most 2048
- * sequences per call.
+ * sequences and 4096 splits per call.
  */
 int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
-                   int n_workgroups, int* n_workgroups_out,
+                   int n_splits, int* n_splits_out,
                    size_t* workspace_bytes_out);
 
 /* Zero `bytes` bytes of device memory with a kernel on `stream` (no
@@ -127,10 +129,12 @@ int ws_workspace_clear(void* workspace, size_t bytes, void* stream);
 /*
  * Split-KV GQA decode attention over the pooled tokens of every sequence.
  * q: [B][Hq][D] bf16, Hq = Hkv * G, G in {1,2,4,8,16}, D = 128.
- * n_workgroups: grid size (0 = choose, see ws_decode_plan); max_len: upper
- * bound of gpu_len[] (must be >= every gpu_len[b]).  One launch: when a row
- * spans several workgroups, the last one to finish combines the partials
- * (arrival counters in the workspace).
+ * n_splits: waves of the plan (0 = choose, see ws_decode_plan); max_len:
+ * upper bound of gpu_len[] (must be >= every gpu_len[b]).  Rows held by one
+ * wave are written final by the streaming launch; rows spread over several
+ * waves are combined from their workspace partials by a second, small launch
+ * on the same stream (the split merge of ws_merge_split without a host
+ * partial).
  * Outputs out: [B][Hq][D] fp32 normalised, lse: [B][Hq] fp32.
  * Replaces _local_bmm_softmax / _resident_layer
  * (roofline/bench_resident_kv.py:150-157, 261-271) and the GPU side of
@@ -141,7 +145,7 @@ int ws_gqa_decode_partial(const uint16_t* q,
                           const int32_t* page_table, const int32_t* gpu_len,
                           int B, int Hq, int Hkv, int D,
                           int page_size, int max_pages, int num_pages,
-                          int max_len, int n_workgroups, float scale,
+                          int max_len, int n_splits, float scale,
                           float* out, float* lse,
                           void* workspace, size_t workspace_bytes,
                           void* stream);
@@ -165,20 +169,18 @@ int ws_gqa_append_decode_partial(const uint16_t* q, const uint16_t* k_new,
                                  const int32_t* len_in, int32_t* len_out,
                                  int B, int Hq, int Hkv, int D,
                                  int page_size, int max_pages, int num_pages,
-                                 int max_len, int n_workgroups, float scale,
+                                 int max_len, int n_splits, float scale,
                                  float* out, float* lse,
                                  void* workspace, size_t workspace_bytes,
                                  void* stream);
 
 /*
  * Deferred-combine form of ws_gqa_append_decode_partial, for a step whose
- * partial is merged with a host partial anyway: rows that one workgroup held
- * are written final to out/lse as before, rows spread over several
- * workgroups leave their partials in the workspace, and ws_merge_split
- * combines them with the host partial in the merge launch.  This takes the
- * cross-workgroup combine (a chain of dependent memory round trips) off the
- * end of the streaming launch.  The workspace must not be reused until the
- * matching ws_merge_split ran.
+ * partial is merged with a host partial anyway: one launch, the streaming
+ * one.  Rows that one wave held are written final to out/lse, rows spread
+ * over several waves leave their partials in the workspace, and
+ * ws_merge_split combines them with the host partial in the merge launch.
+ * The workspace must not be reused until the matching ws_merge_split ran.
  */
 int ws_gqa_append_decode_split(const uint16_t* q, const uint16_t* k_new,
                                const uint16_t* v_new, uint16_t* k_pages,
@@ -186,7 +188,7 @@ int ws_gqa_append_decode_split(const uint16_t* q, const uint16_t* k_new,
                                const int32_t* len_in, int32_t* len_out,
                                int B, int Hq, int Hkv, int D,
                                int page_size, int max_pages, int num_pages,
-                               int max_len, int n_workgroups, float scale,
+                               int max_len, int n_splits, float scale,
                                float* out, float* lse,
                                void* workspace, size_t workspace_bytes,
                                void* stream);
@@ -250,14 +252,14 @@ int ws_mla_append_decode_split(const uint16_t* q_nope, const uint16_t* q_pe,
 /*
  * Finish a deferred-combine step: for every output row, LSE-combine the GPU
  * pieces the step left (its final out/lse, or the partials of the
- * workgroups that shared the row) with the host partial, normalise, and
+ * splits that shared the row) with the host partial, normalise, and
  * write out_bf16 and/or out_f32 [rows][Dv] and lse_out [rows] (any may be
  * NULL but not both outputs).
  *   gpu_len          the lengths after the step (the step's len_out)
  *   rows_per_seq     Hkv (GQA) or 1 (MLA); heads: G (GQA) or 16 (MLA)
  *   Dv               128 (GQA) or 512 (MLA)
  *   page_capacity    page_size * max_pages of the step
- *   n_workgroups     the workgroup count the step ran with (ws_decode_plan)
+ *   n_splits         the split count the step ran with (ws_decode_plan)
  *   out_g, lse_g     the step's out / lse; workspace as given to the step
  *   b_*, fmt_b       host partial as in ws_lse_merge, or b_out = NULL for none
  * rows = B * rows_per_seq * heads, ordered as the step's out.
@@ -266,7 +268,7 @@ int ws_mla_append_decode_split(const uint16_t* q_nope, const uint16_t* q_pe,
  * roofline/bench_resident_kv.py:339-350) together with the split combine.
  */
 int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, int heads,
-                   int Dv, int page_capacity, int n_workgroups,
+                   int Dv, int page_capacity, int n_splits,
                    const float* out_g, const float* lse_g,
                    const void* workspace, size_t workspace_bytes,
                    const void* b_out, const void* b_aux0, const void* b_aux1,
@@ -287,7 +289,7 @@ int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, int heads,
  * branch (system/deepseek.py:397-407) in one launch.
  */
 int ws_mla_merge_split_uv(const int32_t* gpu_len, int B, int heads, int page_capacity,
-                          int n_workgroups, const float* out_g, const float* lse_g,
+                          int n_splits, const float* out_g, const float* lse_g,
                           const void* workspace, size_t workspace_bytes,
                           const void* b_out, const void* b_aux0, const void* b_aux1,
                           int fmt_b, const uint16_t* w_uv, int Dout, uint16_t* out_latent,

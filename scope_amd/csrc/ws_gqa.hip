@@ -1,25 +1,35 @@
 // Split-KV GQA decode attention over the HBM partition (gfx950), optionally
 // fused with the append of the decode step's new token.
 //
-// Work decomposition (ws_plan.h): the grid's workgroups (4 waves each) take
-// equal shares of all 32-token blocks of all kv rows (kv row = b * Hkv + kvh),
-// so a batch of ragged lengths keeps every workgroup streaming for the same
-// time.  A workgroup walks its share as row segments; inside a segment its
-// waves take blocks round robin, each wave requesting its next block's K/V
-// before the MFMAs of the current one run, and the waves combine their
-// (max, sum, out) in LDS at the segment's end.  A row held by one workgroup
-// is written final; otherwise each workgroup stores a partial and the last to
-// arrive combines them (ws_reduce.h), so one launch produces the partition's
-// final partial.
+// Work decomposition (ws_plan.h): the work list is every 32-token block of
+// every kv row (kv row = b * Hkv + kvh), rows in order, and every *wave* of
+// the grid is one split of the plan: split w streams the blocks
+// [floor(w T / n), floor((w + 1) T / n)), so each wave reads the same number
+// of bytes whatever the lengths.  A wave streams its range through a
+// two-stage register ring that runs straight across row boundaries: while
+// block i is consumed, block i + 1 (its K, V and the q rows of its kv row)
+// is in flight, so a wave whose range spans two rows never drains and
+// restarts its loads.  When the consumed block opens a new row, the finished
+// row's piece (normalised out, lse) is written: to out/lse when the wave
+// held the whole row, else to workspace slot w + row, where ws_merge_split
+// (or the one-launch entry points' own merge) finds it.  Waves never wait for
+// each other.
+//
+// The block metadata (kv row, pool token index, valid tokens, the new
+// token's row) is computed 64 blocks at a time, one block per lane, page
+// table reads included, and read in the loop with readlane: the loop issues
+// no load whose address depends on another load in flight.
 //
 // With k_new != nullptr the call also appends one token per sequence: token
 // len_in[b] of sequence b is read from k_new/v_new instead of the page, the
-// workgroup whose segment holds that position writes it into its page slot,
-// and len_out[b] = len_in[b] + 1.  No workgroup reads the slot being written
-// and len_out is not read, so the fused step has no intra-launch race.
+// wave that consumes that block writes it into its page slot from the
+// registers it already holds, and len_out[b] = len_in[b] + 1.  No wave reads
+// the slot being written and len_out is not read, so the fused step has no
+// intra-launch race.
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "ws_attn.h"
 #include "ws_plan.h"
@@ -28,10 +38,18 @@
 namespace ws {
 
 constexpr int kGqaD = 128;
-constexpr int kGqaWaves = 4;
-// Register stages per wave.  Two keep two waves per SIMD (about 230 VGPRs);
-// measured on MI355X, deeper rings at one wave per SIMD stream no faster.
-constexpr int kGqaStages = 2;
+constexpr int kGqaWaves = 2;        // waves per workgroup, each its own split
+constexpr int kGqaStages = 2;       // register stages of a wave's load ring
+constexpr int kGqaSplitsPerCu = 2;  // default splits (waves) per CU
+
+// Calls f(integral_constant<int, I>) ... f(integral_constant<int, N - 1>).
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
 
 struct GqaParams {
   const uint16_t* q;
@@ -47,43 +65,45 @@ struct GqaParams {
   float* out;
   float* lse;
   SplitWorkspace ws;
-  int B, Hkv, page_size, max_pages, num_pages, cap;
+  int B, Hkv, page_size, max_pages, num_pages, cap, n_splits;
   float scale_log2;
 };
 
-// COMBINE: rows held by several workgroups are combined in this launch by the
-// last one to arrive; without it their partials stay in the workspace for
-// ws_merge_split (the combine then rides on the merge launch of the step).
-template <int G, bool APPEND, bool COMBINE>
+// Block metadata, uniform across the wave.
+struct GqaBlock {
+  int row;       // kv row
+  uint32_t tok;  // pool index of the block's first token: (pid * Hkv + kvh) * page_size + off
+  int nt;        // valid tokens (1..32) | kFirst (row's first block) | kLast (row's last
+                 // block) | kBadPage (the page table entry was out of range, clamped)
+  int nr;        // row of the appended token in this block when in [0, 32)
+};
+constexpr int kNtMask = 63;
+constexpr int kFirst = 64;
+constexpr int kLast = 128;
+constexpr int kBadPage = 256;
+
+template <int G, bool APPEND>
 __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_decode_kernel(
     const GqaParams p) {
   constexpr int D = kGqaD;
   constexpr int W = kGqaWaves;
-  constexpr int S = kGqaStages;
   constexpr int NT = 64 * W;
   constexpr int add = APPEND ? 1 : 0;
-  __shared__ float s_m[W][16];
-  __shared__ float s_l[W][16];
-  __shared__ float s_acc[W][G][D];
-  __shared__ float s_w[kReduceMaxWeights];
-  __shared__ float s_red[32 * W + 32];
   __shared__ int s_pref[kMaxSeqs + 1];
   __shared__ int s_scan[W + 1];
-  __shared__ int s_flag;
 
-  const int g = blockIdx.x;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
   const int lane = tid & 63;
   const int n16 = lane & 15;
   const int j = lane >> 4;
   const bool head_ok = n16 < G;
 
   // Lengths (len_in clamped to what the page table row holds) and the plan.
-  if (APPEND && p.len_out && g == 0)
+  if (APPEND && p.len_out && blockIdx.x == 0)
     for (int b = tid; b < p.B; b += NT) p.len_out[b] = plan_len(p.len_in, b, add, p.cap);
-  const Plan plan = plan_build<NT>(p.len_in, add, p.cap, p.B, p.Hkv, gridDim.x, s_pref, s_scan);
-  if (g == 0) {  // sequences without tokens: the empty partial (0, -inf)
+  const Plan plan =
+      plan_build<NT>(p.len_in, add, p.cap, p.B, p.Hkv, p.n_splits, s_pref, s_scan);
+  if (blockIdx.x == 0) {  // sequences without tokens: the empty partial (0, -inf)
     for (int b = 0; b < p.B; ++b) {
       if (s_pref[b + 1] != s_pref[b]) continue;
       const size_t q0 = (size_t)b * p.Hkv * G;
@@ -91,184 +111,211 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
       for (int idx = tid; idx < p.Hkv * G; idx += NT) p.lse[q0 + idx] = neg_inf();
     }
   }
-  if (g >= plan.n) return;
-  const int blk_end = plan_start(plan, g + 1);
-  int blk = plan_start(plan, g);
+  const int split = uniform(blockIdx.x * W + (tid >> 6));
+  if (split >= plan.n) return;  // no barrier below: waves run independently
+  const int x_begin = plan_start(plan, split);
+  const int x_end = plan_start(plan, split + 1);
+  const int nblk = x_end - x_begin;  // >= 1 (plan.n <= T)
 
-  while (blk < blk_end) {
-    // the row segment holding blk (all workgroup-uniform)
-    const int b = plan_seq(s_pref, p.B, blk);
-    const int len = uniform(plan_len(p.len_in, b, add, p.cap));
-    const int len_old = len - add;
+  // Metadata window: lane l describes block xb + l (the range's last block
+  // past its end).
+  int m_row, m_nt, m_nr;
+  uint32_t m_tok;
+  auto fetch_meta = [&](int xb) __attribute__((always_inline)) {
+    const int x = min(xb + lane, x_end - 1);
+    int lo = 0, hi = p.B - 1;  // the sequence holding x: last b with s_pref[b] <= x
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_pref[mid] <= x) lo = mid;
+      else hi = mid - 1;
+    }
+    const int len = plan_len(p.len_in, lo, add, p.cap);
     const int nbb = (len + 31) >> 5;
-    const int seq_start = uniform(s_pref[b]);
-    const int kvh = (blk - seq_start) / nbb;
-    const int row = b * p.Hkv + kvh;
-    const int row_start = seq_start + kvh * nbb;
-    const int row_end = row_start + nbb;
-    const int seg_end = min(blk_end, row_end);
-    const int t_begin = (blk - row_start) * 32;
-    const int t_end = min(len, (seg_end - row_start) * 32);
-    const int q0 = row * G;
-    const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
-    const size_t new_row = (size_t)row * D;
+    const int rel = x - s_pref[lo];
+    const int kvh = rel / nbb;
+    const int t0 = (rel - kvh * nbb) * 32;
+    const int page = t0 / p.page_size;
+    const int raw = p.page_table[(size_t)lo * p.max_pages + page];
+    const int pid = clamp_page(raw, p.num_pages);
+    m_row = lo * p.Hkv + kvh;
+    m_tok = ((uint32_t)pid * (uint32_t)p.Hkv + (uint32_t)kvh) * (uint32_t)p.page_size +
+            (uint32_t)(t0 - page * p.page_size);
+    m_nt = min(32, len - t0) | (t0 == 0 ? kFirst : 0) | (t0 + 32 >= len ? kLast : 0) |
+           (raw == pid ? 0 : kBadPage);
+    m_nr = APPEND ? len - 1 - t0 : -1;
+  };
+  auto read_meta = [&](int l) __attribute__((always_inline)) {
+    GqaBlock m;
+    m.row = __builtin_amdgcn_readlane(m_row, l);
+    m.tok = (uint32_t)__builtin_amdgcn_readlane((int)m_tok, l);
+    m.nt = __builtin_amdgcn_readlane(m_nt, l);
+    m.nr = __builtin_amdgcn_readlane(m_nr, l);
+    return m;
+  };
 
-    // Fused append: write the new token into its page slot.
-    if (APPEND && wave == 0 && lane < 32 && len_old >= t_begin && len_old < t_end) {
-      const int page = len_old / p.page_size;
-      const int pid = pt[page];
-      if (pid >= 0 && pid < p.num_pages) {
-        const size_t dst =
-            (((size_t)pid * p.Hkv + kvh) * p.page_size + (len_old - page * p.page_size)) * D;
-        if (lane < 16)
-          ((u32x4*)(p.k_pages_w + dst))[lane] = ((const u32x4*)(p.k_new + new_row))[lane];
-        else
-          ((u32x4*)(p.v_pages_w + dst))[lane - 16] =
-              ((const u32x4*)(p.v_new + new_row))[lane - 16];
+  // K/V of one block.  Rows past the valid tokens repeat the last valid one
+  // and are masked in the softmax; the appended token's row reads
+  // k_new/v_new.  With valid == false (the request past the range's last
+  // block) every lane reads the first row of q instead: same instructions
+  // and registers, a cache hit, no HBM traffic.
+  auto load_block = [&](const GqaBlock& m, bool valid, u32x4 (&ka)[2][4],
+                        u32x4 (&vr)[8]) __attribute__((always_inline)) {
+    const uint16_t* kb = valid ? p.k_pages + (size_t)m.tok * D : p.q;
+    const uint16_t* vb = valid ? p.v_pages + (size_t)m.tok * D : p.q;
+    const int last = valid ? (m.nt & kNtMask) - 1 : 0;
+    const int new_r = (APPEND && valid) ? m.nr : -1;
+    const size_t new_row = (size_t)m.row * D;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int r = min(16 * tt + n16, last);
+      const uint16_t* kr = (APPEND && r == new_r) ? p.k_new + new_row : kb + (size_t)r * D;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ka[tt][s] = ld_stream(kr + 8 * (4 * s + j));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = min(pv_token(i, j), last);
+      const uint16_t* vrow = (APPEND && r == new_r) ? p.v_new + new_row : vb + (size_t)r * D;
+      vr[i] = ld_stream(vrow + 8 * n16);
+    }
+  };
+  // The q rows of kv row `row` as the QK B operand.  Lanes of padding head
+  // columns (n16 >= G) load head G - 1: MFMA columns are independent and
+  // those columns are never written.
+  u32x4 qb[4];
+  auto load_q = [&](int row) __attribute__((always_inline)) {
+    const u32x4* qp = (const u32x4*)(p.q + (size_t)(row * G + min(n16, G - 1)) * D);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qb[s] = qp[4 * s + j];
+  };
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = neg_inf();
+  float l_run = 0.f;
+
+  auto compute_block = [&](const GqaBlock& m, const u32x4 (&ka)[2][4],
+                           const u32x4 (&vr)[8]) __attribute__((always_inline)) {
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      s0 = mfma16x16x32(ka[0][s], qb[s], s0);
+      s1 = mfma16x16x32(ka[1][s], qb[s], s1);
+    }
+    float alpha;
+    const u32x4 pb =
+        softmax_block(s0, s1, j, m.nt & kNtMask, p.scale_log2, m_run, l_run, alpha);
+    pv_block(acc, vr, pb, alpha);
+    // Fused append: the new token's K row sits in lanes n16 == nr % 16 of
+    // ka[nr / 16] (16 bytes per (lane, s)), its V row in vr[4 (nr / 16) +
+    // nr % 4] of the lanes j == (nr % 16) / 4 (8 columns each).
+    if (APPEND && m.nr >= 0 && m.nr < 32 && !(m.nt & kBadPage)) {
+      const size_t dst = ((size_t)m.tok + m.nr) * D;
+      const int tt = m.nr >> 4;
+      if (n16 == (m.nr & 15)) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+          if (t2 == tt) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) ((u32x4*)(p.k_pages_w + dst))[4 * s + j] = ka[t2][s];
+          }
+      }
+      if (j == ((m.nr & 15) >> 2)) {
+        const int isel = 4 * tt + (m.nr & 3);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (i == isel) ((u32x4*)(p.v_pages_w + dst))[n16] = vr[i];
       }
     }
+  };
 
-    u32x4 qb[4];
-    if (head_ok) {
-      const u32x4* qp = (const u32x4*)(p.q + (size_t)(q0 + n16) * D);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qb[s] = qp[4 * s + j];
-    } else {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qb[s] = u32x4{0u, 0u, 0u, 0u};
-    }
-
-    f32x4 acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = neg_inf();
-    float l_run = 0.f;
-
-    // K/V of a 32-token block starting at t0 (a multiple of 32, so the block
-    // lies in one page).  Rows past t_end repeat the last valid token and are
-    // masked in the softmax.  With valid == false (the prefetch past a wave's
-    // last block) every lane reads the first row of q instead: same
-    // instructions and registers, a cache hit, no HBM traffic.
-    // Physical page of the block at t0 (a scalar load; the ring below issues
-    // it one block ahead, so its latency is not on the block's load path).
-    auto page_id = [&](int t0) { return clamp_page(pt[t0 / p.page_size], p.num_pages); };
-    auto load_block = [&](int t0, int pid, bool valid, u32x4 (&ka)[2][4], u32x4 (&vr)[8]) {
-      const int page = t0 / p.page_size;
-      const size_t tok0 =
-          ((size_t)pid * p.Hkv + kvh) * p.page_size + (t0 - page * p.page_size);
-      const uint16_t* kb = valid ? p.k_pages + tok0 * D : p.q;
-      const uint16_t* vb = valid ? p.v_pages + tok0 * D : p.q;
-      const int last = valid ? min(32, t_end - t0) - 1 : 0;
-      const int new_r = (APPEND && valid) ? len_old - t0 : -1;  // block row of the new token
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int r = min(16 * tt + n16, last);
-        const uint16_t* kr = (APPEND && r == new_r) ? p.k_new + new_row : kb + (size_t)r * D;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) ka[tt][s] = ld_stream(kr + 8 * (4 * s + j));
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int r = min(pv_token(i, j), last);
-        const uint16_t* vrow =
-            (APPEND && r == new_r) ? p.v_new + new_row : vb + (size_t)r * D;
-        vr[i] = ld_stream(vrow + 8 * n16);
-      }
-    };
-    auto compute_block = [&](int t0, const u32x4 (&ka)[2][4], const u32x4 (&vr)[8]) {
-      const int nt = min(32, t_end - t0);
-      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        s0 = mfma16x16x32(ka[0][s], qb[s], s0);
-        s1 = mfma16x16x32(ka[1][s], qb[s], s1);
-      }
-      float alpha;
-      const u32x4 pb = softmax_block(s0, s1, j, nt, p.scale_log2, m_run, l_run, alpha);
-      pv_block(acc, vr, pb, alpha);
-    };
-
-    // Blocks of this wave: t_begin + 32 * (wave + W * i), i < nblk, through a
-    // ring of S register stages: while block i is consumed, blocks
-    // i + 1 .. i + S - 1 are in flight (past the last block the request is the
-    // q-row dummy of load_block).  sched_barrier keeps the compiler from
-    // sinking the loads below the math (which would serialise them again).
-    const int first = t_begin + 32 * wave;
-    const int nblk = first < t_end ? (t_end - first + 32 * W - 1) / (32 * W) : 0;
-    if (nblk > 0) {
-      auto tblk = [&](int k) { return first + 32 * W * min(k, nblk - 1); };
-      u32x4 ka[S][2][4], vr[S][8];
-#pragma unroll
-      for (int st = 0; st < S - 1; ++st)
-        load_block(tblk(st), page_id(tblk(st)), st < nblk, ka[st], vr[st]);
-      int pid_next = page_id(tblk(S - 1));
-      for (int i = 0; i < nblk; i += S) {
-#pragma unroll
-        for (int st = 0; st < S; ++st) {
-          const int blk = i + st;
-          if (blk >= nblk) break;
-          const int nxt = blk + S - 1;
-          load_block(tblk(nxt), pid_next, nxt < nblk, ka[(st + S - 1) % S],
-                     vr[(st + S - 1) % S]);
-          pid_next = page_id(tblk(nxt + 1));
-          __builtin_amdgcn_sched_barrier(0);
-          compute_block(first + 32 * W * blk, ka[st], vr[st]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-    }
-
-    // Combine the waves: per head column, M = max m_w, L = sum l_w 2^(m_w - M).
+  // Writes the piece of kv row `row` held in (m_run, l_run, acc); `whole`:
+  // this wave consumed the row's first and last blocks, so the piece is the
+  // row's final partial.
+  auto flush = [&](int row, bool whole) __attribute__((always_inline)) {
     const float l_tot = wave_sum_xor16_32(l_run);
-    __syncthreads();  // the previous segment is done with the LDS
+    float* dst_out = whole ? p.out + (size_t)row * G * D
+                           : p.ws.part_out + (size_t)(split + row) * G * D;
+    float* dst_lse = whole ? p.lse + (size_t)row * G : p.ws.part_lse + (size_t)(split + row) * G;
     if (head_ok) {
-      if (j == 0) {
-        s_m[wave][n16] = m_run;
-        s_l[wave][n16] = l_tot;
+      const float inv = 1.f / l_tot;
+      float* o = dst_out + n16 * D + 32 * j;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ((float4*)(o + 8 * i))[0] =
+            make_float4(acc[0][i] * inv, acc[1][i] * inv, acc[2][i] * inv, acc[3][i] * inv);
+        ((float4*)(o + 8 * i))[1] =
+            make_float4(acc[4][i] * inv, acc[5][i] * inv, acc[6][i] * inv, acc[7][i] * inv);
       }
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s_acc[wave][n16][acc_col(j, i, e)] = acc[e][i];
+      if (j == 0) dst_lse[n16] = (m_run + __log2f(l_tot)) * kLn2;
     }
-    __syncthreads();
-    const int w_first = plan_owner(plan, row_start);
-    const int nseg = plan_owner(plan, row_end - 1) - w_first + 1;
-    const bool final_write = nseg == 1;
-    float* dst_out = final_write ? p.out + (size_t)q0 * D
-                                 : p.ws.part_out + (size_t)(g + row) * G * D;
-    float* dst_lse = final_write ? p.lse + q0 : p.ws.part_lse + (size_t)(g + row) * G;
-    for (int idx = tid; idx < G * D; idx += NT) {
-      const int h = idx / D;
-      const int d = idx - h * D;
-      float M = neg_inf();
-#pragma unroll
-      for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][h]);
-      float L = 0.f, o = 0.f;
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        const float sc = __builtin_amdgcn_exp2f(s_m[w][h] - M);
-        L += s_l[w][h] * sc;
-        o += s_acc[w][h][d] * sc;
-      }
-      const float ov = o / L;
-      const float lv = (M + __log2f(L)) * kLn2;
-      if (final_write || !COMBINE) {
-        dst_out[idx] = ov;
-        if (d == 0) dst_lse[h] = lv;
-      } else {  // read by the row's last workgroup, maybe on another XCD
-        st_agent(dst_out + idx, ov);
-        if (d == 0) st_agent(dst_lse + h, lv);
-      }
+  };
+
+  // Ring of S register stages: stage st holds the block k with k % S == st
+  // and its metadata mq[st].  Step k requests block k + S - 1 into stage
+  // (k + S - 1) % S, then runs block k's math; past the range's end the
+  // request is the q-row dummy of load_block.  After block k's math, qb
+  // takes the q rows of block k + 1's kv row (an L2 hit, issued every block
+  // so that no load in the loop is conditional), ahead of the next block
+  // requests, so waiting for it costs nothing extra.  sched_barrier keeps
+  // the compiler from sinking the loads below the math (which would
+  // serialise them again).  The loop body is a whole turn of the ring with no
+  // early exit (the last nblk % S blocks run after it): a path around one
+  // step would make the compiler assume that step's loads are still in
+  // flight when the ring comes back to it, and wait.
+  constexpr int S = kGqaStages;
+  int xb = x_begin;
+  fetch_meta(xb);
+  GqaBlock mq[S];
+  u32x4 ka[S][2][4], vr[S][8];
+  mq[0] = read_meta(0);
+  int run_row = mq[0].row;
+  bool run_first = (mq[0].nt & kFirst) != 0;  // the running row's first block was ours
+  bool run_last = false;                      // ... and its last block (so far)
+  load_q(mq[0].row);
+  static_for<0, S - 1>([&](auto i) __attribute__((always_inline)) {
+    constexpr int st = decltype(i)::value;
+    const bool valid = st < nblk;
+    if (st > 0) mq[st] = valid ? read_meta(st) : mq[0];
+    load_block(mq[st], valid, ka[st], vr[st]);
+  });
+  auto step = [&](auto stage, int k) __attribute__((always_inline)) {
+    constexpr int st = decltype(stage)::value;
+    constexpr int ld = (st + S - 1) % S;  // stage of the block requested now
+    constexpr int nx = (st + 1) % S;      // stage of block k + 1
+    const bool valid = k + S - 1 < nblk;
+    if (valid && x_begin + k + S - 1 - xb == 64) {
+      xb += 64;
+      fetch_meta(xb);
     }
-    if (COMBINE && !final_write && arrive_last(p.ws.counters + row, nseg, &s_flag)) {
-      reduce_rows<NT>(p.ws.part_out + (size_t)(w_first + row) * G * D,
-                      p.ws.part_lse + (size_t)(w_first + row) * G, G, G, D, nseg,
-                      p.out + (size_t)q0 * D, p.lse + q0, s_w, s_red);
-      if (tid == 0) p.ws.counters[row] = 0;
+    if (S > 1) mq[ld] = valid ? read_meta(x_begin + k + S - 1 - xb) : mq[st];
+    load_block(mq[ld], valid, ka[ld], vr[ld]);
+    __builtin_amdgcn_sched_barrier(0);
+    const GqaBlock& cur = mq[st];
+    if (cur.row != run_row) {
+      flush(run_row, run_first && run_last);
+      run_row = cur.row;
+      run_first = (cur.nt & kFirst) != 0;
+      m_run = neg_inf();
+      l_run = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    blk = seg_end;
-  }
+    run_last = (cur.nt & kLast) != 0;
+    compute_block(cur, ka[st], vr[st]);
+    __builtin_amdgcn_sched_barrier(0);
+    load_q(mq[nx].row);
+  };
+  int base = 0;
+  for (; base + S <= nblk; base += S)
+    static_for<0, S>([&](auto i) __attribute__((always_inline)) {
+      step(i, base + decltype(i)::value);
+    });
+  static_for<0, S - 1>([&](auto i) __attribute__((always_inline)) {
+    if (base + decltype(i)::value < nblk) step(i, base + decltype(i)::value);
+  });
+  flush(run_row, run_first && run_last);
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -277,22 +324,22 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 using namespace ws;
 
-// Workgroups of a GQA call: n_workgroups when given, else two per CU (the
-// kernel's occupancy), at most what the blocks of the longest possible batch
-// can feed with 8 blocks each, and no more than the in-kernel combine takes
-// for G heads per row.
-static int gqa_workgroups(int n_workgroups, int rows_kv, int G, int max_len) {
-  if (n_workgroups > 0) return n_workgroups;
+// Splits (waves) of a GQA call: n_splits when given, else two per CU (one
+// two-wave workgroup), at most what the blocks of the longest possible batch
+// can feed with 8 blocks each.  Measured on MI355X at 537 MB per launch: two
+// long streams per CU beat four or eight shorter ones (79.7 us against 80.5
+// and 84.0), and a third register stage gains nothing.
+static int gqa_splits(int n_splits, int rows_kv, int max_len) {
+  if (n_splits > 0) return n_splits;
   const long long max_blocks = (long long)rows_kv * ((max_len + 31) / 32);
-  const int n = choose_workgroups(0, kGqaStages <= 2 ? 2 : 1, max_blocks, 8);
-  return std::min(n, kReduceMaxWeights / G);
+  return choose_workgroups(0, kGqaSplitsPerCu, max_blocks, 8);
 }
 
 static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                       uint16_t* k_pages, uint16_t* v_pages, const int32_t* page_table,
                       const int32_t* len_in, int32_t* len_out, int B, int Hq, int Hkv,
                       int D, int page_size, int max_pages, int num_pages, int max_len,
-                      int n_workgroups, float scale, float* out, float* lse,
+                      int n_splits, float scale, float* out, float* lse,
                       void* workspace, size_t workspace_bytes, void* stream,
                       bool combine, const char* name) {
   if (!q || !k_pages || !v_pages || !page_table || !len_in || !out || !lse)
@@ -312,8 +359,10 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
                      "%s: bad paging page_size=%d max_pages=%d num_pages=%d max_len=%d "
                      "(page_size must be a multiple of 32 unless max_pages == 1)",
                      name, page_size, max_pages, num_pages, max_len);
-  if (n_workgroups < 0)
-    return set_error(WS_EINVAL, "%s: n_workgroups %d < 0", name, n_workgroups);
+  if ((long long)num_pages * Hkv * page_size > 0xffffffffLL)
+    return set_error(WS_EINVAL, "%s: pools of %lld tokens exceed the 32-bit token index", name,
+                     (long long)num_pages * Hkv * page_size);
+  if (n_splits < 0) return set_error(WS_EINVAL, "%s: n_splits %d < 0", name, n_splits);
   if (!aligned16(q) || !aligned16(k_pages) || !aligned16(v_pages) || !aligned16(out) ||
       (k_new && (!aligned16(k_new) || !aligned16(v_new))))
     return set_error(WS_EINVAL, "%s: buffers must be 16-byte aligned", name);
@@ -328,10 +377,10 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   if ((long long)rows_kv * ((max_len + 32) / 32) * 4096 >= (1LL << 31))
     return set_error(WS_EINVAL, "%s: %d kv rows of %d tokens exceed the block index range",
                      name, rows_kv, max_len);
-  const int n = gqa_workgroups(n_workgroups, rows_kv, G, max_len);
-  if ((long long)n * G > kReduceMaxWeights)
-    return set_error(WS_EINVAL, "%s: %d workgroups of %d heads exceed the combine (%d)",
-                     name, n, G, kReduceMaxWeights);
+  const int n = gqa_splits(n_splits, rows_kv, max_len);
+  if (n > kReduceMaxWeights)
+    return set_error(WS_EINVAL, "%s: %d splits exceed the merge's %d", name, n,
+                     kReduceMaxWeights);
   const size_t need = ws::workspace_bytes(rows_kv, G, D, n);
   if (!workspace || workspace_bytes < need)
     return set_error(WS_EWORKSPACE, "%s: workspace %zu < %zu bytes", name, workspace_bytes,
@@ -359,18 +408,15 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   prm.num_pages = num_pages;
   prm.cap = (int)std::min<long long>((long long)page_size * max_pages, 1LL << 30);
   prm.scale_log2 = scale * kLog2e;
+  prm.n_splits = n;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(n), block(64 * kGqaWaves);
-#define WS_GQA_CASE(GG)                                                                 \
-  case GG:                                                                              \
-    if (k_new && combine)                                                               \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, true, true>), grid, block, 0, s, prm);  \
-    else if (k_new)                                                                     \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, true, false>), grid, block, 0, s, prm); \
-    else if (combine)                                                                   \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, false, true>), grid, block, 0, s, prm); \
-    else                                                                                \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, false, false>), grid, block, 0, s, prm); \
+  const dim3 grid((n + kGqaWaves - 1) / kGqaWaves), block(64 * kGqaWaves);
+#define WS_GQA_CASE(GG)                                                           \
+  case GG:                                                                        \
+    if (k_new)                                                                    \
+      hipLaunchKernelGGL((gqa_decode_kernel<GG, true>), grid, block, 0, s, prm);  \
+    else                                                                          \
+      hipLaunchKernelGGL((gqa_decode_kernel<GG, false>), grid, block, 0, s, prm); \
     break;
   switch (G) {
     WS_GQA_CASE(1)
@@ -380,7 +426,14 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
     WS_GQA_CASE(16)
   }
 #undef WS_GQA_CASE
-  return check_launch(name);
+  int rc = check_launch(name);
+  if (rc != WS_OK || !combine) return rc;
+  // One-launch entry points: the rows held by several waves are combined by
+  // the split merge on the same stream, in place (D = 128: one column chunk
+  // per row, so each element is read and written by the same thread).
+  rc = merge_split_pieces(len_in, k_new ? 1 : 0, B, Hkv, G, D, prm.cap, n, out, lse, prm.ws,
+                          out, lse, s);
+  return rc != WS_OK ? rc : check_launch(name);
 }
 
 extern "C" int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
@@ -392,7 +445,7 @@ extern "C" int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
   int n;
   size_t bytes;
   if (kind == 0) {
-    n = gqa_workgroups(n_workgroups, rows_kv, heads, max_len);
+    n = gqa_splits(n_workgroups, rows_kv, max_len);
     bytes = ws::workspace_bytes(rows_kv, heads, kGqaD, n);
   } else {
     n = mla_workgroups(n_workgroups, rows_kv, max_len);

@@ -94,6 +94,7 @@ __global__ __launch_bounds__(128) void lse_merge_kernel(
 struct MergeSplitParams {
   const int32_t* gpu_len;
   int B, R, heads, Dv, cap, grid;
+  int add;  // lengths are gpu_len[b] + add (1 when gpu_len is a fused step's len_in)
   const float* out_g;
   const float* lse_g;
   const float* part_out;
@@ -122,8 +123,8 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   const int h = qrow - krow * p.heads;
   const int b = krow / p.R;
   const int r = krow - b * p.R;
-  const Plan plan = plan_build<64>(p.gpu_len, 0, p.cap, p.B, p.R, p.grid, s_pref, s_scan);
-  const int nbb = (plan_len(p.gpu_len, b, 0, p.cap) + 31) >> 5;
+  const Plan plan = plan_build<64>(p.gpu_len, p.add, p.cap, p.B, p.R, p.grid, s_pref, s_scan);
+  const int nbb = (plan_len(p.gpu_len, b, p.add, p.cap) + 31) >> 5;
   int n = 1;
   const float* src = p.out_g + (size_t)qrow * p.Dv;  // piece s at src + s * sstride
   const float* lsrc = p.lse_g + qrow;                // lse of piece s at lsrc[s * lstride]
@@ -242,8 +243,8 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     for (int j = 0; j < 8; ++j) wv[g][j] = wrow[j * 8 + lane8];
   }
   const Plan plan =
-      plan_build<kUvThreads>(p.gpu_len, 0, p.cap, p.B, 1, p.grid, s_pref, s_scan);
-  const int nbb = (plan_len(p.gpu_len, b, 0, p.cap) + 31) >> 5;
+      plan_build<kUvThreads>(p.gpu_len, p.add, p.cap, p.B, 1, p.grid, s_pref, s_scan);
+  const int nbb = (plan_len(p.gpu_len, b, p.add, p.cap) + 31) >> 5;
   int n = 1;
   const float* src = p.out_g + (size_t)qrow * p.Dv;
   const float* lsrc = p.lse_g + qrow;
@@ -360,6 +361,39 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
   }
 }
 
+
+// Split combine without a host partial (the one-launch GQA entry points):
+// one 64-lane workgroup per output row, Dv <= 256 so a row is one column
+// chunk and out/lse may alias out_g/lse_g.
+int merge_split_pieces(const int32_t* len, int len_add, int B, int R, int heads, int Dv,
+                       int cap, int n, const float* out_g, const float* lse_g,
+                       const SplitWorkspace& w, float* out, float* lse, hipStream_t stream) {
+  if (Dv > 4 * kMergeChunk4)
+    return set_error(WS_EINVAL, "merge_split_pieces: Dv %d > %d", Dv, 4 * kMergeChunk4);
+  MergeSplitParams prm;
+  prm.gpu_len = len;
+  prm.B = B;
+  prm.R = R;
+  prm.heads = heads;
+  prm.Dv = Dv;
+  prm.cap = cap;
+  prm.grid = n;
+  prm.add = len_add;
+  prm.out_g = out_g;
+  prm.lse_g = lse_g;
+  prm.part_out = w.part_out;
+  prm.part_lse = w.part_lse;
+  prm.b_out = nullptr;
+  prm.b_aux0 = nullptr;
+  prm.b_aux1 = nullptr;
+  prm.out_bf16 = nullptr;
+  prm.out_f32 = out;
+  prm.lse_out = lse;
+  hipLaunchKernelGGL(merge_split_kernel<-1>, dim3((unsigned)(B * R * heads)), dim3(64), 0,
+                     stream, prm);
+  return WS_OK;
+}
+
 }  // namespace ws
 
 using namespace ws;
@@ -406,6 +440,7 @@ extern "C" int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, i
   prm.Dv = Dv;
   prm.cap = page_capacity;
   prm.grid = n_workgroups;
+  prm.add = 0;
   prm.out_g = out_g;
   prm.lse_g = lse_g;
   prm.part_out = w.part_out;
@@ -515,6 +550,7 @@ extern "C" int ws_mla_merge_split_uv(const int32_t* gpu_len, int B, int heads,
   prm.Dv = Dv;
   prm.cap = page_capacity;
   prm.grid = n_workgroups;
+  prm.add = 0;
   prm.out_g = out_g;
   prm.lse_g = lse_g;
   prm.part_out = w.part_out;

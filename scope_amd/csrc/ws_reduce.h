@@ -59,6 +59,13 @@ __host__ __device__ inline SplitWorkspace carve_workspace(void* base, int rows_k
 int choose_workgroups(int n_workgroups, int per_cu, long long max_blocks, int min_blocks);
 // Workgroups of an MLA call (ws_mla.hip).
 int mla_workgroups(int n_workgroups, int B, int max_len);
+// Combines the pieces of a split decode step with no host partial: rows held
+// by several splits are LSE-combined from the workspace, the others copied;
+// lengths are len[b] + len_add; out/lse may alias out_g/lse_g (Dv <= 256).
+// Launches on `stream`; returns WS_OK or an error code (ws_merge.hip).
+int merge_split_pieces(const int32_t* len, int len_add, int B, int R, int heads, int Dv,
+                       int cap, int n, const float* out_g, const float* lse_g,
+                       const SplitWorkspace& w, float* out, float* lse, hipStream_t stream);
 
 // Partials travel between workgroups (possibly on different XCDs, whose L2
 // caches are not coherent with each other) through device-scope atomic

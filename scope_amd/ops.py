@@ -172,9 +172,11 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
 def decode_plan(kind: int, rows_kv: int, heads: int, max_len: int,
                 n_workgroups: int = 0):
-    """(n_workgroups, workspace_bytes) of a decode call: kind 0 = GQA
+    """(n_splits, workspace_bytes) of a decode call: kind 0 = GQA
     (rows_kv = B * Hkv, heads = group size), 1 = MLA (rows_kv = B, heads = 16).
-    n_workgroups 0 lets the library choose for the current device."""
+    A split is one wave for GQA and one workgroup for MLA; the keyword keeps
+    the name n_workgroups.  0 lets the library choose for the current
+    device."""
     n, wsb = ctypes.c_int(0), ctypes.c_size_t(0)
     _check(lib().ws_decode_plan(kind, rows_kv, heads, max_len, n_workgroups,
                                 ctypes.byref(n), ctypes.byref(wsb)), "ws_decode_plan")
@@ -401,7 +403,7 @@ def mla_append_decode_partial(q_nope, q_pe, c_new, pe_new, latent_pages, page_ta
 
 class SplitStep:
     """A deferred-combine decode step: its GPU pieces (out_g/lse_g finals and
-    the workgroup partials in `workspace`) wait for merge_split.  Holds every
+    the split partials in `workspace`) wait for merge_split.  Holds every
     buffer the merge reads, so the step's workspace is not reused early."""
 
     def __init__(self, gpu_len, B, rows_per_seq, heads, Dv, cap, nwg, out_g, lse_g,
@@ -421,7 +423,7 @@ def gqa_append_decode_split(q, k_new, v_new, k_pages, v_pages, page_table, len_i
                             len_out, scale, max_len, n_workgroups=0, workspace=None):
     """Deferred-combine fused step (ws_gqa_append_decode_split): append and
     attend like gqa_append_decode_partial, but rows spread over several
-    workgroups are combined later by merge_split.  len_out is required (the
+    splits (waves) are combined later by merge_split.  len_out is required (the
     merge reads the post-step lengths).  Returns a SplitStep."""
     dev = k_pages.device
     _require(q, "q", torch.bfloat16, dev, 3)

@@ -42,10 +42,10 @@ def test_version_and_plan():
     n, wsb = ops.decode_plan(1, 8, 16, 16384, 64)
     assert n == 64 and wsb == 65536 + pad((64 + 8) * 16 * 4) + (64 + 8) * 16 * 512 * 4
     # the library's choice never exceeds the blocks available (8 per GQA
-    # workgroup, 4 per MLA workgroup) nor the combine's 4096 weights
+    # split, i.e. per wave) nor the merge's 4096 splits
     for rows, G, L in ((128, 4, 15773), (16, 8, 131072), (4, 8, 4096), (1, 1, 1), (2, 16, 1 << 20)):
         n, _ = ops.decode_plan(0, rows, G, L, 0)
-        assert 1 <= n <= max(1, -(-rows * -(-L // 32) // 8)) and n * G <= 4096
+        assert 1 <= n <= max(1, -(-rows * -(-L // 32) // 8)) and n <= 4096
     n, _ = ops.decode_plan(1, 8, 16, 8192, 0)
     assert 1 <= n <= 8 * 256 // 4
     with pytest.raises(ops.WsError):

@@ -364,13 +364,13 @@ def test_gqa_many_workgroups_in_kernel_reduce():
     assert _counters_zero()
 
 
-def test_gqa_combine_capacity_error():
-    # 1000 workgroups x 16 heads > 4096 weights of the in-kernel combine:
-    # rejected on the host before any launch
+def test_gqa_split_capacity_error():
+    # 5000 splits > the 4096 pieces a merge takes: rejected on the host before
+    # any launch
     k_pages, v_pages, pt, gl, ks, vs = gqa_pool([64], 1, 128, 64, seed=2)
     q = bf16_randn((1, 16, 128), 3).to(DEV)
     with pytest.raises(ops.WsError, match="exceed"):
-        ops.gqa_decode_partial(q, k_pages, v_pages, pt, gl, 0.1, 64, n_workgroups=1000)
+        ops.gqa_decode_partial(q, k_pages, v_pages, pt, gl, 0.1, 64, n_workgroups=5000)
 
 
 def test_workspace_clear_kernel():
