@@ -13,8 +13,9 @@
 //        operand layout (lane = head column, 8 k-slots) once two 16-token
 //        tiles are placed side by side in k.
 // Softmax is online in the log2 domain (scores pre-multiplied by
-// scale * log2(e)); the running max is shared by the four lanes of a head
-// column with two xor-shuffles per 32-token block.  P is rounded to bf16 for
+// scale * log2(e)); the block max is shared by the four lanes of a head
+// column with two lane exchanges per 32-token block, and the accumulators are
+// rescaled lazily (kLazyRescaleLog2).  P is rounded to bf16 for
 // the PV MFMA (as the reference's GPU partial rounds its probabilities,
 // roofline/bench_resident_kv.py:156) while the softmax sum stays fp32.
 #pragma once
@@ -33,14 +34,23 @@ __device__ __forceinline__ int pv_token(int i, int j) {
   return 16 * (i >> 2) + 4 * j + (i & 3);
 }
 
+// Lazy rescaling: the accumulators stay relative to a reference max m_run
+// that moves only when some head's block max exceeds it by more than this
+// (log2 domain), so most blocks skip the rescale of the accumulators.  The
+// probabilities then stay below 2^8: exact enough in bf16 (a relative
+// format) and far from any fp32 limit.
+constexpr float kLazyRescaleLog2 = 8.f;
+
 // Online-softmax update of one 32-token block.  s0/s1 are the QK accumulators
 // of tokens [0,16) and [16,32) (lane holds tokens 4j+i of head n16); nt is the
-// number of valid tokens.  Returns P^T packed as the PV B operand and alpha,
-// the rescale factor of the previous accumulators.
+// number of valid tokens.  Returns P^T packed as the PV B operand; `rescale`
+// (the same in every lane) says whether the reference max moved, in which
+// case alpha is the factor for the previous accumulators.  Every lane of the
+// wave must be active.
 __device__ __forceinline__ u32x4 softmax_block(const f32x4& s0, const f32x4& s1,
                                                int j, int nt, float scale_log2,
                                                float& m_run, float& l_run,
-                                               float& alpha) {
+                                               float& alpha, bool& rescale) {
   float x[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -51,17 +61,22 @@ __device__ __forceinline__ u32x4 softmax_block(const f32x4& s0, const f32x4& s1,
 #pragma unroll
   for (int i = 1; i < 8; ++i) bm = fmaxf(bm, x[i]);
   bm = wave_max_xor16_32(bm);
-  const float m_new = fmaxf(m_run, bm);
-  alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+  rescale = __builtin_amdgcn_ballot_w64(bm > m_run + kLazyRescaleLog2) != 0;
+  alpha = 1.f;
+  if (rescale) {
+    const float m_new = fmaxf(m_run, bm);
+    alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    l_run *= alpha;
+    m_run = m_new;
+  }
   float p[8];
   float ps = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    p[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+    p[i] = __builtin_amdgcn_exp2f(x[i] - m_run);
     ps += p[i];
   }
-  l_run = l_run * alpha + ps;
-  m_run = m_new;
+  l_run += ps;
   u32x4 pb;
   pb[0] = pack_bf16x2(p[0], p[1]);
   pb[1] = pack_bf16x2(p[2], p[3]);
@@ -72,9 +87,14 @@ __device__ __forceinline__ u32x4 softmax_block(const f32x4& s0, const f32x4& s1,
 
 // PV update of 8 output tiles from the 8 V vectors vr[i] (token pv_token(i,j),
 // 8 columns starting at 8*n16 of the lane's 128-column slice).  Tile e covers
-// columns 8*m + e of the slice.
+// columns 8*m + e of the slice.  The accumulators are scaled by alpha first
+// when the softmax moved its reference max.
 __device__ __forceinline__ void pv_block(f32x4 (&acc)[8], const u32x4 (&vr)[8],
-                                         const u32x4& pb, float alpha) {
+                                         const u32x4& pb, float alpha, bool rescale) {
+  if (rescale) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = acc[e] * alpha;
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int w = e >> 1;
@@ -90,7 +110,6 @@ __device__ __forceinline__ void pv_block(f32x4 (&acc)[8], const u32x4 (&vr)[8],
       va[2] = pair_lo(vr[4][w], vr[5][w]);
       va[3] = pair_lo(vr[6][w], vr[7][w]);
     }
-    acc[e] = acc[e] * alpha;
     acc[e] = mfma16x16x32(va, pb, acc[e]);
   }
 }

@@ -62,15 +62,36 @@ __device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b,
       __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Lane l's value and lane l ^ 16's (l ^ 32's) value, from gfx950's
+// v_permlane16_swap (v_permlane32_swap): plain VALU exchanges, where a
+// shuffle would be an LDS-crossbar round trip on the softmax's critical path.
+// With both operands v, the swap leaves, in every lane, the lower-row (lower-
+// half) value in the first result and the upper one in the second.
+__device__ __forceinline__ void pair_xor16(float v, float& lo, float& hi) {
+  const uint32_t a = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(a, a, false, false);
+  lo = __builtin_bit_cast(float, (uint32_t)r[0]);
+  hi = __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+__device__ __forceinline__ void pair_xor32(float v, float& lo, float& hi) {
+  const uint32_t a = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+  lo = __builtin_bit_cast(float, (uint32_t)r[0]);
+  hi = __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+// Max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lanes of a head
+// column), every lane of the wave active.
 __device__ __forceinline__ float wave_max_xor16_32(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  float lo, hi;
+  pair_xor16(v, lo, hi);
+  pair_xor32(fmaxf(lo, hi), lo, hi);
+  return fmaxf(lo, hi);
 }
 __device__ __forceinline__ float wave_sum_xor16_32(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  float lo, hi;
+  pair_xor16(v, lo, hi);
+  pair_xor32(lo + hi, lo, hi);
+  return lo + hi;
 }
 
 }  // namespace ws

@@ -204,9 +204,10 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
       s1 = mfma16x16x32(ka[1][s], qb[s], s1);
     }
     float alpha;
-    const u32x4 pb =
-        softmax_block(s0, s1, j, m.nt & kNtMask, p.scale_log2, m_run, l_run, alpha);
-    pv_block(acc, vr, pb, alpha);
+    bool rescale;
+    const u32x4 pb = softmax_block(s0, s1, j, m.nt & kNtMask, p.scale_log2, m_run, l_run,
+                                   alpha, rescale);
+    pv_block(acc, vr, pb, alpha, rescale);
     // Fused append: the new token's K row sits in lanes n16 == nr % 16 of
     // ka[nr / 16] (16 bytes per (lane, s)), its V row in vr[4 (nr / 16) +
     // nr % 4] of the lanes j == (nr % 16) / 4 (8 columns each).

@@ -21,6 +21,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "ws_attn.h"
 #include "ws_plan.h"
@@ -83,13 +84,13 @@ template <bool APPEND>
 __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
   constexpr int NT = 256;
   constexpr int add = APPEND ? 1 : 0;
-  __shared__ u32x4 s_lat[2][kTileChunks];  // the block being consumed and the next
-  __shared__ f32x4 sbuf[2][2][64];         // [latent half][token tile][lane] score partials
+  __shared__ u32x4 s_lat[3][kTileChunks];  // block k (PV), k + 1 (QK), k + 2 (being written)
+  __shared__ f32x4 sbuf[2][2][2][64];      // [block parity][latent half][token tile][lane]
   __shared__ int s_pref[kMaxSeqs + 1];
   __shared__ int s_scan[NT / 64 + 1];
   const int g = blockIdx.x;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int n16 = lane & 15;
   const int j = lane >> 4;
@@ -151,81 +152,140 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     float m_run = neg_inf();
     float l_run = 0.f;
 
-    // Block k of the segment, as this thread's 9 chunks (chunk c = tid + 256 u
-    // is row c / 72, 16-byte column c % 72): one fully coalesced 4 KB read per
-    // instruction across the workgroup.  Rows past t_end repeat the last
-    // valid row (masked in the softmax); past the segment's last block every
-    // lane reads the first 16 bytes of q_nope instead (a cache hit).
+    // Block k of the segment, as this thread's 9 chunks: the 32 rows' c_kv
+    // parts are 8 loads of 4 whole rows (1 KB per wave) and their k_pe parts
+    // one load.  Rows past t_end repeat the last valid row (masked in the
+    // softmax); past the segment's last block every lane reads the first 16
+    // bytes of q_nope instead (a cache hit).
+    // Addresses are selected as byte offsets from one global base (a pointer
+    // select per chunk compiles to divergent branches, and an integer round
+    // trip loses the address space, turning the loads into flat loads whose
+    // completion the compiler can only wait for all at once).
+    const char* g0 = (const char*)p.latent;
+    const long long nc_off =
+        APPEND ? (const char*)(p.c_new + (size_t)b * p.c_stride) - g0 : 0;
+    const long long npe_off =
+        APPEND ? (const char*)(p.pe_new + (size_t)b * p.pe_stride) - g0 - 16 * (kMlaC / 8) : 0;
+    const long long dummy_off = (const char*)dummy - g0;
+    const int pe_row = tid >> 3;
+    const int pe_col = kMlaC / 8 + (tid & 7);
+    // Page ids of the segment's blocks, 64 at a time (lane l: block
+    // pid_base + l), read with readlane: the ring issues no load whose
+    // address waits on another load (a page-table read per block would make
+    // every block wait for all loads in flight).
+    int pid_base = 0;
+    int m_pid = 0;
+    auto fetch_pids = [&]() {
+      const int t0 = t_begin + 32 * min(pid_base + lane, nblk - 1);
+      m_pid = clamp_page(pt[t0 / p.page_size], p.num_pages);
+    };
+    fetch_pids();
     auto gload = [&](int k, u32x4 (&dst)[kChunksPerThread]) {
       const bool valid = k < nblk;
-      const int t0 = t_begin + 32 * min(k, nblk - 1);
+      const int kc = min(k, nblk - 1);
+      if (kc - pid_base >= 64) {
+        pid_base += 64;
+        fetch_pids();
+      }
+      const int t0 = t_begin + 32 * kc;
       const int page = t0 / p.page_size;
-      const int pid = clamp_page(pt[page], p.num_pages);
-      const uint16_t* lb =
-          p.latent + ((size_t)pid * p.page_size + (t0 - page * p.page_size)) * (size_t)kMlaL;
+      const int pid = __builtin_amdgcn_readlane(m_pid, kc - pid_base);
+      const long long lb =
+          (long long)((size_t)pid * p.page_size + (t0 - page * p.page_size)) * (kMlaL * 2);
       const int last = min(32, t_end - t0) - 1;
       const int new_r = (APPEND && valid) ? len_old - t0 : -1;
+      // Chunks 0..7 of a thread: row 4 u + wave, 16-byte column `lane` of
+      // the row's c_kv part (each load reads whole rows, so its row, clamp
+      // and new-token test are uniform); chunk 8: row tid / 8, k_pe column
+      // tid % 8.
 #pragma unroll
-      for (int u = 0; u < kChunksPerThread; ++u) {
-        const int c = tid + NT * u;
-        const int r = min(c / 72, last);
-        const int q = c - (c / 72) * 72;
-        const u32x4* src = !valid ? dummy
-                           : (APPEND && r == new_r) ? new_chunk(p, b, q)
-                                                    : (const u32x4*)(lb + (size_t)r * kMlaL) + q;
-        dst[u] = ld_stream(src);
+      for (int u = 0; u < 8; ++u) {
+        const int r = min(4 * u + wave, last);
+        const long long row = (APPEND && r == new_r) ? nc_off : lb + r * (kMlaL * 2);
+        const long long off = valid ? row + 16 * lane : dummy_off;
+        dst[u] = ld_stream(g0 + off);
+      }
+      {
+        const int r = min(pe_row, last);
+        long long off = lb + r * (kMlaL * 2) + 16 * pe_col;
+        if (APPEND) off = r == new_r ? npe_off + 16 * pe_col : off;
+        off = valid ? off : dummy_off;
+        dst[8] = ld_stream(g0 + off);
       }
     };
     auto lwrite = [&](u32x4* tile, const u32x4 (&src)[kChunksPerThread]) {
 #pragma unroll
-      for (int u = 0; u < kChunksPerThread; ++u) {
-        const int c = tid + NT * u;
-        tile[(c / 72) * kRowChunks + (c - (c / 72) * 72)] = src[u];
-      }
+      for (int u = 0; u < 8; ++u) tile[(4 * u + wave) * kRowChunks + lane] = src[u];
+      tile[pe_row * kRowChunks + pe_col] = src[8];
     };
-    // One block from its LDS tile: QK partial of token tile tt over latent
-    // half kh, score partials meet in LDS, shared softmax, PV of this wave's
-    // 128 output columns.
-    auto compute = [&](int k, const u32x4* tile) {
-      const int nt = min(32, t_end - (t_begin + 32 * k));
+    // QK partial of block k from its LDS tile: token tile tt over latent
+    // half kh, into score buffer `par`.
+    auto qk = [&](const u32x4* tile, int par) {
       const u32x4* krow = tile + (16 * tt + n16) * kRowChunks + j;
       f32x4 sp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < 9; ++u) sp = mfma16x16x32(krow[4 * (9 * kh + u)], qb[u], sp);
-      sbuf[kh][tt][lane] = sp;
-      __syncthreads();
-      const f32x4 s0 = sbuf[0][0][lane] + sbuf[1][0][lane];
-      const f32x4 s1 = sbuf[0][1][lane] + sbuf[1][1][lane];
+      sbuf[par][kh][tt][lane] = sp;
+    };
+    // Softmax of block k from the four score partials in buffer `par`, then
+    // PV of this wave's 128 output columns from the block's tile.
+    auto finish = [&](int k, const u32x4* tile, int par) {
+      const int nt = min(32, t_end - (t_begin + 32 * k));
+      const f32x4 s0 = sbuf[par][0][0][lane] + sbuf[par][1][0][lane];
+      const f32x4 s1 = sbuf[par][0][1][lane] + sbuf[par][1][1][lane];
       float alpha;
-      const u32x4 pb = softmax_block(s0, s1, j, nt, p.scale_log2, m_run, l_run, alpha);
+      bool rescale;
+      const u32x4 pb =
+          softmax_block(s0, s1, j, nt, p.scale_log2, m_run, l_run, alpha, rescale);
       u32x4 vr[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) vr[i] = tile[pv_token(i, j) * kRowChunks + (col0 >> 3) + n16];
-      pv_block(acc, vr, pb, alpha);
+      pv_block(acc, vr, pb, alpha, rescale);
     };
 
-    // Pipeline: registers hold blocks k + 1 .. k + kMlaDepth in flight while
-    // block k is consumed from one LDS tile and block k + 1 is written to the
-    // other.  Block m lives in register slot m % kMlaDepth; the loop is
-    // unrolled by kMlaDepth so every slot index is static.
+    // Pipeline over three LDS tiles (block m in tile m % 3) and three
+    // register slots (block m in slot m % 3).  Step k, between two barriers:
+    // block k + 2 from its register slot into its tile and the request of
+    // block k + 5 into that slot (first, so the requests queue while the math
+    // runs), softmax + PV of block k (its scores were exchanged before the
+    // barrier), QK of block k + 1 into the other score buffer (independent of
+    // block k's math, so the two overlap).  One
+    // barrier per block; blocks k + 3 .. k + 5 are in flight meanwhile.  The
+    // loop body is a whole turn of the ring with no early exit (the last
+    // nblk % 3 blocks run after it): a path around part of the turn makes the
+    // compiler assume the younger slots' loads may be the ones a slot write
+    // waits for, and it then waits for every load in flight.
     u32x4 st[kMlaDepth][kChunksPerThread];
 #pragma unroll
     for (int m = 0; m < kMlaDepth; ++m) gload(m, st[m]);
     __syncthreads();  // the previous segment is done with the tiles and sbuf
     lwrite(s_lat[0], st[0]);
-    gload(kMlaDepth, st[0]);
+    gload(3, st[0]);
+    if (nblk > 1) lwrite(s_lat[1], st[1]);
+    gload(4, st[1]);
     __syncthreads();
-    for (int k = 0; k < nblk; k += kMlaDepth) {
-#pragma unroll
-      for (int s = 0; s < kMlaDepth; ++s) {
-        const int kk = k + s;
-        if (kk >= nblk) break;
-        compute(kk, s_lat[kk & 1]);
-        if (kk + 1 < nblk) lwrite(s_lat[(kk + 1) & 1], st[(s + 1) % kMlaDepth]);
-        gload(kk + 1 + kMlaDepth, st[(s + 1) % kMlaDepth]);
-        __syncthreads();
-      }
+    qk(s_lat[0], 0);
+    __syncthreads();
+    auto step = [&](auto slot, int kk) {
+      constexpr int s = decltype(slot)::value;  // kk % 3
+      if (kk + 2 < nblk) lwrite(s_lat[(s + 2) % 3], st[(s + 2) % 3]);
+      gload(kk + 5, st[(s + 2) % 3]);
+      finish(kk, s_lat[s], kk & 1);
+      if (kk + 1 < nblk) qk(s_lat[(s + 1) % 3], (kk + 1) & 1);
+      __syncthreads();
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    static_assert(kMlaDepth == 3, "the ring turn below is written for three slots");
+    int k = 0;
+    for (; k + 3 <= nblk; k += 3) {
+      step(S0{}, k);
+      step(S1{}, k + 1);
+      step(S2{}, k + 2);
     }
+    if (k < nblk) step(S0{}, k);
+    if (k + 1 < nblk) step(S1{}, k + 1);
 
     const float l_tot = wave_sum_xor16_32(l_run);
     const float inv_l = 1.f / l_tot;
