@@ -189,9 +189,9 @@ class GqaGpuPartition(_PagedBase):
 
     def step_split(self, layer: int, q: torch.Tensor, k_new: torch.Tensor,
                    v_new: torch.Tensor, scale: float, n_workgroups=0) -> "ops.SplitStep":
-        """step() with the combine of rows shared by several workgroups left to
-        ops.merge_split, which does it in the same launch as the merge with the
-        host partial.  Returns the ops.SplitStep to finish."""
+        """step() with the combine of rows shared by several splits (one wave
+        each) left to ops.merge_split, which does it in the same launch as the
+        merge with the host partial.  Returns the ops.SplitStep to finish."""
         for b in range(self.batch):
             self.reserve(b, int(self.lens[layer, b]) + 1)
         max_len = self.max_len(layer) + 1
