@@ -15,9 +15,9 @@ Reported on one JSON line (stdout):
   value      algorithmic HBM GB/s of the whole step (bytes below / step time)
   ms_per_step, us_per_layer
   roofline   the fused append + GQA partial kernel: algorithmic bytes per
-             launch / its mean duration from HIP events around every launch of
-             the timed region,
-             against the 8 TB/s HBM peak; traffic from the committed rocprofv3
+             launch / its mean duration from timing-only HIP events
+             (hipEventDisableSystemFence) around every launch of the timed
+             region, against the 8 TB/s HBM peak; traffic from the committed rocprofv3
              FETCH_SIZE / WRITE_SIZE summary when one exists for this workload
   cpu_baseline  the oracle's C restatement of the reference CPU kernel over a
              bounded sample of the same GPU-share tokens, on the host cores
@@ -98,14 +98,77 @@ def _randn_bf16(shape, gen, sigma, dev):
     return t
 
 
-class _Timer:
-    """Per-launch HIP events on the stream the kernels are launched on."""
+_HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # hip_runtime_api.h
+_hip_rt = None
 
-    def __init__(self, n):
+
+def _hip_runtime():
+    """The HIP runtime torch itself loaded (its streams are only valid there),
+    found by path in this process's mappings."""
+    global _hip_rt
+    if _hip_rt is None:
         import torch
 
-        self.a = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-        self.b = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        torch.cuda.init()
+        with open("/proc/self/maps") as f:
+            paths = {ln.split()[-1] for ln in f if "libamdhip64.so" in ln}
+        if not paths:
+            raise RuntimeError("libamdhip64.so is not loaded")
+        L = ctypes.CDLL(sorted(paths)[0])
+        vp = ctypes.c_void_p
+        L.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(vp), ctypes.c_uint]
+        L.hipEventRecord.argtypes = [vp, vp]
+        L.hipEventSynchronize.argtypes = [vp]
+        L.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        L.hipEventDestroy.argtypes = [vp]
+        _hip_rt = L
+    return _hip_rt
+
+
+class HipTimingEvent:
+    """A timing-only HIP event (hipEventDisableSystemFence) recorded on the
+    current torch stream.  A default event's record also performs a
+    system-scope release (an L2 writeback so the host could read the results),
+    which lands in the launch it brackets: 2-3 us of a 60 us kernel that
+    writes 8 MB.  Device work ordered after the kernel on the same stream needs
+    no such fence, so the timing events skip it."""
+
+    def __init__(self):
+        self._rt = _hip_runtime()
+        self.ev = ctypes.c_void_p()
+        rc = self._rt.hipEventCreateWithFlags(ctypes.byref(self.ev),
+                                              _HIP_EVENT_DISABLE_SYSTEM_FENCE)
+        if rc:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+
+    def record(self):
+        import torch
+
+        rc = self._rt.hipEventRecord(self.ev,
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_time(self, end):
+        """Milliseconds from this event to `end` (waits for `end`)."""
+        ms = ctypes.c_float()
+        rc = (self._rt.hipEventSynchronize(end.ev)
+              or self._rt.hipEventElapsedTime(ctypes.byref(ms), self.ev, end.ev))
+        if rc:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def __del__(self):
+        if self.ev:
+            self._rt.hipEventDestroy(self.ev)
+
+
+class _Timer:
+    """Per-launch timing events on the stream the kernels are launched on."""
+
+    def __init__(self, n):
+        self.a = [HipTimingEvent() for _ in range(n)]
+        self.b = [HipTimingEvent() for _ in range(n)]
 
     def mean_us(self, n):
         return 1e3 * sum(self.a[i].elapsed_time(self.b[i]) for i in range(n)) / n
@@ -179,8 +242,8 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
     timer = _Timer(steps)
-    t_ev0 = torch.cuda.Event(enable_timing=True)
-    t_ev1 = torch.cuda.Event(enable_timing=True)
+    t_ev0 = HipTimingEvent()
+    t_ev1 = HipTimingEvent()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     t_ev0.record()
@@ -284,8 +347,8 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label, wg=0):
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
     timer = _Timer(steps)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    e0 = HipTimingEvent()
+    e1 = HipTimingEvent()
     torch.cuda.synchronize()
     e0.record()
     for i in range(steps):
@@ -480,8 +543,8 @@ def epilogue_bench(*, B, L, steps, seed, dev, label):
     for name, fn in (("merge_then_bmm_us", unfused), ("fused_uv_us", fused)):
         for _ in range(5):
             fn()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
+        e0 = HipTimingEvent()
+        e1 = HipTimingEvent()
         torch.cuda.synchronize()
         e0.record()
         for _ in range(steps):
@@ -609,8 +672,8 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
     p = lambda t: ctypes.c_void_p(t.data_ptr())
     cap = PAGE * g_table.shape[1]
     ev_q = torch.cuda.Event()
-    e_a = [torch.cuda.Event(enable_timing=True) for _ in range(layers)]
-    e_b = [torch.cuda.Event(enable_timing=True) for _ in range(layers)]
+    e_a = [HipTimingEvent() for _ in range(layers)]
+    e_b = [HipTimingEvent() for _ in range(layers)]
     f_step, f_merge = L.ws_mla_append_decode_split, L.ws_merge_split
 
     def one_step(i, timed):

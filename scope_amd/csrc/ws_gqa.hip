@@ -90,6 +90,7 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
   constexpr int NT = 64 * W;
   constexpr int add = APPEND ? 1 : 0;
   __shared__ int s_pref[kMaxSeqs + 1];
+  __shared__ int s_len[kMaxSeqs];
   __shared__ int s_scan[W + 1];
 
   const int tid = threadIdx.x;
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
   if (APPEND && p.len_out && blockIdx.x == 0)
     for (int b = tid; b < p.B; b += NT) p.len_out[b] = plan_len(p.len_in, b, add, p.cap);
   const Plan plan =
-      plan_build<NT>(p.len_in, add, p.cap, p.B, p.Hkv, p.n_splits, s_pref, s_scan);
+      plan_build<NT>(p.len_in, add, p.cap, p.B, p.Hkv, p.n_splits, s_pref, s_scan, s_len);
   if (blockIdx.x == 0) {  // sequences without tokens: the empty partial (0, -inf)
     for (int b = 0; b < p.B; ++b) {
       if (s_pref[b + 1] != s_pref[b]) continue;
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
       if (s_pref[mid] <= x) lo = mid;
       else hi = mid - 1;
     }
-    const int len = plan_len(p.len_in, lo, add, p.cap);
+    const int len = s_len[lo];
     const int nbb = (len + 31) >> 5;
     const int rel = x - s_pref[lo];
     const int kvh = rel / nbb;

@@ -15,9 +15,10 @@
 // sequence) and mla_reduce_kernel combines them: a sequence carries 32 KB of
 // partial per workgroup, more than one workgroup combines quickly.
 //
-// With c_new != nullptr, token len_in[b] is the new latent: it is read from
-// c_new/pe_new, the workgroup whose segment holds it writes it into its page
-// slot, and len_out[b] = len_in[b] + 1.
+// With c_new != nullptr, token len_in[b] is the new latent: the ring reads
+// its row from c_new/pe_new, the workgroup whose segment holds it writes it
+// from its LDS tile into its page slot at the segment's end, and
+// len_out[b] = len_in[b] + 1.
 #include <math.h>
 
 #include <algorithm>
@@ -52,12 +53,6 @@ struct MlaParams {
   float scale_log2;
 };
 
-// Pointer to the 16-byte chunk q (0..71) of the new token's latent.
-__device__ __forceinline__ const u32x4* new_chunk(const MlaParams& p, int b, int q) {
-  return q < kMlaC / 8 ? (const u32x4*)(p.c_new + (size_t)b * p.c_stride) + q
-                       : (const u32x4*)(p.pe_new + (size_t)b * p.pe_stride) + (q - kMlaC / 8);
-}
-
 __device__ __forceinline__ void store_cols(float* __restrict__ dst, const f32x4 (&acc)[8],
                                            int j, float inv_l) {
 #pragma unroll
@@ -87,6 +82,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
   __shared__ u32x4 s_lat[3][kTileChunks];  // block k (PV), k + 1 (QK), k + 2 (being written)
   __shared__ f32x4 sbuf[2][2][2][64];      // [block parity][latent half][token tile][lane]
   __shared__ int s_pref[kMaxSeqs + 1];
+  __shared__ int s_len[kMaxSeqs];
   __shared__ int s_scan[NT / 64 + 1];
   const int g = blockIdx.x;
   const int tid = threadIdx.x;
@@ -100,7 +96,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
 
   if (APPEND && p.len_out && g == 0)
     for (int b = tid; b < p.B; b += NT) p.len_out[b] = plan_len(p.len_in, b, add, p.cap);
-  const Plan plan = plan_build<NT>(p.len_in, add, p.cap, p.B, 1, gridDim.x, s_pref, s_scan);
+  const Plan plan =
+      plan_build<NT>(p.len_in, add, p.cap, p.B, 1, gridDim.x, s_pref, s_scan, s_len);
   if (g == 0) {  // sequences without tokens: the empty partial (0, -inf)
     for (int b = 0; b < p.B; ++b) {
       if (s_pref[b + 1] != s_pref[b]) continue;
@@ -110,13 +107,14 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     }
   }
   if (g >= plan.n) return;
+  const int blk_begin = plan_start(plan, g);
   const int blk_end = plan_start(plan, g + 1);
-  int blk = plan_start(plan, g);
+  int blk = blk_begin;
   const u32x4* dummy = (const u32x4*)p.q_nope;
 
   while (blk < blk_end) {
     const int b = plan_seq(s_pref, p.B, blk);
-    const int len = uniform(plan_len(p.len_in, b, add, p.cap));
+    const int len = uniform(s_len[b]);
     const int len_old = len - add;
     const int row_start = uniform(s_pref[b]);
     const int row_end = uniform(s_pref[b + 1]);
@@ -127,24 +125,38 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     const int orow = b * kMlaH + n16;
     const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
 
-    if (APPEND && tid < kMlaL / 8 && len_old >= t_begin && len_old < t_end) {
-      const int page = len_old / p.page_size;
-      const int pid = pt[page];
-      if (pid >= 0 && pid < p.num_pages)
-        ((u32x4*)(p.latent_w + ((size_t)pid * p.page_size + (len_old - page * p.page_size)) *
-                                   kMlaL))[tid] = *new_chunk(p, b, tid);
-    }
+    // Page ids of the segment's blocks, 64 at a time (lane l: block
+    // pid_base + l), read with readlane: the ring issues no load whose
+    // address waits on another load (a page-table read per block would make
+    // every block wait for all loads in flight).  They are requested first:
+    // the first KV requests wait for them.  An id outside the pool
+    // is kept clamped with bit 31 set: the loads read the clamped page, the
+    // append skips it.  (The clamp also keeps the wait for the page-table
+    // load inside the refill branch: the raw value flowing out of it would
+    // make the compiler wait for every load in flight on each block.)
+    int pid_base = 0;
+    int m_pid = 0;
+    auto fetch_pids = [&]() {
+      const int t0 = t_begin + 32 * min(pid_base + lane, nblk - 1);
+      const int raw = pt[t0 / p.page_size];
+      const int pid = clamp_page(raw, p.num_pages);
+      m_pid = pid | (raw == pid ? 0 : (int)0x80000000u);
+    };
+    fetch_pids();
 
     // Q^T for this wave's 9 QK k-steps: k = 32 * (9 * kh + u) + 8 * j .. + 8.
+    // Requested after the first KV block (the first QK needs it later).
     u32x4 qb[9];
+    auto load_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < 9; ++u) {
-      const int k0 = 32 * (9 * kh + u) + 8 * j;
-      if (k0 < kMlaC)
-        qb[u] = ((const u32x4*)(p.q_nope + (size_t)orow * kMlaC))[k0 >> 3];
-      else
-        qb[u] = ((const u32x4*)(p.q_pe + (size_t)orow * 64))[(k0 - kMlaC) >> 3];
-    }
+      for (int u = 0; u < 9; ++u) {
+        const int k0 = 32 * (9 * kh + u) + 8 * j;
+        if (k0 < kMlaC)
+          qb[u] = ((const u32x4*)(p.q_nope + (size_t)orow * kMlaC))[k0 >> 3];
+        else
+          qb[u] = ((const u32x4*)(p.q_pe + (size_t)orow * 64))[(k0 - kMlaC) >> 3];
+      }
+    };
 
     f32x4 acc[8];
 #pragma unroll
@@ -169,17 +181,6 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     const long long dummy_off = (const char*)dummy - g0;
     const int pe_row = tid >> 3;
     const int pe_col = kMlaC / 8 + (tid & 7);
-    // Page ids of the segment's blocks, 64 at a time (lane l: block
-    // pid_base + l), read with readlane: the ring issues no load whose
-    // address waits on another load (a page-table read per block would make
-    // every block wait for all loads in flight).
-    int pid_base = 0;
-    int m_pid = 0;
-    auto fetch_pids = [&]() {
-      const int t0 = t_begin + 32 * min(pid_base + lane, nblk - 1);
-      m_pid = clamp_page(pt[t0 / p.page_size], p.num_pages);
-    };
-    fetch_pids();
     auto gload = [&](int k, u32x4 (&dst)[kChunksPerThread]) {
       const bool valid = k < nblk;
       const int kc = min(k, nblk - 1);
@@ -189,7 +190,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
       }
       const int t0 = t_begin + 32 * kc;
       const int page = t0 / p.page_size;
-      const int pid = __builtin_amdgcn_readlane(m_pid, kc - pid_base);
+      const int pid = __builtin_amdgcn_readlane(m_pid, kc - pid_base) & 0x7fffffff;
       const long long lb =
           (long long)((size_t)pid * p.page_size + (t0 - page * p.page_size)) * (kMlaL * 2);
       const int last = min(32, t_end - t0) - 1;
@@ -222,9 +223,15 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     // half kh, into score buffer `par`.
     auto qk = [&](const u32x4* tile, int par) {
       const u32x4* krow = tile + (16 * tt + n16) * kRowChunks + j;
+      // All nine operand reads go out before the first MFMA (the MFMA chain
+      // is serial; read by read, each would wait a full LDS round trip).
+      u32x4 kr[9];
+#pragma unroll
+      for (int u = 0; u < 9; ++u) kr[u] = krow[4 * (9 * kh + u)];
+      __builtin_amdgcn_sched_barrier(0);
       f32x4 sp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int u = 0; u < 9; ++u) sp = mfma16x16x32(krow[4 * (9 * kh + u)], qb[u], sp);
+      for (int u = 0; u < 9; ++u) sp = mfma16x16x32(kr[u], qb[u], sp);
       sbuf[par][kh][tt][lane] = sp;
     };
     // Softmax of block k from the four score partials in buffer `par`, then
@@ -256,8 +263,10 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     // compiler assume the younger slots' loads may be the ones a slot write
     // waits for, and it then waits for every load in flight.
     u32x4 st[kMlaDepth][kChunksPerThread];
-#pragma unroll
-    for (int m = 0; m < kMlaDepth; ++m) gload(m, st[m]);
+    gload(0, st[0]);
+    load_q();
+    gload(1, st[1]);
+    gload(2, st[2]);
     __syncthreads();  // the previous segment is done with the tiles and sbuf
     lwrite(s_lat[0], st[0]);
     gload(3, st[0]);
@@ -287,11 +296,24 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     if (k < nblk) step(S0{}, k);
     if (k + 1 < nblk) step(S1{}, k + 1);
 
+    // The appended token is its sequence's last, so a segment that holds it
+    // ends with its block, whose tile is still intact: row len_old - t0 of
+    // tile (nblk - 1) % 3 holds its 72 chunks (read from c_new / pe_new by
+    // the ring), which go from LDS into the token's page slot.
+    if (APPEND && len_old >= t_begin && len_old < t_end) {
+      const int t0 = t_begin + 32 * (nblk - 1);
+      const int pid = __builtin_amdgcn_readlane(m_pid, nblk - 1 - pid_base);
+      const int page = t0 / p.page_size;
+      if (tid < kMlaL / 8 && pid >= 0)  // bit 31: the page id is outside the pool
+        ((u32x4*)(p.latent_w +
+                  ((size_t)pid * p.page_size + (len_old - page * p.page_size)) * kMlaL))[tid] =
+            s_lat[(nblk - 1) % 3][(len_old - t0) * kRowChunks + tid];
+    }
+
     const float l_tot = wave_sum_xor16_32(l_run);
     const float inv_l = 1.f / l_tot;
     const float lse_v = (m_run + __log2f(l_tot)) * kLn2;
-    const int nseg = plan_owner(plan, row_end - 1) - plan_owner(plan, row_start) + 1;
-    if (nseg == 1) {
+    if (row_start >= blk_begin && row_end <= blk_end) {  // the whole sequence is here
       store_cols(p.out + (size_t)orow * kMlaC + col0, acc, j, inv_l);
       if (wave == 0 && j == 0) p.lse[orow] = lse_v;
     } else {

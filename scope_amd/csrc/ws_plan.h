@@ -22,7 +22,8 @@ constexpr int kMaxSeqs = 2048;
 
 struct Plan {
   int T;  // total blocks (the host keeps it below 2^31 / grid)
-  int n;  // workgroups with work (min(grid, T))
+  int n;  // workgroups with work (min(grid, T)), at most 4096
+  int q, r;  // T = q n + r
 };
 
 // Workgroup-uniform value moved to a scalar register.
@@ -37,11 +38,13 @@ __device__ __forceinline__ int plan_len(const int32_t* len_in, int b, int add, i
 }
 
 // Builds s_pref[0..B] (exclusive prefix of blocks per sequence, R rows each)
-// with the NT threads of the workgroup and returns the plan.  s_scan holds
-// NT / 64 + 1 ints.  Every thread must call it (it synchronises).
+// with the NT threads of the workgroup and returns the plan; with s_len, also
+// the lengths s_len[0..B) (plan_len), so callers need not read len_in again.
+// s_scan holds NT / 64 + 1 ints.  Every thread must call it (it
+// synchronises).
 template <int NT>
 __device__ Plan plan_build(const int32_t* len_in, int add, int cap, int B, int R,
-                           int grid, int* s_pref, int* s_scan) {
+                           int grid, int* s_pref, int* s_scan, int* s_len = nullptr) {
   constexpr int NW = NT / 64;
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -50,7 +53,11 @@ __device__ Plan plan_build(const int32_t* len_in, int add, int cap, int B, int R
   const int b0 = min(B, t * chunk);
   const int b1 = min(B, b0 + chunk);
   int local = 0;
-  for (int b = b0; b < b1; ++b) local += R * ((plan_len(len_in, b, add, cap) + 31) >> 5);
+  for (int b = b0; b < b1; ++b) {
+    const int l = plan_len(len_in, b, add, cap);
+    if (s_len) s_len[b] = l;
+    local += R * ((l + 31) >> 5);
+  }
   // inclusive scan of `local` across the wave
   int incl = local;
 #pragma unroll
@@ -73,23 +80,30 @@ __device__ Plan plan_build(const int32_t* len_in, int add, int cap, int B, int R
   int run = s_scan[wave] + incl - local;
   for (int b = b0; b < b1; ++b) {
     s_pref[b] = run;
-    run += R * ((plan_len(len_in, b, add, cap) + 31) >> 5);
+    run += R * (((s_len ? s_len[b] : plan_len(len_in, b, add, cap)) + 31) >> 5);
   }
   if (t == 0) s_pref[B] = s_scan[NW];
   __syncthreads();
   Plan p;
   p.T = uniform(s_scan[NW]);
   p.n = min(grid, p.T);
+  p.q = p.n > 0 ? (int)((unsigned)p.T / (unsigned)p.n) : 0;
+  p.r = p.T - p.q * p.n;
   return p;
 }
 
+// floor(g T / n) as g q + floor(g r / n): 32-bit products (g r < n^2 <= 2^24)
+// and one 32-bit division, for 0 <= g <= n.
 __device__ __forceinline__ int plan_start(const Plan& p, int g) {
-  return (int)((long long)g * p.T / p.n);
+  return g * p.q + (int)((unsigned)(g * p.r) / (unsigned)p.n);
 }
 
-// Workgroup whose range holds block blk.
+// Workgroup whose range holds block blk: ceil((blk + 1) n / T) - 1.  The
+// double quotient is exact enough: the operands are integers below 2^53, and
+// a quotient that is not an integer lies at least 1 / T > 2^-31 below the
+// next one, far above the rounding error of a quotient of at most 4096.
 __device__ __forceinline__ int plan_owner(const Plan& p, int blk) {
-  return (int)(((long long)(blk + 1) * p.n + p.T - 1) / p.T) - 1;
+  return (int)ceil((double)(blk + 1) * (double)p.n / (double)p.T) - 1;
 }
 
 // Sequence holding block blk: the last b with s_pref[b] <= blk (B >= 1).
