@@ -235,22 +235,33 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
   // Writes the piece of kv row `row` held in (m_run, l_run, acc); `whole`:
   // this wave consumed the row's first and last blocks, so the piece is the
   // row's final partial.
+  // (The final partial goes to out / lse in fp32, a piece to its workspace
+  // slot in bf16.)
   auto flush = [&](int row, bool whole) __attribute__((always_inline)) {
     const float l_tot = wave_sum_xor16_32(l_run);
-    float* dst_out = whole ? p.out + (size_t)row * G * D
-                           : p.ws.part_out + (size_t)(split + row) * G * D;
-    float* dst_lse = whole ? p.lse + (size_t)row * G : p.ws.part_lse + (size_t)(split + row) * G;
     if (head_ok) {
       const float inv = 1.f / l_tot;
-      float* o = dst_out + n16 * D + 32 * j;
+      const float lse_v = (m_run + __log2f(l_tot)) * kLn2;
+      if (whole) {
+        float* o = p.out + ((size_t)row * G + n16) * D + 32 * j;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ((float4*)(o + 8 * i))[0] =
-            make_float4(acc[0][i] * inv, acc[1][i] * inv, acc[2][i] * inv, acc[3][i] * inv);
-        ((float4*)(o + 8 * i))[1] =
-            make_float4(acc[4][i] * inv, acc[5][i] * inv, acc[6][i] * inv, acc[7][i] * inv);
+        for (int i = 0; i < 4; ++i) {
+          ((float4*)(o + 8 * i))[0] =
+              make_float4(acc[0][i] * inv, acc[1][i] * inv, acc[2][i] * inv, acc[3][i] * inv);
+          ((float4*)(o + 8 * i))[1] =
+              make_float4(acc[4][i] * inv, acc[5][i] * inv, acc[6][i] * inv, acc[7][i] * inv);
+        }
+        if (j == 0) p.lse[(size_t)row * G + n16] = lse_v;
+      } else {
+        const size_t slot = (size_t)(split + row) * G + n16;
+        uint16_t* o = p.ws.part_out + slot * D + 32 * j;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          store_piece8(o + 8 * i, acc[0][i] * inv, acc[1][i] * inv, acc[2][i] * inv,
+                       acc[3][i] * inv, acc[4][i] * inv, acc[5][i] * inv, acc[6][i] * inv,
+                       acc[7][i] * inv);
+        if (j == 0) p.ws.part_lse[slot] = lse_v;
       }
-      if (j == 0) dst_lse[n16] = (m_run + __log2f(l_tot)) * kLn2;
     }
   };
 

@@ -97,7 +97,7 @@ struct MergeSplitParams {
   int add;  // lengths are gpu_len[b] + add (1 when gpu_len is a fused step's len_in)
   const float* out_g;
   const float* lse_g;
-  const float* part_out;
+  const uint16_t* part_out;  // bf16 pieces
   const float* part_lse;
   const void* b_out;
   const void* b_aux0;
@@ -125,9 +125,12 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   const int r = krow - b * p.R;
   const Plan plan = plan_build<64>(p.gpu_len, p.add, p.cap, p.B, p.R, p.grid, s_pref, s_scan);
   const int nbb = (plan_len(p.gpu_len, b, p.add, p.cap) + 31) >> 5;
+  // One piece: the step's final partial (out_g, fp32); several: their bf16
+  // workspace slots, piece s at pieces + s * sstride.
   int n = 1;
-  const float* src = p.out_g + (size_t)qrow * p.Dv;  // piece s at src + s * sstride
-  const float* lsrc = p.lse_g + qrow;                // lse of piece s at lsrc[s * lstride]
+  const float* src = p.out_g + (size_t)qrow * p.Dv;
+  const uint16_t* pieces = nullptr;
+  const float* lsrc = p.lse_g + qrow;  // lse of piece s at lsrc[s * lstride]
   size_t sstride = 0, lstride = 0;
   if (nbb > 0 && plan.n > 0) {
     const int row_start = s_pref[b] + r * nbb;
@@ -136,7 +139,7 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
     if (nseg > 1) {
       n = nseg;
       const size_t slot0 = (size_t)(w_first + krow) * p.heads + h;
-      src = p.part_out + slot0 * p.Dv;
+      pieces = p.part_out + slot0 * p.Dv;
       lsrc = p.part_lse + slot0;
       sstride = (size_t)p.heads * p.Dv;
       lstride = p.heads;
@@ -171,25 +174,14 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   if (blockIdx.y == 0 && t == 0 && p.lse_out)
     p.lse_out[qrow] = L > 0.f ? mx + __logf(L) : neg_inf();
   if (!col_ok) return;
-  const float4* src4 = (const float4*)src + c;
-  const size_t sstride4 = sstride / 4;
   // an empty host side has weight 0 and must not turn its output into NaN
   float4 a = wb > 0.f ? make_float4(wb * ob.x, wb * ob.y, wb * ob.z, wb * ob.w)
                       : make_float4(0.f, 0.f, 0.f, 0.f);
-  int s = 0;
-  for (; s + 8 <= n; s += 8) {
-    float4 v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = src4[(size_t)(s + u) * sstride4];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float w = s_w[s + u];
-      a.x += w * v[u].x; a.y += w * v[u].y; a.z += w * v[u].z; a.w += w * v[u].w;
-    }
-  }
-  for (; s < n; ++s) {
-    const float w = s_w[s];
-    const float4 v = src4[(size_t)s * sstride4];
+  if (pieces) {
+    accum_pieces(pieces + 4 * c, sstride, n, s_w, a);
+  } else {
+    const float w = s_w[0];
+    const float4 v = ((const float4*)src)[c];
     a.x += w * v.x; a.y += w * v.y; a.z += w * v.z; a.w += w * v.w;
   }
   const float4 o = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
@@ -247,6 +239,7 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
   const int nbb = (plan_len(p.gpu_len, b, p.add, p.cap) + 31) >> 5;
   int n = 1;
   const float* src = p.out_g + (size_t)qrow * p.Dv;
+  const uint16_t* pieces = nullptr;
   const float* lsrc = p.lse_g + qrow;
   size_t sstride = 0, lstride = 0;
   if (nbb > 0 && plan.n > 0) {
@@ -256,7 +249,7 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     if (nseg > 1) {
       n = nseg;
       const size_t slot0 = (size_t)(w_first + b) * p.heads + h;
-      src = p.part_out + slot0 * p.Dv;
+      pieces = p.part_out + slot0 * p.Dv;
       lsrc = p.part_lse + slot0;
       sstride = (size_t)p.heads * p.Dv;
       lstride = p.heads;
@@ -296,24 +289,13 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     const float mx = s_ml[0];
     const float inv = s_ml[1];
     const float wb = (FMT >= 0 && mx != neg_inf()) ? __expf(lb - mx) : 0.f;
-    const float4* src4 = (const float4*)src + c;
-    const size_t sstride4 = sstride / 4;
     float4 a = wb > 0.f ? make_float4(wb * ob.x, wb * ob.y, wb * ob.z, wb * ob.w)
                         : make_float4(0.f, 0.f, 0.f, 0.f);
-    int s = 0;
-    for (; s + 8 <= n; s += 8) {
-      float4 v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = src4[(size_t)(s + u) * sstride4];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = s_w[s + u];
-        a.x += w * v[u].x; a.y += w * v[u].y; a.z += w * v[u].z; a.w += w * v[u].w;
-      }
-    }
-    for (; s < n; ++s) {
-      const float w = s_w[s];
-      const float4 v = src4[(size_t)s * sstride4];
+    if (pieces) {
+      accum_pieces(pieces + 4 * c, sstride, n, s_w, a);
+    } else {
+      const float w = s_w[0];
+      const float4 v = ((const float4*)src)[c];
       a.x += w * v.x; a.y += w * v.y; a.z += w * v.z; a.w += w * v.w;
     }
     const float4 o = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);

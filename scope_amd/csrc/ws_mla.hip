@@ -47,8 +47,8 @@ struct MlaParams {
   long long c_stride, pe_stride;
   float* out;
   float* lse;
-  float* part_out;  // [slot][16][512]
-  float* part_lse;  // [slot][16]
+  uint16_t* part_out;  // [slot][16][512] bf16
+  float* part_lse;     // [slot][16]
   int B, page_size, max_pages, num_pages, cap;
   float scale_log2;
 };
@@ -63,6 +63,16 @@ __device__ __forceinline__ void store_cols(float* __restrict__ dst, const f32x4 
     o[1] = make_float4(acc[4][i] * inv_l, acc[5][i] * inv_l, acc[6][i] * inv_l,
                        acc[7][i] * inv_l);
   }
+}
+
+// The same columns as a bf16 piece.
+__device__ __forceinline__ void store_cols_piece(uint16_t* __restrict__ dst,
+                                                 const f32x4 (&acc)[8], int j, float inv_l) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    store_piece8(dst + 32 * j + 8 * i, acc[0][i] * inv_l, acc[1][i] * inv_l, acc[2][i] * inv_l,
+                 acc[3][i] * inv_l, acc[4][i] * inv_l, acc[5][i] * inv_l, acc[6][i] * inv_l,
+                 acc[7][i] * inv_l);
 }
 
 // LDS tile of one 32-token block: row-major latent rows of 72 16-byte chunks
@@ -318,7 +328,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
       if (wave == 0 && j == 0) p.lse[orow] = lse_v;
     } else {
       const size_t prow = (size_t)(g + b) * kMlaH + n16;
-      store_cols(p.part_out + prow * kMlaC + col0, acc, j, inv_l);
+      store_cols_piece(p.part_out + prow * kMlaC + col0, acc, j, inv_l);
       if (wave == 0 && j == 0) p.part_lse[prow] = lse_v;
     }
     blk = seg_end;
@@ -364,25 +374,8 @@ __global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int g
   __syncthreads();
   if (chunk == 0 && t == 0) p.lse[hrow] = mx + __logf(sum);
   const int c = chunk * 64 + t;  // float4 column
-  const float4* src = (const float4*)(p.part_out + slot0 * kMlaC) + c;
-  const size_t sstride = (size_t)kMlaH * kMlaC / 4;
   float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-  int s = 0;
-  for (; s + 8 <= n; s += 8) {
-    float4 v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(s + u) * sstride];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float w = s_w[s + u];
-      a.x += w * v[u].x; a.y += w * v[u].y; a.z += w * v[u].z; a.w += w * v[u].w;
-    }
-  }
-  for (; s < n; ++s) {
-    const float w = s_w[s];
-    const float4 v = src[(size_t)s * sstride];
-    a.x += w * v.x; a.y += w * v.y; a.z += w * v.z; a.w += w * v.w;
-  }
+  accum_pieces(p.part_out + slot0 * kMlaC + 4 * c, (size_t)kMlaH * kMlaC, n, s_w, a);
   const float inv = 1.f / sum;
   ((float4*)(p.out + (size_t)hrow * kMlaC))[c] =
       make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);

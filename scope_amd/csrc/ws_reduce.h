@@ -1,21 +1,23 @@
-// Cross-workgroup split reduction shared by the decode kernels.
+// Split pieces shared by the decode kernels and the merges.
 //
-// A decode call splits every row's tokens into tokens_per_split chunks; each
-// chunk's workgroup produces a partial (out normalised fp32, lse natural log).
-// When a row has more than one chunk, each workgroup stores its partial in the
-// workspace and bumps the row's arrival counter; the workgroup that arrives
-// last combines all partials of the row (reduce_rows) and resets the counter
-// to zero, so the workspace needs zeroed counters only once, before its first
-// use.
+// A decode call cuts every row's blocks between its splits (ws_plan.h).  A
+// split that holds a whole row writes the row's final partial (out
+// normalised fp32, lse natural log) straight to the caller's out / lse; a
+// row spread over several splits leaves one piece per split in the
+// workspace, and a later launch on the same stream (merge_split_kernel,
+// merge_split_uv_kernel, mla_reduce_kernel) rebuilds the plan to find and
+// LSE-combine them.
 //
 // Workspace layout (ws_decode_workspace_bytes), for a call over rows_kv rows
-// of `heads` output rows each, run by n workgroups:
+// of `heads` output rows each, run by n splits:
 //   [counters int32 x kCounterSlots]
 //   [slot lse f32 x (n + rows_kv) x heads, padded to 256 B]
-//   [slot out f32 x (n + rows_kv) x heads x Dv]
-// (slot = workgroup + row, ws_plan.h).  The counter block has a fixed size,
-// so calls of any shape that share one workspace never write partials over
-// another call's counters.
+//   [slot out bf16 x (n + rows_kv) x heads x Dv]
+// (slot = split + row, ws_plan.h).  Pieces are normalised and rounded to
+// bf16 (their weights stay fp32): a 32-token block carries 36 KB of latent
+// and an MLA piece 16 x 512 outputs, so at 256 splits fp32 pieces cost
+// 8 MB of writes and reads per call.  The counter block has a fixed size
+// and is kept zero, so calls of any shape may share one workspace.
 #pragma once
 
 #include "ws_common.h"
@@ -32,12 +34,12 @@ __host__ __device__ inline size_t align256(size_t n) { return (n + 255) & ~(size
 struct SplitWorkspace {
   int32_t* counters;
   float* part_lse;
-  float* part_out;
+  uint16_t* part_out;  // bf16
 };
 
 __host__ __device__ inline size_t workspace_bytes(int rows_kv, int heads, int Dv, int n) {
   const size_t slots = (size_t)n + rows_kv;
-  return (size_t)kCounterSlots * 4 + align256(slots * heads * 4) + slots * heads * Dv * 4;
+  return (size_t)kCounterSlots * 4 + align256(slots * heads * 4) + slots * heads * Dv * 2;
 }
 
 __host__ __device__ inline SplitWorkspace carve_workspace(void* base, int rows_kv,
@@ -49,7 +51,7 @@ __host__ __device__ inline SplitWorkspace carve_workspace(void* base, int rows_k
   p += (size_t)kCounterSlots * 4;
   w.part_lse = (float*)p;
   p += align256(slots * heads * 4);
-  w.part_out = (float*)p;
+  w.part_out = (uint16_t*)p;
   return w;
 }
 
@@ -67,126 +69,46 @@ int merge_split_pieces(const int32_t* len, int len_add, int B, int R, int heads,
                        int cap, int n, const float* out_g, const float* lse_g,
                        const SplitWorkspace& w, float* out, float* lse, hipStream_t stream);
 
-// Partials travel between workgroups (possibly on different XCDs, whose L2
-// caches are not coherent with each other) through device-scope atomic
-// stores and loads: each access is coherent by itself, so no cache-wide
-// writeback or invalidate is needed.
-__device__ __forceinline__ void st_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Called by every thread of a workgroup after it stored its partial with
-// st_agent.  Returns true in the workgroup that stored the row's last
-// partial; that workgroup then reads every partial with ld_agent.  Each wave
-// first waits until its own stores have completed, so the arrival count is
-// bumped only after the whole workgroup's partial is visible device-wide.
-// `flag` is an LDS int.
-__device__ __forceinline__ bool arrive_last(int32_t* counter, int n_arrivals,
-                                            int* flag) {
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    *flag = (prev == n_arrivals - 1);
-  }
-  __syncthreads();
-  return *flag != 0;
+// Eight outputs of a piece, rounded to bf16, as one 16-byte store.
+__device__ __forceinline__ void store_piece8(uint16_t* dst, float a0, float a1, float a2,
+                                             float a3, float a4, float a5, float a6,
+                                             float a7) {
+  u32x4 v;
+  v[0] = pack_bf16x2(a0, a1);
+  v[1] = pack_bf16x2(a2, a3);
+  v[2] = pack_bf16x2(a4, a5);
+  v[3] = pack_bf16x2(a6, a7);
+  *(u32x4*)dst = v;
 }
 
-// LSE-combine n partials of nrows rows, stored by other workgroups with
-// st_agent: partial s of row r is out po[(s * slot_rows + r) * Dv .. + Dv],
-// lse pl[s * slot_rows + r]; the result goes to out[r * Dv ..], lse[r].
-// nrows in {1, 2, 4, 8, 16}; Dv % 4 == 0; n * nrows <= kReduceMaxWeights.
-// sw: LDS of n * nrows floats; sred: LDS of 32 * (NT / 64) + 32 floats.
-// Kept out of line: its 32 loads in flight would otherwise share the register
-// budget of the decode loop it is called from.
-template <int NT>
-__device__ __noinline__ void reduce_rows(const float* __restrict__ po, const float* __restrict__ pl,
-                            int slot_rows, int nrows, int Dv, int n,
-                            float* __restrict__ out, float* __restrict__ lse,
-                            float* sw, float* sred) {
-  constexpr int NW = NT / 64;
-  const int t = threadIdx.x;
-  const int wave = t >> 6;
-  const int lane = t & 63;
-  float* s_max = sred;                // [NW][16]
-  float* s_sum = sred + 16 * NW;      // [NW][16]
-  float* s_M = sred + 32 * NW;        // [16]
-  float* s_L = s_M + 16;              // [16]
-  const int total = n * nrows;
+// Four bf16 outputs of a piece (8 bytes) as floats.
+__device__ __forceinline__ float4 load_piece4(const uint16_t* src) {
+  const uint2 v = *(const uint2*)src;
+  return make_float4(__builtin_bit_cast(float, v.x << 16),
+                     __builtin_bit_cast(float, v.x & 0xffff0000u),
+                     __builtin_bit_cast(float, v.y << 16),
+                     __builtin_bit_cast(float, v.y & 0xffff0000u));
+}
 
-  // Since NT is a multiple of nrows, thread t always meets row t % nrows.
-  float mx = neg_inf();
-  for (int idx = t; idx < total; idx += NT) {
-    const int s = idx / nrows;
-    const int r = idx - s * nrows;
-    const float v = ld_agent(pl + (size_t)s * slot_rows + r);
-    sw[idx] = v;
-    mx = fmaxf(mx, v);
-  }
-  for (int o = nrows; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if (lane < nrows) s_max[wave * 16 + lane] = mx;
-  __syncthreads();
-  if (t < nrows) {
-    float M = neg_inf();
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_max[w * 16 + t]);
-    s_M[t] = M;
-  }
-  __syncthreads();
-
-  float sum = 0.f;
-  const float Mr = s_M[t % nrows];
-  for (int idx = t; idx < total; idx += NT) {
-    const float w = __expf(sw[idx] - Mr);
-    sw[idx] = w;
-    sum += w;
-  }
-  for (int o = nrows; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
-  if (lane < nrows) s_sum[wave * 16 + lane] = sum;
-  __syncthreads();
-  if (t < nrows) {
-    float L = 0.f;
-    for (int w = 0; w < NW; ++w) L += s_sum[w * 16 + t];
-    s_L[t] = L;
-    lse[t] = s_M[t] + __logf(L);
-  }
-  __syncthreads();
-
-  const int c4 = Dv >> 2;
-  const size_t sstride = (size_t)slot_rows * Dv;
-  for (int idx = t; idx < nrows * c4; idx += NT) {
-    const int r = idx / c4;
-    const int c = idx - r * c4;
-    const float* src = po + (size_t)r * Dv + 4 * c;
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    int s = 0;
-    // eight partials (32 independent loads) in flight per round
-    for (; s + 8 <= n; s += 8) {
-      float v[8][4];
+// a += sum_s w[s] * (four bf16 outputs of piece s at src + s * stride),
+// eight pieces' loads in flight per round.
+__device__ __forceinline__ void accum_pieces(const uint16_t* src, size_t stride, int n,
+                                             const float* w, float4& a) {
+  int s = 0;
+  for (; s + 8 <= n; s += 8) {
+    float4 v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 8; ++u) v[u] = load_piece4(src + (size_t)(s + u) * stride);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) v[u][k] = ld_agent(src + (size_t)(s + u) * sstride + k);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = sw[(s + u) * nrows + r];
-        a.x += w * v[u][0]; a.y += w * v[u][1]; a.z += w * v[u][2]; a.w += w * v[u][3];
-      }
+    for (int u = 0; u < 8; ++u) {
+      const float ws = w[s + u];
+      a.x += ws * v[u].x; a.y += ws * v[u].y; a.z += ws * v[u].z; a.w += ws * v[u].w;
     }
-    for (; s < n; ++s) {
-      const float w = sw[s * nrows + r];
-      const float* v = src + (size_t)s * sstride;
-      a.x += w * ld_agent(v); a.y += w * ld_agent(v + 1);
-      a.z += w * ld_agent(v + 2); a.w += w * ld_agent(v + 3);
-    }
-    const float inv = 1.f / s_L[r];
-    ((float4*)out)[(size_t)r * c4 + c] =
-        make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+  }
+  for (; s < n; ++s) {
+    const float ws = w[s];
+    const float4 v = load_piece4(src + (size_t)s * stride);
+    a.x += ws * v.x; a.y += ws * v.y; a.z += ws * v.z; a.w += ws * v.w;
   }
 }
 
