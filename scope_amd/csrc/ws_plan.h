@@ -37,11 +37,23 @@ __device__ __forceinline__ int plan_len(const int32_t* len_in, int b, int add, i
   return l + add;
 }
 
+__device__ __forceinline__ Plan plan_of(int T, int grid) {
+  Plan p;
+  p.T = T;
+  p.n = min(grid, T);
+  p.q = p.n > 0 ? (int)((unsigned)T / (unsigned)p.n) : 0;
+  p.r = T - p.q * p.n;
+  return p;
+}
+
 // Builds s_pref[0..B] (exclusive prefix of blocks per sequence, R rows each)
 // with the NT threads of the workgroup and returns the plan; with s_len, also
 // the lengths s_len[0..B) (plan_len), so callers need not read len_in again.
-// s_scan holds NT / 64 + 1 ints.  Every thread must call it (it
-// synchronises).
+// s_scan holds NT / 64 + 1 ints.  Every thread must call it.  With at most
+// 64 sequences every wave builds the whole plan by itself (lane b: sequence
+// b) and writes the same values, reading back only what it wrote: no barrier
+// between the kernel start and its first loads.  Otherwise the workgroup
+// builds it together, behind barriers.
 template <int NT>
 __device__ Plan plan_build(const int32_t* len_in, int add, int cap, int B, int R,
                            int grid, int* s_pref, int* s_scan, int* s_len = nullptr) {
@@ -49,6 +61,22 @@ __device__ Plan plan_build(const int32_t* len_in, int add, int cap, int B, int R
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
+  if (B >= 1 && B <= 64) {
+    const int l = lane < B ? plan_len(len_in, lane, add, cap) : 0;
+    const int nb = R * ((l + 31) >> 5);
+    int incl = nb;
+    for (int o = 1; o < B; o <<= 1) {
+      const int v = __shfl_up(incl, o);
+      if (lane >= o) incl += v;
+    }
+    if (lane < B) {
+      s_pref[lane] = incl - nb;
+      if (s_len) s_len[lane] = l;
+    }
+    const int T = __builtin_amdgcn_readlane(incl, B - 1);
+    if (lane == 0) s_pref[B] = T;
+    return plan_of(T, grid);
+  }
   const int chunk = (B + NT - 1) / NT;
   const int b0 = min(B, t * chunk);
   const int b1 = min(B, b0 + chunk);
@@ -84,12 +112,7 @@ __device__ Plan plan_build(const int32_t* len_in, int add, int cap, int B, int R
   }
   if (t == 0) s_pref[B] = s_scan[NW];
   __syncthreads();
-  Plan p;
-  p.T = uniform(s_scan[NW]);
-  p.n = min(grid, p.T);
-  p.q = p.n > 0 ? (int)((unsigned)p.T / (unsigned)p.n) : 0;
-  p.r = p.T - p.q * p.n;
-  return p;
+  return plan_of(uniform(s_scan[NW]), grid);
 }
 
 // floor(g T / n) as g q + floor(g r / n): 32-bit products (g r < n^2 <= 2^24)
