@@ -205,6 +205,13 @@ def test_mla_config3_shape_subset():
     _mla_check([8192, 8192], seed=3000)
 
 
+@pytest.mark.parametrize("wg,PS", [(1, 64), (2, 64), (1, 32)])
+def test_mla_long_segments_refill_page_windows(wg, PS):
+    # a workgroup reads its segment's page ids 64 blocks at a time; segments
+    # of 157 and 122 blocks cross one or two window refills
+    _mla_check([5000, 2100, 700], wg=wg, seed=61, PS=PS)
+
+
 # ---------------------------------------------------------------------------
 # split reduce and merge
 
@@ -380,11 +387,13 @@ def test_workspace_clear_kernel():
     assert not ws.any().item()
 
 
-@pytest.mark.parametrize("wg", [0, 3])
-def test_mla_append_decode_fused_steps(wg):
-    _say(f"mla fused append+decode wg={wg}")
+@pytest.mark.parametrize("wg,lens", [(0, [0, 5, 64, 300]), (3, [0, 5, 64, 300]),
+                                     (1, [0, 5, 300, 4200])])
+def test_mla_append_decode_fused_steps(wg, lens):
+    # wg 1 with 4200 tokens: the new token's segment ends two page-id
+    # windows past its start
+    _say(f"mla fused append+decode wg={wg} lens={lens}")
     H, PS = 16, 64
-    lens = [0, 5, 64, 300]
     B, steps = len(lens), 2
     total = [L + steps for L in lens]
     lat, pt, gl, cs, pes = mla_pool(total, PS, seed=44)
