@@ -110,13 +110,12 @@ int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
  *
  * Splits take equal shares of all 32-token blocks of all rows, so ragged
  * batches stay balanced; a row shared by several splits is combined from
- * their partials.  Workspace layout: [arrival counters int32 x 16384 (one per
- * kv row; a call takes at most 16384 kv rows)][partial lse fp32][partial out
- * bf16], one partial slot per (split, row) pair.  The workspace must be 256-byte
- * aligned and its counters zero before its first use (ws_workspace_clear, or
- * memory that is zero); every completed call leaves them zero again.  Calls
- * that share a workspace must be ordered on one stream.  At most 2048
- * sequences and 4096 splits per call.
+ * their partials.  Workspace layout: [partial lse fp32, padded to 256
+ * bytes][partial out bf16], one partial slot per (split, row) pair.  The
+ * workspace must be 256-byte aligned; it needs no initial contents (every
+ * call writes the slots it reads back).  Calls that share a workspace must
+ * be ordered on one stream.  At most 2048 sequences and 4096 splits per
+ * call.
  */
 int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
                    int n_splits, int* n_splits_out,

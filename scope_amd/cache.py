@@ -100,9 +100,8 @@ class _PagedBase:
         return int(self.lens[layer].max()) if self.batch else 0
 
     def workspace(self, nbytes: int) -> torch.Tensor:
-        """The partition's decode workspace, zeroed once and grown on demand.
-        Calls that share it are ordered on the device's stream, and every
-        completed call leaves its arrival counters zero."""
+        """The partition's decode workspace, grown on demand.  Calls that
+        share it are ordered on the device's stream."""
         ws = getattr(self, "_ws", None)
         if ws is None or ws.numel() < nbytes:
             ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)

@@ -383,13 +383,10 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   if (len_out && len_out == len_in)
     return set_error(WS_EINVAL, "%s: len_out must not alias len_in", name);
   if (B == 0) return WS_OK;
+  if ((long long)B * Hkv * ((max_len + 32) / 32) * 4096 >= (1LL << 31))
+    return set_error(WS_EINVAL, "%s: %lld kv rows of %d tokens exceed the block index range",
+                     name, (long long)B * Hkv, max_len);
   const int rows_kv = B * Hkv;
-  if (rows_kv > kCounterSlots)
-    return set_error(WS_EINVAL, "%s: %d kv rows exceed the %d row counters", name, rows_kv,
-                     kCounterSlots);
-  if ((long long)rows_kv * ((max_len + 32) / 32) * 4096 >= (1LL << 31))
-    return set_error(WS_EINVAL, "%s: %d kv rows of %d tokens exceed the block index range",
-                     name, rows_kv, max_len);
   const int n = gqa_splits(n_splits, rows_kv, max_len);
   if (n > kReduceMaxWeights)
     return set_error(WS_EINVAL, "%s: %d splits exceed the merge's %d", name, n,

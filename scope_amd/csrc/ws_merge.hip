@@ -406,8 +406,8 @@ extern "C" int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, i
                                          (uintptr_t)b_out) & 15u || ((uintptr_t)out_bf16 & 7u))
     return set_error(WS_EINVAL, "ws_merge_split: misaligned buffer");
   const long long rows_kv = (long long)B * rows_per_seq;
-  if (rows_kv > kCounterSlots)
-    return set_error(WS_EINVAL, "ws_merge_split: %lld rows exceed %d", rows_kv, kCounterSlots);
+  if (rows_kv > (1 << 24))
+    return set_error(WS_EINVAL, "ws_merge_split: %lld rows exceed %d", rows_kv, 1 << 24);
   const size_t need = ws::workspace_bytes((int)rows_kv, heads, Dv, n_workgroups);
   if (workspace_bytes < need)
     return set_error(WS_EWORKSPACE, "ws_merge_split: workspace %zu < %zu bytes",

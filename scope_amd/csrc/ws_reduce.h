@@ -8,16 +8,15 @@
 // merge_split_uv_kernel, mla_reduce_kernel) rebuilds the plan to find and
 // LSE-combine them.
 //
-// Workspace layout (ws_decode_workspace_bytes), for a call over rows_kv rows
-// of `heads` output rows each, run by n splits:
-//   [counters int32 x kCounterSlots]
+// Workspace layout (ws_decode_plan), for a call over rows_kv rows of `heads`
+// output rows each, run by n splits:
 //   [slot lse f32 x (n + rows_kv) x heads, padded to 256 B]
 //   [slot out bf16 x (n + rows_kv) x heads x Dv]
 // (slot = split + row, ws_plan.h).  Pieces are normalised and rounded to
 // bf16 (their weights stay fp32): a 32-token block carries 36 KB of latent
 // and an MLA piece 16 x 512 outputs, so at 256 splits fp32 pieces cost
-// 8 MB of writes and reads per call.  The counter block has a fixed size
-// and is kept zero, so calls of any shape may share one workspace.
+// 8 MB of writes and reads per call.  Every call writes the slots it reads
+// back, so the workspace needs no initial contents.
 #pragma once
 
 #include "ws_common.h"
@@ -26,20 +25,17 @@ namespace ws {
 
 // Most (partial, row) weights one reduction keeps in LDS.
 constexpr int kReduceMaxWeights = 4096;
-// Arrival counters at the head of every workspace (one per kv row).
-constexpr int kCounterSlots = 16384;
 
 __host__ __device__ inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 struct SplitWorkspace {
-  int32_t* counters;
   float* part_lse;
   uint16_t* part_out;  // bf16
 };
 
 __host__ __device__ inline size_t workspace_bytes(int rows_kv, int heads, int Dv, int n) {
   const size_t slots = (size_t)n + rows_kv;
-  return (size_t)kCounterSlots * 4 + align256(slots * heads * 4) + slots * heads * Dv * 2;
+  return align256(slots * heads * 4) + slots * heads * Dv * 2;
 }
 
 __host__ __device__ inline SplitWorkspace carve_workspace(void* base, int rows_kv,
@@ -47,8 +43,6 @@ __host__ __device__ inline SplitWorkspace carve_workspace(void* base, int rows_k
   SplitWorkspace w;
   char* p = (char*)base;
   const size_t slots = (size_t)n + rows_kv;
-  w.counters = (int32_t*)p;
-  p += (size_t)kCounterSlots * 4;
   w.part_lse = (float*)p;
   p += align256(slots * heads * 4);
   w.part_out = (uint16_t*)p;

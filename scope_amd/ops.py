@@ -158,10 +158,10 @@ _workspaces: dict = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device scratch for split partials and the split arrival counters,
-    grown on demand.  It starts zeroed (the counters must be zero before first
-    use; every completed decode call leaves them zero), and is reused in
-    stream order by calls on the stream that launches the decode kernels."""
+    """Per-device scratch for split partials, grown on demand and reused in
+    stream order by calls on the stream that launches the decode kernels
+    (each call writes the slots it reads back, so no initial contents are
+    needed; it starts zeroed all the same)."""
     key = device.index if device.index is not None else torch.cuda.current_device()
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:

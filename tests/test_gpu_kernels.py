@@ -302,13 +302,6 @@ def test_lse_merge_formats(fmt, Dv):
 # fused append + partial (one launch per decode step)
 
 
-def _counters_zero():
-    """The fixed 16384-slot counter block of the ops layer's workspace is all
-    zero again after the calls completed."""
-    ws = next(iter(ops._workspaces.values()))
-    return not ws[: 16384 * 4].any().item()
-
-
 @pytest.mark.parametrize("Hkv,G,wg", [(8, 4, 0), (8, 4, 5), (4, 8, 64), (2, 16, 3)])
 def test_gqa_append_decode_fused_steps(Hkv, G, wg):
     _say(f"gqa fused append+decode Hkv={Hkv} G={G} wg={wg}")
@@ -360,15 +353,13 @@ def test_gqa_append_decode_fused_steps(Hkv, G, wg):
         for b in range(B):
             assert np.array_equal(gk[b], bits(ks[b][h])), (b, h)
             assert np.array_equal(gv[b], bits(vs[b][h])), (b, h)
-    assert _counters_zero()
 
 
-def test_gqa_many_workgroups_in_kernel_reduce():
-    # one row spread over 512 workgroups (2 blocks each): the last workgroup
-    # to arrive combines 512 partials
-    _say("gqa one row over 512 workgroups")
+def test_gqa_one_row_over_many_splits():
+    # one row spread over 512 splits (2 blocks each): the combine takes 512
+    # pieces
+    _say("gqa one row over 512 splits")
     _gqa_check([32768], Hkv=1, G=8, wg=512, seed=31, port_check=False)
-    assert _counters_zero()
 
 
 def test_gqa_split_capacity_error():
@@ -434,15 +425,13 @@ def test_mla_append_decode_fused_steps(wg, lens):
 
 
 def test_workspace_shared_across_shapes():
-    # one workspace serves GQA and MLA calls of different row counts in turn;
-    # partials of one call never land on another call's arrival counters
+    # one workspace serves GQA and MLA calls of different row counts in turn
     _say("workspace shared across shapes")
     _gqa_check([900, 700], Hkv=2, G=4, wg=9, seed=51, port_check=False)
     _mla_check([700, 650, 600], wg=11, seed=52)
     _gqa_check([800] * 12, Hkv=8, G=4, wg=300, seed=53, port_check=False)
     _mla_check([300], wg=5, seed=54)
     _gqa_check([1000] * 3, Hkv=8, G=8, wg=200, seed=55, port_check=False)
-    assert _counters_zero()
 
 
 # ---------------------------------------------------------------------------
