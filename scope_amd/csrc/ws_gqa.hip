@@ -10,10 +10,10 @@
 // block i is consumed, block i + 1 (its K, V and the q rows of its kv row)
 // is in flight, so a wave whose range spans two rows never drains and
 // restarts its loads.  When the consumed block opens a new row, the finished
-// row's piece (normalised out, lse) is written: to out/lse when the wave
-// held the whole row, else to workspace slot w + row, where ws_merge_split
-// (or the one-launch entry points' own merge) finds it.  Waves never wait for
-// each other.
+// row's piece (normalised out, lse) is written: to out/lse (fp32) when the
+// wave held the whole row, else to workspace slot w + row (out in bf16),
+// where ws_merge_split (or the one-launch entry points' own merge) finds it.
+// Waves never wait for each other.
 //
 // The block metadata (kv row, pool token index, valid tokens, the new
 // token's row) is computed 64 blocks at a time, one block per lane, page

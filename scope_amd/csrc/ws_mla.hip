@@ -10,10 +10,11 @@
 // computes the QK partial of token tile (w & 1) over latent half (w >> 1)
 // (9 k-steps), the four score tiles meet in LDS, every wave runs the same
 // online softmax, and wave w accumulates output columns [128w, 128w + 128).
-// A sequence held by one workgroup is
-// written final; otherwise each workgroup stores a partial (slot workgroup +
-// sequence) and mla_reduce_kernel combines them: a sequence carries 32 KB of
-// partial per workgroup, more than one workgroup combines quickly.
+// A sequence held by one workgroup is written final (fp32 out / lse);
+// otherwise each workgroup stores a bf16 piece (slot workgroup + sequence,
+// 16 KB) and a later launch combines them: mla_reduce_kernel for the
+// one-launch entry points, ws_merge_split / ws_mla_merge_split_uv for the
+// split step.
 //
 // With c_new != nullptr, token len_in[b] is the new latent: the ring reads
 // its row from c_new/pe_new, the workgroup whose segment holds it writes it
