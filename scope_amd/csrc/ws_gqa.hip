@@ -91,6 +91,7 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
   constexpr int add = APPEND ? 1 : 0;
   __shared__ int s_pref[kMaxSeqs + 1];
   __shared__ int s_len[kMaxSeqs];
+  __shared__ int s_wpref[kSeqPlanMax + 1];
   __shared__ int s_scan[W + 1];
 
   const int tid = threadIdx.x;
@@ -103,7 +104,8 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
   if (APPEND && p.len_out && blockIdx.x == 0)
     for (int b = tid; b < p.B; b += NT) p.len_out[b] = plan_len(p.len_in, b, add, p.cap);
   const Plan plan =
-      plan_build<NT>(p.len_in, add, p.cap, p.B, p.Hkv, p.n_splits, s_pref, s_scan, s_len);
+      plan_build<NT>(p.len_in, add, p.cap, p.B, p.Hkv, p.n_splits, s_pref, s_scan, s_len,
+                     s_wpref, uniform(blockIdx.x * W + (tid >> 6)));
   if (blockIdx.x == 0) {  // sequences without tokens: the empty partial (0, -inf)
     for (int b = 0; b < p.B; ++b) {
       if (s_pref[b + 1] != s_pref[b]) continue;
@@ -113,10 +115,10 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
     }
   }
   const int split = uniform(blockIdx.x * W + (tid >> 6));
-  if (split >= plan.n) return;  // no barrier below: waves run independently
-  const int x_begin = plan_start(plan, split);
-  const int x_end = plan_start(plan, split + 1);
-  const int nblk = x_end - x_begin;  // >= 1 (plan.n <= T)
+  if (!plan.has_work) return;  // no barrier below: waves run independently
+  const int x_begin = uniform(plan.begin);  // (the compiler cannot tell on its own)
+  const int x_end = uniform(plan.end);
+  const int nblk = x_end - x_begin;  // >= 1
 
   // Metadata window: lane l describes block xb + l (the range's last block
   // past its end).

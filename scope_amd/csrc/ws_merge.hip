@@ -115,6 +115,7 @@ constexpr int kMergeChunk4 = 64;
 template <int FMT>
 __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams p) {
   __shared__ int s_pref[kMaxSeqs + 1];
+  __shared__ int s_wpref[kSeqPlanMax + 1];
   __shared__ int s_scan[2];
   __shared__ float s_w[kReduceMaxWeights];
   const int qrow = blockIdx.x;
@@ -123,7 +124,8 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   const int h = qrow - krow * p.heads;
   const int b = krow / p.R;
   const int r = krow - b * p.R;
-  const Plan plan = plan_build<64>(p.gpu_len, p.add, p.cap, p.B, p.R, p.grid, s_pref, s_scan);
+  const Plan plan = plan_build<64>(p.gpu_len, p.add, p.cap, p.B, p.R, p.grid, s_pref, s_scan,
+                                   nullptr, s_wpref);
   const int nbb = (plan_len(p.gpu_len, b, p.add, p.cap) + 31) >> 5;
   // One piece: the step's final partial (out_g, fp32); several: their bf16
   // workspace slots, piece s at pieces + s * sstride.
@@ -134,8 +136,8 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   size_t sstride = 0, lstride = 0;
   if (nbb > 0 && plan.n > 0) {
     const int row_start = s_pref[b] + r * nbb;
-    const int w_first = plan_owner(plan, row_start);
-    const int nseg = plan_owner(plan, row_start + nbb - 1) - w_first + 1;
+    int w_first, nseg;
+    plan_row_splits(plan, b, row_start, nbb, s_wpref, w_first, nseg);
     if (nseg > 1) {
       n = nseg;
       const size_t slot0 = (size_t)(w_first + krow) * p.heads + h;
@@ -214,6 +216,7 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     const MergeSplitParams p, const uint16_t* __restrict__ w_uv, int Dout,
     uint16_t* __restrict__ out_v) {
   __shared__ int s_pref[kMaxSeqs + 1];
+  __shared__ int s_wpref[kSeqPlanMax + 1];
   __shared__ int s_scan[kUvThreads / 64 + 1];
   __shared__ float s_w[kReduceMaxWeights];
   __shared__ float s_row[512];
@@ -235,7 +238,8 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     for (int j = 0; j < 8; ++j) wv[g][j] = wrow[j * 8 + lane8];
   }
   const Plan plan =
-      plan_build<kUvThreads>(p.gpu_len, p.add, p.cap, p.B, 1, p.grid, s_pref, s_scan);
+      plan_build<kUvThreads>(p.gpu_len, p.add, p.cap, p.B, 1, p.grid, s_pref, s_scan, nullptr,
+                             s_wpref);
   const int nbb = (plan_len(p.gpu_len, b, p.add, p.cap) + 31) >> 5;
   int n = 1;
   const float* src = p.out_g + (size_t)qrow * p.Dv;
@@ -244,8 +248,8 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
   size_t sstride = 0, lstride = 0;
   if (nbb > 0 && plan.n > 0) {
     const int row_start = s_pref[b];
-    const int w_first = plan_owner(plan, row_start);
-    const int nseg = plan_owner(plan, row_start + nbb - 1) - w_first + 1;
+    int w_first, nseg;
+    plan_row_splits(plan, b, row_start, nbb, s_wpref, w_first, nseg);
     if (nseg > 1) {
       n = nseg;
       const size_t slot0 = (size_t)(w_first + b) * p.heads + h;

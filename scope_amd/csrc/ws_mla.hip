@@ -94,6 +94,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
   __shared__ f32x4 sbuf[2][2][2][64];      // [block parity][latent half][token tile][lane]
   __shared__ int s_pref[kMaxSeqs + 1];
   __shared__ int s_len[kMaxSeqs];
+  __shared__ int s_wpref[kSeqPlanMax + 1];
   __shared__ int s_scan[NT / 64 + 1];
   const int g = blockIdx.x;
   const int tid = threadIdx.x;
@@ -107,8 +108,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
 
   if (APPEND && p.len_out && g == 0)
     for (int b = tid; b < p.B; b += NT) p.len_out[b] = plan_len(p.len_in, b, add, p.cap);
-  const Plan plan =
-      plan_build<NT>(p.len_in, add, p.cap, p.B, 1, gridDim.x, s_pref, s_scan, s_len);
+  const Plan plan = plan_build<NT>(p.len_in, add, p.cap, p.B, 1, gridDim.x, s_pref, s_scan,
+                                   s_len, s_wpref, g);
   if (g == 0) {  // sequences without tokens: the empty partial (0, -inf)
     for (int b = 0; b < p.B; ++b) {
       if (s_pref[b + 1] != s_pref[b]) continue;
@@ -117,14 +118,15 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
       if (tid < kMlaH) p.lse[b * kMlaH + tid] = neg_inf();
     }
   }
-  if (g >= plan.n) return;
-  const int blk_begin = plan_start(plan, g);
-  const int blk_end = plan_start(plan, g + 1);
+  if (!plan.has_work) return;
+  const int blk_begin = uniform(plan.begin);  // (the compiler cannot tell on its own)
+  const int blk_end = uniform(plan.end);
   int blk = blk_begin;
   const u32x4* dummy = (const u32x4*)p.q_nope;
 
   while (blk < blk_end) {
-    const int b = plan_seq(s_pref, p.B, blk);
+    const int b = uniform((blk == blk_begin && plan.b0 >= 0) ? plan.b0
+                                                             : plan_seq(s_pref, p.B, blk));
     const int len = uniform(s_len[b]);
     const int len_old = len - add;
     const int row_start = uniform(s_pref[b]);
@@ -343,6 +345,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
 // partials.
 __global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int grid) {
   __shared__ int s_pref[kMaxSeqs + 1];
+  __shared__ int s_wpref[kSeqPlanMax + 1];
   __shared__ int s_scan[2];
   __shared__ float s_w[kReduceMaxWeights];
   const int hrow = blockIdx.x;  // b * 16 + h
@@ -351,11 +354,12 @@ __global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int g
   const int b = hrow / kMlaH;
   const int h = hrow - b * kMlaH;
   const int add = p.c_new ? 1 : 0;
-  const Plan plan = plan_build<64>(p.len_in, add, p.cap, p.B, 1, grid, s_pref, s_scan);
+  const Plan plan =
+      plan_build<64>(p.len_in, add, p.cap, p.B, 1, grid, s_pref, s_scan, nullptr, s_wpref);
   const int row_start = s_pref[b], row_end = s_pref[b + 1];
   if (row_end == row_start) return;
-  const int w_first = plan_owner(plan, row_start);
-  const int n = plan_owner(plan, row_end - 1) - w_first + 1;
+  int w_first, n;
+  plan_row_splits(plan, b, row_start, row_end - row_start, s_wpref, w_first, n);
   if (n == 1) return;
   const size_t slot0 = (size_t)(w_first + b) * kMlaH + h;  // partial row of split 0
   float mx = neg_inf();

@@ -135,6 +135,13 @@ def test_gqa_ragged_lengths_and_workgroups(wg):
     _gqa_check(lens, Hkv=8, G=4, wg=wg, seed=5)
 
 
+@pytest.mark.parametrize("wg", [0, 2, 5, 9, 40])
+def test_gqa_one_kv_head_sequence_aligned_plan(wg):
+    # one kv row per sequence: the plan may give every sequence its own splits
+    # (0, 9, 40: sequence-aligned; 2, 5: equal shares across sequences)
+    _gqa_check([0, 40, 300, 1000, 65], Hkv=1, G=8, wg=wg, seed=9)
+
+
 def test_gqa_page_size_128_and_32():
     _gqa_check([500, 129], Hkv=4, G=8, PS=128, seed=6)
     _gqa_check([500, 129], Hkv=4, G=8, PS=32, seed=6)
