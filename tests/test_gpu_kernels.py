@@ -135,6 +135,13 @@ def test_gqa_ragged_lengths_and_workgroups(wg):
     _gqa_check(lens, Hkv=8, G=4, wg=wg, seed=5)
 
 
+@pytest.mark.parametrize("wg", [0, 37])
+def test_gqa_more_than_64_sequences(wg):
+    # 70 sequences: the plan is built by the whole workgroup behind barriers
+    lens = [int(x) for x in np.random.default_rng(70 + wg).integers(0, 150, 70)]
+    _gqa_check(lens, Hkv=2, G=4, wg=wg, seed=63, port_check=False)
+
+
 @pytest.mark.parametrize("wg", [0, 2, 5, 9, 40])
 def test_gqa_one_kv_head_sequence_aligned_plan(wg):
     # one kv row per sequence: the plan may give every sequence its own splits
@@ -210,6 +217,14 @@ def test_mla_ragged(wg):
 def test_mla_config3_shape_subset():
     # DS-V2-Lite absorbed: H 16, latent 576, N(0, 0.5), L 16384 with r 0.5
     _mla_check([8192, 8192], seed=3000)
+
+
+@pytest.mark.parametrize("B,wg", [(64, 0), (64, 40), (65, 0), (65, 40)])
+def test_mla_plan_at_the_per_wave_limit(B, wg):
+    # 64 sequences: every wave builds the plan alone (sequence-aligned when it
+    # fits); 65: the workgroup builds the equal-share plan behind barriers
+    lens = [int(x) for x in np.random.default_rng(B + wg).integers(0, 200, B)]
+    _mla_check(lens, wg=wg, seed=62)
 
 
 @pytest.mark.parametrize("wg,PS", [(1, 64), (2, 64), (1, 32)])
