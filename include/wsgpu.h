@@ -121,10 +121,6 @@ int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
                    int n_splits, int* n_splits_out,
                    size_t* workspace_bytes_out);
 
-/* Zero `bytes` bytes of device memory with a kernel on `stream` (no
- * hipMemset node, so the call may be captured in a HIP graph). */
-int ws_workspace_clear(void* workspace, size_t bytes, void* stream);
-
 /*
  * Split-KV GQA decode attention over the pooled tokens of every sequence.
  * q: [B][Hq][D] bf16, Hq = Hkv * G, G in {1,2,4,8,16}, D = 128.

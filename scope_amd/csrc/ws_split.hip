@@ -1,5 +1,4 @@
-// Workgroup count choice, workspace clearing and the standalone split
-// reduction.
+// Workgroup count choice and the standalone split reduction.
 //
 // split_reduce_kernel combines per-split partials [split][row][Dv] for
 // callers that schedule their own splits, with one 64-thread workgroup per
@@ -115,32 +114,9 @@ static int launch_split_reduce(const float* part_out, const float* part_lse,
   return check_launch("split_reduce");
 }
 
-__global__ __launch_bounds__(256) void clear_kernel(u32x4* __restrict__ p, size_t n16,
-                                                    uint8_t* __restrict__ tail,
-                                                    int n_tail) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n16) p[i] = u32x4{0u, 0u, 0u, 0u};
-  if (i < (size_t)n_tail) tail[i] = 0;
-}
-
 }  // namespace ws
 
 using namespace ws;
-
-extern "C" int ws_workspace_clear(void* workspace, size_t bytes, void* stream) {
-  if (!workspace) return set_error(WS_EINVAL, "ws_workspace_clear: null workspace");
-  if ((uintptr_t)workspace & 15u)
-    return set_error(WS_EINVAL, "ws_workspace_clear: workspace must be 16-byte aligned");
-  if (bytes == 0) return WS_OK;
-  const size_t n16 = bytes / 16;
-  const int n_tail = (int)(bytes - n16 * 16);
-  const size_t threads = n16 > (size_t)n_tail ? n16 : (size_t)n_tail;
-  const size_t blocks = (threads + 255) / 256;
-  hipLaunchKernelGGL(clear_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     (hipStream_t)stream, (u32x4*)workspace, n16,
-                     (uint8_t*)workspace + n16 * 16, n_tail);
-  return check_launch("ws_workspace_clear");
-}
 
 extern "C" int ws_split_reduce(const float* part_out, const float* part_lse,
                                const int32_t* gpu_len, int rows, int heads_per_len,

@@ -27,7 +27,6 @@ EXPORTS = (
     "ws_version",
     "ws_kv_append",
     "ws_latent_append",
-    "ws_workspace_clear",
     "ws_decode_plan",
     "ws_gqa_decode_partial",
     "ws_gqa_append_decode_partial",
@@ -81,8 +80,6 @@ def lib() -> ctypes.CDLL:
         L.ws_latent_append.restype = i32
         L.ws_latent_append.argtypes = [vp, i64, vp, i64, vp, vp, vp, i32, i32,
                                        i32, i32, i32, i32, vp]
-        L.ws_workspace_clear.restype = i32
-        L.ws_workspace_clear.argtypes = [vp, sz, vp]
         L.ws_decode_plan.restype = i32
         L.ws_decode_plan.argtypes = [i32, i32, i32, i32, i32,
                                      ctypes.POINTER(i32), ctypes.POINTER(sz)]
@@ -181,12 +178,6 @@ def decode_plan(kind: int, rows_kv: int, heads: int, max_len: int,
     _check(lib().ws_decode_plan(kind, rows_kv, heads, max_len, n_workgroups,
                                 ctypes.byref(n), ctypes.byref(wsb)), "ws_decode_plan")
     return n.value, wsb.value
-
-
-def workspace_clear(ws: torch.Tensor) -> None:
-    """Zero a workspace tensor with the library's fill kernel."""
-    _check(lib().ws_workspace_clear(_ptr(ws), ws.numel() * ws.element_size(),
-                                    _stream(ws.device)), "ws_workspace_clear")
 
 
 # ---------------------------------------------------------------------------

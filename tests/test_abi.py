@@ -54,7 +54,6 @@ def test_version_and_plan():
         ops.decode_plan(0, 16, 8, 100, -1)
 
 
-
 def test_host_side_argument_checks():
     L = ops.lib()
     rc = L.ws_kv_append(None, None, None, None, None, None, 1, 1, 128, 1, 64, 1, 1, 1, None)
@@ -94,8 +93,6 @@ def test_host_side_argument_checks():
                                  4096, 16, 1.0, fake, fake, ctypes.c_void_p(0x1010),
                                  1 << 30, None)
     assert rc == -1 and b"256-byte" in L.ws_last_error()
-    rc = L.ws_workspace_clear(None, 16, None)
-    assert rc == -1
     rc = L.ws_lse_merge(fake, fake, fake, fake, None, 1, None, fake, None, 4, 128, None)
     assert rc == -1 and b"b_aux1" in L.ws_last_error()
     rc = L.ws_lse_merge(fake, fake, fake, fake, None, 9, None, fake, None, 4, 128, None)

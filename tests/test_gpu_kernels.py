@@ -393,13 +393,6 @@ def test_gqa_split_capacity_error():
         ops.gqa_decode_partial(q, k_pages, v_pages, pt, gl, 0.1, 64, n_workgroups=5000)
 
 
-def test_workspace_clear_kernel():
-    ws = torch.full((1000,), 7, dtype=torch.uint8, device=DEV)
-    ops.workspace_clear(ws)
-    torch.cuda.synchronize()
-    assert not ws.any().item()
-
-
 @pytest.mark.parametrize("wg,lens", [(0, [0, 5, 64, 300]), (3, [0, 5, 64, 300]),
                                      (1, [0, 5, 300, 4200])])
 def test_mla_append_decode_fused_steps(wg, lens):
