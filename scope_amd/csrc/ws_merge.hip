@@ -124,6 +124,15 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   const int h = qrow - krow * p.heads;
   const int b = krow / p.R;
   const int r = krow - b * p.R;
+  // The host partial's address depends on nothing the plan computes: its
+  // loads go out first.
+  const int c = blockIdx.y * kMergeChunk4 + t;  // float4 column
+  const bool col_ok = c < (p.Dv >> 2);
+  float lb = neg_inf();
+  float4 ob = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (FMT >= 0)
+    load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, col_ok ? c : 0, lb,
+                                 ob);
   const Plan plan = plan_build<64>(p.gpu_len, p.add, p.cap, p.B, p.R, p.grid, s_pref, s_scan,
                                    nullptr, s_wpref);
   const int nbb = (plan_len(p.gpu_len, b, p.add, p.cap) + 31) >> 5;
@@ -147,14 +156,15 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
       lstride = p.heads;
     }
   }
+  // The pieces' columns are requested with their lse values.
+  const int cc = col_ok ? c : 0;
+  uint2 pv[8];
+  float4 v1 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (!pieces)
+    v1 = ((const float4*)src)[cc];
+  else if (n <= 8)
+    preload_pieces(pieces + 4 * cc, sstride, n, pv);
   // weights: M over the GPU pieces and the host partial
-  const int c = blockIdx.y * kMergeChunk4 + t;  // float4 column
-  const bool col_ok = c < (p.Dv >> 2);
-  float lb = neg_inf();
-  float4 ob = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (FMT >= 0)
-    load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, col_ok ? c : 0, lb,
-                                 ob);
   float mx = lb;
   for (int s = t; s < n; s += 64) {
     const float v = lsrc[(size_t)s * lstride];
@@ -180,11 +190,13 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   float4 a = wb > 0.f ? make_float4(wb * ob.x, wb * ob.y, wb * ob.z, wb * ob.w)
                       : make_float4(0.f, 0.f, 0.f, 0.f);
   if (pieces) {
-    accum_pieces(pieces + 4 * c, sstride, n, s_w, a);
+    if (n <= 8)
+      accum_preloaded(pv, n, s_w, a);
+    else
+      accum_pieces(pieces + 4 * c, sstride, n, s_w, a);
   } else {
     const float w = s_w[0];
-    const float4 v = ((const float4*)src)[c];
-    a.x += w * v.x; a.y += w * v.y; a.z += w * v.z; a.w += w * v.w;
+    a.x += w * v1.x; a.y += w * v1.y; a.z += w * v1.z; a.w += w * v1.w;
   }
   const float4 o = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
   if (p.out_f32) ((float4*)(p.out_f32 + (size_t)qrow * p.Dv))[c] = o;
@@ -237,6 +249,13 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) wv[g][j] = wrow[j * 8 + lane8];
   }
+  // So do the host partial's.
+  const int c = t;  // float4 column (threads < 128)
+  const bool merging = c < (p.Dv >> 2);
+  float lb = neg_inf();
+  float4 ob = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (FMT >= 0 && merging)
+    load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, c, lb, ob);
   const Plan plan =
       plan_build<kUvThreads>(p.gpu_len, p.add, p.cap, p.B, 1, p.grid, s_pref, s_scan, nullptr,
                              s_wpref);
@@ -259,12 +278,15 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
       lstride = p.heads;
     }
   }
-  const int c = t;  // float4 column (threads < 128)
-  const bool merging = c < (p.Dv >> 2);
-  float lb = neg_inf();
-  float4 ob = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (FMT >= 0 && merging)
-    load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, c, lb, ob);
+  // The merging threads' piece columns are requested with the lse values.
+  uint2 pv[8];
+  float4 v1 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (merging) {
+    if (!pieces)
+      v1 = ((const float4*)src)[c];
+    else if (n <= 8)
+      preload_pieces(pieces + 4 * c, sstride, n, pv);
+  }
   if (t < 64) {  // wave 0: the pieces' weights
     float mx = lb;
     for (int s = t; s < n; s += 64) {
@@ -296,11 +318,13 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     float4 a = wb > 0.f ? make_float4(wb * ob.x, wb * ob.y, wb * ob.z, wb * ob.w)
                         : make_float4(0.f, 0.f, 0.f, 0.f);
     if (pieces) {
-      accum_pieces(pieces + 4 * c, sstride, n, s_w, a);
+      if (n <= 8)
+        accum_preloaded(pv, n, s_w, a);
+      else
+        accum_pieces(pieces + 4 * c, sstride, n, s_w, a);
     } else {
       const float w = s_w[0];
-      const float4 v = ((const float4*)src)[c];
-      a.x += w * v.x; a.y += w * v.y; a.z += w * v.z; a.w += w * v.w;
+      a.x += w * v1.x; a.y += w * v1.y; a.z += w * v1.z; a.w += w * v1.w;
     }
     const float4 o = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
     uint2 packed;

@@ -362,6 +362,10 @@ __global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int g
   plan_row_splits(plan, b, row_start, row_end - row_start, s_wpref, w_first, n);
   if (n == 1) return;
   const size_t slot0 = (size_t)(w_first + b) * kMlaH + h;  // partial row of split 0
+  const int c = chunk * 64 + t;  // float4 column
+  // the pieces' columns are requested with their lse values
+  uint2 pv[8];
+  if (n <= 8) preload_pieces(p.part_out + slot0 * kMlaC + 4 * c, (size_t)kMlaH * kMlaC, n, pv);
   float mx = neg_inf();
   for (int s = t; s < n; s += 64) {
     const float v = p.part_lse[slot0 + (size_t)s * kMlaH];
@@ -378,9 +382,11 @@ __global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int g
   for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
   __syncthreads();
   if (chunk == 0 && t == 0) p.lse[hrow] = mx + __logf(sum);
-  const int c = chunk * 64 + t;  // float4 column
   float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-  accum_pieces(p.part_out + slot0 * kMlaC + 4 * c, (size_t)kMlaH * kMlaC, n, s_w, a);
+  if (n <= 8)
+    accum_preloaded(pv, n, s_w, a);
+  else
+    accum_pieces(p.part_out + slot0 * kMlaC + 4 * c, (size_t)kMlaH * kMlaC, n, s_w, a);
   const float inv = 1.f / sum;
   ((float4*)(p.out + (size_t)hrow * kMlaC))[c] =
       make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);

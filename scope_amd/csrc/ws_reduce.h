@@ -75,35 +75,61 @@ __device__ __forceinline__ void store_piece8(uint16_t* dst, float a0, float a1, 
   *(u32x4*)dst = v;
 }
 
-// Four bf16 outputs of a piece (8 bytes) as floats.
-__device__ __forceinline__ float4 load_piece4(const uint16_t* src) {
-  const uint2 v = *(const uint2*)src;
+// Four bf16 piece outputs (8 bytes) as floats.
+__device__ __forceinline__ float4 piece4_f32(uint2 v) {
   return make_float4(__builtin_bit_cast(float, v.x << 16),
                      __builtin_bit_cast(float, v.x & 0xffff0000u),
                      __builtin_bit_cast(float, v.y << 16),
                      __builtin_bit_cast(float, v.y & 0xffff0000u));
 }
 
-// a += sum_s w[s] * (four bf16 outputs of piece s at src + s * stride),
-// eight pieces' loads in flight per round.
+// a += ws * (four outputs of one piece).
+__device__ __forceinline__ void accum_piece(float4& a, float ws, uint2 raw) {
+  const float4 v = piece4_f32(raw);
+  a.x += ws * v.x; a.y += ws * v.y; a.z += ws * v.z; a.w += ws * v.w;
+}
+
+// a += sum_s w[s] * (four bf16 outputs of piece s at src + s * stride), in
+// order of s, with eight pieces' loads in flight per round (the last n % 8
+// pieces' loads also go out together).
 __device__ __forceinline__ void accum_pieces(const uint16_t* src, size_t stride, int n,
                                              const float* w, float4& a) {
   int s = 0;
   for (; s + 8 <= n; s += 8) {
-    float4 v[8];
+    uint2 v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = load_piece4(src + (size_t)(s + u) * stride);
+    for (int u = 0; u < 8; ++u) v[u] = *(const uint2*)(src + (size_t)(s + u) * stride);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float ws = w[s + u];
-      a.x += ws * v[u].x; a.y += ws * v[u].y; a.z += ws * v[u].z; a.w += ws * v[u].w;
-    }
+    for (int u = 0; u < 8; ++u) accum_piece(a, w[s + u], v[u]);
   }
-  for (; s < n; ++s) {
-    const float ws = w[s];
-    const float4 v = load_piece4(src + (size_t)s * stride);
-    a.x += ws * v.x; a.y += ws * v.y; a.z += ws * v.z; a.w += ws * v.w;
+  if (s < n) {
+    uint2 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = *(const uint2*)(src + (size_t)min(s + u, n - 1) * stride);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s + u < n) accum_piece(a, w[s + u], v[u]);
   }
+}
+
+// The raw bytes of a row's pieces when it has at most eight (a row with
+// fewer repeats its last one), requested before the weights are known: the
+// piece loads share their round trip with the lse loads, and nothing waits
+// for them until the accumulation.
+__device__ __forceinline__ void preload_pieces(const uint16_t* src, size_t stride, int n,
+                                               uint2 (&v)[8]) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u) v[u] = *(const uint2*)(src + (size_t)min(u, n - 1) * stride);
+}
+
+// accum_pieces over the n <= 8 pieces preload_pieces fetched: the same terms
+// in the same order, so the result is bit-identical to accum_pieces.
+__device__ __forceinline__ void accum_preloaded(const uint2 (&v)[8], int n, const float* w,
+                                                float4& a) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    if (u < n) accum_piece(a, w[u], v[u]);
 }
 
 }  // namespace ws
