@@ -90,11 +90,18 @@ __device__ __forceinline__ void accum_piece(float4& a, float ws, uint2 raw) {
 }
 
 // a += sum_s w[s] * (four bf16 outputs of piece s at src + s * stride), in
-// order of s, with eight pieces' loads in flight per round (the last n % 8
-// pieces' loads also go out together).
+// order of s, with sixteen pieces' loads in flight per round while sixteen
+// remain, then eight (the last n % 8 pieces' loads also go out together).
 __device__ __forceinline__ void accum_pieces(const uint16_t* src, size_t stride, int n,
                                              const float* w, float4& a) {
   int s = 0;
+  for (; s + 16 <= n; s += 16) {
+    uint2 v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = *(const uint2*)(src + (size_t)(s + u) * stride);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) accum_piece(a, w[s + u], v[u]);
+  }
   for (; s + 8 <= n; s += 8) {
     uint2 v[8];
 #pragma unroll
