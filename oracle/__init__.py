@@ -1,8 +1,8 @@
 """Oracle for the GPU KV-partition path — TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
-anything from this package, and only as the checker (or, for bench.py, as the
-timed CPU baseline).  The product (scope_amd) never imports it.
+anything from this package, and only to compare results against (or, for
+bench.py, as the timed CPU baseline).  The product (scope_amd) never imports it.
 
 Contents
   attn_np.py        numpy restatement of the reference's decode-attention math:
@@ -12,8 +12,8 @@ Contents
                     boundary integer model.
   cpu_attn_port.c   C restatement of the reference CPU partial kernels
                     (kernel/cpu_attn.cpp: fused_cpu_attn, fused_cpu_attn_mla,
-                    fused_cpu_attn_mla_compressed) with OpenMP, used as the
-                    checker at full sizes and as the CPU baseline.
+                    fused_cpu_attn_mla_compressed) with OpenMP, used to verify
+                    results at full sizes and as the CPU baseline.
   port.py           ctypes binding of the C restatement.
   Makefile          builds oracle/_build/libwsoracle.so with gcc.
 
