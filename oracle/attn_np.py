@@ -67,11 +67,13 @@ def gqa_attention_fp64(q, k, v, scale):
     S, Dv = k.shape[1], v.shape[2]
     if S == 0:
         return np.zeros((N, G, Dv)), np.full((N, G), -np.inf)
-    s = np.einsum("ngd,nsd->ngs", q, k) * float(scale)
+    # matmul (BLAS) rather than einsum: the full-size parity tests call this
+    # over sequences of up to 131072 tokens
+    s = np.matmul(q, k.transpose(0, 2, 1)) * float(scale)
     m = s.max(axis=-1, keepdims=True)
     e = np.exp(s - m)
     l = e.sum(axis=-1, keepdims=True)
-    out = np.einsum("ngs,nsd->ngd", e, v) / l
+    out = np.matmul(e, v) / l
     return out, (m + np.log(l))[..., 0]
 
 
@@ -91,11 +93,12 @@ def mla_attention_fp64(q_nope, q_pe, c_kv, k_pe, scale):
     qp = qp.reshape(B, H, -1)
     if S == 0:
         return np.zeros((B * H, c.shape[2])), np.full((B * H,), -np.inf)
-    s = (np.einsum("bhk,bsk->bhs", qn, c) + np.einsum("bhk,bsk->bhs", qp, pe)) * float(scale)
+    s = (np.matmul(qn, c.transpose(0, 2, 1)) + np.matmul(qp, pe.transpose(0, 2, 1))) \
+        * float(scale)
     m = s.max(axis=-1, keepdims=True)
     e = np.exp(s - m)
     l = e.sum(axis=-1, keepdims=True)
-    out = np.einsum("bhs,bsc->bhc", e, c) / l
+    out = np.matmul(e, c) / l
     return out.reshape(B * H, -1), (m + np.log(l))[..., 0].reshape(B * H)
 
 

@@ -75,29 +75,29 @@ static void gqa_tile(const float* qf, const void* k, const void* v, int is_bf16,
     }
     for (int g = 0; g < G; ++g) {
       const float* qg = qf + (size_t)g * Dk;
-      float nm = m[g];
+      float m_new = m[g];
       for (int r = 0; r < nb; ++r) {
         const float* kr = kbuf + (size_t)r * Dk;
         float acc = 0.f;
 #pragma omp simd reduction(+ : acc)
         for (int d = 0; d < Dk; ++d) acc += qg[d] * kr[d];
         sc[r] = acc * scale;
-        if (sc[r] > nm) nm = sc[r];
+        if (sc[r] > m_new) m_new = sc[r];
       }
-      const float eo = expf(m[g] - nm);
-      float se = 0.f;
+      const float decay = expf(m[g] - m_new);
+      float blk_sum = 0.f;
       float* og = o + (size_t)g * Dv;
 #pragma omp simd
-      for (int d = 0; d < Dv; ++d) og[d] *= eo;
+      for (int d = 0; d < Dv; ++d) og[d] *= decay;
       for (int r = 0; r < nb; ++r) {
-        const float e = expf(sc[r] - nm);
-        se += e;
+        const float e = expf(sc[r] - m_new);
+        blk_sum += e;
         const float* vr = vbuf + (size_t)r * Dv;
 #pragma omp simd
         for (int d = 0; d < Dv; ++d) og[d] += e * vr[d];
       }
-      s[g] = eo * s[g] + se;
-      m[g] = nm;
+      s[g] = decay * s[g] + blk_sum;
+      m[g] = m_new;
     }
   }
 }
@@ -156,26 +156,26 @@ void ws_oracle_gqa(const void* q, const void* k, const void* v, int is_bf16,
 #pragma omp parallel for schedule(static) num_threads(n_threads)
   for (int b = 0; b < B_kv; ++b) {
     for (int g = 0; g < G; ++g) {
-      float gmax = -INFINITY;
+      float row_max = -INFINITY;
       for (int ti = 0; ti < n_tiles; ++ti) {
         const float tm = t_m[((size_t)b * n_tiles + ti) * G + g];
-        if (tm > gmax) gmax = tm;
+        if (tm > row_max) row_max = tm;
       }
-      float gsum = 0.f;
+      float row_sum = 0.f;
       float* og = out + ((size_t)b * G + g) * Dv;
       for (int ti = 0; ti < n_tiles; ++ti) {
         const size_t tk = (size_t)b * n_tiles + ti;
-        const float w = expf(t_m[tk * G + g] - gmax);
-        gsum += w * t_s[tk * G + g];
+        const float w = expf(t_m[tk * G + g] - row_max);
+        row_sum += w * t_s[tk * G + g];
         const float* to = t_o + (tk * G + g) * Dv;
         for (int d = 0; d < Dv; ++d) og[d] += w * to[d];
       }
       if (normalize) {
-        const float inv = 1.f / gsum;
+        const float inv = 1.f / row_sum;
         for (int d = 0; d < Dv; ++d) og[d] *= inv;
       }
-      mx[(size_t)b * G + g] = gmax;
-      sm[(size_t)b * G + g] = gsum;
+      mx[(size_t)b * G + g] = row_max;
+      sm[(size_t)b * G + g] = row_sum;
     }
   }
   free(t_o);
@@ -183,7 +183,7 @@ void ws_oracle_gqa(const void* q, const void* k, const void* v, int is_bf16,
   free(t_s);
 }
 
-enum { CLR = 512, QRD = 64 };
+enum { LATENT_W = 512, ROPE_W = 64 };
 
 __attribute__((target_clones("avx512f", "avx2", "default")))
 static void mla_tile(const float* qn, const float* qp, const uint16_t* c,
@@ -194,38 +194,38 @@ static void mla_tile(const float* qn, const float* qp, const uint16_t* c,
   for (int t = s0; t < s1; t += BLK) {
     const int nb = (s1 - t) < BLK ? (s1 - t) : BLK;
     for (int r = 0; r < nb; ++r) {
-      for (int d = 0; d < CLR; ++d) cbuf[r * CLR + d] = bf(c[(size_t)(t + r) * CLR + d]);
-      for (int d = 0; d < QRD; ++d) pbuf[r * QRD + d] = bf(pe[(size_t)(t + r) * QRD + d]);
+      for (int d = 0; d < LATENT_W; ++d) cbuf[r * LATENT_W + d] = bf(c[(size_t)(t + r) * LATENT_W + d]);
+      for (int d = 0; d < ROPE_W; ++d) pbuf[r * ROPE_W + d] = bf(pe[(size_t)(t + r) * ROPE_W + d]);
     }
     for (int h = 0; h < H; ++h) {
-      const float* qh = qn + (size_t)h * CLR;
-      const float* qph = qp + (size_t)h * QRD;
-      float nm = m[h];
+      const float* qh = qn + (size_t)h * LATENT_W;
+      const float* qph = qp + (size_t)h * ROPE_W;
+      float m_new = m[h];
       for (int r = 0; r < nb; ++r) {
         float acc = 0.f;
-        const float* cr = cbuf + r * CLR;
-        const float* pr = pbuf + r * QRD;
+        const float* cr = cbuf + r * LATENT_W;
+        const float* pr = pbuf + r * ROPE_W;
 #pragma omp simd reduction(+ : acc)
-        for (int d = 0; d < CLR; ++d) acc += qh[d] * cr[d];
+        for (int d = 0; d < LATENT_W; ++d) acc += qh[d] * cr[d];
 #pragma omp simd reduction(+ : acc)
-        for (int d = 0; d < QRD; ++d) acc += qph[d] * pr[d];
+        for (int d = 0; d < ROPE_W; ++d) acc += qph[d] * pr[d];
         sc[r] = acc * scale;
-        if (sc[r] > nm) nm = sc[r];
+        if (sc[r] > m_new) m_new = sc[r];
       }
-      const float eo = expf(m[h] - nm);
-      float se = 0.f;
-      float* oh = o + (size_t)h * CLR;
+      const float decay = expf(m[h] - m_new);
+      float blk_sum = 0.f;
+      float* oh = o + (size_t)h * LATENT_W;
 #pragma omp simd
-      for (int d = 0; d < CLR; ++d) oh[d] *= eo;
+      for (int d = 0; d < LATENT_W; ++d) oh[d] *= decay;
       for (int r = 0; r < nb; ++r) {
-        const float e = expf(sc[r] - nm);
-        se += e;
-        const float* cr = cbuf + r * CLR;
+        const float e = expf(sc[r] - m_new);
+        blk_sum += e;
+        const float* cr = cbuf + r * LATENT_W;
 #pragma omp simd
-        for (int d = 0; d < CLR; ++d) oh[d] += e * cr[d];
+        for (int d = 0; d < LATENT_W; ++d) oh[d] += e * cr[d];
       }
-      s[h] = eo * s[h] + se;
-      m[h] = nm;
+      s[h] = decay * s[h] + blk_sum;
+      m[h] = m_new;
     }
   }
 }
@@ -247,33 +247,33 @@ void ws_oracle_mla_compressed(const uint16_t* q_proj, const uint16_t* q_pe,
     mx[i] = -INFINITY;
     sm[i] = 0.f;
   }
-  memset(out, 0, sizeof(float) * (size_t)B * H * CLR);
+  memset(out, 0, sizeof(float) * (size_t)B * H * LATENT_W);
   if (S <= 0 || B <= 0) return;
   int n_tiles = n_threads / B;
   if (n_tiles < 1) n_tiles = 1;
-  const int tile_len = (S + n_tiles - 1) / n_tiles;
-  const int n_act = (S + tile_len - 1) / tile_len;
-  const int tasks = B * n_act;
-  float* t_o = (float*)calloc((size_t)tasks * H * CLR, sizeof(float));
+  const int tile_tokens = (S + n_tiles - 1) / n_tiles;
+  const int tiles_used = (S + tile_tokens - 1) / tile_tokens;
+  const int tasks = B * tiles_used;
+  float* t_o = (float*)calloc((size_t)tasks * H * LATENT_W, sizeof(float));
   float* t_m = (float*)malloc(sizeof(float) * (size_t)tasks * H);
   float* t_s = (float*)calloc((size_t)tasks * H, sizeof(float));
   for (int64_t i = 0; i < (int64_t)tasks * H; ++i) t_m[i] = -INFINITY;
 
 #pragma omp parallel num_threads(n_threads)
   {
-    float* qn = (float*)malloc(sizeof(float) * (size_t)H * CLR);
-    float* qp = (float*)malloc(sizeof(float) * (size_t)H * QRD);
-    float* cbuf = (float*)malloc(sizeof(float) * 8 * CLR);
-    float* pbuf = (float*)malloc(sizeof(float) * 8 * QRD);
+    float* qn = (float*)malloc(sizeof(float) * (size_t)H * LATENT_W);
+    float* qp = (float*)malloc(sizeof(float) * (size_t)H * ROPE_W);
+    float* cbuf = (float*)malloc(sizeof(float) * 8 * LATENT_W);
+    float* pbuf = (float*)malloc(sizeof(float) * 8 * ROPE_W);
 #pragma omp for schedule(static)
     for (int task = 0; task < tasks; ++task) {
-      const int b = task / n_act, ti = task % n_act;
-      const int s0 = ti * tile_len;
-      const int s1 = (s0 + tile_len < S) ? s0 + tile_len : S;
-      for (int i = 0; i < H * CLR; ++i) qn[i] = bf(q_proj[(size_t)b * H * CLR + i]);
-      for (int i = 0; i < H * QRD; ++i) qp[i] = bf(q_pe[(size_t)b * H * QRD + i]);
-      mla_tile(qn, qp, c_kv + (size_t)b * S * CLR, k_pe + (size_t)b * S * QRD,
-               H, s0, s1, scale, t_o + (size_t)task * H * CLR,
+      const int b = task / tiles_used, ti = task % tiles_used;
+      const int s0 = ti * tile_tokens;
+      const int s1 = (s0 + tile_tokens < S) ? s0 + tile_tokens : S;
+      for (int i = 0; i < H * LATENT_W; ++i) qn[i] = bf(q_proj[(size_t)b * H * LATENT_W + i]);
+      for (int i = 0; i < H * ROPE_W; ++i) qp[i] = bf(q_pe[(size_t)b * H * ROPE_W + i]);
+      mla_tile(qn, qp, c_kv + (size_t)b * S * LATENT_W, k_pe + (size_t)b * S * ROPE_W,
+               H, s0, s1, scale, t_o + (size_t)task * H * LATENT_W,
                t_m + (size_t)task * H, t_s + (size_t)task * H, cbuf, pbuf);
     }
     free(qn);
@@ -284,22 +284,22 @@ void ws_oracle_mla_compressed(const uint16_t* q_proj, const uint16_t* q_pe,
 
   for (int b = 0; b < B; ++b) {
     for (int h = 0; h < H; ++h) {
-      float gmax = -INFINITY;
-      for (int ti = 0; ti < n_act; ++ti) {
-        const float tm = t_m[((size_t)b * n_act + ti) * H + h];
-        if (tm > gmax) gmax = tm;
+      float row_max = -INFINITY;
+      for (int ti = 0; ti < tiles_used; ++ti) {
+        const float tm = t_m[((size_t)b * tiles_used + ti) * H + h];
+        if (tm > row_max) row_max = tm;
       }
-      float gsum = 0.f;
-      float* og = out + ((size_t)b * H + h) * CLR;
-      for (int ti = 0; ti < n_act; ++ti) {
-        const size_t tk = (size_t)b * n_act + ti;
-        const float w = expf(t_m[tk * H + h] - gmax);
-        gsum += w * t_s[tk * H + h];
-        const float* to = t_o + (tk * H + h) * CLR;
-        for (int d = 0; d < CLR; ++d) og[d] += w * to[d];
+      float row_sum = 0.f;
+      float* og = out + ((size_t)b * H + h) * LATENT_W;
+      for (int ti = 0; ti < tiles_used; ++ti) {
+        const size_t tk = (size_t)b * tiles_used + ti;
+        const float w = expf(t_m[tk * H + h] - row_max);
+        row_sum += w * t_s[tk * H + h];
+        const float* to = t_o + (tk * H + h) * LATENT_W;
+        for (int d = 0; d < LATENT_W; ++d) og[d] += w * to[d];
       }
-      mx[(size_t)b * H + h] = gmax;
-      sm[(size_t)b * H + h] = gsum;
+      mx[(size_t)b * H + h] = row_max;
+      sm[(size_t)b * H + h] = row_sum;
     }
   }
   free(t_o);

@@ -282,12 +282,14 @@ class _PagedTwoSided:
         ev.record()
         return out, ev
 
-    def _merge(self, step, part, dev, w_uv=None):
+    def _merge(self, step, part, dev, w_uv=None, return_lse=False):
         b = None if part is None else tuple(x.to(dev, non_blocking=True) for x in part)
         if w_uv is not None:
-            return ops.merge_split_uv(step, w_uv, b, ops.PARTIAL_LSE_F32)[0]
-        out, _ = ops.merge_split(step, b, ops.PARTIAL_LSE_F32, want_lse=False)
-        return out
+            out_v, _, lse = ops.merge_split_uv(step, w_uv, b, ops.PARTIAL_LSE_F32,
+                                               want_lse=return_lse)
+            return (out_v, lse) if return_lse else out_v
+        out, lse = ops.merge_split(step, b, ops.PARTIAL_LSE_F32, want_lse=return_lse)
+        return (out, lse) if return_lse else out
 
 
 class PagedMlaCache(_PagedTwoSided):
@@ -330,13 +332,15 @@ class PagedMlaCache(_PagedTwoSided):
 
     def step(self, layer: int, q_nope: torch.Tensor, q_pe: torch.Tensor,
              c_new: torch.Tensor, pe_new: torch.Tensor, scale: float, host_threads: int = 0,
-             n_workgroups: int = 0, w_uv: torch.Tensor | None = None) -> torch.Tensor:
+             n_workgroups: int = 0, w_uv: torch.Tensor | None = None,
+             return_lse: bool = False):
         """One decode step of `layer`: append c_new [B, 1, 512] / pe_new
         [B, 1, 64] to the GPU side and attend over both sides.  q_nope
         [B*16, 512] (W_UK-absorbed), q_pe [B*16, 64] on the GPU.  Returns the
         merged latent [B*16, 512] bf16, or with w_uv [16, Dout, 512] the
         projected attention output [B, 16 * Dout] bf16 (the merge and the
-        W_UV epilogue in one launch), ready for o_proj."""
+        W_UV epilogue in one launch), ready for o_proj.  With return_lse, a
+        pair (that output, merged lse [B*16] fp32)."""
         g = self.gpu
         dev = q_nope.device
         with_host = bool(self.host.lens.any())
@@ -352,7 +356,7 @@ class PagedMlaCache(_PagedTwoSided):
                 scale, host_threads,
                 torch.empty((rows, ops.MLA_C), dtype=torch.float32, pin_memory=True),
                 torch.empty((rows,), dtype=torch.float32, pin_memory=True))
-        return self._merge(step, part, dev, w_uv)
+        return self._merge(step, part, dev, w_uv, return_lse)
 
 
 class PagedKVCache(_PagedTwoSided):
@@ -397,10 +401,12 @@ class PagedKVCache(_PagedTwoSided):
                                    v[:, host_tokens:].to(dev))
 
     def step(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
-             scale: float, host_threads: int = 0, n_workgroups: int = 0) -> torch.Tensor:
+             scale: float, host_threads: int = 0, n_workgroups: int = 0,
+             return_lse: bool = False):
         """One decode step of `layer`: append k_new / v_new [B, Hkv, 1, D] to the
         GPU side and attend over both sides.  q [B, Hq, D] on the GPU.
-        Returns [B, Hq, D] bf16."""
+        Returns [B, Hq, D] bf16; with return_lse, a pair (that output,
+        merged lse [B, Hq] fp32)."""
         g = self.gpu
         dev = q.device
         with_host = bool(self.host.lens.any())
@@ -416,6 +422,9 @@ class PagedKVCache(_PagedTwoSided):
                 self.host.lens_t, scale, host_threads,
                 torch.empty((B, Hq, D), dtype=torch.float32, pin_memory=True),
                 torch.empty((B, Hq), dtype=torch.float32, pin_memory=True))
+        if return_lse:
+            out, lse = self._merge(step, part, dev, return_lse=True)
+            return out.view(q.shape), lse.view(q.shape[:2])
         return self._merge(step, part, dev).view(q.shape)
 
 

@@ -14,6 +14,7 @@ import torch
 
 from helpers import OUT_ATOL, OUT_RTOL, assert_close, bits
 from oracle import attn_np as O
+from oracle import port
 from scope_amd import host, ops
 from scope_amd.cache import GqaGpuPartition, MlaGpuPartition
 
@@ -65,8 +66,15 @@ def test_mixtral_b16_full_size_share_invariance():
     # (a) the boundary does not change the attention
     for r in (0.5, 0.75):
         assert_close(outs[r], outs[0.25], 5e-3, 5e-3, f"share {r} vs 0.25")
-    # (b) sampled rows against fp64 over the whole sequence
+    # (b) every row against the oracle's C restatement of the reference CPU
+    # kernel (pinned to fp64), sampled rows against fp64, over the whole
+    # sequence
     qb = bits(q).reshape(B, Hkv, G, D)
+    for b in range(B):
+        po, _, _ = port.cpu_attn(qb[b], bits(k[b]), bits(v[b]), scale, normalize=True,
+                                 n_threads=16)
+        for r, o in outs.items():
+            assert_close(o[b], po, OUT_ATOL, OUT_RTOL, f"r={r} b={b} vs C port")
     for b in (0, 5, 13):
         for kvh in (0, 7):
             want, _ = O.gqa_attention_fp64(qb[b, kvh][None], bits(k[b][kvh:kvh + 1]),
