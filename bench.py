@@ -380,6 +380,9 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label, wg=0):
         "partial_frac": round(kernel_bytes / part_us / 1e3 / HBM_PEAK_GBS, 4),
         "partial_tflops": round(flops / part_us / 1e6, 2),
         "mfma_frac_bf16_dense": round(flops / part_us / 1e6 / 2500.0, 4),
+        "partial_bytes": int(kernel_bytes),
+        "partial_flops": int(flops),
+        "step_bytes": int(step_bytes),
     }
 
 
