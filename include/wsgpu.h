@@ -35,7 +35,8 @@
  *   - Row order follows the reference: GQA query head h = kvh * G + g,
  *     out index [b][h][d]; MLA row b * H + h.
  *   - Every entry point is stream-ordered on `stream` (a hipStream_t; NULL is
- *     the default stream), allocates nothing and keeps no global mutable state.
+ *     the default stream) and allocates nothing.  None keeps global mutable
+ *     state except ws_gqa_append_decode_partial_noalloc (its static scratch).
  *     Device pointers are not dereferenced on the host.
  *   - Return value: 0 on success, a negative WS_E* code on a bad argument or a
  *     failed launch; ws_last_error() then describes it (thread-local string).
@@ -321,6 +322,30 @@ int ws_lse_merge(const float* out_g, const float* lse_g,
                  const void* b_out, const void* b_aux0, const void* b_aux1,
                  int fmt_b, uint16_t* out_bf16, float* out_f32,
                  float* lse_out, int rows, int Dv, void* stream);
+
+/*
+ * ws_gqa_append_decode_partial for callers that cannot allocate device
+ * memory: no counterpart in the reference (its decode step allocates through
+ * torch); it is for code under HIP graph capture and serving loops that
+ * forbid hipMalloc.  Same arguments and results as
+ * ws_gqa_append_decode_partial without the workspace: the split pieces live
+ * in a static device array of ws_noalloc_scratch_bytes() (8 MiB) per GPU,
+ * held until the process ends.  A call whose plan needs more returns
+ * WS_EWORKSPACE before launching anything.  The call allocates nothing (no
+ * hipMalloc, no library allocation); its first call on a device looks up the
+ * array's address there.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, unordered threads) race;
+ * calls ordered on one stream do not.  The array needs no initial contents.
+ */
+size_t ws_noalloc_scratch_bytes(void);
+int ws_gqa_append_decode_partial_noalloc(const uint16_t* q, const uint16_t* k_new,
+                                         const uint16_t* v_new, uint16_t* k_pages,
+                                         uint16_t* v_pages, const int32_t* page_table,
+                                         const int32_t* len_in, int32_t* len_out,
+                                         int B, int Hq, int Hkv, int D,
+                                         int page_size, int max_pages, int num_pages,
+                                         int max_len, int n_splits, float scale,
+                                         float* out, float* lse, void* stream);
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,8 @@ EXPORTS = (
     "ws_mla_merge_split_uv",
     "ws_split_reduce",
     "ws_lse_merge",
+    "ws_noalloc_scratch_bytes",
+    "ws_gqa_append_decode_partial_noalloc",
 )
 
 # Formats of the second operand of lse_merge (include/wsgpu.h).
@@ -112,6 +114,11 @@ def lib() -> ctypes.CDLL:
         L.ws_split_reduce.restype = i32
         L.ws_split_reduce.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp,
                                       vp, vp]
+        L.ws_noalloc_scratch_bytes.restype = sz
+        L.ws_noalloc_scratch_bytes.argtypes = []
+        L.ws_gqa_append_decode_partial_noalloc.restype = i32
+        L.ws_gqa_append_decode_partial_noalloc.argtypes = [vp] * 8 + [i32] * 9 + [f32, vp, vp,
+                                                                               vp]
         L.ws_lse_merge.restype = i32
         L.ws_lse_merge.argtypes = [vp, vp, vp, vp, vp, i32, vp, vp, vp, i32,
                                    i32, vp]
@@ -347,6 +354,42 @@ def gqa_append_decode_partial(q, k_new, v_new, k_pages, v_pages, page_table, len
         _ptr(len_in), _ptr(len_out), B, Hq, Hkv, D, PS, page_table.shape[1], P,
         int(max_len), nwg, float(scale), _ptr(out), _ptr(lse), _ptr(ws), wsb,
         _stream(dev)), "ws_gqa_append_decode_partial")
+    return out, lse
+
+
+def gqa_append_decode_partial_noalloc(q, k_new, v_new, k_pages, v_pages, page_table, len_in,
+                                      len_out, scale, max_len, out, lse, n_workgroups=0):
+    """gqa_append_decode_partial without a workspace or any allocation: the
+    caller passes out [B, Hq, D] fp32 and lse [B, Hq] fp32, and the split
+    pieces live in the library's static scratch (ws_noalloc_scratch_bytes()
+    per GPU).  Calls that overlap on one GPU race on that scratch; calls on
+    one stream do not.  Usable under HIP graph capture."""
+    dev = k_pages.device
+    for t, n, dt, nd in ((q, "q", torch.bfloat16, 3), (k_new, "k_new", torch.bfloat16, 4),
+                         (v_new, "v_new", torch.bfloat16, 4), (k_pages, "k_pages", torch.bfloat16, 4),
+                         (v_pages, "v_pages", torch.bfloat16, 4),
+                         (page_table, "page_table", torch.int32, 2),
+                         (len_in, "len_in", torch.int32, 1), (out, "out", torch.float32, 3),
+                         (lse, "lse", torch.float32, 2)):
+        _require(t, n, dt, dev, nd)
+    B, Hq, D = q.shape
+    P, Hkv, PS, D2 = k_pages.shape
+    if v_pages.shape != k_pages.shape or D2 != D or out.shape != q.shape or \
+            lse.shape != (B, Hq):
+        raise ValueError("k/v pools, out and lse must match q")
+    if k_new.shape != (B, Hkv, 1, D) or v_new.shape != k_new.shape:
+        raise ValueError(f"k_new/v_new must be [B, Hkv, 1, D] = {(B, Hkv, 1, D)}")
+    if page_table.shape[0] != B or len_in.shape[0] != B:
+        raise ValueError("page_table/len_in batch mismatch")
+    if len_out is not None:
+        _require(len_out, "len_out", torch.int32, dev, 1)
+        if len_out.shape[0] != B or len_out.data_ptr() == len_in.data_ptr():
+            raise ValueError("len_out must be a separate [B] int32 tensor")
+    _check(lib().ws_gqa_append_decode_partial_noalloc(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
+        _ptr(len_in), _ptr(len_out), B, Hq, Hkv, D, PS, page_table.shape[1], P, int(max_len),
+        int(n_workgroups), float(scale), _ptr(out), _ptr(lse), _stream(dev)),
+        "ws_gqa_append_decode_partial_noalloc")
     return out, lse
 
 
