@@ -6,16 +6,46 @@
 // append (prefill into the partition) spreads over many chunks, which all
 // read the old length, and len_add_kernel bumps it afterwards on the same
 // stream.
+//
+// A sequence's append is all or nothing: if its length is negative (an
+// earlier error) or any slot [len, len + n_new) lies past the page table's
+// capacity or in a page id outside the pool, none of its tokens is written
+// and its length becomes -1 (with update_len), which every later decode
+// call turns into NaN outputs for that sequence.
 #include "ws_common.h"
 
 namespace ws {
 
 constexpr int kChunkVecs = 256 * 8;  // 32 KB of each tensor per workgroup
 
-__global__ __launch_bounds__(256) void len_add_kernel(int32_t* __restrict__ gpu_len, int B,
-                                                      int n_new) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b < B) gpu_len[b] += n_new;
+// Whether every slot [len, len + n_new) of the sequence whose page-table row
+// is pt_row lies in a page of the pool.  Every thread of the workgroup must
+// call it; the result is the same in all of them.
+__device__ __forceinline__ bool append_ok(const int32_t* __restrict__ pt_row, int len,
+                                          int n_new, int page_size, int max_pages,
+                                          int num_pages) {
+  if (len < 0 || (long long)len + n_new > (long long)page_size * max_pages) return false;
+  const int p0 = len / page_size;
+  const int p1 = (len + n_new - 1) / page_size;
+  int bad = 0;
+  for (int pg = p0 + (int)threadIdx.x; pg <= p1; pg += blockDim.x) {
+    const int pid = pt_row[pg];
+    bad |= (pid < 0 || pid >= num_pages);
+  }
+  return !__syncthreads_or(bad);
+}
+
+// Length update of a multi-chunk append: one workgroup per sequence.
+__global__ __launch_bounds__(256) void len_add_kernel(int32_t* __restrict__ gpu_len,
+                                                      const int32_t* __restrict__ page_table,
+                                                      int n_new, int page_size, int max_pages,
+                                                      int num_pages) {
+  const int b = blockIdx.x;
+  const int len = gpu_len[b];
+  const bool ok = append_ok(page_table + (size_t)b * max_pages, len, n_new, page_size,
+                            max_pages, num_pages);
+  __syncthreads();  // every thread has read gpu_len[b]
+  if (threadIdx.x == 0) gpu_len[b] = ok ? len + n_new : -1;
 }
 
 __global__ __launch_bounds__(256) void kv_append_kernel(
@@ -26,8 +56,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     int update_len) {
   const int b = blockIdx.x;
   const int len = gpu_len[b];
+  const bool ok = append_ok(page_table + (size_t)b * max_pages, len, n_new, page_size,
+                            max_pages, num_pages);
   const int per_token = Hkv * dvec;     // vectors of one token of one tensor
-  const int total = n_new * per_token;  // vectors of one tensor
+  const int total = ok ? n_new * per_token : 0;  // vectors of one tensor
   const int end = min(total, (int)(blockIdx.y + 1) * kChunkVecs);
   for (int idx = blockIdx.y * kChunkVecs + threadIdx.x; idx < end; idx += blockDim.x) {
     // source order [Hkv][n_new][dvec]
@@ -37,9 +69,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     const int h = rest / n_new;
     const int pos = len + i;
     const int page = pos / page_size;
-    if (page >= max_pages) continue;
-    const int pid = page_table[(size_t)b * max_pages + page];
-    if (pid < 0 || pid >= num_pages) continue;
+    const int pid = page_table[(size_t)b * max_pages + page];  // checked by append_ok
     const size_t src = (((size_t)b * Hkv + h) * n_new + i) * dvec + dv;
     const size_t dst =
         (((size_t)pid * Hkv + h) * page_size + (pos % page_size)) * dvec + dv;
@@ -48,7 +78,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
   }
   if (update_len) {
     __syncthreads();
-    if (threadIdx.x == 0) gpu_len[b] = len + n_new;
+    if (threadIdx.x == 0) gpu_len[b] = ok ? len + n_new : -1;
   }
 }
 
@@ -63,18 +93,18 @@ __global__ __launch_bounds__(256) void latent_append_kernel(
     int num_pages, int update_len) {
   const int b = blockIdx.x;
   const int len = gpu_len[b];
+  const bool ok = append_ok(page_table + (size_t)b * max_pages, len, n_new, page_size,
+                            max_pages, num_pages);
   constexpr int vec_row = kLatent / 8;    // 72 vectors per token
   constexpr int vec_c = kLatentC / 8;     // 64 of them from c_kv
-  const int total = n_new * vec_row;
+  const int total = ok ? n_new * vec_row : 0;
   const int end = min(total, (int)(blockIdx.y + 1) * kChunkVecs);
   for (int idx = blockIdx.y * kChunkVecs + threadIdx.x; idx < end; idx += blockDim.x) {
     const int v = idx % vec_row;
     const int i = idx / vec_row;
     const int pos = len + i;
     const int page = pos / page_size;
-    if (page >= max_pages) continue;
-    const int pid = page_table[(size_t)b * max_pages + page];
-    if (pid < 0 || pid >= num_pages) continue;
+    const int pid = page_table[(size_t)b * max_pages + page];  // checked by append_ok
     const size_t row = (size_t)b * n_new + i;
     const u32x4 val = (v < vec_c) ? c_new[row * c_stride_vec + v]
                                   : pe_new[row * pe_stride_vec + (v - vec_c)];
@@ -83,7 +113,7 @@ __global__ __launch_bounds__(256) void latent_append_kernel(
   }
   if (update_len) {
     __syncthreads();
-    if (threadIdx.x == 0) gpu_len[b] = len + n_new;
+    if (threadIdx.x == 0) gpu_len[b] = ok ? len + n_new : -1;
   }
 }
 
@@ -126,8 +156,8 @@ extern "C" int ws_kv_append(const uint16_t* k_new, const uint16_t* v_new,
                      gpu_len, Hkv, D / 8, n_new, page_size, max_pages, num_pages,
                      chunks == 1 ? update_len : 0);
   if (update_len && chunks > 1)
-    hipLaunchKernelGGL(len_add_kernel, dim3((B + 255) / 256), dim3(256), 0, s, gpu_len, B,
-                       n_new);
+    hipLaunchKernelGGL(len_add_kernel, dim3(B), dim3(256), 0, s, gpu_len, page_table, n_new,
+                       page_size, max_pages, num_pages);
   return check_launch("ws_kv_append");
 }
 
@@ -159,7 +189,7 @@ extern "C" int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
                      (u32x4*)latent_pages, page_table, gpu_len, n_new, page_size, max_pages,
                      num_pages, chunks == 1 ? update_len : 0);
   if (update_len && chunks > 1)
-    hipLaunchKernelGGL(len_add_kernel, dim3((B + 255) / 256), dim3(256), 0, s, gpu_len, B,
-                       n_new);
+    hipLaunchKernelGGL(len_add_kernel, dim3(B), dim3(256), 0, s, gpu_len, page_table, n_new,
+                       page_size, max_pages, num_pages);
   return check_launch("ws_latent_append");
 }

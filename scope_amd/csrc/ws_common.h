@@ -21,6 +21,13 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+__device__ __forceinline__ float qnan() { return __builtin_nanf(""); }
+
+// max that keeps a NaN: a partial poisoned by a bad page id or length stays
+// NaN through every merge (fmaxf would drop it and hide the error).
+__device__ __forceinline__ float max_nan(float a, float b) {
+  return (a != a || b != b) ? qnan() : fmaxf(a, b);
+}
 
 // v_perm_b32 pairing of two bf16 words: low halves or high halves of (lo, hi)
 // into one dword [lo_part | hi_part << 16].

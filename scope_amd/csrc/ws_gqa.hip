@@ -102,16 +102,17 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
 
   // Lengths (len_in clamped to what the page table row holds) and the plan.
   if (APPEND && p.len_out && blockIdx.x == 0)
-    for (int b = tid; b < p.B; b += NT) p.len_out[b] = plan_len(p.len_in, b, add, p.cap);
+    for (int b = tid; b < p.B; b += NT) p.len_out[b] = step_len_out(p.len_in, b, add, p.cap);
   const Plan plan =
       plan_build<NT>(p.len_in, add, p.cap, p.B, p.Hkv, p.n_splits, s_pref, s_scan, s_len,
                      s_wpref, uniform(blockIdx.x * W + (tid >> 6)));
-  if (blockIdx.x == 0) {  // sequences without tokens: the empty partial (0, -inf)
-    for (int b = 0; b < p.B; ++b) {
+  if (blockIdx.x == 0) {  // sequences without tokens: the empty partial (0, -inf),
+    for (int b = 0; b < p.B; ++b) {  // or NaN for an invalid length
       if (s_pref[b + 1] != s_pref[b]) continue;
+      const bool ok = len_ok(p.len_in[b], add, p.cap);
       const size_t q0 = (size_t)b * p.Hkv * G;
-      for (int idx = tid; idx < p.Hkv * G * D; idx += NT) p.out[q0 * D + idx] = 0.f;
-      for (int idx = tid; idx < p.Hkv * G; idx += NT) p.lse[q0 + idx] = neg_inf();
+      for (int idx = tid; idx < p.Hkv * G * D; idx += NT) p.out[q0 * D + idx] = ok ? 0.f : qnan();
+      for (int idx = tid; idx < p.Hkv * G; idx += NT) p.lse[q0 + idx] = ok ? neg_inf() : qnan();
     }
   }
   const int split = uniform(blockIdx.x * W + (tid >> 6));
@@ -236,14 +237,15 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
 
   // Writes the piece of kv row `row` held in (m_run, l_run, acc); `whole`:
   // this wave consumed the row's first and last blocks, so the piece is the
-  // row's final partial.
+  // row's final partial; `bad`: one of its blocks had a page id outside the
+  // pool (read clamped), so the piece is NaN.
   // (The final partial goes to out / lse in fp32, a piece to its workspace
   // slot in bf16.)
-  auto flush = [&](int row, bool whole) __attribute__((always_inline)) {
+  auto flush = [&](int row, bool whole, bool bad) __attribute__((always_inline)) {
     const float l_tot = wave_sum_xor16_32(l_run);
     if (head_ok) {
-      const float inv = 1.f / l_tot;
-      const float lse_v = (m_run + __log2f(l_tot)) * kLn2;
+      const float inv = bad ? qnan() : 1.f / l_tot;
+      const float lse_v = bad ? qnan() : (m_run + __log2f(l_tot)) * kLn2;
       if (whole) {
         float* o = p.out + ((size_t)row * G + n16) * D + 32 * j;
 #pragma unroll
@@ -288,6 +290,7 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
   int run_row = mq[0].row;
   bool run_first = (mq[0].nt & kFirst) != 0;  // the running row's first block was ours
   bool run_last = false;                      // ... and its last block (so far)
+  bool run_bad = false;                       // a block of the running row had a bad page
   load_q(mq[0].row);
   static_for<0, S - 1>([&](auto i) __attribute__((always_inline)) {
     constexpr int st = decltype(i)::value;
@@ -309,15 +312,17 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
     __builtin_amdgcn_sched_barrier(0);
     const GqaBlock& cur = mq[st];
     if (cur.row != run_row) {
-      flush(run_row, run_first && run_last);
+      flush(run_row, run_first && run_last, run_bad);
       run_row = cur.row;
       run_first = (cur.nt & kFirst) != 0;
+      run_bad = false;
       m_run = neg_inf();
       l_run = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     run_last = (cur.nt & kLast) != 0;
+    run_bad |= (cur.nt & kBadPage) != 0;
     compute_block(cur, ka[st], vr[st]);
     __builtin_amdgcn_sched_barrier(0);
     load_q(mq[nx].row);
@@ -330,7 +335,7 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
   static_for<0, S - 1>([&](auto i) __attribute__((always_inline)) {
     if (base + decltype(i)::value < nblk) step(i, base + decltype(i)::value);
   });
-  flush(run_row, run_first && run_last);
+  flush(run_row, run_first && run_last, run_bad);
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

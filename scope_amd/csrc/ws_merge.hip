@@ -20,7 +20,7 @@ __device__ __forceinline__ void load_b(const void* b_out, const void* aux0,
   } else if (FMT == WS_TRIPLE_UNNORM_F32 || FMT == WS_TRIPLE_NORM_F32) {
     const float m = ((const float*)aux0)[row];
     const float s = ((const float*)aux1)[row];
-    lse_b = (s > 0.f) ? m + __logf(s) : neg_inf();
+    lse_b = (s == 0.f) ? neg_inf() : m + __logf(s);
     o_b = ((const float4*)((const float*)b_out + (size_t)row * Dv))[c];
     if (FMT == WS_TRIPLE_UNNORM_F32) {
       const float inv = (s > 0.f) ? 1.f / s : 0.f;
@@ -32,7 +32,7 @@ __device__ __forceinline__ void load_b(const void* b_out, const void* aux0,
   } else {  // WS_TRIPLE_NORM_BF16
     const float m = bf16_to_f32(((const uint16_t*)aux0)[row]);
     const float s = bf16_to_f32(((const uint16_t*)aux1)[row]);
-    lse_b = (s > 0.f) ? m + __logf(s) : neg_inf();
+    lse_b = (s == 0.f) ? neg_inf() : m + __logf(s);
     const uint2 raw =
         ((const uint2*)((const uint16_t*)b_out + (size_t)row * Dv))[c];
     o_b = make_float4(bf16_to_f32(raw.x & 0xffffu), bf16_to_f32(raw.x >> 16),
@@ -53,7 +53,7 @@ __global__ __launch_bounds__(128) void lse_merge_kernel(
   float lb;
   float4 ob;
   load_b<FMT>(b_out, b_aux0, b_aux1, row, Dv, c, lb, ob);
-  const float M = fmaxf(la, lb);
+  const float M = max_nan(la, lb);
   float4 r;
   float lse_r;
   if (M == neg_inf()) {
@@ -169,9 +169,9 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   for (int s = t; s < n; s += 64) {
     const float v = lsrc[(size_t)s * lstride];
     s_w[s] = v;
-    mx = fmaxf(mx, v);
+    mx = max_nan(mx, v);
   }
-  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  for (int o = 1; o < 64; o <<= 1) mx = max_nan(mx, __shfl_xor(mx, o));
   float sum = 0.f;
   for (int s = t; s < n; s += 64) {
     const float w = mx == neg_inf() ? 0.f : __expf(s_w[s] - mx);
@@ -182,9 +182,9 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
   const float wb = (FMT >= 0 && mx != neg_inf()) ? __expf(lb - mx) : 0.f;
   const float L = sum + wb;
   __syncthreads();
-  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const float inv = L == 0.f ? 0.f : 1.f / L;
   if (blockIdx.y == 0 && t == 0 && p.lse_out)
-    p.lse_out[qrow] = L > 0.f ? mx + __logf(L) : neg_inf();
+    p.lse_out[qrow] = L == 0.f ? neg_inf() : mx + __logf(L);
   if (!col_ok) return;
   // an empty host side has weight 0 and must not turn its output into NaN
   float4 a = wb > 0.f ? make_float4(wb * ob.x, wb * ob.y, wb * ob.z, wb * ob.w)
@@ -292,9 +292,9 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     for (int s = t; s < n; s += 64) {
       const float v = lsrc[(size_t)s * lstride];
       s_w[s] = v;
-      mx = fmaxf(mx, v);
+      mx = max_nan(mx, v);
     }
-    for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    for (int o = 1; o < 64; o <<= 1) mx = max_nan(mx, __shfl_xor(mx, o));
     float sum = 0.f;
     for (int s = t; s < n; s += 64) {
       const float w = mx == neg_inf() ? 0.f : __expf(s_w[s] - mx);
@@ -306,8 +306,8 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     const float L = sum + wb;
     if (t == 0) {
       s_ml[0] = mx;
-      s_ml[1] = L > 0.f ? 1.f / L : 0.f;
-      if (p.lse_out) p.lse_out[qrow] = L > 0.f ? mx + __logf(L) : neg_inf();
+      s_ml[1] = L == 0.f ? 0.f : 1.f / L;
+      if (p.lse_out) p.lse_out[qrow] = L == 0.f ? neg_inf() : mx + __logf(L);
     }
   }
   __syncthreads();

@@ -107,15 +107,16 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
   const int col0 = 128 * wave;
 
   if (APPEND && p.len_out && g == 0)
-    for (int b = tid; b < p.B; b += NT) p.len_out[b] = plan_len(p.len_in, b, add, p.cap);
+    for (int b = tid; b < p.B; b += NT) p.len_out[b] = step_len_out(p.len_in, b, add, p.cap);
   const Plan plan = plan_build<NT>(p.len_in, add, p.cap, p.B, 1, gridDim.x, s_pref, s_scan,
                                    s_len, s_wpref, g);
-  if (g == 0) {  // sequences without tokens: the empty partial (0, -inf)
-    for (int b = 0; b < p.B; ++b) {
+  if (g == 0) {  // sequences without tokens: the empty partial (0, -inf), or
+    for (int b = 0; b < p.B; ++b) {  // NaN for an invalid length
       if (s_pref[b + 1] != s_pref[b]) continue;
+      const bool ok = len_ok(p.len_in[b], add, p.cap);
       for (int idx = tid; idx < kMlaH * kMlaC; idx += NT)
-        p.out[(size_t)b * kMlaH * kMlaC + idx] = 0.f;
-      if (tid < kMlaH) p.lse[b * kMlaH + tid] = neg_inf();
+        p.out[(size_t)b * kMlaH * kMlaC + idx] = ok ? 0.f : qnan();
+      if (tid < kMlaH) p.lse[b * kMlaH + tid] = ok ? neg_inf() : qnan();
     }
   }
   if (!plan.has_work) return;
@@ -149,6 +150,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     // make the compiler wait for every load in flight on each block.)
     int pid_base = 0;
     int m_pid = 0;
+    int seg_bad = 0;  // bit 31: a block of the segment had a page id outside the pool
     auto fetch_pids = [&]() {
       const int t0 = t_begin + 32 * min(pid_base + lane, nblk - 1);
       const int raw = pt[t0 / p.page_size];
@@ -203,7 +205,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
       }
       const int t0 = t_begin + 32 * kc;
       const int page = t0 / p.page_size;
-      const int pid = __builtin_amdgcn_readlane(m_pid, kc - pid_base) & 0x7fffffff;
+      const int pid_raw = __builtin_amdgcn_readlane(m_pid, kc - pid_base);
+      seg_bad |= pid_raw;
+      const int pid = pid_raw & 0x7fffffff;
       const long long lb =
           (long long)((size_t)pid * p.page_size + (t0 - page * p.page_size)) * (kMlaL * 2);
       const int last = min(32, t_end - t0) - 1;
@@ -324,8 +328,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     }
 
     const float l_tot = wave_sum_xor16_32(l_run);
-    const float inv_l = 1.f / l_tot;
-    const float lse_v = (m_run + __log2f(l_tot)) * kLn2;
+    const bool bad = seg_bad < 0;  // a bad page id was read (clamped): the piece is NaN
+    const float inv_l = bad ? qnan() : 1.f / l_tot;
+    const float lse_v = bad ? qnan() : (m_run + __log2f(l_tot)) * kLn2;
     if (row_start >= blk_begin && row_end <= blk_end) {  // the whole sequence is here
       store_cols(p.out + (size_t)orow * kMlaC + col0, acc, j, inv_l);
       if (wave == 0 && j == 0) p.lse[orow] = lse_v;
@@ -370,9 +375,9 @@ __global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int g
   for (int s = t; s < n; s += 64) {
     const float v = p.part_lse[slot0 + (size_t)s * kMlaH];
     s_w[s] = v;
-    mx = fmaxf(mx, v);
+    mx = max_nan(mx, v);
   }
-  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  for (int o = 1; o < 64; o <<= 1) mx = max_nan(mx, __shfl_xor(mx, o));
   float sum = 0.f;
   for (int s = t; s < n; s += 64) {
     const float w = __expf(s_w[s] - mx);

@@ -45,12 +45,25 @@ constexpr int kAlignSlack = 3;
 // Workgroup-uniform value moved to a scalar register.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// Sequence length used by the kernels: len_in[b] clamped to [0, cap - add],
-// plus `add` (1 when the call appends the step's new token).
+// A length the call can serve: 0 <= l <= cap - add (room for the appended
+// token when add == 1).  A length outside that range (a caller's mistake, or
+// the -1 a fused step leaves after one) is not clamped: the sequence gets no
+// blocks, its outputs are NaN and a fused step writes len_out = -1.
+__device__ __forceinline__ bool len_ok(int l, int add, int cap) {
+  return l >= 0 && l <= cap - add;
+}
+
+// Sequence length used by the kernels: len_in[b] + add (1 when the call
+// appends the step's new token), or 0 for a length outside the valid range.
 __device__ __forceinline__ int plan_len(const int32_t* len_in, int b, int add, int cap) {
-  int l = len_in[b];
-  l = max(0, min(l, cap - add));
-  return l + add;
+  const int l = len_in[b];
+  return len_ok(l, add, cap) ? l + add : 0;
+}
+
+// len_out of a fused step: the new length, or -1 for an invalid len_in.
+__device__ __forceinline__ int step_len_out(const int32_t* len_in, int b, int add, int cap) {
+  const int l = len_in[b];
+  return len_ok(l, add, cap) ? l + add : -1;
 }
 
 __device__ __forceinline__ Plan plan_of(int T, int grid) {

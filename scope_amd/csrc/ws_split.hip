@@ -25,22 +25,24 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(
   const int t = threadIdx.x;
   const int c4 = Dv >> 2;
   const int c = chunk * kSplitChunk4 + t;
-  const int len = gpu_len[row / heads_per_len] + len_add;
+  const int len0 = gpu_len[row / heads_per_len];
+  const int len = len0 + len_add;
   int n = len > 0 ? (len + tokens_per_split - 1) / tokens_per_split : 0;
   if (n > n_splits) n = n_splits;
   if (n == 1 && untouched_single) return;
-  if (n == 0) {
-    if (c < c4) ((float4*)out)[(size_t)row * c4 + c] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (chunk == 0 && t == 0) lse[row] = neg_inf();
+  if (n == 0) {  // empty: (0, -inf); a negative length is an error: NaN
+    const float v = len0 < 0 ? qnan() : 0.f;
+    if (c < c4) ((float4*)out)[(size_t)row * c4 + c] = make_float4(v, v, v, v);
+    if (chunk == 0 && t == 0) lse[row] = len0 < 0 ? qnan() : neg_inf();
     return;
   }
   float mx = neg_inf();
   for (int s = t; s < n; s += 64) {
     const float v = part_lse[(size_t)s * rows + row];
     s_w[s] = v;
-    mx = fmaxf(mx, v);
+    mx = max_nan(mx, v);
   }
-  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  for (int o = 1; o < 64; o <<= 1) mx = max_nan(mx, __shfl_xor(mx, o));
   float sum = 0.f;
   for (int s = t; s < n; s += 64) {
     const float w = __expf(s_w[s] - mx);
