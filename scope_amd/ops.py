@@ -162,11 +162,14 @@ _workspaces: dict = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device scratch for split partials, grown on demand and reused in
-    stream order by calls on the stream that launches the decode kernels
-    (each call writes the slots it reads back, so no initial contents are
-    needed; it starts zeroed all the same)."""
-    key = device.index if device.index is not None else torch.cuda.current_device()
+    """Scratch for the split partials of the one-launch entry points, one per
+    (device, stream): calls on one stream reuse it in stream order, calls on
+    different streams never share it.  Grown on demand (the old buffer is
+    freed through torch's stream-ordered allocator, so a launch still
+    queued on this stream keeps its memory until it ran).  Each call writes
+    the slots it reads back, so no initial contents are needed."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, torch.cuda.current_stream(idx).cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
