@@ -190,6 +190,36 @@ int ws_gqa_append_decode_split(const uint16_t* q, const uint16_t* k_new,
                                void* stream);
 
 /*
+ * ws_gqa_decode_partial / ws_gqa_append_decode_partial with separate key and
+ * value widths: k_pages [num_pages][Hkv][page_size][Dk], v_pages
+ * [num_pages][Hkv][page_size][Dv], q [B][Hq][Dk], k_new [B][Hkv][1][Dk],
+ * v_new [B][Hkv][1][Dv], out [B][Hq][Dv].  (Dk, Dv) = (128, 128) is the GQA
+ * call; (192, 128) with group size 1 is the decompressed DeepSeek-V2
+ * attention (128 nope + 64 rope key columns, 128 value columns, 16 heads).
+ * Workspace as ws_decode_plan kind 0 (its value width is 128).
+ * Replaces _local_bmm_softmax / _resident_layer with the reference's ds2
+ * model entry, QHD 192 / VHD 128 / GROUPS 1 (roofline/bench_resident_kv.py:10,
+ * 150-157, 261-271), the GPU side of the fused_cpu_attn_mla split
+ * (kernel/cpu_attn.cpp:638-672).
+ */
+int ws_attn_decode_partial(const uint16_t* q, const uint16_t* k_pages,
+                           const uint16_t* v_pages, const int32_t* page_table,
+                           const int32_t* gpu_len, int B, int Hq, int Hkv,
+                           int Dk, int Dv, int page_size, int max_pages,
+                           int num_pages, int max_len, int n_splits, float scale,
+                           float* out, float* lse, void* workspace,
+                           size_t workspace_bytes, void* stream);
+int ws_attn_append_decode_partial(const uint16_t* q, const uint16_t* k_new,
+                                  const uint16_t* v_new, uint16_t* k_pages,
+                                  uint16_t* v_pages, const int32_t* page_table,
+                                  const int32_t* len_in, int32_t* len_out,
+                                  int B, int Hq, int Hkv, int Dk, int Dv,
+                                  int page_size, int max_pages, int num_pages,
+                                  int max_len, int n_splits, float scale,
+                                  float* out, float* lse, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/*
  * Split-KV absorbed-MLA decode attention.
  * q_nope: [B*H][512] bf16 (q_nope already multiplied by W_UK), q_pe: [B*H][64].
  * score = (q_nope . c + q_pe . pe) * scale over the shared 576-wide latent,

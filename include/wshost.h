@@ -68,6 +68,19 @@ int wh_gqa_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v
                    int D, int page_size, int max_pages, int num_pages, float scale,
                    float* out, float* lse, int n_threads);
 
+/* wh_gqa_partial with separate key and value widths: q [B, Hq, Dk],
+ * k_pages [num_pages, Hkv, page_size, Dk], v_pages [num_pages, Hkv,
+ * page_size, Dv], out [B, Hq, Dv].  (Dk, Dv): equal multiples of 32 up to 256,
+ * or (192, 128), the decompressed DeepSeek-V2 layout (128 nope + 64 rope key
+ * columns, 128 value columns; the reference's ds2 model entry,
+ * roofline/bench_resident_kv.py:10).
+ * Replaces fused_cpu_attn_mla with Dk != Dv (kernel/cpu_attn.cpp:638-672),
+ * returning (out, lse) instead of its unnormalised triple. */
+int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                    const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                    int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
+                    float* out, float* lse, int n_threads);
+
 /* Absorbed-MLA host partial (16 heads, 512-wide latent + 64-wide rope key).
  * Replaces fused_cpu_attn_mla_compressed (kernel/cpu_attn.cpp:852-1022) as
  * called by the decode branch of _mla_compressed_forward

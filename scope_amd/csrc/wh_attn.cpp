@@ -221,46 +221,40 @@ void for_pages(const int32_t* table_row, int page_size, int t0, int t1, F f) {
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-const char* wh_last_error(void) { return g_err; }
-
-const char* wh_version(void) { return "wshost 0.1 avx512bf16"; }
-
-int wh_isa_supported(void) { return isa_ok() ? 1 : 0; }
-
-int wh_gqa_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
-                   const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
-                   int D, int page_size, int max_pages, int num_pages, float scale,
-                   float* out, float* lse, int n_threads) {
+int attn_partial(const char* fn, const uint16_t* q, const uint16_t* k_pages,
+                 const uint16_t* v_pages, const int32_t* page_table, const int32_t* lens, int B,
+                 int Hq, int Hkv, int Dk, int D, int page_size, int max_pages, int num_pages,
+                 float scale, float* out, float* lse, int n_threads) {
   g_err[0] = '\0';
-  if (!isa_ok()) return fail(WH_ENOTSUP, "wh_gqa_partial: this CPU lacks AVX-512 F/BW/BF16");
+  if (!isa_ok()) return fail(WH_ENOTSUP, "%s: this CPU lacks AVX-512 F/BW/BF16", fn);
   if (B < 0 || Hkv < 1 || Hq < 1 || Hq % Hkv != 0)
-    return fail(WH_EINVAL, "wh_gqa_partial: bad shape B=%d Hq=%d Hkv=%d", B, Hq, Hkv);
+    return fail(WH_EINVAL, "%s: bad shape B=%d Hq=%d Hkv=%d", fn, B, Hq, Hkv);
   const int G = Hq / Hkv;
-  if (G > 16) return fail(WH_EINVAL, "wh_gqa_partial: group size %d > 16", G);
-  if (D < 32 || D > 256 || D % 32 != 0)
-    return fail(WH_EINVAL, "wh_gqa_partial: head_dim %d is not a multiple of 32 in [32, 256]", D);
+  if (G > 16) return fail(WH_EINVAL, "%s: group size %d > 16", fn, G);
+  if (!wh::gqa_dims_supported(Dk, D))
+    return fail(WH_EINVAL,
+                "%s: head_dim Dk=%d Dv=%d unsupported (equal multiples of 32 in [32, 256], "
+                "or 192 / 128)",
+                fn, Dk, D);
   if (B == 0) return WH_OK;
   if (!q || !k_pages || !v_pages || !page_table || !lens || !out || !lse)
-    return fail(WH_EINVAL, "wh_gqa_partial: null pointer");
-  if (int rc = check_pages("wh_gqa_partial", page_table, lens, B, page_size, max_pages,
-                           num_pages))
-    return rc;
+    return fail(WH_EINVAL, "%s: null pointer", fn);
+  if (int rc = check_pages(fn, page_table, lens, B, page_size, max_pages, num_pages)) return rc;
   const int R = B * Hkv;
   std::vector<int32_t> row_len((size_t)R);
   for (int r = 0; r < R; ++r) row_len[r] = lens[r / Hkv];
   const Plan P = make_plan(row_len.data(), R);
   const float sl2 = scale * kLog2e;
-  const size_t head_elems = (size_t)page_size * D;  // one KV head of one page
   auto seg = [&](int r, int t0, int t1, float* st) {
     const int b = r / Hkv, kvh = r % Hkv;
     StateView s = view(st, G);
     for_pages(page_table + (size_t)b * max_pages, page_size, t0, t1,
               [&](int pid, int a, int e) {
-                const size_t base = ((size_t)pid * Hkv + kvh) * head_elems;
-                wh::gqa_attend(q + (size_t)r * G * D, k_pages + base, v_pages + base, G, D, a,
-                               e, sl2, s.m, s.l, s.o);
+                const size_t head = ((size_t)pid * Hkv + kvh) * page_size;  // first token
+                wh::gqa_attend(q + (size_t)r * G * Dk, k_pages + head * Dk, v_pages + head * D,
+                               G, Dk, D, a, e, sl2, s.m, s.l, s.o);
               });
   };
   auto fin = [&](int r, const float* st) {
@@ -275,6 +269,32 @@ int wh_gqa_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v
   run_plan(P, R, G, D, n_threads, row_len.data(), seg, fin, empty,
            [D](size_t i) { return (int)(i / D); });
   return WH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* wh_last_error(void) { return g_err; }
+
+const char* wh_version(void) { return "wshost 0.1 avx512bf16"; }
+
+int wh_isa_supported(void) { return isa_ok() ? 1 : 0; }
+
+int wh_gqa_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                   const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                   int D, int page_size, int max_pages, int num_pages, float scale,
+                   float* out, float* lse, int n_threads) {
+  return attn_partial("wh_gqa_partial", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv, D,
+                      D, page_size, max_pages, num_pages, scale, out, lse, n_threads);
+}
+
+int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                    const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                    int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
+                    float* out, float* lse, int n_threads) {
+  return attn_partial("wh_attn_partial", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv, Dk,
+                      Dv, page_size, max_pages, num_pages, scale, out, lse, n_threads);
 }
 
 int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,

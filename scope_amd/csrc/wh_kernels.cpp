@@ -126,14 +126,15 @@ inline void gqa_pv(float* og, const uint32_t* vst, const uint32_t* pw, int np, _
   for (int r = 0; r < W; ++r) _mm512_storeu_ps(og + 16 * r, acc[r]);
 }
 
-template <int D>
+// DK: key width (q rows and k tokens), D: value width (v tokens and o).
+template <int DK, int D>
 void gqa_attend_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G, int t0,
                   int t1, float sl2, float* m, float* l, float* o) {
   constexpr int NZ = D / 16;  // zmm per value row
   alignas(64) float sc[16][32];
   alignas(64) uint32_t vst[16 * D];
   alignas(64) uint32_t pw[16];
-  alignas(64) uint16_t tile[16 * D];
+  alignas(64) uint16_t tile[16 * DK];
   const __m512 ninf = _mm512_set1_ps(-INFINITY);
   const __m512 vsl2 = _mm512_set1_ps(sl2);
   for (int tb = t0; tb < t1; tb += 32) {
@@ -145,15 +146,15 @@ void gqa_attend_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G
         for (int g = 0; g < G; ++g) _mm512_store_ps(sc[g] + 16 * half, ninf);
         continue;
       }
-      const uint16_t* kb = k + (size_t)(tb + 16 * half) * D;
+      const uint16_t* kb = k + (size_t)(tb + 16 * half) * DK;
       if (valid < 16) {  // copy the tail into a zeroed tile: no read past the range
         std::memset(tile, 0, sizeof(tile));
-        std::memcpy(tile, kb, sizeof(uint16_t) * valid * D);
+        std::memcpy(tile, kb, sizeof(uint16_t) * valid * DK);
         kb = tile;
       }
       const __mmask16 vm = valid < 16 ? (__mmask16)((1u << valid) - 1) : (__mmask16)0xFFFF;
       for (int g = 0; g < G; ++g) {
-        const __m512 s = _mm512_mul_ps(gqa_scores16<D>(q + (size_t)g * D, kb), vsl2);
+        const __m512 s = _mm512_mul_ps(gqa_scores16<DK>(q + (size_t)g * DK, kb), vsl2);
         _mm512_store_ps(sc[g] + 16 * half, _mm512_mask_blend_ps(vm, ninf, s));
       }
     }
@@ -188,17 +189,23 @@ void gqa_attend_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G
 
 }  // namespace
 
-void gqa_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G, int D,
-                int t0, int t1, float sl2, float* m, float* l, float* o) {
-  switch (D) {
-    case 32: return gqa_attend_d<32>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 64: return gqa_attend_d<64>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 96: return gqa_attend_d<96>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 128: return gqa_attend_d<128>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 160: return gqa_attend_d<160>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 192: return gqa_attend_d<192>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 224: return gqa_attend_d<224>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 256: return gqa_attend_d<256>(q, k, v, G, t0, t1, sl2, m, l, o);
+bool gqa_dims_supported(int Dk, int Dv) {
+  return (Dk == Dv && Dk >= 32 && Dk <= 256 && Dk % 32 == 0) || (Dk == 192 && Dv == 128);
+}
+
+void gqa_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G, int Dk,
+                int Dv, int t0, int t1, float sl2, float* m, float* l, float* o) {
+  if (Dk == 192 && Dv == 128) return gqa_attend_d<192, 128>(q, k, v, G, t0, t1, sl2, m, l, o);
+  if (Dk != Dv) return;  // rejected by the caller
+  switch (Dk) {
+    case 32: return gqa_attend_d<32, 32>(q, k, v, G, t0, t1, sl2, m, l, o);
+    case 64: return gqa_attend_d<64, 64>(q, k, v, G, t0, t1, sl2, m, l, o);
+    case 96: return gqa_attend_d<96, 96>(q, k, v, G, t0, t1, sl2, m, l, o);
+    case 128: return gqa_attend_d<128, 128>(q, k, v, G, t0, t1, sl2, m, l, o);
+    case 160: return gqa_attend_d<160, 160>(q, k, v, G, t0, t1, sl2, m, l, o);
+    case 192: return gqa_attend_d<192, 192>(q, k, v, G, t0, t1, sl2, m, l, o);
+    case 224: return gqa_attend_d<224, 224>(q, k, v, G, t0, t1, sl2, m, l, o);
+    case 256: return gqa_attend_d<256, 256>(q, k, v, G, t0, t1, sl2, m, l, o);
     default: return;  // rejected by the caller
   }
 }

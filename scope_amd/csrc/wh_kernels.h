@@ -27,12 +27,14 @@ inline int stage_col(int s) {
 // the caller's buffers).  Wide enough for the 576-column MLA latent.
 extern const uint16_t kZeroRow[1024];
 
-// GQA: q holds G rows of D bf16 (the query heads sharing one KV head); token
-// t of the row is k + t*D / v + t*D.  D is a multiple of 32, at most 256;
-// G at most 16.  m, l: G floats; o: G*D floats (staging order).
-// scale_log2 = softmax scale * log2(e).
-void gqa_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G, int D,
-                int t0, int t1, float scale_log2, float* m, float* l, float* o);
+// GQA: q holds G rows of Dk bf16 (the query heads sharing one KV head); token
+// t of the row is k + t*Dk / v + t*Dv.  (Dk, Dv): Dk == Dv a multiple of 32
+// up to 256, or (192, 128) (gqa_dims_supported); G at most 16.  m, l: G
+// floats; o: G*Dv floats (staging order).  scale_log2 = softmax scale *
+// log2(e).
+bool gqa_dims_supported(int Dk, int Dv);
+void gqa_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G, int Dk,
+                int Dv, int t0, int t1, float scale_log2, float* m, float* l, float* o);
 
 // MLA (absorbed, 16 heads): qt is the query in pair-transposed form
 // (mla_prepare_q); token t's latent is c + t*c_tok (512 bf16, also the value)

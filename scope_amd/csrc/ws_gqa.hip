@@ -37,7 +37,8 @@
 
 namespace ws {
 
-constexpr int kGqaD = 128;
+constexpr int kGqaD = 128;   // value width (and key width of the Dk == Dv calls)
+constexpr int kGqaDk192 = 192;  // key width of the decompressed DeepSeek-V2 layout
 constexpr int kGqaWaves = 2;        // waves per workgroup, each its own split
 constexpr int kGqaStages = 2;       // register stages of a wave's load ring
 constexpr int kGqaSplitsPerCu = 2;  // default splits (waves) per CU
@@ -60,7 +61,7 @@ struct GqaParams {
   const int32_t* page_table;
   const int32_t* len_in;
   int32_t* len_out;
-  const uint16_t* k_new;  // [B][Hkv][1][D] or nullptr
+  const uint16_t* k_new;  // [B][Hkv][1][DK] or nullptr (v_new [B][Hkv][1][D])
   const uint16_t* v_new;
   float* out;
   float* lse;
@@ -82,10 +83,15 @@ constexpr int kFirst = 64;
 constexpr int kLast = 128;
 constexpr int kBadPage = 256;
 
-template <int G, bool APPEND>
-__global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_decode_kernel(
+// (The 192-wide key ring needs more than the 256 registers of two waves per
+// SIMD; the grid holds one workgroup per CU, so one wave per SIMD costs no
+// occupancy the launch would use.)
+template <int G, int DK, bool APPEND>
+__global__ __launch_bounds__(64 * kGqaWaves, (kGqaStages <= 2 && DK == kGqaD) ? 2 : 1) void
+gqa_decode_kernel(
     const GqaParams p) {
-  constexpr int D = kGqaD;
+  constexpr int D = kGqaD;     // value width
+  constexpr int KS = DK / 32;  // QK k-steps (32 key columns each)
   constexpr int W = kGqaWaves;
   constexpr int NT = 64 * W;
   constexpr int add = APPEND ? 1 : 0;
@@ -162,35 +168,36 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
   // k_new/v_new.  With valid == false (the request past the range's last
   // block) every lane reads the first row of q instead: same instructions
   // and registers, a cache hit, no HBM traffic.
-  auto load_block = [&](const GqaBlock& m, bool valid, u32x4 (&ka)[2][4],
+  auto load_block = [&](const GqaBlock& m, bool valid, u32x4 (&ka)[2][KS],
                         u32x4 (&vr)[8]) __attribute__((always_inline)) {
-    const uint16_t* kb = valid ? p.k_pages + (size_t)m.tok * D : p.q;
+    const uint16_t* kb = valid ? p.k_pages + (size_t)m.tok * DK : p.q;
     const uint16_t* vb = valid ? p.v_pages + (size_t)m.tok * D : p.q;
     const int last = valid ? (m.nt & kNtMask) - 1 : 0;
     const int new_r = (APPEND && valid) ? m.nr : -1;
-    const size_t new_row = (size_t)m.row * D;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       const int r = min(16 * tt + n16, last);
-      const uint16_t* kr = (APPEND && r == new_r) ? p.k_new + new_row : kb + (size_t)r * D;
+      const uint16_t* kr =
+          (APPEND && r == new_r) ? p.k_new + (size_t)m.row * DK : kb + (size_t)r * DK;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ka[tt][s] = ld_stream(kr + 8 * (4 * s + j));
+      for (int s = 0; s < KS; ++s) ka[tt][s] = ld_stream(kr + 8 * (4 * s + j));
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = min(pv_token(i, j), last);
-      const uint16_t* vrow = (APPEND && r == new_r) ? p.v_new + new_row : vb + (size_t)r * D;
+      const uint16_t* vrow =
+          (APPEND && r == new_r) ? p.v_new + (size_t)m.row * D : vb + (size_t)r * D;
       vr[i] = ld_stream(vrow + 8 * n16);
     }
   };
   // The q rows of kv row `row` as the QK B operand.  Lanes of padding head
   // columns (n16 >= G) load head G - 1: MFMA columns are independent and
   // those columns are never written.
-  u32x4 qb[4];
+  u32x4 qb[KS];
   auto load_q = [&](int row) __attribute__((always_inline)) {
-    const u32x4* qp = (const u32x4*)(p.q + (size_t)(row * G + min(n16, G - 1)) * D);
+    const u32x4* qp = (const u32x4*)(p.q + (size_t)(row * G + min(n16, G - 1)) * DK);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qb[s] = qp[4 * s + j];
+    for (int s = 0; s < KS; ++s) qb[s] = qp[4 * s + j];
   };
 
   f32x4 acc[8];
@@ -199,11 +206,11 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
   float m_run = neg_inf();
   float l_run = 0.f;
 
-  auto compute_block = [&](const GqaBlock& m, const u32x4 (&ka)[2][4],
+  auto compute_block = [&](const GqaBlock& m, const u32x4 (&ka)[2][KS],
                            const u32x4 (&vr)[8]) __attribute__((always_inline)) {
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < KS; ++s) {
       s0 = mfma16x16x32(ka[0][s], qb[s], s0);
       s1 = mfma16x16x32(ka[1][s], qb[s], s1);
     }
@@ -217,13 +224,14 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
     // nr % 4] of the lanes j == (nr % 16) / 4 (8 columns each).
     if (APPEND && m.nr >= 0 && m.nr < 32 && !(m.nt & kBadPage)) {
       const size_t dst = ((size_t)m.tok + m.nr) * D;
+      const size_t dst_k = ((size_t)m.tok + m.nr) * DK;
       const int tt = m.nr >> 4;
       if (n16 == (m.nr & 15)) {
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2)
           if (t2 == tt) {
 #pragma unroll
-            for (int s = 0; s < 4; ++s) ((u32x4*)(p.k_pages_w + dst))[4 * s + j] = ka[t2][s];
+            for (int s = 0; s < KS; ++s) ((u32x4*)(p.k_pages_w + dst_k))[4 * s + j] = ka[t2][s];
           }
       }
       if (j == ((m.nr & 15) >> 2)) {
@@ -285,7 +293,7 @@ __global__ __launch_bounds__(64 * kGqaWaves, kGqaStages <= 2 ? 2 : 1) void gqa_d
   int xb = x_begin;
   fetch_meta(xb);
   GqaBlock mq[S];
-  u32x4 ka[S][2][4], vr[S][8];
+  u32x4 ka[S][2][KS], vr[S][8];
   mq[0] = read_meta(0);
   int run_row = mq[0].row;
   bool run_first = (mq[0].nt & kFirst) != 0;  // the running row's first block was ours
@@ -358,7 +366,7 @@ static int gqa_splits(int n_splits, int rows_kv, int max_len) {
 static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
                       uint16_t* k_pages, uint16_t* v_pages, const int32_t* page_table,
                       const int32_t* len_in, int32_t* len_out, int B, int Hq, int Hkv,
-                      int D, int page_size, int max_pages, int num_pages, int max_len,
+                      int Dk, int D, int page_size, int max_pages, int num_pages, int max_len,
                       int n_splits, float scale, float* out, float* lse,
                       void* workspace, size_t workspace_bytes, void* stream,
                       bool combine, const char* name) {
@@ -370,8 +378,11 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   const int G = Hq / Hkv;
   if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16)
     return set_error(WS_EINVAL, "%s: group size %d unsupported (1,2,4,8,16)", name, G);
-  if (D != kGqaD)
-    return set_error(WS_EINVAL, "%s: head_dim %d unsupported (128)", name, D);
+  if (D != kGqaD || (Dk != kGqaD && Dk != kGqaDk192))
+    return set_error(WS_EINVAL, "%s: head_dim Dk=%d Dv=%d unsupported (128/128, 192/128)",
+                     name, Dk, D);
+  if (Dk == kGqaDk192 && G != 1)
+    return set_error(WS_EINVAL, "%s: Dk=192 takes group size 1 (got %d)", name, G);
   if (page_size <= 0 || max_pages <= 0 || num_pages <= 0 || max_len < 0 ||
       (page_size % 32 && max_pages != 1) ||
       (long long)max_len > (long long)page_size * max_pages)
@@ -428,19 +439,23 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   prm.n_splits = n;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((n + kGqaWaves - 1) / kGqaWaves), block(64 * kGqaWaves);
-#define WS_GQA_CASE(GG)                                                           \
-  case GG:                                                                        \
-    if (k_new)                                                                    \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, true>), grid, block, 0, s, prm);  \
-    else                                                                          \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, false>), grid, block, 0, s, prm); \
+#define WS_GQA_CASE(GG, DKK)                                                           \
+  case GG:                                                                             \
+    if (k_new)                                                                         \
+      hipLaunchKernelGGL((gqa_decode_kernel<GG, DKK, true>), grid, block, 0, s, prm);  \
+    else                                                                               \
+      hipLaunchKernelGGL((gqa_decode_kernel<GG, DKK, false>), grid, block, 0, s, prm); \
     break;
-  switch (G) {
-    WS_GQA_CASE(1)
-    WS_GQA_CASE(2)
-    WS_GQA_CASE(4)
-    WS_GQA_CASE(8)
-    WS_GQA_CASE(16)
+  if (Dk == kGqaD) {
+    switch (G) {
+      WS_GQA_CASE(1, kGqaD)
+      WS_GQA_CASE(2, kGqaD)
+      WS_GQA_CASE(4, kGqaD)
+      WS_GQA_CASE(8, kGqaD)
+      WS_GQA_CASE(16, kGqaD)
+    }
+  } else {
+    switch (G) { WS_GQA_CASE(1, kGqaDk192) }
   }
 #undef WS_GQA_CASE
   int rc = check_launch(name);
@@ -480,7 +495,7 @@ extern "C" int ws_gqa_decode_partial(
     float scale, float* out, float* lse, void* workspace, size_t workspace_bytes,
     void* stream) {
   return gqa_launch(q, nullptr, nullptr, (uint16_t*)k_pages, (uint16_t*)v_pages,
-                    page_table, gpu_len, nullptr, B, Hq, Hkv, D, page_size, max_pages,
+                    page_table, gpu_len, nullptr, B, Hq, Hkv, D, D, page_size, max_pages,
                     num_pages, max_len, n_workgroups, scale, out, lse, workspace,
                     workspace_bytes, stream, true, "ws_gqa_decode_partial");
 }
@@ -494,7 +509,7 @@ extern "C" int ws_gqa_append_decode_partial(
   if (!k_new)
     return set_error(WS_EINVAL, "ws_gqa_append_decode_partial: k_new is null");
   return gqa_launch(q, k_new, v_new, k_pages, v_pages, page_table, len_in, len_out, B,
-                    Hq, Hkv, D, page_size, max_pages, num_pages, max_len, n_workgroups,
+                    Hq, Hkv, D, D, page_size, max_pages, num_pages, max_len, n_workgroups,
                     scale, out, lse, workspace, workspace_bytes, stream, true,
                     "ws_gqa_append_decode_partial");
 }
@@ -508,7 +523,32 @@ extern "C" int ws_gqa_append_decode_split(
   if (!k_new)
     return set_error(WS_EINVAL, "ws_gqa_append_decode_split: k_new is null");
   return gqa_launch(q, k_new, v_new, k_pages, v_pages, page_table, len_in, len_out, B,
-                    Hq, Hkv, D, page_size, max_pages, num_pages, max_len, n_workgroups,
+                    Hq, Hkv, D, D, page_size, max_pages, num_pages, max_len, n_workgroups,
                     scale, out, lse, workspace, workspace_bytes, stream, false,
                     "ws_gqa_append_decode_split");
+}
+
+extern "C" int ws_attn_decode_partial(
+    const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+    const int32_t* page_table, const int32_t* gpu_len, int B, int Hq, int Hkv, int Dk, int Dv,
+    int page_size, int max_pages, int num_pages, int max_len, int n_splits, float scale,
+    float* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  return gqa_launch(q, nullptr, nullptr, (uint16_t*)k_pages, (uint16_t*)v_pages,
+                    page_table, gpu_len, nullptr, B, Hq, Hkv, Dk, Dv, page_size, max_pages,
+                    num_pages, max_len, n_splits, scale, out, lse, workspace,
+                    workspace_bytes, stream, true, "ws_attn_decode_partial");
+}
+
+extern "C" int ws_attn_append_decode_partial(
+    const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new, uint16_t* k_pages,
+    uint16_t* v_pages, const int32_t* page_table, const int32_t* len_in, int32_t* len_out,
+    int B, int Hq, int Hkv, int Dk, int Dv, int page_size, int max_pages, int num_pages,
+    int max_len, int n_splits, float scale, float* out, float* lse, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  if (!k_new)
+    return set_error(WS_EINVAL, "ws_attn_append_decode_partial: k_new is null");
+  return gqa_launch(q, k_new, v_new, k_pages, v_pages, page_table, len_in, len_out, B,
+                    Hq, Hkv, Dk, Dv, page_size, max_pages, num_pages, max_len, n_splits,
+                    scale, out, lse, workspace, workspace_bytes, stream, true,
+                    "ws_attn_append_decode_partial");
 }

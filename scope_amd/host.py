@@ -32,6 +32,7 @@ LIB_PATH = os.path.join(_HERE, "lib", "libwshost.so")
 
 # Entry points declared in include/wshost.h.
 EXPORTS = ("wh_last_error", "wh_version", "wh_isa_supported", "wh_gqa_partial",
+           "wh_attn_partial",
            "wh_mla_partial")
 
 MLA_HEADS = 16
@@ -64,6 +65,8 @@ def lib() -> ctypes.CDLL:
         L.wh_gqa_partial.restype = i32
         L.wh_gqa_partial.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, f32,
                                      vp, vp, i32]
+        L.wh_attn_partial.restype = i32
+        L.wh_attn_partial.argtypes = [vp, vp, vp, vp, vp] + [i32] * 8 + [f32, vp, vp, i32]
         L.wh_mla_partial.restype = i32
         L.wh_mla_partial.argtypes = [vp, vp, vp, i32, vp, i32, vp, vp, i32, i32, i32, i32, f32,
                                      vp, vp, i32]
@@ -164,6 +167,32 @@ def gqa_partial(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, p
     if prepare:
         return call
     call()
+    return out, lse
+
+
+def attn_partial(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, page_table,
+                 lens, scale: float, threads: int = 0, out: torch.Tensor | None = None,
+                 lse: torch.Tensor | None = None):
+    """gqa_partial with separate key / value widths (wh_attn_partial):
+    q [B, Hq, Dk], k_pages [num_pages, Hkv, page_size, Dk], v_pages
+    [num_pages, Hkv, page_size, Dv] -> (out fp32 [B, Hq, Dv], lse fp32
+    [B, Hq]).  (Dk, Dv): equal, or (192, 128)."""
+    B, Hq, Dk = q.shape
+    _cpu(q, torch.bfloat16, "q")
+    _cpu(k_pages, torch.bfloat16, "k_pages")
+    _cpu(v_pages, torch.bfloat16, "v_pages")
+    if k_pages.dim() != 4 or v_pages.dim() != 4 or k_pages.shape[:3] != v_pages.shape[:3] \
+            or k_pages.shape[3] != Dk:
+        raise ValueError(f"pools must be [num_pages, Hkv, page_size, Dk / Dv], got "
+                         f"{tuple(k_pages.shape)} / {tuple(v_pages.shape)}")
+    num_pages, Hkv, ps, _ = k_pages.shape
+    Dv = v_pages.shape[3]
+    table = _table(page_table, B)
+    lens = _lens(lens, B)
+    out, lse = _outputs(out, lse, (B, Hq, Dv), (B, Hq))
+    _check(lib().wh_attn_partial(_p(q), _p(k_pages), _p(v_pages), _p(table), _p(lens), B, Hq,
+                                 Hkv, Dk, Dv, ps, table.shape[1], num_pages,
+                                 ctypes.c_float(scale), _p(out), _p(lse), int(threads)))
     return out, lse
 
 

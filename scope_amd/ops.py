@@ -38,6 +38,8 @@ EXPORTS = (
     "ws_mla_merge_split_uv",
     "ws_split_reduce",
     "ws_lse_merge",
+    "ws_attn_decode_partial",
+    "ws_attn_append_decode_partial",
     "ws_noalloc_scratch_bytes",
     "ws_gqa_append_decode_partial_noalloc",
 )
@@ -114,6 +116,11 @@ def lib() -> ctypes.CDLL:
         L.ws_split_reduce.restype = i32
         L.ws_split_reduce.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp,
                                       vp, vp]
+        L.ws_attn_decode_partial.restype = i32
+        L.ws_attn_decode_partial.argtypes = [vp] * 5 + [i32] * 10 + [f32, vp, vp, vp, sz, vp]
+        L.ws_attn_append_decode_partial.restype = i32
+        L.ws_attn_append_decode_partial.argtypes = [vp] * 8 + [i32] * 10 + [f32, vp, vp, vp,
+                                                                             sz, vp]
         L.ws_noalloc_scratch_bytes.restype = sz
         L.ws_noalloc_scratch_bytes.argtypes = []
         L.ws_gqa_append_decode_partial_noalloc.restype = i32
@@ -278,6 +285,60 @@ def gqa_decode_partial(q, k_pages, v_pages, page_table, gpu_len, scale, max_len,
         _ptr(q), _ptr(k_pages), _ptr(v_pages), _ptr(page_table), _ptr(gpu_len),
         B, Hq, Hkv, D, PS, page_table.shape[1], P, int(max_len), nwg, float(scale),
         _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev)), "ws_gqa_decode_partial")
+    return out, lse
+
+
+def attn_decode_partial(q, k_pages, v_pages, page_table, gpu_len, scale, max_len,
+                        n_workgroups=0, k_new=None, v_new=None, len_out=None, out=None,
+                        lse=None):
+    """Decode attention with separate key / value widths (ws_attn_decode_partial,
+    or ws_attn_append_decode_partial with k_new / v_new): q [B, Hq, Dk],
+    k_pages [P, Hkv, PS, Dk], v_pages [P, Hkv, PS, Dv] bf16 ->
+    (out [B, Hq, Dv] fp32 normalised, lse [B, Hq] fp32).  (Dk, Dv) is
+    (128, 128) or (192, 128) with one query head per KV head.  With k_new
+    [B, Hkv, 1, Dk] / v_new [B, Hkv, 1, Dv], token gpu_len[b] is appended
+    first (fused step; len_out gets the new lengths, max_len must bound
+    gpu_len + 1)."""
+    dev = k_pages.device
+    _require(q, "q", torch.bfloat16, dev, 3)
+    _require(k_pages, "k_pages", torch.bfloat16, dev, 4)
+    _require(v_pages, "v_pages", torch.bfloat16, dev, 4)
+    _require(page_table, "page_table", torch.int32, dev, 2)
+    _require(gpu_len, "gpu_len", torch.int32, dev, 1)
+    B, Hq, Dk = q.shape
+    P, Hkv, PS, Dk2 = k_pages.shape
+    Dv = v_pages.shape[3]
+    if Dk2 != Dk or v_pages.shape[:3] != k_pages.shape[:3]:
+        raise ValueError(f"pools {tuple(k_pages.shape)} / {tuple(v_pages.shape)} do not "
+                         f"match q {tuple(q.shape)}")
+    if page_table.shape[0] != B or gpu_len.shape[0] != B:
+        raise ValueError("page_table/gpu_len batch mismatch")
+    if out is None:
+        out = torch.empty((B, Hq, Dv), dtype=torch.float32, device=dev)
+    if lse is None:
+        lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
+    _require(out, "out", torch.float32, dev, 3)
+    _require(lse, "lse", torch.float32, dev, 2)
+    nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
+    ws = _workspace(dev, wsb)
+    tail = (B, Hq, Hkv, Dk, Dv, PS, page_table.shape[1], P, int(max_len), nwg, float(scale),
+            _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev))
+    if k_new is None:
+        _check(lib().ws_attn_decode_partial(_ptr(q), _ptr(k_pages), _ptr(v_pages),
+                                            _ptr(page_table), _ptr(gpu_len), *tail),
+               "ws_attn_decode_partial")
+        return out, lse
+    _require(k_new, "k_new", torch.bfloat16, dev, 4)
+    _require(v_new, "v_new", torch.bfloat16, dev, 4)
+    if k_new.shape != (B, Hkv, 1, Dk) or v_new.shape != (B, Hkv, 1, Dv):
+        raise ValueError(f"k_new / v_new must be [B, Hkv, 1, Dk] / [B, Hkv, 1, Dv]")
+    if len_out is not None:
+        _require(len_out, "len_out", torch.int32, dev, 1)
+        if len_out.shape[0] != B or len_out.data_ptr() == gpu_len.data_ptr():
+            raise ValueError("len_out must be a separate [B] int32 tensor")
+    _check(lib().ws_attn_append_decode_partial(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
+        _ptr(gpu_len), _ptr(len_out), *tail), "ws_attn_append_decode_partial")
     return out, lse
 
 

@@ -27,19 +27,22 @@ def local_bmm_softmax(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: 
                       n_workgroups: int = 0):
     """_local_bmm_softmax (roofline/bench_resident_kv.py:150-157).
 
-    q [N, G, D], k/v [N, S, D] bf16 contiguous on the GPU ->
-    (o [N, G, D] fp32, max [N, G, 1] fp32, sum [N, G, 1] fp32), equivalent triple.
+    q [N, G, Dk], k [N, S, Dk], v [N, S, Dv] bf16 contiguous on the GPU ->
+    (o [N, G, Dv] fp32, max [N, G, 1] fp32, sum [N, G, 1] fp32), equivalent
+    triple.  Dk == Dv == 128 for the GQA model entries; Dk 192 / Dv 128 with
+    G = 1 for the ds2 entry (roofline/bench_resident_kv.py:10).
     """
-    N, G, D = q.shape
+    N, G, Dk = q.shape
     S = k.shape[1]
+    Dv = v.shape[2]
     if S == 0:
-        return (torch.zeros((N, G, D), dtype=torch.float32, device=q.device),
+        return (torch.zeros((N, G, Dv), dtype=torch.float32, device=q.device),
                 torch.full((N, G, 1), float("-inf"), dtype=torch.float32, device=q.device),
                 torch.zeros((N, G, 1), dtype=torch.float32, device=q.device))
     pt, ln = _dense_paging(N, S, q.device)
-    out, lse = ops.gqa_decode_partial(q.contiguous(), k.contiguous().view(N, 1, S, D),
-                                      v.contiguous().view(N, 1, S, D), pt, ln, scale, S,
-                                      n_workgroups)
+    out, lse = ops.attn_decode_partial(q.contiguous(), k.contiguous().view(N, 1, S, Dk),
+                                       v.contiguous().view(N, 1, S, Dv), pt, ln, scale, S,
+                                       n_workgroups)
     return out, lse.unsqueeze(-1), torch.ones_like(lse).unsqueeze(-1)
 
 
@@ -60,18 +63,20 @@ def pairwise_merge(o1, m1, s1, o2, m2, s2):
 def resident_layer(q, k_buf, v_buf, new_k, new_v, scale):
     """_resident_layer (roofline/bench_resident_kv.py:261-271): write the new
     token into the last slot of the resident buffers and attend over all of
-    them, in one launch.  k_buf/v_buf [N, cap, D], new_k/new_v [N, 1, D],
-    q [N, G, D]; returns the equivalent triple like local_bmm_softmax."""
-    N, cap, D = k_buf.shape
+    them, in one launch.  k_buf [N, cap, Dk], v_buf [N, cap, Dv], new_k
+    [N, 1, Dk], new_v [N, 1, Dv], q [N, G, Dk]; returns the equivalent triple
+    like local_bmm_softmax."""
+    N, cap, Dk = k_buf.shape
+    Dv = v_buf.shape[2]
     if N <= 0 or cap <= 0:
         G = q.shape[1]
-        return (torch.zeros((max(N, 0), G, D), dtype=torch.float32, device=q.device),
+        return (torch.zeros((max(N, 0), G, Dv), dtype=torch.float32, device=q.device),
                 torch.full((max(N, 0), G, 1), float("-inf"), dtype=torch.float32,
                            device=q.device),
                 torch.zeros((max(N, 0), G, 1), dtype=torch.float32, device=q.device))
     pt, ln = _dense_paging(N, cap - 1, q.device)
-    out, lse = ops.gqa_append_decode_partial(
-        q.contiguous(), new_k.contiguous().view(N, 1, 1, D),
-        new_v.contiguous().view(N, 1, 1, D), k_buf.view(N, 1, cap, D),
-        v_buf.view(N, 1, cap, D), pt, ln, None, scale, cap)
+    out, lse = ops.attn_decode_partial(
+        q.contiguous(), k_buf.view(N, 1, cap, Dk), v_buf.view(N, 1, cap, Dv), pt, ln, scale,
+        cap, k_new=new_k.contiguous().view(N, 1, 1, Dk),
+        v_new=new_v.contiguous().view(N, 1, 1, Dv))
     return out, lse.unsqueeze(-1), torch.ones_like(lse).unsqueeze(-1)

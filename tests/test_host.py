@@ -281,3 +281,49 @@ def test_prepared_call_reads_its_buffers_at_call_time():
     np.testing.assert_array_equal(o2.numpy(), want_o.numpy())
     np.testing.assert_array_equal(l2.numpy(), want_l.numpy())
     assert not np.array_equal(o1.numpy(), o2.numpy())
+
+
+@needs_isa
+@pytest.mark.parametrize("Hkv,G,Dk,Dv,page_size,threads", [
+    (16, 1, 192, 128, 64, 7),   # decompressed DeepSeek-V2: 16 heads, 192-wide keys
+    (2, 4, 192, 128, 32, 3),
+    (3, 2, 96, 96, 64, 4),      # Dk == Dv through the same entry point
+])
+def test_attn_partial_separate_key_value_widths(Hkv, G, Dk, Dv, page_size, threads):
+    """wh_attn_partial (the fused_cpu_attn_mla contract with Dk != Dv,
+    kernel/cpu_attn.cpp:638-672) against fp64 and the oracle's C restatement."""
+    from oracle import port
+    rng = np.random.default_rng(Dk + Hkv)
+    lens = [page_size * 2 + 9, 1, 0, 333]
+    B = len(lens)
+    table, num_pages = _paged(rng, lens, page_size)
+    q = bf16_randn((B, Hkv * G, Dk), 11)
+    kp = bf16_randn((num_pages, Hkv, page_size, Dk), 12)
+    vp = bf16_randn((num_pages, Hkv, page_size, Dv), 13)
+    scale = 192 ** -0.5
+    out, lse = host.attn_partial(q, kp, vp, table, lens, scale, threads)
+    assert tuple(out.shape) == (B, Hkv * G, Dv)
+    tb = table.numpy()
+    for b, L in enumerate(lens):
+        k = _gather(bits(kp), tb, b, L, page_size)
+        v = _gather(bits(vp), tb, b, L, page_size)
+        qb = bits(q[b]).reshape(Hkv, G, Dk)
+        ow, lw = O.gqa_attention_fp64(qb, k, v, scale)
+        assert_close(out[b].numpy().reshape(Hkv, G, Dv), ow, OUT_ATOL, OUT_RTOL, f"out b={b}")
+        assert_close(lse[b].numpy().reshape(Hkv, G), lw, LSE_ATOL, LSE_RTOL, f"lse b={b}")
+        if L:
+            po, pm, ps = port.cpu_attn(qb, np.ascontiguousarray(k), np.ascontiguousarray(v),
+                                       scale, normalize=False, n_threads=2)
+            assert_close(out[b].numpy().reshape(Hkv, G, Dv), po / ps, OUT_ATOL, OUT_RTOL,
+                         f"vs C port b={b}")
+            assert_close(lse[b].numpy().reshape(Hkv, G), (pm + np.log(ps))[..., 0], LSE_ATOL,
+                         LSE_RTOL, f"lse vs C port b={b}")
+
+
+@needs_isa
+def test_attn_partial_rejects_other_width_pairs():
+    q = bf16_randn((1, 2, 192), 1)
+    kp = bf16_randn((1, 2, 32, 192), 2)
+    vp = bf16_randn((1, 2, 32, 64), 3)
+    with pytest.raises(host.WhError, match="head_dim"):
+        host.attn_partial(q, kp, vp, torch.zeros((1, 1), dtype=torch.int32), [5], 0.1, 1)
