@@ -101,7 +101,7 @@ int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
 
 /*
  * Plan of a decode call: kind 0 (GQA: rows_kv = B * Hkv, heads = the group
- * size G) or 1 (MLA: rows_kv = B, heads = H = 16), over sequences of at most
+ * size G) or 1 (MLA: rows_kv = B, heads = H, a multiple of 16), over sequences of at most
  * max_len tokens.  n_splits is the number of pieces the call cuts its work
  * into: one per wave for GQA (two per workgroup, each streaming on its
  * own), one per workgroup for MLA.  0 = the library's choice for the current
@@ -223,7 +223,10 @@ int ws_attn_append_decode_partial(const uint16_t* q, const uint16_t* k_new,
  * Split-KV absorbed-MLA decode attention.
  * q_nope: [B*H][512] bf16 (q_nope already multiplied by W_UK), q_pe: [B*H][64].
  * score = (q_nope . c + q_pe . pe) * scale over the shared 576-wide latent,
- * out = softmax . c (512-wide).  H = 16.
+ * out = softmax . c (512-wide).  H: any multiple of 16 (16 for
+ * DeepSeek-V2-Lite, 128 for DeepSeek-V2; nH = q rows / B as in
+ * kernel/cpu_attn.cpp:860); each group of 16 heads is planned as a sequence of
+ * its own over the shared latent, and a sequence's new latent is written once.
  * Outputs out: [B*H][512] fp32 normalised, lse: [B*H] fp32.
  * Replaces the GPU partial of _mla_compressed_forward
  * (system/deepseek.py:364-392; also roofline/bench_rstar_revalidate_ds2.py:74-86).
@@ -282,7 +285,8 @@ int ws_mla_append_decode_split(const uint16_t* q_nope, const uint16_t* q_pe,
  * write out_bf16 and/or out_f32 [rows][Dv] and lse_out [rows] (any may be
  * NULL but not both outputs).
  *   gpu_len          the lengths after the step (the step's len_out)
- *   rows_per_seq     Hkv (GQA) or 1 (MLA); heads: G (GQA) or 16 (MLA)
+ *   rows_per_seq     Hkv (GQA) or 1 (MLA); heads: G (GQA) or H (MLA, a
+ *                    multiple of 16)
  *   Dv               128 (GQA) or 512 (MLA)
  *   page_capacity    page_size * max_pages of the step
  *   n_splits         the split count the step ran with (ws_decode_plan)

@@ -81,11 +81,12 @@ int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* 
                     int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
                     float* out, float* lse, int n_threads);
 
-/* Absorbed-MLA host partial (16 heads, 512-wide latent + 64-wide rope key).
- * Replaces fused_cpu_attn_mla_compressed (kernel/cpu_attn.cpp:852-1022) as
- * called by the decode branch of _mla_compressed_forward
- * (system/deepseek.py:355).
- *   q_nope [B*16, 512], q_pe [B*16, 64] bf16 (row b*16 + h, the order of
+/* Absorbed-MLA host partial (H heads, a multiple of 16: 16 for
+ * DeepSeek-V2-Lite, 128 for DeepSeek-V2; 512-wide latent + 64-wide rope key).
+ * Replaces fused_cpu_attn_mla_compressed (kernel/cpu_attn.cpp:852-1022, nH =
+ * q_proj rows / B at 860) as called by the decode branch of
+ * _mla_compressed_forward (system/deepseek.py:355).
+ *   q_nope [B*H, 512], q_pe [B*H, 64] bf16 (row b*H + h, the order of
  *          system/deepseek.py:337-338)
  *   c_pages, pe_pages: latent (also the value, 512 wide) and rope key (64
  *          wide) of token i of page p at c_pages + (p*page_size + i)*c_stride
@@ -94,11 +95,11 @@ int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* 
  *          pe_pages = c_pages + 512, the reference's separate arrays are
  *          c_stride = 512, pe_stride = 64
  *   page_table, lens: as for GQA
- *   out    [B*16, 512] fp32 normalised partial; lse [B*16] fp32
+ *   out    [B*H, 512] fp32 normalised partial; lse [B*H] fp32
  * Returns WH_OK or a negative WH_E* code. */
 int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
                    int c_stride, const uint16_t* pe_pages, int pe_stride,
-                   const int32_t* page_table, const int32_t* lens, int B, int page_size,
+                   const int32_t* page_table, const int32_t* lens, int B, int H, int page_size,
                    int max_pages, int num_pages, float scale, float* out, float* lse,
                    int n_threads);
 

@@ -299,13 +299,15 @@ int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* 
 
 int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
                    int c_stride, const uint16_t* pe_pages, int pe_stride,
-                   const int32_t* page_table, const int32_t* lens, int B, int page_size,
+                   const int32_t* page_table, const int32_t* lens, int B, int H, int page_size,
                    int max_pages, int num_pages, float scale, float* out, float* lse,
                    int n_threads) {
   using namespace wh;
   g_err[0] = '\0';
   if (!isa_ok()) return fail(WH_ENOTSUP, "wh_mla_partial: this CPU lacks AVX-512 F/BW/BF16");
   if (B < 0) return fail(WH_EINVAL, "wh_mla_partial: bad batch %d", B);
+  if (H < kMlaHeads || H % kMlaHeads)
+    return fail(WH_EINVAL, "wh_mla_partial: %d heads is not a multiple of %d", H, kMlaHeads);
   if (c_stride < kMlaC || pe_stride < kMlaPe)
     return fail(WH_EINVAL, "wh_mla_partial: token strides %d / %d below 512 / 64", c_stride,
                 pe_stride);
@@ -315,10 +317,16 @@ int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t*
   if (int rc = check_pages("wh_mla_partial", page_table, lens, B, page_size, max_pages,
                            num_pages))
     return rc;
-  const int H = kMlaHeads, Dv = kMlaC;
-  const Plan P = make_plan(lens, B);
+  // Rows of the plan: (sequence b, 16-head group g), v = b * ng + g, whose
+  // query / output rows are v * 16 + h = b * H + 16 g + h.
+  const int ng = H / kMlaHeads;
+  const int R = B * ng;
+  const int Hg = kMlaHeads, Dv = kMlaC;
+  std::vector<int32_t> row_len((size_t)R);
+  for (int v = 0; v < R; ++v) row_len[v] = lens[v / ng];
+  const Plan P = make_plan(row_len.data(), R);
   const float sl2 = scale * kLog2e;
-  auto seg = [&](int b, int t0, int t1, float* st) {
+  auto seg = [&](int v, int t0, int t1, float* st) {
     // per-thread scratch: the pair-transposed query, then the staged value
     // pairs (64-byte aligned: the kernel stores them with aligned stores)
     thread_local std::vector<uint32_t> scratch;
@@ -326,9 +334,9 @@ int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t*
     uint32_t* qt = scratch.data();
     qt += (64 - ((uintptr_t)qt & 63)) / 4 % 16;
     uint32_t* vs = qt + kMlaQtWords;
-    mla_prepare_q(q_nope + (size_t)b * H * kMlaC, q_pe + (size_t)b * H * kMlaPe, qt);
-    StateView s = view(st, H);
-    for_pages(page_table + (size_t)b * max_pages, page_size, t0, t1,
+    mla_prepare_q(q_nope + (size_t)v * Hg * kMlaC, q_pe + (size_t)v * Hg * kMlaPe, qt);
+    StateView s = view(st, Hg);
+    for_pages(page_table + (size_t)(v / ng) * max_pages, page_size, t0, t1,
               [&](int pid, int a, int e) {
                 const size_t tok0 = (size_t)pid * page_size;
                 mla_attend(qt, c_pages + tok0 * c_stride, (size_t)c_stride,
@@ -336,16 +344,16 @@ int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t*
                            s.o, vs);
               });
   };
-  auto fin = [&](int b, const float* st) {
+  auto fin = [&](int v, const float* st) {
     write_final(
-        st, H, Dv, lse + (size_t)b * H, [&](int h, int s) { return st[2 * H + s * H + h]; },
-        [&](int h) { return out + ((size_t)b * H + h) * Dv; });
+        st, Hg, Dv, lse + (size_t)v * Hg, [&](int h, int s) { return st[2 * Hg + s * Hg + h]; },
+        [&](int h) { return out + ((size_t)v * Hg + h) * Dv; });
   };
-  auto empty = [&](int b) {
-    std::memset(out + (size_t)b * H * Dv, 0, sizeof(float) * H * Dv);
-    for (int h = 0; h < H; ++h) lse[(size_t)b * H + h] = -INFINITY;
+  auto empty = [&](int v) {
+    std::memset(out + (size_t)v * Hg * Dv, 0, sizeof(float) * Hg * Dv);
+    for (int h = 0; h < Hg; ++h) lse[(size_t)v * Hg + h] = -INFINITY;
   };
-  run_plan(P, B, H, Dv, n_threads, lens, seg, fin, empty,
+  run_plan(P, R, Hg, Dv, n_threads, row_len.data(), seg, fin, empty,
            [](size_t i) { return (int)(i % kMlaHeads); });
   return WH_OK;
 }

@@ -472,16 +472,17 @@ extern "C" int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
                               int n_workgroups, int* n_workgroups_out,
                               size_t* workspace_bytes_out) {
   if ((kind != 0 && kind != 1) || rows_kv < 0 || max_len < 0 || n_workgroups < 0 ||
-      heads <= 0 || heads > 16)
+      heads <= 0 || (kind == 0 && heads > 16) || (kind == 1 && heads % 16))
     return set_error(WS_EINVAL, "ws_decode_plan: bad arguments");
   int n;
   size_t bytes;
   if (kind == 0) {
     n = gqa_splits(n_workgroups, rows_kv, max_len);
     bytes = ws::workspace_bytes(rows_kv, heads, kGqaD, n);
-  } else {
-    n = mla_workgroups(n_workgroups, rows_kv, max_len);
-    bytes = ws::workspace_bytes(rows_kv, heads, 512, n);
+  } else {  // one plan sequence per (sequence, 16-head group)
+    const int rows = rows_kv * (heads / 16);
+    n = mla_workgroups(n_workgroups, rows, max_len);
+    bytes = ws::workspace_bytes(rows, 16, 512, n);
   }
   if (n_workgroups_out) *n_workgroups_out = n;
   if (workspace_bytes_out) *workspace_bytes_out = bytes;

@@ -93,7 +93,9 @@ __global__ __launch_bounds__(128) void lse_merge_kernel(
 // so plain loads see its writes.
 struct MergeSplitParams {
   const int32_t* gpu_len;
-  int B, R, heads, Dv, cap, grid;
+  // B: plan sequences; ng > 1 for absorbed MLA with H = 16 ng heads, whose
+  // plan sequences are (sequence, 16-head group) pairs (ws_plan.h seq_of).
+  int B, ng, R, heads, Dv, cap, grid;
   int add;  // lengths are gpu_len[b] + add (1 when gpu_len is a fused step's len_in)
   const float* out_g;
   const float* lse_g;
@@ -134,8 +136,8 @@ __global__ __launch_bounds__(64) void merge_split_kernel(const MergeSplitParams 
     load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, col_ok ? c : 0, lb,
                                  ob);
   const Plan plan = plan_build<64>(p.gpu_len, p.add, p.cap, p.B, p.R, p.grid, s_pref, s_scan,
-                                   nullptr, s_wpref);
-  const int nbb = (plan_len(p.gpu_len, b, p.add, p.cap) + 31) >> 5;
+                                   nullptr, s_wpref, -1, p.ng);
+  const int nbb = (plan_len(p.gpu_len, seq_of(b, p.ng), p.add, p.cap) + 31) >> 5;
   // One piece: the step's final partial (out_g, fp32); several: their bf16
   // workspace slots, piece s at pieces + s * sstride.
   int n = 1;
@@ -237,6 +239,8 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
   const int t = threadIdx.x;
   const int b = qrow / p.heads;
   const int h = qrow - b * p.heads;
+  const int pv_seq = qrow >> 4;  // plan sequence (b, 16-head group) and head in it
+  const int h16 = qrow & 15;
   // The W_UV rows of the first kUvGroup passes do not depend on the merge:
   // their loads go out first and land while the plan and the merge run.
   const int lane8 = t & 7;
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     load_b<(FMT >= 0 ? FMT : 0)>(p.b_out, p.b_aux0, p.b_aux1, qrow, p.Dv, c, lb, ob);
   const Plan plan =
       plan_build<kUvThreads>(p.gpu_len, p.add, p.cap, p.B, 1, p.grid, s_pref, s_scan, nullptr,
-                             s_wpref);
+                             s_wpref, -1, p.ng);
   const int nbb = (plan_len(p.gpu_len, b, p.add, p.cap) + 31) >> 5;
   int n = 1;
   const float* src = p.out_g + (size_t)qrow * p.Dv;
@@ -266,16 +270,16 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
   const float* lsrc = p.lse_g + qrow;
   size_t sstride = 0, lstride = 0;
   if (nbb > 0 && plan.n > 0) {
-    const int row_start = s_pref[b];
+    const int row_start = s_pref[pv_seq];
     int w_first, nseg;
-    plan_row_splits(plan, b, row_start, nbb, s_wpref, w_first, nseg);
-    if (nseg > 1) {
+    plan_row_splits(plan, pv_seq, row_start, nbb, s_wpref, w_first, nseg);
+    if (nseg > 1) {  // pieces hold 16 heads each
       n = nseg;
-      const size_t slot0 = (size_t)(w_first + b) * p.heads + h;
+      const size_t slot0 = (size_t)(w_first + pv_seq) * 16 + h16;
       pieces = p.part_out + slot0 * p.Dv;
       lsrc = p.part_lse + slot0;
-      sstride = (size_t)p.heads * p.Dv;
-      lstride = p.heads;
+      sstride = (size_t)16 * p.Dv;
+      lstride = 16;
     }
   }
   // The merging threads' piece columns are requested with the lse values.
@@ -383,6 +387,7 @@ int merge_split_pieces(const int32_t* len, int len_add, int B, int R, int heads,
   MergeSplitParams prm;
   prm.gpu_len = len;
   prm.B = B;
+  prm.ng = 1;
   prm.R = R;
   prm.heads = heads;
   prm.Dv = Dv;
@@ -419,9 +424,15 @@ extern "C" int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, i
     return set_error(WS_EINVAL, "ws_merge_split: null input pointer");
   if (!out_bf16 && !out_f32)
     return set_error(WS_EINVAL, "ws_merge_split: no output");
-  if (B < 0 || B > kMaxSeqs || rows_per_seq <= 0 || heads <= 0 || heads > 16 || Dv <= 0 ||
-      Dv % 4 || Dv > 512 || page_capacity <= 0 || n_workgroups <= 0)
+  // an absorbed-MLA step with H = 16 ng heads planned (sequence, head group) pairs
+  const int ng = (Dv == 512 && rows_per_seq == 1 && heads > 16 && heads % 16 == 0)
+                     ? heads / 16 : 1;
+  if (B < 0 || (long long)B * ng > kMaxSeqs || rows_per_seq <= 0 || heads <= 0 ||
+      (heads > 16 && ng == 1) || Dv <= 0 || Dv % 4 || Dv > 512 || page_capacity <= 0 ||
+      n_workgroups <= 0)
     return set_error(WS_EINVAL, "ws_merge_split: bad sizes");
+  const int Bp = B * ng;      // plan sequences
+  heads /= ng;                // heads per plan row
   if (b_out && (!b_aux0 || (fmt_b != WS_PARTIAL_LSE_F32 && !b_aux1)))
     return set_error(WS_EINVAL, "ws_merge_split: host partial without its lse / max / sum");
   if (b_out && fmt_b != WS_PARTIAL_LSE_F32 && fmt_b != WS_TRIPLE_UNNORM_F32 &&
@@ -433,7 +444,7 @@ extern "C" int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, i
   if (((uintptr_t)workspace & 255u) || ((uintptr_t)out_g | (uintptr_t)out_f32 |
                                          (uintptr_t)b_out) & 15u || ((uintptr_t)out_bf16 & 7u))
     return set_error(WS_EINVAL, "ws_merge_split: misaligned buffer");
-  const long long rows_kv = (long long)B * rows_per_seq;
+  const long long rows_kv = (long long)Bp * rows_per_seq;
   if (rows_kv > (1 << 24))
     return set_error(WS_EINVAL, "ws_merge_split: %lld rows exceed %d", rows_kv, 1 << 24);
   const size_t need = ws::workspace_bytes((int)rows_kv, heads, Dv, n_workgroups);
@@ -444,7 +455,8 @@ extern "C" int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, i
   const SplitWorkspace w = carve_workspace((void*)workspace, (int)rows_kv, heads, n_workgroups);
   MergeSplitParams prm;
   prm.gpu_len = gpu_len;
-  prm.B = B;
+  prm.B = Bp;
+  prm.ng = ng;
   prm.R = rows_per_seq;
   prm.heads = heads;
   prm.Dv = Dv;
@@ -530,10 +542,12 @@ extern "C" int ws_mla_merge_split_uv(const int32_t* gpu_len, int B, int heads,
   constexpr int Dv = 512;
   if (!gpu_len || !out_g || !lse_g || !workspace || !w_uv || !out_v)
     return set_error(WS_EINVAL, "ws_mla_merge_split_uv: null pointer");
-  if (B < 0 || B > kMaxSeqs || heads <= 0 || heads > 16 || page_capacity <= 0 ||
-      n_workgroups <= 0 || Dout <= 0 || Dout % 32 || Dout > 512)
+  if (B < 0 || heads < 16 || heads % 16 || (long long)B * (heads / 16) > kMaxSeqs ||
+      page_capacity <= 0 || n_workgroups <= 0 || Dout <= 0 || Dout % 32 || Dout > 512)
     return set_error(WS_EINVAL, "ws_mla_merge_split_uv: bad sizes B=%d heads=%d Dout=%d", B,
                      heads, Dout);
+  const int ng = heads / 16;
+  const int Bp = B * ng;  // plan sequences (sequence, 16-head group)
   if (b_out && (!b_aux0 || (fmt_b != WS_PARTIAL_LSE_F32 && !b_aux1)))
     return set_error(WS_EINVAL, "ws_mla_merge_split_uv: host partial without its lse / max / sum");
   if (b_out && fmt_b != WS_PARTIAL_LSE_F32 && fmt_b != WS_TRIPLE_UNNORM_F32 &&
@@ -546,15 +560,16 @@ extern "C" int ws_mla_merge_split_uv(const int32_t* gpu_len, int B, int heads,
                                          (uintptr_t)w_uv) & 15u ||
       ((uintptr_t)out_latent & 7u) || ((uintptr_t)out_v & 1u))
     return set_error(WS_EINVAL, "ws_mla_merge_split_uv: misaligned buffer");
-  const size_t need = ws::workspace_bytes(B, heads, Dv, n_workgroups);
+  const size_t need = ws::workspace_bytes(Bp, 16, Dv, n_workgroups);
   if (workspace_bytes < need)
     return set_error(WS_EWORKSPACE, "ws_mla_merge_split_uv: workspace %zu < %zu bytes",
                      workspace_bytes, need);
   if (B == 0) return WS_OK;
-  const SplitWorkspace w = carve_workspace((void*)workspace, B, heads, n_workgroups);
+  const SplitWorkspace w = carve_workspace((void*)workspace, Bp, 16, n_workgroups);
   MergeSplitParams prm;
   prm.gpu_len = gpu_len;
-  prm.B = B;
+  prm.B = Bp;
+  prm.ng = ng;
   prm.R = 1;
   prm.heads = heads;
   prm.Dv = Dv;

@@ -50,7 +50,9 @@ struct MlaParams {
   float* lse;
   uint16_t* part_out;  // [slot][16][512] bf16
   float* part_lse;     // [slot][16]
-  int B, page_size, max_pages, num_pages, cap;
+  // B: plan sequences v = b * ng + g, one per (sequence b, 16-head group g);
+  // rows of q / out are v * 16 + h, i.e. b * H + 16 g + h with H = 16 ng.
+  int B, ng, page_size, max_pages, num_pages, cap;
   float scale_log2;
 };
 
@@ -107,13 +109,14 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
   const int col0 = 128 * wave;
 
   if (APPEND && p.len_out && g == 0)
-    for (int b = tid; b < p.B; b += NT) p.len_out[b] = step_len_out(p.len_in, b, add, p.cap);
+    for (int b = tid; b < p.B / p.ng; b += NT)
+      p.len_out[b] = step_len_out(p.len_in, b, add, p.cap);
   const Plan plan = plan_build<NT>(p.len_in, add, p.cap, p.B, 1, gridDim.x, s_pref, s_scan,
-                                   s_len, s_wpref, g);
+                                   s_len, s_wpref, g, p.ng);
   if (g == 0) {  // sequences without tokens: the empty partial (0, -inf), or
     for (int b = 0; b < p.B; ++b) {  // NaN for an invalid length
       if (s_pref[b + 1] != s_pref[b]) continue;
-      const bool ok = len_ok(p.len_in[b], add, p.cap);
+      const bool ok = len_ok(p.len_in[seq_of(b, p.ng)], add, p.cap);
       for (int idx = tid; idx < kMlaH * kMlaC; idx += NT)
         p.out[(size_t)b * kMlaH * kMlaC + idx] = ok ? 0.f : qnan();
       if (tid < kMlaH) p.lse[b * kMlaH + tid] = ok ? neg_inf() : qnan();
@@ -136,8 +139,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     const int t_begin = (blk - row_start) * 32;
     const int t_end = min(len, (seg_end - row_start) * 32);
     const int nblk = seg_end - blk;
-    const int orow = b * kMlaH + n16;
-    const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
+    const int orow = b * kMlaH + n16;  // b: plan sequence (sequence, head group)
+    const int sb = uniform(seq_of(b, p.ng));  // the sequence whose latent it reads
+    const int32_t* pt = p.page_table + (size_t)sb * p.max_pages;
 
     // Page ids of the segment's blocks, 64 at a time (lane l: block
     // pid_base + l), read with readlane: the ring issues no load whose
@@ -190,9 +194,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     // completion the compiler can only wait for all at once).
     const char* g0 = (const char*)p.latent;
     const long long nc_off =
-        APPEND ? (const char*)(p.c_new + (size_t)b * p.c_stride) - g0 : 0;
+        APPEND ? (const char*)(p.c_new + (size_t)sb * p.c_stride) - g0 : 0;
     const long long npe_off =
-        APPEND ? (const char*)(p.pe_new + (size_t)b * p.pe_stride) - g0 - 16 * (kMlaC / 8) : 0;
+        APPEND ? (const char*)(p.pe_new + (size_t)sb * p.pe_stride) - g0 - 16 * (kMlaC / 8) : 0;
     const long long dummy_off = (const char*)dummy - g0;
     const int pe_row = tid >> 3;
     const int pe_col = kMlaC / 8 + (tid & 7);
@@ -316,8 +320,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     // The appended token is its sequence's last, so a segment that holds it
     // ends with its block, whose tile is still intact: row len_old - t0 of
     // tile (nblk - 1) % 3 holds its 72 chunks (read from c_new / pe_new by
-    // the ring), which go from LDS into the token's page slot.
-    if (APPEND && len_old >= t_begin && len_old < t_end) {
+    // the ring), which go from LDS into the token's page slot.  (Head group
+    // 0 of the sequence writes it.)
+    if (APPEND && len_old >= t_begin && len_old < t_end && b == sb * p.ng) {
       const int t0 = t_begin + 32 * (nblk - 1);
       const int pid = __builtin_amdgcn_readlane(m_pid, nblk - 1 - pid_base);
       const int page = t0 / p.page_size;
@@ -359,8 +364,8 @@ __global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int g
   const int b = hrow / kMlaH;
   const int h = hrow - b * kMlaH;
   const int add = p.c_new ? 1 : 0;
-  const Plan plan =
-      plan_build<64>(p.len_in, add, p.cap, p.B, 1, grid, s_pref, s_scan, nullptr, s_wpref);
+  const Plan plan = plan_build<64>(p.len_in, add, p.cap, p.B, 1, grid, s_pref, s_scan, nullptr,
+                                   s_wpref, -1, p.ng);
   const int row_start = s_pref[b], row_end = s_pref[b + 1];
   if (row_end == row_start) return;
   int w_first, n;
@@ -419,9 +424,12 @@ static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
                       void* stream, bool combine, const char* name) {
   if (!q_nope || !q_pe || !latent_pages || !page_table || !len_in || !out || !lse)
     return set_error(WS_EINVAL, "%s: null pointer", name);
-  if (B < 0 || B > kMaxSeqs || H != kMlaH)
-    return set_error(WS_EINVAL, "%s: B=%d H=%d unsupported (H 16, B <= %d)", name, B, H,
-                     kMaxSeqs);
+  // H = 16 ng: each 16-head group is its own plan sequence over the shared latent
+  if (B < 0 || H < kMlaH || H % kMlaH || (long long)B * (H / kMlaH) > kMaxSeqs)
+    return set_error(WS_EINVAL,
+                     "%s: B=%d H=%d unsupported (H a multiple of 16, B * H / 16 <= %d)", name, B,
+                     H, kMaxSeqs);
+  const int ng = H / kMlaH;
   if (page_size <= 0 || max_pages <= 0 || num_pages <= 0 || max_len < 0 ||
       (page_size % 32 && max_pages != 1) ||
       (long long)max_len > (long long)page_size * max_pages)
@@ -440,17 +448,18 @@ static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
   if (len_out && len_out == len_in)
     return set_error(WS_EINVAL, "%s: len_out must not alias len_in", name);
   if (B == 0) return WS_OK;
-  if ((long long)B * ((max_len + 32) / 32) * 4096 >= (1LL << 31))
+  const int Bv = B * ng;  // plan sequences (sequence, head group)
+  if ((long long)Bv * ((max_len + 32) / 32) * 4096 >= (1LL << 31))
     return set_error(WS_EINVAL, "%s: %d sequences of %d tokens exceed the block index range",
-                     name, B, max_len);
-  const int n = mla_workgroups(n_workgroups, B, max_len);
-  const size_t need = ws::workspace_bytes(B, kMlaH, kMlaC, n);
+                     name, Bv, max_len);
+  const int n = mla_workgroups(n_workgroups, Bv, max_len);
+  const size_t need = ws::workspace_bytes(Bv, kMlaH, kMlaC, n);
   if (!workspace || workspace_bytes < need)
     return set_error(WS_EWORKSPACE, "%s: workspace %zu < %zu bytes", name, workspace_bytes,
                      need);
   if (((uintptr_t)workspace & 255u) != 0)
     return set_error(WS_EINVAL, "%s: workspace must be 256-byte aligned", name);
-  const SplitWorkspace w = carve_workspace(workspace, B, kMlaH, n);
+  const SplitWorkspace w = carve_workspace(workspace, Bv, kMlaH, n);
   MlaParams prm;
   prm.q_nope = q_nope;
   prm.q_pe = q_pe;
@@ -467,7 +476,8 @@ static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
   prm.lse = lse;
   prm.part_out = w.part_out;
   prm.part_lse = w.part_lse;
-  prm.B = B;
+  prm.B = Bv;
+  prm.ng = ng;
   prm.page_size = page_size;
   prm.max_pages = max_pages;
   prm.num_pages = num_pages;
@@ -480,7 +490,7 @@ static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
     hipLaunchKernelGGL(mla_decode_kernel<false>, dim3(n), dim3(256), 0, s, prm);
   int rc = check_launch(name);
   if (rc || n == 1 || !combine) return rc;
-  hipLaunchKernelGGL(mla_reduce_kernel, dim3(B * kMlaH, kMlaC / 256), dim3(64), 0, s, prm,
+  hipLaunchKernelGGL(mla_reduce_kernel, dim3(Bv * kMlaH, kMlaC / 256), dim3(64), 0, s, prm,
                      n);
   return check_launch(name);
 }

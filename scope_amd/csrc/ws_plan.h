@@ -60,6 +60,12 @@ __device__ __forceinline__ int plan_len(const int32_t* len_in, int b, int add, i
   return len_ok(l, add, cap) ? l + add : 0;
 }
 
+// Length slot of plan sequence v.  A call whose sequences carry ng groups
+// of 16 query heads over one shared latent (absorbed MLA with H = 16 ng)
+// plans over v = b ng + group: each group is its own plan sequence with
+// sequence b's length.
+__device__ __forceinline__ int seq_of(int v, int ng) { return ng == 1 ? v : v / ng; }
+
 // len_out of a fused step: the new length, or -1 for an invalid len_in.
 __device__ __forceinline__ int step_len_out(const int32_t* len_in, int b, int add, int cap) {
   const int l = len_in[b];
@@ -106,16 +112,19 @@ __device__ __forceinline__ int plan_start(const Plan& p, int g) {
 // A split that passes its index g >= 0 gets its range in has_work / begin /
 // end (and, with at most 64 sequences, the sequence of its first block in
 // b0), computed from registers.
+//
+// ng > 1: B counts plan sequences v = b ng + group, whose lengths are
+// len_in[v / ng] (seq_of).
 template <int NT>
 __device__ Plan plan_build(const int32_t* len_in, int add, int cap, int B, int R,
                            int grid, int* s_pref, int* s_scan, int* s_len = nullptr,
-                           int* s_wpref = nullptr, int g = -1) {
+                           int* s_wpref = nullptr, int g = -1, int ng = 1) {
   constexpr int NW = NT / 64;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
   if (B >= 1 && B <= 64) {
-    const int l = lane < B ? plan_len(len_in, lane, add, cap) : 0;
+    const int l = lane < B ? plan_len(len_in, seq_of(lane, ng), add, cap) : 0;
     const int nb = R * ((l + 31) >> 5);
     const int incl = __ockl_wfscan_add_i32(nb, true);
     if (lane < B) {
@@ -178,7 +187,7 @@ __device__ Plan plan_build(const int32_t* len_in, int add, int cap, int B, int R
   const int b1 = min(B, b0 + chunk);
   int local = 0;
   for (int b = b0; b < b1; ++b) {
-    const int l = plan_len(len_in, b, add, cap);
+    const int l = plan_len(len_in, seq_of(b, ng), add, cap);
     if (s_len) s_len[b] = l;
     local += R * ((l + 31) >> 5);
   }
@@ -204,7 +213,7 @@ __device__ Plan plan_build(const int32_t* len_in, int add, int cap, int B, int R
   int run = s_scan[wave] + incl - local;
   for (int b = b0; b < b1; ++b) {
     s_pref[b] = run;
-    run += R * (((s_len ? s_len[b] : plan_len(len_in, b, add, cap)) + 31) >> 5);
+    run += R * (((s_len ? s_len[b] : plan_len(len_in, seq_of(b, ng), add, cap)) + 31) >> 5);
   }
   if (t == 0) s_pref[B] = s_scan[NW];
   __syncthreads();

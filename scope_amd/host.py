@@ -68,8 +68,8 @@ def lib() -> ctypes.CDLL:
         L.wh_attn_partial.restype = i32
         L.wh_attn_partial.argtypes = [vp, vp, vp, vp, vp] + [i32] * 8 + [f32, vp, vp, i32]
         L.wh_mla_partial.restype = i32
-        L.wh_mla_partial.argtypes = [vp, vp, vp, i32, vp, i32, vp, vp, i32, i32, i32, i32, f32,
-                                     vp, vp, i32]
+        L.wh_mla_partial.argtypes = [vp, vp, vp, i32, vp, i32, vp, vp] + [i32] * 5 + [f32, vp,
+                                                                                     vp, i32]
         _lib = L
     return _lib
 
@@ -249,16 +249,21 @@ def _mla_call(q_nope, q_pe, c, c_stride, pe, pe_stride, page_table, lens, page_s
     _cpu(q_nope, torch.bfloat16, "q_nope")
     _cpu(q_pe, torch.bfloat16, "q_pe")
     rows = q_nope.shape[0]
-    if rows % MLA_HEADS or q_nope.shape != (rows, MLA_C) or q_pe.shape != (rows, MLA_PE):
-        raise ValueError(f"q_nope must be [B*16, 512] and q_pe [B*16, 64], got "
-                         f"{tuple(q_nope.shape)} / {tuple(q_pe.shape)}")
-    B = rows // MLA_HEADS
+    table = torch.as_tensor(page_table, dtype=torch.int32)
+    B = table.shape[0] if table.dim() == 2 else 0
+    # H = q rows / B, any multiple of 16 (kernel/cpu_attn.cpp:860 takes nH the same way)
+    if B == 0 or rows % (B * MLA_HEADS) or q_nope.shape != (rows, MLA_C) or \
+            q_pe.shape != (rows, MLA_PE):
+        raise ValueError(f"q_nope must be [B*H, 512] and q_pe [B*H, 64] with H a multiple "
+                         f"of 16 and B = page_table rows, got {tuple(q_nope.shape)} / "
+                         f"{tuple(q_pe.shape)}, {B} sequences")
+    H = rows // B
     table = _table(page_table, B)
     lens = _lens(lens, B)
     out, lse = _outputs(out, lse, (rows, MLA_C), (rows,))
     call = Prepared(lib().wh_mla_partial,
                     (_p(q_nope), _p(q_pe), _p(c), int(c_stride), _p(pe), int(pe_stride),
-                     _p(table), _p(lens), B, int(page_size), table.shape[1], int(num_pages),
+                     _p(table), _p(lens), B, H, int(page_size), table.shape[1], int(num_pages),
                      ctypes.c_float(scale), _p(out), _p(lse), int(threads)),
                     (q_nope, q_pe, c, pe, table, lens, out, lse))
     if prepare:

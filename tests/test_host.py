@@ -327,3 +327,27 @@ def test_attn_partial_rejects_other_width_pairs():
     vp = bf16_randn((1, 2, 32, 64), 3)
     with pytest.raises(host.WhError, match="head_dim"):
         host.attn_partial(q, kp, vp, torch.zeros((1, 1), dtype=torch.int32), [5], 0.1, 1)
+
+
+@needs_isa
+@pytest.mark.parametrize("H,lens,threads", [(32, [300, 0, 77], 5), (128, [1000, 64], 16)])
+def test_mla_partial_any_multiple_of_16_heads(H, lens, threads):
+    """H = q rows / B as in fused_cpu_attn_mla_compressed (kernel/cpu_attn.cpp:860):
+    DeepSeek-V2's 128 heads over one shared latent."""
+    B = len(lens)
+    cap = max(lens)
+    qn = bf16_randn((B * H, 512), 400 + H, 0.5)
+    qp = bf16_randn((B * H, 64), 401 + H, 0.5)
+    c = bf16_randn((B, cap, 512), 402 + H, 0.5)
+    pe = bf16_randn((B, cap, 64), 403 + H, 0.5)
+    scale = 192 ** -0.5
+    out, lse = host.mla_partial_dense(qn, qp, c, pe, lens, scale, threads)
+    assert tuple(out.shape) == (B * H, 512)
+    for b, L in enumerate(lens):
+        h = slice(b * H, (b + 1) * H)
+        ow, lw = O.mla_attention_fp64(bits(qn[h]), bits(qp[h]), bits(c[b:b + 1, :L]),
+                                      bits(pe[b:b + 1, :L]), scale)
+        assert_close(out[h].numpy(), ow, OUT_ATOL, OUT_RTOL, f"H={H} out b={b}")
+        assert_close(lse[h].numpy(), lw, LSE_ATOL, LSE_RTOL, f"H={H} lse b={b}")
+    with pytest.raises(ValueError, match="multiple"):
+        host.mla_partial_dense(qn[:B * 24], qp[:B * 24], c, pe, lens, scale, threads)
