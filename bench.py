@@ -559,23 +559,12 @@ def epilogue_bench(*, B, L, steps, seed, dev, label):
 
 
 def host_read_gbs(threads, nbytes=1 << 30, reps=5):
-    """Host DRAM read bandwidth: a multi-threaded sum over an nbytes fp32
-    array (torch's CPU reduction on `threads` threads), best of `reps`."""
-    import torch
+    """Host DRAM streaming read bandwidth (wh_host_read_gbs: `threads` OpenMP
+    threads summing a buffer they first touched with 512-bit loads), best of
+    `reps` passes."""
+    from scope_amd import host
 
-    old = torch.get_num_threads()
-    torch.set_num_threads(threads)
-    try:
-        x = torch.ones(nbytes // 4, dtype=torch.float32)
-        x.sum()
-        best = float("inf")
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            x.sum()
-            best = min(best, time.perf_counter() - t0)
-        return round(nbytes / best / 1e9, 1)
-    finally:
-        torch.set_num_threads(old)
+    return round(host.host_read_gbs(nbytes, threads, reps), 1)
 
 
 def share_model(rows):
@@ -740,6 +729,75 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
         "host_partial_gbs": round(h_bytes / (cpu / layers) / 1e9, 2) if with_host else None,
         "layer_bytes": int(g_bytes + h_bytes),
     }
+
+
+def share_control_bench(*, B, layers, lens, start_share, budget_frac, steps, seed, dev, threads,
+                        label):
+    """The share controller driving a two-sided paged MLA cache
+    (scope_amd.paged.PagedMlaCache + scheduler.ShareController) through
+    `steps` decode steps of a `layers`-layer model, with an HBM budget of
+    budget_frac of the cache's bytes, starting from share start_share.
+    Returns the per-step share, wall time per layer and the moves."""
+    import torch
+
+    from scope_amd.paged import PagedMlaCache
+    from scope_amd.scheduler import ShareController, ShareScheduler, Side
+
+    H = 16
+    lens = [int(x) for x in lens]
+    bpt = 1152
+    total = sum(lens) * bpt * layers
+    sched = ShareScheduler(gpu=Side(15e-6, 5e12), host=Side(40e-6, 50e9), xfer_s=60e-6,
+                           hbm_budget_bytes=budget_frac * total)
+    ctl = ShareController(sched, bpt, layers, PAGE)
+    host0 = ctl.targets_for(start_share, lens)
+    need_h = sum(-(-L // PAGE) for L in lens) + B  # host pages for any share
+    need_g = int(budget_frac * sum(lens) / PAGE) + 2 * B + (steps + PAGE) * B // PAGE
+    cache = PagedMlaCache(layers, B, max_tokens=max(lens) + steps + 1, page_size=PAGE,
+                          host_pages=need_h, gpu_pages=need_g, device=dev)
+    cache.reserve_layout(lens, host0)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    cache.gpu.latent.normal_(0.0, 0.5, generator=gen)
+    rnd = _randn_bf16((need_h, PAGE, 576), gen, 0.5, dev).cpu()
+    for l in range(layers):
+        cache.host.data[0][l].copy_(rnd)
+    del rnd
+    rows = B * H
+    qn = [_randn_bf16((rows, 512), gen, 0.5, dev) for _ in range(layers)]
+    qp = [_randn_bf16((rows, 64), gen, 0.5, dev) for _ in range(layers)]
+    kv_new = _randn_bf16((layers, B, 1, 576), gen, 0.5, dev)
+    cache.attach(ctl)
+    scale = 192 ** -0.5
+    per_step = []
+    for i in range(steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for l in range(layers):
+            cache.step(l, qn[l], qp[l], kv_new[l, :, :, :512], kv_new[l, :, :, 512:], scale,
+                       host_threads=threads)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        moved = [m for m in ctl.moves if m.step == i + 1]
+        per_step.append({
+            "step": i, "share_after": round(ctl.shares[-1], 4),
+            "ms": round(dt * 1e3, 2),
+            "us_per_layer_excl_move": round((dt - sum(m.seconds for m in moved)) / layers * 1e6,
+                                            1),
+            "move_ms": round(sum(m.seconds for m in moved) * 1e3, 1),
+            "move_pages_per_layer": sum(m.pages for m in moved)})
+        log(f"share control step {i}: share {per_step[-1]['share_after']}, "
+            f"{per_step[-1]['us_per_layer_excl_move']} us/layer, move "
+            f"{per_step[-1]['move_ms']} ms")
+    moves = [{"step": m.step, "from": round(m.share_from, 4), "to": round(m.share_to, 4),
+              "pages_per_layer": m.pages, "ms": round(m.seconds * 1e3, 1),
+              "gbs": round(m.pages * PAGE * bpt * layers / m.seconds / 1e9, 1)}
+             for m in ctl.moves]
+    return {"label": label, "batch": B, "layers": layers, "start_share": start_share,
+            "hbm_budget_frac": budget_frac, "host_threads": threads,
+            "capacity_share_start": round(sched.capacity_share(sum(lens) * bpt, layers), 4),
+            "chosen": [round(r, 4) for r in ctl.chosen], "steps": per_step, "moves": moves,
+            "gpu_rate_gbs": round(sched.gpu.rate_bps / 1e9, 1),
+            "host_rate_gbs": round(sched.host.rate_bps / 1e9, 1)}
 
 
 # ---------------------------------------------------------------------------
@@ -1101,6 +1159,11 @@ def main():
                               "length_model": "lognormal(ln 4096, 1.0) clipped [256, 65536]",
                               "by_share": rows,
                               "scheduler": share_model(rows)}
+        sc = share_control_bench(B=32, layers=args.model_layers, lens=m_lens, start_share=0.1,
+                                 budget_frac=0.5, steps=10, seed=args.seed + 23, dev=dev,
+                                 threads=th, label="dsv2lite_mla_b32_share_control")
+        extra["mla_model"]["share_control"] = sc
+        torch.cuda.empty_cache()
         sm = extra["mla_model"]["scheduler"]
         log(f"share model: gpu {sm['gpu_fit']}, host {sm['host_fit']}, r_balance "
             f"{sm['r_balance']}, predicted/measured us per layer "

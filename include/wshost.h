@@ -30,6 +30,7 @@
 #ifndef WSHOST_H
 #define WSHOST_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -102,6 +103,14 @@ int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t*
                    const int32_t* page_table, const int32_t* lens, int B, int H, int page_size,
                    int max_pages, int num_pages, float scale, float* out, float* lse,
                    int n_threads);
+
+/* Streaming read bandwidth of the host memory in GB/s (the host side's
+ * roofline for the share scheduler): n_threads OpenMP threads (<= 0: the
+ * default) sum a buffer of `bytes` (>= 1 MiB) that they first touched, best
+ * of `reps` passes after one warm-up.  No counterpart in the reference (its
+ * share tables are calibrated offline).  Returns 0 on bad arguments or a CPU
+ * without AVX-512. */
+double wh_host_read_gbs(size_t bytes, int n_threads, int reps);
 
 #ifdef __cplusplus
 }

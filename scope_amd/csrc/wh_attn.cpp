@@ -358,4 +358,36 @@ int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t*
   return WH_OK;
 }
 
+double wh_host_read_gbs(size_t bytes, int n_threads, int reps) {
+  if (bytes < ((size_t)1 << 20) || reps < 1) return 0.0;
+  if (!isa_ok()) return 0.0;
+  const int n = n_threads > 0 ? n_threads : omp_get_max_threads();
+  const size_t words = bytes / 64 * 8;  // 64-byte lines of 8 doubles
+  std::unique_ptr<double[]> buf(new double[words]);
+  double best = 0.0;
+#pragma omp parallel num_threads(n)
+  {
+    // first touch by the reading threads (their pages on their memory)
+#pragma omp for schedule(static)
+    for (size_t i = 0; i < words; ++i) buf[i] = 1.0;
+    for (int r = 0; r <= reps; ++r) {
+#pragma omp barrier
+      double t0 = 0.0;
+#pragma omp master
+      t0 = omp_get_wtime();
+      const int nt = omp_get_num_threads(), it = omp_get_thread_num();
+      const size_t lines = words / 8;
+      const size_t l0 = lines * it / nt, l1 = lines * (it + 1) / nt;
+      const double sum = wh::sum_lines(buf.get() + 8 * l0, 8 * (l1 - l0));
+#pragma omp barrier
+#pragma omp master
+      {
+        const double dt = omp_get_wtime() - t0;
+        if (r > 0 && sum >= 0.0 && dt > 0.0) best = std::max(best, (double)(words * 8) / dt / 1e9);
+      }
+    }
+  }
+  return best;
+}
+
 }  // extern "C"

@@ -228,18 +228,24 @@ namespace {
 // Scores (lanes = heads) of 16 tokens: latent row j at c + j*CT, rope row at
 // pe + j*PT (token strides known at compile time, so each row is an
 // immediate displacement off one base register).
+// pf_c / pf_pe: the next 16 tokens' rows, prefetched one cache line per
+// pair step (256 lines from pf_c, 32 from pf_pe: the 16 rows of either
+// compiled layout), so the next group streams in while this one computes;
+// nullptr for none.
 template <int CT, int PT>
 inline void mla_scores16(const uint32_t* qt, const uint16_t* c, const uint16_t* pe,
-                         __m512* acc) {
+                         __m512* acc, const char* pf_c = nullptr, const char* pf_pe = nullptr) {
 #pragma GCC unroll 16
   for (int j = 0; j < 16; ++j) acc[j] = _mm512_setzero_ps();
   for (int p = 0; p < kMlaC / 2; ++p) {
+    if (pf_c) _mm_prefetch(pf_c + 64 * p, _MM_HINT_T0);
     const __m512bh qv = (__m512bh)_mm512_loadu_si512(qt + 16 * p);
 #pragma GCC unroll 16
     for (int j = 0; j < 16; ++j)
       acc[j] = _mm512_dpbf16_ps(acc[j], qv, bcast_pair(c + j * CT + 2 * p));
   }
   for (int p = 0; p < kMlaPe / 2; ++p) {
+    if (pf_pe) _mm_prefetch(pf_pe + 64 * p, _MM_HINT_T0);
     const __m512bh qv = (__m512bh)_mm512_loadu_si512(qt + 16 * (kMlaC / 2 + p));
 #pragma GCC unroll 16
     for (int j = 0; j < 16; ++j)
@@ -287,10 +293,17 @@ void mla_attend_t(const uint32_t* qt, const uint16_t* c, size_t c_tok, const uin
         pb = tpe;
       }
       __m512 acc[16];
-      if (cb == tc)
+      if (cb == tc) {
         mla_scores16<kMlaC, kMlaPe>(qt, cb, pb, acc);
-      else
-        mla_scores16<(dense ? CT : kMlaC), (dense ? PT : kMlaPe)>(qt, cb, pb, acc);
+      } else {
+        // the 16 tokens after these (in this range: the caller's range is one
+        // page, so nothing past its end is touched)
+        const bool more = t + 32 <= (size_t)t1;
+        const char* pf_c = more ? (const char*)(cb + 16 * c_tok) : nullptr;
+        const char* pf_pe = !more ? nullptr
+                            : (CT == PT ? pf_c + 256 * 64 : (const char*)(pb + 16 * pe_tok));
+        mla_scores16<(dense ? CT : kMlaC), (dense ? PT : kMlaPe)>(qt, cb, pb, acc, pf_c, pf_pe);
+      }
 #pragma GCC unroll 16
       for (int j = 0; j < 16; ++j) _mm512_store_ps(sc[16 * grp + j], _mm512_mul_ps(acc[j], vsl2));
     }
@@ -336,6 +349,17 @@ void mla_attend_t(const uint32_t* qt, const uint16_t* c, size_t c_tok, const uin
 }
 
 }  // namespace
+
+double sum_lines(const double* p, size_t words) {
+  __m512d a0 = _mm512_setzero_pd(), a1 = _mm512_setzero_pd();
+  size_t i = 0;
+  for (; i + 16 <= words; i += 16) {
+    a0 = _mm512_add_pd(a0, _mm512_loadu_pd(p + i));
+    a1 = _mm512_add_pd(a1, _mm512_loadu_pd(p + i + 8));
+  }
+  if (i < words) a0 = _mm512_add_pd(a0, _mm512_loadu_pd(p + i));
+  return _mm512_reduce_add_pd(_mm512_add_pd(a0, a1));
+}
 
 void mla_attend(const uint32_t* qt, const uint16_t* c, size_t c_tok, const uint16_t* pe,
                 size_t pe_tok, int t0, int t1, float sl2, float* m, float* l, float* o,

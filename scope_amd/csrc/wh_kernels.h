@@ -51,4 +51,8 @@ void mla_attend(const uint32_t* qt, const uint16_t* c, size_t c_tok, const uint1
                 size_t pe_tok, int t0, int t1, float scale_log2, float* m, float* l, float* o,
                 uint32_t* vst);
 
+// Sum of `words` doubles (a multiple of 8) streamed with 512-bit loads: the
+// reading side of the host bandwidth probe.
+double sum_lines(const double* p, size_t words);
+
 }  // namespace wh

@@ -32,7 +32,7 @@ LIB_PATH = os.path.join(_HERE, "lib", "libwshost.so")
 
 # Entry points declared in include/wshost.h.
 EXPORTS = ("wh_last_error", "wh_version", "wh_isa_supported", "wh_gqa_partial",
-           "wh_attn_partial",
+           "wh_attn_partial", "wh_host_read_gbs",
            "wh_mla_partial")
 
 MLA_HEADS = 16
@@ -67,11 +67,19 @@ def lib() -> ctypes.CDLL:
                                      vp, vp, i32]
         L.wh_attn_partial.restype = i32
         L.wh_attn_partial.argtypes = [vp, vp, vp, vp, vp] + [i32] * 8 + [f32, vp, vp, i32]
+        L.wh_host_read_gbs.restype = ctypes.c_double
+        L.wh_host_read_gbs.argtypes = [ctypes.c_size_t, i32, i32]
         L.wh_mla_partial.restype = i32
         L.wh_mla_partial.argtypes = [vp, vp, vp, i32, vp, i32, vp, vp] + [i32] * 5 + [f32, vp,
                                                                                      vp, i32]
         _lib = L
     return _lib
+
+
+def host_read_gbs(nbytes: int = 1 << 30, threads: int = 0, reps: int = 5) -> float:
+    """Streaming read bandwidth of host memory in GB/s with `threads` threads
+    (wh_host_read_gbs): the host side's roofline."""
+    return float(lib().wh_host_read_gbs(int(nbytes), int(threads), int(reps)))
 
 
 def isa_supported() -> bool:

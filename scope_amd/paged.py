@@ -23,6 +23,8 @@ only then.
 """
 from __future__ import annotations
 
+import time
+
 import numpy as np
 import torch
 
@@ -100,6 +102,27 @@ class _PagedTwoSided:
     def _write_gpu_row(self, b: int) -> None:
         g = self.gpu
         g.page_table[b].copy_(torch.from_numpy(g.host_table[b].copy()))
+
+    def reserve_layout(self, lens, host_tokens) -> None:
+        """Give every sequence b lens[b] tokens, host_tokens[b] of them (a page
+        multiple) in host pages and the rest in HBM pages, in every layer,
+        without writing any data: for callers that fill the page pools
+        themselves (bulk prefill, benchmarks).  The cache must be empty."""
+        ps = self.page_size
+        g = self.gpu
+        if len(lens) != self.batch or len(host_tokens) != self.batch:
+            raise ValueError(f"need {self.batch} lengths and host token counts")
+        if self.host.lens.any() or g.lens.any():
+            raise RuntimeError("reserve_layout needs an empty cache")
+        for b, (L, h) in enumerate(zip(lens, host_tokens)):
+            L, h = int(L), int(h)
+            if h % ps or not 0 <= h <= L:
+                raise ValueError(f"sequence {b}: host tokens {h} must be a page multiple "
+                                 f"in [0, {L}]")
+            self._host_reserve(b, h)
+            self.host.lens[b] = h
+            g.reserve(b, L - h)
+            self._set_gpu_lens(b, L - h)
 
     # -- boundary movement ---------------------------------------------------
 
@@ -271,16 +294,70 @@ class _PagedTwoSided:
 
     # -- decode-step plumbing -----------------------------------------------
 
-    @staticmethod
-    def _to_host(*ts):
+    def _pinned(self, name, shape, dtype):
+        """A pinned host buffer of the cache, allocated once per (name, shape).
+        One buffer per role is enough: every host partial waits for the
+        query copy of its own layer, which the stream orders after the
+        previous layer's partial -> GPU copy out of the same buffers."""
+        bufs = self.__dict__.setdefault("_pin_bufs", {})
+        key = (name, tuple(shape), dtype)
+        t = bufs.get(key)
+        if t is None:
+            t = torch.empty(shape, dtype=dtype, pin_memory=True)
+            bufs[key] = t
+        return t
+
+    def _to_host(self, *ts):
         out = []
-        for t in ts:
-            h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+        for i, t in enumerate(ts):
+            h = self._pinned(f"q{i}", t.shape, t.dtype)
             h.copy_(t, non_blocking=True)
             out.append(h)
-        ev = torch.cuda.Event()
+        ev = self.__dict__.get("_q_event")
+        if ev is None:
+            ev = self._q_event = torch.cuda.Event()
         ev.record()
         return out, ev
+
+    # -- online share control --------------------------------------------------
+
+    controller = None  # a scheduler.ShareController, or None
+
+    def attach(self, controller) -> None:
+        """Let `controller` (scheduler.ShareController) move the boundary after
+        every decode step, from the per-layer times this cache measures."""
+        self.controller = controller
+        self._timing = [(torch.cuda.Event(enable_timing=True),
+                         torch.cuda.Event(enable_timing=True)) for _ in range(self.num_layers)]
+        self._layer_log = []
+
+    def _layer_done(self, layer: int, host_s: float) -> None:
+        """Record a layer's partials for the controller; after the last layer
+        of a decode step, fold them into the scheduler and move the boundary
+        if it chooses to."""
+        g = self.gpu
+        self._layer_log.append((layer, float(g.lens[layer].sum()), float(self.host.lens.sum()),
+                                host_s))
+        if layer != self.num_layers - 1:
+            return
+        ctl = self.controller
+        bpt = ctl.bytes_per_token
+        for l, g_tok, h_tok, h_s in self._layer_log:
+            a, e = self._timing[l]
+            e.synchronize()
+            ctl.observe_layer(g_tok * bpt, a.elapsed_time(e) * 1e-3, h_tok * bpt, h_s)
+        self._layer_log = []
+        lens = [self.seq_len(b) for b in range(self.batch)]
+        host_now = [int(x) for x in self.host.lens]
+        targets = ctl.decide(lens, host_now)
+        if targets is None:
+            return
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        self.set_boundaries(targets)
+        pages = sum(abs(t - h) for t, h in zip(targets, host_now)) // self.page_size
+        ctl.record_move(ctl.share_of(lens, host_now), ctl.share_of(lens, targets), pages,
+                        time.perf_counter() - t0)
 
     def _merge(self, step, part, dev, w_uv=None, return_lse=False):
         b = None if part is None else tuple(x.to(dev, non_blocking=True) for x in part)
@@ -346,17 +423,27 @@ class PagedMlaCache(_PagedTwoSided):
         with_host = bool(self.host.lens.any())
         if with_host:
             (qn_h, qp_h), ev = self._to_host(q_nope, q_pe)
+        timing = self._timing[layer] if self.controller is not None else None
+        if timing:
+            timing[0].record()
         step = g.step_split(layer, q_nope, q_pe, c_new, pe_new, scale, n_workgroups)
+        if timing:
+            timing[1].record()
         part = None
+        host_s = 0.0
         if with_host:
             ev.synchronize()
             rows = q_nope.shape[0]
+            t0 = time.perf_counter()
             part = host.mla_partial(
                 qn_h, qp_h, self.host.data[0][layer], self.host.table_t, self.host.lens_t,
-                scale, host_threads,
-                torch.empty((rows, ops.MLA_C), dtype=torch.float32, pin_memory=True),
-                torch.empty((rows,), dtype=torch.float32, pin_memory=True))
-        return self._merge(step, part, dev, w_uv, return_lse)
+                scale, host_threads, self._pinned("out", (rows, ops.MLA_C), torch.float32),
+                self._pinned("lse", (rows,), torch.float32))
+            host_s = time.perf_counter() - t0
+        res = self._merge(step, part, dev, w_uv, return_lse)
+        if timing:
+            self._layer_done(layer, host_s)
+        return res
 
 
 class PagedKVCache(_PagedTwoSided):
@@ -412,20 +499,30 @@ class PagedKVCache(_PagedTwoSided):
         with_host = bool(self.host.lens.any())
         if with_host:
             (q_h,), ev = self._to_host(q)
+        timing = self._timing[layer] if self.controller is not None else None
+        if timing:
+            timing[0].record()
         step = g.step_split(layer, q, k_new, v_new, scale, n_workgroups)
+        if timing:
+            timing[1].record()
         part = None
+        host_s = 0.0
         if with_host:
             ev.synchronize()
             B, Hq, D = q.shape
+            t0 = time.perf_counter()
             part = host.gqa_partial(
                 q_h, self.host.data[0][layer], self.host.data[1][layer], self.host.table_t,
                 self.host.lens_t, scale, host_threads,
-                torch.empty((B, Hq, D), dtype=torch.float32, pin_memory=True),
-                torch.empty((B, Hq), dtype=torch.float32, pin_memory=True))
+                self._pinned("out", (B, Hq, D), torch.float32),
+                self._pinned("lse", (B, Hq), torch.float32))
+            host_s = time.perf_counter() - t0
+        out, lse = self._merge(step, part, dev, return_lse=True)
+        if timing:
+            self._layer_done(layer, host_s)
         if return_lse:
-            out, lse = self._merge(step, part, dev, return_lse=True)
             return out.view(q.shape), lse.view(q.shape[:2])
-        return self._merge(step, part, dev).view(q.shape)
+        return out.view(q.shape)
 
 
 def absorb_q(q_nope: torch.Tensor, w_uk: torch.Tensor) -> torch.Tensor:

@@ -134,3 +134,108 @@ def fit_side(points) -> Side:
     if slope <= 0:
         raise ValueError("time does not grow with bytes; cannot fit a rate")
     return Side(fixed_s=max(0.0, mt - slope * mb), rate_bps=1.0 / slope)
+
+
+# --------------------------------------------------------------------------
+# Online control of a two-sided paged cache
+
+
+@dataclass
+class ShareMove:
+    """One boundary move made by the controller."""
+    step: int
+    share_from: float
+    share_to: float
+    pages: int          # pages moved, summed over sequences (per layer)
+    seconds: float      # wall time of the move (all layers)
+
+
+class ShareController:
+    """Keeps a two-sided paged cache (scope_amd.paged) at the share the
+    scheduler chooses, from the times the decode loop measures.
+
+    Per layer the cache reports the GPU partial's event time and the host
+    partial's wall time with the bytes each side streamed (observe_layer),
+    which the scheduler folds into its rates with the reference's EMA form
+    (system/qwenoffload.py:1160-1165, system/mixoffload.py:1466-1474).  After
+    the last layer of a decode step, decide() asks the scheduler for the share
+    of the current lengths within the HBM budget and returns new host-token
+    targets per sequence when they move the boundary by at least
+    min_move_pages pages per sequence on average (smaller moves are not worth
+    their copies, and this hysteresis keeps the share from oscillating);
+    the cache then moves its pages (set_boundaries).
+
+    The reference adapts a split ratio toward equal GPU and CPU times and
+    clamps it to [0.1, 0.9]; here the target comes from the roofline model of
+    both sides plus the HBM capacity, so a cache larger than its HBM budget
+    converges to the capacity share instead of oscillating around a balance
+    point the budget does not allow.
+    """
+
+    def __init__(self, sched: ShareScheduler, bytes_per_token: int, layers: int,
+                 page_size: int, min_move_pages: float = 1.0, granularity: float = 0.0):
+        if bytes_per_token <= 0 or layers <= 0 or page_size <= 0:
+            raise ValueError("bytes_per_token, layers and page_size must be positive")
+        self.sched = sched
+        self.bytes_per_token = bytes_per_token
+        self.layers = layers
+        self.page_size = page_size
+        self.min_move_pages = min_move_pages
+        self.granularity = granularity
+        self.steps = 0
+        self.moves: list[ShareMove] = []
+        self.shares: list[float] = []   # share after each decide()
+        self.chosen: list[float] = []   # the scheduler's choice at each decide()
+
+    def observe_layer(self, gpu_bytes: float, gpu_s: float, host_bytes: float,
+                      host_s: float) -> None:
+        """One layer's measured partials (bytes streamed, seconds)."""
+        if gpu_bytes > 0 and gpu_s > 0:
+            self.sched.observe("gpu", gpu_bytes, gpu_s)
+        if host_bytes > 0 and host_s > 0:
+            self.sched.observe("host", host_bytes, host_s)
+
+    @staticmethod
+    def share_of(lens, host_tokens) -> float:
+        total = sum(int(x) for x in lens)
+        return 1.0 if total == 0 else 1.0 - sum(int(h) for h in host_tokens) / total
+
+    def targets_for(self, r: float, lens, round_up: bool = False) -> list[int]:
+        """Host tokens per sequence at share r: L - floor(r L), rounded down to
+        a page (the GPU takes the rest), as the cache's set_share does; with
+        round_up, rounded up instead (at most L's last full page), so the GPU
+        side stays within r L: the rounding used when HBM capacity sets r."""
+        ps = self.page_size
+        out = []
+        for L in lens:
+            L = int(L)
+            h = L - int(math.floor(r * L))
+            out.append(min(-(-h // ps) * ps, (L // ps) * ps) if round_up else (h // ps) * ps)
+        return out
+
+    def decide(self, lens, host_tokens):
+        """After a decode step: host-token targets per sequence if the chosen
+        share moves the boundary by at least min_move_pages pages per
+        sequence, or if the GPU side has outgrown the HBM budget (decode
+        appends land on the GPU side); else None."""
+        self.steps += 1
+        W = float(sum(int(x) for x in lens)) * self.bytes_per_token
+        r = self.sched.choose(W, self.layers, self.granularity)
+        self.chosen.append(r)
+        cap = self.sched.capacity_share(W, self.layers)
+        targets = self.targets_for(r, lens, round_up=cap < 1.0 and r >= cap - 1e-12)
+        budget = self.sched.hbm_budget_bytes
+        gpu_bytes = (sum(int(x) for x in lens) - sum(int(h) for h in host_tokens)) \
+            * self.bytes_per_token * self.layers
+        over = budget is not None and gpu_bytes > budget
+        moved = sum(abs(t - int(h)) for t, h in zip(targets, host_tokens)) // self.page_size
+        same = all(t == int(h) for t, h in zip(targets, host_tokens))
+        if same or (moved < self.min_move_pages * max(1, len(lens)) and not over):
+            self.shares.append(self.share_of(lens, host_tokens))
+            return None
+        self.shares.append(self.share_of(lens, targets))
+        return targets
+
+    def record_move(self, share_from: float, share_to: float, pages: int,
+                    seconds: float) -> None:
+        self.moves.append(ShareMove(self.steps, share_from, share_to, pages, seconds))
