@@ -181,8 +181,9 @@ class _Timer:
 def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_host,
                    label, wg=0):
     """Times `steps` decode steps (fused append + GQA partial, then the merge
-    with the host partial) and returns a dict of results.  lens: total KV
-    lengths; the GPU holds floor(share*L) of each."""
+    with the host partial; with_host False: the one-launch whole step) and
+    returns a dict of results.  lens: total KV lengths; the GPU holds
+    floor(share*L) of each."""
     import torch
 
     from scope_amd import ops
@@ -192,7 +193,7 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
     L = ops.lib()
     rng = np.random.default_rng(seed)
     gpu_tokens = np.array([int(math.floor(share * int(x))) for x in lens], np.int64)
-    extra = warmup + steps + 1
+    extra = warmup + 2 * steps + 1
     table, num_pages = _page_table(gpu_tokens, extra, rng)
     gen = torch.Generator(device=dev).manual_seed(seed)
     k_pages = _randn_bf16((num_pages, Hkv, PAGE, D), gen, 1.0, dev)
@@ -209,9 +210,6 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
     h_out = _randn_bf16((rows, D), gen, 0.3, dev)
     h_max = (torch.randn(rows, generator=gen, device=dev) + 4).to(torch.bfloat16)
     h_sum = (torch.rand(rows, generator=gen, device=dev) * 50 + 1).to(torch.bfloat16)
-    if not with_host:  # r = 1: nothing on the host, merge with the empty partial
-        h_max.fill_(float("-inf"))
-        h_sum.zero_()
     out_g = torch.empty((rows, D), dtype=torch.float32, device=dev)
     lse_g = torch.empty((rows,), dtype=torch.float32, device=dev)
     out = torch.empty((rows, D), dtype=torch.bfloat16, device=dev)
@@ -234,6 +232,13 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
                 ctypes.c_size_t(wsb), p(h_out), p(h_max), p(h_sum), ops.TRIPLE_NORM_BF16,
                 p(out), None, None, stream) for k in (0, 1)]
     f_step, f_merge = L.ws_gqa_append_decode_split, L.ws_merge_split
+    if not with_host:
+        # r = 1: nothing on the host; the whole step is one launch
+        # (ws_gqa_append_decode_full: bf16 output + lse, split rows combined
+        # in the kernel)
+        f_step = L.ws_gqa_append_decode_full
+        a_tail = (nwg, scale, p(out), None, p(lse_g), p(ws), ctypes.c_size_t(wsb), stream)
+        f_merge = lambda *a: 0
 
     for i in range(warmup):
         rc = f_step(*a_head, len_ptrs[i % 2], len_ptrs[(i + 1) % 2], *a_mid,
@@ -241,7 +246,11 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
         rc |= f_merge(*a_merge[(i + 1) % 2])
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
-    timer = _Timer(steps)
+    # Pass 1, the step time: `steps` steps queued back to back with nothing
+    # between them but the step's launches (events only around the whole pass).
+    # Pass 2, the partial kernel's time: the same steps with a timing-only
+    # event pair around every step launch (the events' own cost stays out
+    # of pass 1).
     t_ev0 = HipTimingEvent()
     t_ev1 = HipTimingEvent()
     torch.cuda.synchronize()
@@ -249,10 +258,8 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
     t_ev0.record()
     for i in range(steps):
         a_i = warmup + i
-        timer.a[i].record()
         rc = f_step(*a_head, len_ptrs[a_i % 2], len_ptrs[(a_i + 1) % 2], *a_mid,
                     max_len0 + a_i + 1, *a_tail)
-        timer.b[i].record()
         rc |= f_merge(*a_merge[(a_i + 1) % 2])
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
@@ -260,18 +267,38 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
     t_host = time.perf_counter() - t0
     torch.cuda.synchronize()
     t_wall = time.perf_counter() - t0
-    final_len = lens2[(warmup + steps) % 2].cpu().numpy()
-    if not np.array_equal(final_len, gpu_tokens + warmup + steps):
-        raise RuntimeError(f"{label}: lengths did not advance by one per step")
     step_us = 1e3 * t_ev0.elapsed_time(t_ev1) / steps
+    timer = _Timer(steps)
+    for i in range(steps):
+        a_i = warmup + steps + i
+        timer.a[i].record()
+        rc = f_step(*a_head, len_ptrs[a_i % 2], len_ptrs[(a_i + 1) % 2], *a_mid,
+                    max_len0 + a_i + 1, *a_tail)
+        timer.b[i].record()
+        rc |= f_merge(*a_merge[(a_i + 1) % 2])
+        if rc:
+            raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
+    torch.cuda.synchronize()
+    final_len = lens2[(warmup + 2 * steps) % 2].cpu().numpy()
+    if not np.array_equal(final_len, gpu_tokens + warmup + 2 * steps):
+        raise RuntimeError(f"{label}: lengths did not advance by one per step")
     part_us = timer.mean_us(steps)
-    # tokens attended during the timed region: g + warmup + 1 .. g + warmup + steps
+    # tokens attended in pass 1: g + warmup + 1 .. g + warmup + steps (pass 2
+    # attends `steps` more per sequence; its partial bytes are the pass-1
+    # bytes plus B * steps tokens, which the step figures below leave out)
     mean_tokens = float(gpu_tokens.sum()) + B * (warmup + (steps + 1) / 2.0)
     kv_tok = Hkv * 2 * D * 2
     pages_read = float(sum(-(-(int(g) + warmup + steps // 2) // PAGE) for g in gpu_tokens))
-    kernel_bytes = (mean_tokens * kv_tok + rows * D * 2 + rows * (D + 1) * 4
-                    + pages_read * 4 + B * kv_tok)
-    step_bytes = kernel_bytes + rows * (D * 2 + 4) + rows * D * 2
+    if with_host:  # partial: out fp32 + lse; the merge reads it and the host triple
+        kernel_bytes = (mean_tokens * kv_tok + rows * D * 2 + rows * (D + 1) * 4
+                        + pages_read * 4 + B * kv_tok)
+        step_bytes = kernel_bytes + rows * (D * 2 + 4) + rows * D * 2
+    else:  # one launch: bf16 output + lse
+        kernel_bytes = (mean_tokens * kv_tok + rows * D * 2 + rows * (D * 2 + 4)
+                        + pages_read * 4 + B * kv_tok)
+        step_bytes = kernel_bytes
+    # the partial kernel's bytes in pass 2 (B * steps tokens more per launch)
+    part_bytes = kernel_bytes + B * steps * kv_tok
     return {
         "label": label,
         "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
@@ -279,13 +306,14 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
         "gpu_tokens": int(gpu_tokens.sum()),
         "max_gpu_tokens": max_len0,
         "workgroups": nwg,
+        "launches_per_step": 2 if with_host else 1,
         "us_per_layer": round(step_us, 2),
         "step_gbs": round(step_bytes / step_us / 1e3, 1),
         "partial_us": round(part_us, 2),
-        "partial_gbs": round(kernel_bytes / part_us / 1e3, 1),
-        "partial_frac": round(kernel_bytes / part_us / 1e3 / HBM_PEAK_GBS, 4),
+        "partial_gbs": round(part_bytes / part_us / 1e3, 1),
+        "partial_frac": round(part_bytes / part_us / 1e3 / HBM_PEAK_GBS, 4),
         "step_bytes": int(step_bytes),
-        "partial_bytes": int(kernel_bytes),
+        "partial_bytes": int(part_bytes),
         "host_loop_us_per_step": round(1e6 * t_host / steps, 2),
         "wall_us_per_step": round(1e6 * t_wall / steps, 2),
         "_data": (k_pages, v_pages, table, gpu_tokens, q),
@@ -306,7 +334,7 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label, wg=0):
     L = ops.lib()
     rng = np.random.default_rng(seed)
     gpu_tokens = np.array([int(math.floor(share * int(x))) for x in lens], np.int64)
-    extra = warmup + steps + 1
+    extra = warmup + 2 * steps + 1
     table, num_pages = _page_table(gpu_tokens, extra, rng)
     gen = torch.Generator(device=dev).manual_seed(seed)
     latent = _randn_bf16((num_pages, PAGE, 576), gen, 0.5, dev)
@@ -346,13 +374,25 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label, wg=0):
                     max_len0 + i + 1, *a_tail) | f_merge(*a_merge[(i + 1) % 2])
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
-    timer = _Timer(steps)
+    # pass 1: step time with no event between launches; pass 2: per-launch
+    # timing events around the step kernel (as gqa_step_bench)
     e0 = HipTimingEvent()
     e1 = HipTimingEvent()
     torch.cuda.synchronize()
     e0.record()
     for i in range(steps):
         a_i = warmup + i
+        rc = f_step(*a_head, len_ptrs[a_i % 2], len_ptrs[(a_i + 1) % 2], *a_mid,
+                    max_len0 + a_i + 1, *a_tail)
+        rc |= f_merge(*a_merge[(a_i + 1) % 2])
+        if rc:
+            raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
+    e1.record()
+    torch.cuda.synchronize()
+    step_us = 1e3 * e0.elapsed_time(e1) / steps
+    timer = _Timer(steps)
+    for i in range(steps):
+        a_i = warmup + steps + i
         timer.a[i].record()
         rc = f_step(*a_head, len_ptrs[a_i % 2], len_ptrs[(a_i + 1) % 2], *a_mid,
                     max_len0 + a_i + 1, *a_tail)
@@ -360,16 +400,16 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label, wg=0):
         rc |= f_merge(*a_merge[(a_i + 1) % 2])
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
-    e1.record()
     torch.cuda.synchronize()
-    step_us = 1e3 * e0.elapsed_time(e1) / steps
     part_us = timer.mean_us(steps)
     mean_tokens = float(gpu_tokens.sum()) + B * (warmup + (steps + 1) / 2.0)
     pages_read = float(sum(-(-(int(g) + warmup + steps // 2) // PAGE) for g in gpu_tokens))
     kernel_bytes = (mean_tokens * 1152 + rows * 576 * 2 + rows * 513 * 4 + pages_read * 4
                     + B * 1152)
     step_bytes = kernel_bytes + rows * 514 * 4 + rows * 512 * 2
-    flops = mean_tokens * H * (2 * 576 + 2 * 512)
+    # pass 2 attends `steps` more tokens per sequence than pass 1
+    kernel_bytes += B * steps * 1152
+    flops = (mean_tokens + B * steps) * H * (2 * 576 + 2 * 512)
     return {
         "label": label, "batch": B, "heads": H, "share": share,
         "gpu_tokens": int(gpu_tokens.sum()), "workgroups": nwg,
@@ -948,7 +988,7 @@ WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "host", "model", "
 EXTRA_WORKLOADS = ("mla32k",)
 
 # The kernel the headline roofline is measured on (its rocprofv3 name).
-HEAD_KERNEL = "ws::gqa_decode_kernel<4, true>"
+HEAD_KERNEL = "ws::gqa_decode_kernel<4, 128, true>"
 
 
 def committed_traffic(workload_key, kernel=HEAD_KERNEL):

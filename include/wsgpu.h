@@ -112,11 +112,13 @@ int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
  * Splits take equal shares of all 32-token blocks of all rows, so ragged
  * batches stay balanced; a row shared by several splits is combined from
  * their partials.  Workspace layout: [partial lse fp32, padded to 256
- * bytes][partial out bf16], one partial slot per (split, row) pair.  The
+ * bytes][partial out bf16], one partial slot per (split, row) pair (after a
+ * 256-byte-padded array of one 64-bit arrival counter per row).  The
  * workspace must be 256-byte aligned; it needs no initial contents (every
- * call writes the slots it reads back).  Calls that share a workspace must
- * be ordered on one stream.  At most 2048 sequences and 4096 splits per
- * call.
+ * call writes the slots it reads back, and the row arrival counters at its
+ * start carry a per-launch tag, so stale bytes of any earlier call are never
+ * taken for a count).  Calls that share a workspace must be ordered on one
+ * stream.  At most 2048 sequences and 4096 splits per call.
  */
 int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
                    int n_splits, int* n_splits_out,
@@ -126,11 +128,10 @@ int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
  * Split-KV GQA decode attention over the pooled tokens of every sequence.
  * q: [B][Hq][D] bf16, Hq = Hkv * G, G in {1,2,4,8,16}, D = 128.
  * n_splits: waves of the plan (0 = choose, see ws_decode_plan); max_len:
- * upper bound of gpu_len[] (must be >= every gpu_len[b]).  Rows held by one
- * wave are written final by the streaming launch; rows spread over several
- * waves are combined from their workspace partials by a second, small launch
- * on the same stream (the split merge of ws_merge_split without a host
- * partial).
+ * upper bound of gpu_len[] (must be >= every gpu_len[b]).  One launch: rows
+ * held by one wave are written final as it streams; a row spread over
+ * several waves is combined from their workspace partials by the last of
+ * those waves to finish (an arrival counter per row in the workspace).
  * Outputs out: [B][Hq][D] fp32 normalised, lse: [B][Hq] fp32.
  * Replaces _local_bmm_softmax / _resident_layer
  * (roofline/bench_resident_kv.py:150-157, 261-271) and the GPU side of
@@ -169,6 +170,26 @@ int ws_gqa_append_decode_partial(const uint16_t* q, const uint16_t* k_new,
                                  float* out, float* lse,
                                  void* workspace, size_t workspace_bytes,
                                  void* stream);
+
+/*
+ * The whole decode step of a GPU partition that holds every token (share
+ * r = 1, no host partial) in one launch: ws_gqa_append_decode_partial that
+ * also writes the normalised output in bf16.  out_bf16 [B][Hq][D] and/or
+ * out [B][Hq][D] fp32 (either may be NULL, not both), lse [B][Hq] fp32.
+ * Replaces _resident_layer followed by the final o / sum and bf16 cast when
+ * the host share is empty (roofline/bench_resident_kv.py:261-271, 350;
+ * system/mixoffload.py:1477-1480).
+ */
+int ws_gqa_append_decode_full(const uint16_t* q, const uint16_t* k_new,
+                              const uint16_t* v_new, uint16_t* k_pages,
+                              uint16_t* v_pages, const int32_t* page_table,
+                              const int32_t* len_in, int32_t* len_out,
+                              int B, int Hq, int Hkv, int D,
+                              int page_size, int max_pages, int num_pages,
+                              int max_len, int n_splits, float scale,
+                              uint16_t* out_bf16, float* out, float* lse,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream);
 
 /*
  * Deferred-combine form of ws_gqa_append_decode_partial, for a step whose

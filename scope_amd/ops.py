@@ -33,6 +33,7 @@ EXPORTS = (
     "ws_mla_decode_partial",
     "ws_mla_append_decode_partial",
     "ws_gqa_append_decode_split",
+    "ws_gqa_append_decode_full",
     "ws_mla_append_decode_split",
     "ws_merge_split",
     "ws_mla_merge_split_uv",
@@ -95,6 +96,9 @@ def lib() -> ctypes.CDLL:
         L.ws_gqa_append_decode_partial.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp,
                                                    i32, i32, i32, i32, i32, i32, i32,
                                                    i32, i32, f32, vp, vp, vp, sz, vp]
+        L.ws_gqa_append_decode_full.restype = i32
+        L.ws_gqa_append_decode_full.argtypes = [vp] * 8 + [i32] * 9 + [f32, vp, vp, vp, vp, sz,
+                                                                        vp]
         L.ws_mla_decode_partial.restype = i32
         L.ws_mla_decode_partial.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32,
                                             i32, i32, i32, i32, f32, vp, vp,
@@ -419,6 +423,56 @@ def gqa_append_decode_partial(q, k_new, v_new, k_pages, v_pages, page_table, len
         int(max_len), nwg, float(scale), _ptr(out), _ptr(lse), _ptr(ws), wsb,
         _stream(dev)), "ws_gqa_append_decode_partial")
     return out, lse
+
+
+def gqa_append_decode_full(q, k_new, v_new, k_pages, v_pages, page_table, len_in, len_out,
+                           scale, max_len, n_workgroups=0, out_bf16=None, out=None, lse=None,
+                           want_fp32=False):
+    """The whole decode step of a partition that holds every token (no host
+    share), in one launch: gqa_append_decode_partial that also writes the
+    normalised output in bf16.  Returns (out_bf16 [B, Hq, D], lse [B, Hq])
+    or, with want_fp32 (or an `out` given), (out_bf16, out fp32, lse)."""
+    dev = k_pages.device
+    for t, n, dt, nd in ((q, "q", torch.bfloat16, 3), (k_new, "k_new", torch.bfloat16, 4),
+                         (v_new, "v_new", torch.bfloat16, 4),
+                         (k_pages, "k_pages", torch.bfloat16, 4),
+                         (v_pages, "v_pages", torch.bfloat16, 4),
+                         (page_table, "page_table", torch.int32, 2),
+                         (len_in, "len_in", torch.int32, 1)):
+        _require(t, n, dt, dev, nd)
+    B, Hq, D = q.shape
+    P, Hkv, PS, D2 = k_pages.shape
+    if v_pages.shape != k_pages.shape or D2 != D:
+        raise ValueError("k/v page pools must match q's head_dim")
+    if k_new.shape != (B, Hkv, 1, D) or v_new.shape != k_new.shape:
+        raise ValueError(f"k_new/v_new must be [B, Hkv, 1, D] = {(B, Hkv, 1, D)}")
+    if page_table.shape[0] != B or len_in.shape[0] != B:
+        raise ValueError("page_table/len_in batch mismatch")
+    if len_out is not None:
+        _require(len_out, "len_out", torch.int32, dev, 1)
+        if len_out.shape[0] != B or len_out.data_ptr() == len_in.data_ptr():
+            raise ValueError("len_out must be a separate [B] int32 tensor")
+    if out_bf16 is None:
+        out_bf16 = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=dev)
+    _require(out_bf16, "out_bf16", torch.bfloat16, dev, 3)
+    if out is None and want_fp32:
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device=dev)
+    if out is not None:
+        _require(out, "out", torch.float32, dev, 3)
+    if lse is None:
+        lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
+    _require(lse, "lse", torch.float32, dev, 2)
+    if out_bf16.shape != q.shape or (out is not None and out.shape != q.shape) or \
+            lse.shape != (B, Hq):
+        raise ValueError("out_bf16/out must be [B, Hq, D] and lse [B, Hq]")
+    nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
+    ws = _workspace(dev, wsb)
+    _check(lib().ws_gqa_append_decode_full(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
+        _ptr(len_in), _ptr(len_out), B, Hq, Hkv, D, PS, page_table.shape[1], P,
+        int(max_len), nwg, float(scale), _ptr(out_bf16), _ptr(out), _ptr(lse), _ptr(ws), wsb,
+        _stream(dev)), "ws_gqa_append_decode_full")
+    return (out_bf16, out, lse) if out is not None else (out_bf16, lse)
 
 
 def gqa_append_decode_partial_noalloc(q, k_new, v_new, k_pages, v_pages, page_table, len_in,

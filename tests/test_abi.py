@@ -36,11 +36,12 @@ def test_version_and_plan():
     L = ops.lib()
     assert L.ws_version().decode().startswith("wsgpu")
     pad = lambda n: -(-n // 256) * 256
-    # explicit split counts are kept; workspace = lse slots + bf16 piece slots
+    # explicit split counts are kept; workspace = row arrival counters + lse
+    # slots + bf16 piece slots
     n, wsb = ops.decode_plan(0, 16, 8, 32768, 100)
-    assert n == 100 and wsb == pad((100 + 16) * 8 * 4) + (100 + 16) * 8 * 128 * 2
+    assert n == 100 and wsb == pad(16 * 8) + pad((100 + 16) * 8 * 4) + (100 + 16) * 8 * 128 * 2
     n, wsb = ops.decode_plan(1, 8, 16, 16384, 64)
-    assert n == 64 and wsb == pad((64 + 8) * 16 * 4) + (64 + 8) * 16 * 512 * 2
+    assert n == 64 and wsb == pad(8 * 8) + pad((64 + 8) * 16 * 4) + (64 + 8) * 16 * 512 * 2
     # the library's choice never exceeds the blocks available (8 per GQA
     # split, i.e. per wave) nor the merge's 4096 splits
     for rows, G, L in ((128, 4, 15773), (16, 8, 131072), (4, 8, 4096), (1, 1, 1), (2, 16, 1 << 20)):

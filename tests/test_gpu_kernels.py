@@ -377,6 +377,79 @@ def test_gqa_append_decode_fused_steps(Hkv, G, wg):
             assert np.array_equal(gv[b], bits(vs[b][h])), (b, h)
 
 
+@pytest.mark.parametrize("Hkv,G,wg", [(8, 4, 0), (8, 8, 7), (2, 16, 64), (1, 1, 300),
+                                      (4, 2, 1)])
+def test_gqa_append_decode_full_step(Hkv, G, wg):
+    """The one-launch whole step (bf16 normalised output): against fp64, its
+    fp32 output bit-identical to the one-launch partial's, its bf16 output
+    the fp32 one rounded to nearest even, appends bit-exact."""
+    _say(f"gqa full step Hkv={Hkv} G={G} wg={wg}")
+    D, PS = 128, 64
+    lens = [0, 1, 31, 64, 500, 2049]
+    B = len(lens)
+    total = [L + 1 for L in lens]
+    k_pages, v_pages, pt, gl, ks, vs = gqa_pool(total, Hkv, D, PS, seed=23)
+    for b, L in enumerate(lens):
+        k_pages[pt[b, L // PS].long(), :, L % PS] = 0
+        v_pages[pt[b, L // PS].long(), :, L % PS] = 0
+    q = bf16_randn((B, Hkv * G, D), 24).to(DEV)
+    k_new = torch.stack([k[:, L:L + 1] for k, L in zip(ks, lens)]).to(DEV).contiguous()
+    v_new = torch.stack([v[:, L:L + 1] for v, L in zip(vs, lens)]).to(DEV).contiguous()
+    len_in = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    len_out = torch.zeros_like(len_in)
+    scale = D ** -0.5
+    ob, of, lse = ops.gqa_append_decode_full(q, k_new, v_new, k_pages, v_pages, pt, len_in,
+                                             len_out, scale, max(total), wg, want_fp32=True)
+    ob2, lse2 = ops.gqa_append_decode_full(q, k_new, v_new, k_pages, v_pages, pt, len_in,
+                                           None, scale, max(total), wg)
+    # the partial step appends the same bits again into the same slots
+    o1, l1 = ops.gqa_append_decode_partial(q, k_new, v_new, k_pages, v_pages, pt, len_in,
+                                           None, scale, max(total), wg)
+    torch.cuda.synchronize()
+    assert len_out.cpu().tolist() == total
+    assert torch.equal(of.cpu(), o1.cpu()) and torch.equal(lse.cpu(), l1.cpu())
+    assert torch.equal(ob.cpu(), ob2.cpu()) and torch.equal(lse.cpu(), lse2.cpu())
+    assert np.array_equal(bits(ob), bits(of.to(torch.bfloat16)))
+    got, gl_ = ob.float().cpu().numpy(), lse.cpu().numpy()
+    qb = bits(q).reshape(B, Hkv, G, D)
+    for b in range(B):
+        want, wl = O.gqa_attention_fp64(qb[b], bits(ks[b]), bits(vs[b]), scale)
+        assert_close(got[b].reshape(Hkv, G, D), want, OUT_ATOL, OUT_RTOL, f"b={b}")
+        assert_close(gl_[b].reshape(Hkv, G), wl, LSE_ATOL, LSE_RTOL, f"lse b={b}")
+    kp, vp = bits(k_pages), bits(v_pages)
+    tab = pt.cpu().numpy()
+    for h in range(Hkv):
+        gk = O.gather_paged(kp, tab, total, head=h)
+        gv = O.gather_paged(vp, tab, total, head=h)
+        for b in range(B):
+            assert np.array_equal(gk[b], bits(ks[b][h])), (b, h)
+            assert np.array_equal(gv[b], bits(vs[b][h])), (b, h)
+
+
+def test_gqa_full_step_bad_lengths_give_nan_rows():
+    """A length past the page table's capacity makes its rows NaN (out_bf16,
+    out and lse) and len_out -1; the other rows are untouched by it."""
+    _say("gqa full step bad length")
+    Hkv, G, D, PS = 2, 4, 128, 64
+    lens = [100, 300]
+    k_pages, v_pages, pt, gl, ks, vs = gqa_pool([L + 1 for L in lens], Hkv, D, PS, seed=25)
+    q = bf16_randn((2, Hkv * G, D), 26).to(DEV)
+    k_new = torch.stack([k[:, L:L + 1] for k, L in zip(ks, lens)]).to(DEV).contiguous()
+    v_new = torch.stack([v[:, L:L + 1] for v, L in zip(vs, lens)]).to(DEV).contiguous()
+    cap = pt.shape[1] * PS
+    len_in = torch.tensor([lens[0], cap + 5], dtype=torch.int32, device=DEV)
+    len_out = torch.zeros_like(len_in)
+    ob, of, lse = ops.gqa_append_decode_full(q, k_new, v_new, k_pages, v_pages, pt, len_in,
+                                             len_out, D ** -0.5, cap, 3, want_fp32=True)
+    torch.cuda.synchronize()
+    assert len_out.cpu().tolist() == [lens[0] + 1, -1]
+    assert torch.isnan(ob[1].float()).all() and torch.isnan(of[1]).all()
+    assert torch.isnan(lse[1]).all()
+    qb = bits(q).reshape(2, Hkv, G, D)
+    want, wl = O.gqa_attention_fp64(qb[0], bits(ks[0]), bits(vs[0]), D ** -0.5)
+    assert_close(ob[0].float().cpu().numpy().reshape(Hkv, G, D), want, OUT_ATOL, OUT_RTOL, "ok")
+
+
 def test_gqa_one_row_over_many_splits():
     # one row spread over 512 splits (2 blocks each): the combine takes 512
     # pieces
