@@ -181,8 +181,8 @@ class _Timer:
 def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_host,
                    label, wg=0):
     """Times `steps` decode steps (fused append + GQA partial, then the merge
-    with the host partial; with_host False: the one-launch whole step) and
-    returns a dict of results.  lens: total KV lengths; the GPU holds
+    with the host partial, or with no host partial when with_host is False)
+    and returns a dict of results.  lens: total KV lengths; the GPU holds
     floor(share*L) of each."""
     import torch
 
@@ -231,14 +231,11 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
     a_merge = [(len_ptrs[k], B, Hkv, G, D, cap, nwg, p(out_g), p(lse_g), p(ws),
                 ctypes.c_size_t(wsb), p(h_out), p(h_max), p(h_sum), ops.TRIPLE_NORM_BF16,
                 p(out), None, None, stream) for k in (0, 1)]
+    if not with_host:  # r = 1: nothing on the host; the merge only combines the pieces
+        a_merge = [(len_ptrs[k], B, Hkv, G, D, cap, nwg, p(out_g), p(lse_g), p(ws),
+                    ctypes.c_size_t(wsb), None, None, None, 0, p(out), None, None, stream)
+                   for k in (0, 1)]
     f_step, f_merge = L.ws_gqa_append_decode_split, L.ws_merge_split
-    if not with_host:
-        # r = 1: nothing on the host; the whole step is one launch
-        # (ws_gqa_append_decode_full: bf16 output + lse, split rows combined
-        # in the kernel)
-        f_step = L.ws_gqa_append_decode_full
-        a_tail = (nwg, scale, p(out), None, p(lse_g), p(ws), ctypes.c_size_t(wsb), stream)
-        f_merge = lambda *a: 0
 
     for i in range(warmup):
         rc = f_step(*a_head, len_ptrs[i % 2], len_ptrs[(i + 1) % 2], *a_mid,
@@ -247,7 +244,7 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
         if rc:
             raise RuntimeError(f"{label}: {L.ws_last_error().decode()}")
     # Pass 1, the step time: `steps` steps queued back to back with nothing
-    # between them but the step's launches (events only around the whole pass).
+    # between them but the two launches (events only around the whole pass).
     # Pass 2, the partial kernel's time: the same steps with a timing-only
     # event pair around every step launch (the events' own cost stays out
     # of pass 1).
@@ -289,14 +286,10 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
     mean_tokens = float(gpu_tokens.sum()) + B * (warmup + (steps + 1) / 2.0)
     kv_tok = Hkv * 2 * D * 2
     pages_read = float(sum(-(-(int(g) + warmup + steps // 2) // PAGE) for g in gpu_tokens))
-    if with_host:  # partial: out fp32 + lse; the merge reads it and the host triple
-        kernel_bytes = (mean_tokens * kv_tok + rows * D * 2 + rows * (D + 1) * 4
-                        + pages_read * 4 + B * kv_tok)
-        step_bytes = kernel_bytes + rows * (D * 2 + 4) + rows * D * 2
-    else:  # one launch: bf16 output + lse
-        kernel_bytes = (mean_tokens * kv_tok + rows * D * 2 + rows * (D * 2 + 4)
-                        + pages_read * 4 + B * kv_tok)
-        step_bytes = kernel_bytes
+    kernel_bytes = (mean_tokens * kv_tok + rows * D * 2 + rows * (D + 1) * 4
+                    + pages_read * 4 + B * kv_tok)
+    # the merge: the host triple read (r < 1), the bf16 output written
+    step_bytes = kernel_bytes + (rows * (D * 2 + 4) if with_host else 0) + rows * D * 2
     # the partial kernel's bytes in pass 2 (B * steps tokens more per launch)
     part_bytes = kernel_bytes + B * steps * kv_tok
     return {
@@ -306,7 +299,6 @@ def gqa_step_bench(*, B, Hkv, G, lens, share, steps, warmup, seed, dev, with_hos
         "gpu_tokens": int(gpu_tokens.sum()),
         "max_gpu_tokens": max_len0,
         "workgroups": nwg,
-        "launches_per_step": 2 if with_host else 1,
         "us_per_layer": round(step_us, 2),
         "step_gbs": round(step_bytes / step_us / 1e3, 1),
         "partial_us": round(part_us, 2),
@@ -651,9 +643,9 @@ def lognormal_lens(B, seed, median=4096, sigma=1.0, lo=256, hi=65536):
 def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads, label):
     """One decode step of a `layers`-layer absorbed-MLA model over a
     token-range-partitioned latent cache, per layer in dependency order:
-    q -> host (pinned), GPU split step (append + partial over the HBM pages)
-    while the host partial (wh_mla_partial) attends the host pages, host
-    partial -> GPU, merge.  The q copy of layer l+1 is ordered after layer l's
+    q -> host (pinned, ws_copy), GPU split step (append + partial over the
+    HBM pages) while the host partial (wh_mla_partial) attends the host
+    pages, merge (reading the host partial from pinned memory in place).  The q copy of layer l+1 is ordered after layer l's
     merge on the stream, as the real model's next query would be.  Returns
     the per-layer critical path and its parts."""
     import torch
@@ -689,8 +681,6 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
     qn_h, qp_h = q_h[:rows * 512].view(rows, 512), q_h[rows * 512:].view(rows, 64)
     part_h = torch.empty((rows * 513,), dtype=torch.float32, pin_memory=True)
     oc_h, lc_h = part_h[:rows * 512].view(rows, 512), part_h[rows * 512:]
-    part_d = torch.empty((rows * 513,), dtype=torch.float32, device=dev)
-    oc_d, lc_d = part_d[:rows * 512].view(rows, 512), part_d[rows * 512:]
     h_lens = torch.from_numpy(h_tok.astype(np.int32))
     h_tab = torch.from_numpy(h_table)
     with_host = bool(h_tok.sum() > 0)
@@ -711,8 +701,8 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
     def one_step(i, timed):
         cpu_s = 0.0
         for l in range(layers):
-            if with_host:
-                q_h.copy_(qbuf[l], non_blocking=True)
+            if with_host:  # the query to the host by the library's copy kernel
+                ops.copy_(q_h, qbuf[l])
                 ev_q.record()
             li, lo = p(lens_d[l, i % 2]), p(lens_d[l, (i + 1) % 2])
             if timed:
@@ -729,9 +719,9 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
                 t0 = time.perf_counter()
                 h_calls[l]()
                 cpu_s += time.perf_counter() - t0
-                part_d.copy_(part_h, non_blocking=True)
+                # the merge reads the host partial in place (pinned memory)
                 rc |= f_merge(lo, B, 1, H, 512, cap, nwg, p(out_g), p(lse_g), p(ws),
-                              ctypes.c_size_t(wsb), p(oc_d), p(lc_d), None,
+                              ctypes.c_size_t(wsb), p(oc_h), p(lc_h), None,
                               ops.PARTIAL_LSE_F32, p(out), None, None, stream)
             else:
                 rc |= f_merge(lo, B, 1, H, 512, cap, nwg, p(out_g), p(lse_g), p(ws),

@@ -70,6 +70,18 @@ const char* ws_last_error(void);
 const char* ws_version(void);
 
 /*
+ * Copy `bytes` (a multiple of 4) from src to dst with a copy kernel on
+ * `stream`; either side may be device memory or pinned host memory
+ * (hipHostMalloc, mapped into the device's address space), so it moves a
+ * decode step's query to the host partial without a DMA copy's set-up
+ * latency.  16-byte aligned pointers, no overlap.  Replaces the query's
+ * .cpu() of the two-sided layer (system/deepseek.py:345-346,
+ * system/mixoffload.py:1328).  (The host partial needs no copy back: the
+ * merges read their host operand from pinned host memory in place.)
+ */
+int ws_copy(void* dst, const void* src, size_t bytes, void* stream);
+
+/*
  * Append n_new tokens per sequence to the GQA pools at positions
  * gpu_len[b] .. gpu_len[b] + n_new - 1, then (if update_len) gpu_len[b] += n_new.
  * k_new, v_new: [B][Hkv][n_new][D] bf16 (the reference's k4d/v4d layout).
@@ -106,19 +118,17 @@ int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
  * into: one per wave for GQA (two per workgroup, each streaming on its
  * own), one per workgroup for MLA.  0 = the library's choice for the current
  * device: two GQA waves (one workgroup) or one MLA workgroup per CU, fewer
- * when the batch is small.  Writes the resolved split count and the
+ * when the batch is small (a GQA split keeps at least two 32-token blocks).  Writes the resolved split count and the
  * workspace bytes the call needs; the same count goes to ws_merge_split.
  *
  * Splits take equal shares of all 32-token blocks of all rows, so ragged
  * batches stay balanced; a row shared by several splits is combined from
  * their partials.  Workspace layout: [partial lse fp32, padded to 256
- * bytes][partial out bf16], one partial slot per (split, row) pair (after a
- * 256-byte-padded array of one 64-bit arrival counter per row).  The
+ * bytes][partial out bf16], one partial slot per (split, row) pair.  The
  * workspace must be 256-byte aligned; it needs no initial contents (every
- * call writes the slots it reads back, and the row arrival counters at its
- * start carry a per-launch tag, so stale bytes of any earlier call are never
- * taken for a count).  Calls that share a workspace must be ordered on one
- * stream.  At most 2048 sequences and 4096 splits per call.
+ * call writes the slots it reads back).  Calls that share a workspace must
+ * be ordered on one stream.  At most 2048 sequences and 4096 splits per
+ * call.
  */
 int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
                    int n_splits, int* n_splits_out,
@@ -128,10 +138,11 @@ int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
  * Split-KV GQA decode attention over the pooled tokens of every sequence.
  * q: [B][Hq][D] bf16, Hq = Hkv * G, G in {1,2,4,8,16}, D = 128.
  * n_splits: waves of the plan (0 = choose, see ws_decode_plan); max_len:
- * upper bound of gpu_len[] (must be >= every gpu_len[b]).  One launch: rows
- * held by one wave are written final as it streams; a row spread over
- * several waves is combined from their workspace partials by the last of
- * those waves to finish (an arrival counter per row in the workspace).
+ * upper bound of gpu_len[] (must be >= every gpu_len[b]).  Rows held by one
+ * wave are written final by the streaming launch; rows spread over several
+ * waves are combined from their workspace partials by a second, small launch
+ * on the same stream (the split merge of ws_merge_split without a host
+ * partial).
  * Outputs out: [B][Hq][D] fp32 normalised, lse: [B][Hq] fp32.
  * Replaces _local_bmm_softmax / _resident_layer
  * (roofline/bench_resident_kv.py:150-157, 261-271) and the GPU side of
@@ -173,9 +184,10 @@ int ws_gqa_append_decode_partial(const uint16_t* q, const uint16_t* k_new,
 
 /*
  * The whole decode step of a GPU partition that holds every token (share
- * r = 1, no host partial) in one launch: ws_gqa_append_decode_partial that
- * also writes the normalised output in bf16.  out_bf16 [B][Hq][D] and/or
- * out [B][Hq][D] fp32 (either may be NULL, not both), lse [B][Hq] fp32.
+ * r = 1, no host partial): ws_gqa_append_decode_partial that also writes the
+ * normalised output in bf16 (its combine launch writes both).  out_bf16
+ * [B][Hq][D] bf16, out [B][Hq][D] fp32 and lse [B][Hq] fp32 are all
+ * required.
  * Replaces _resident_layer followed by the final o / sum and bf16 cast when
  * the host share is empty (roofline/bench_resident_kv.py:261-271, 350;
  * system/mixoffload.py:1477-1480).
@@ -365,7 +377,10 @@ int ws_split_reduce(const float* part_out, const float* part_lse,
 /*
  * Merge the GPU partial (out_g, lse_g) with a second partial in format fmt_b
  * (WS_PARTIAL_LSE_F32: b_out fp32, b_aux0 = lse fp32; WS_TRIPLE_*: b_aux0 =
- * max, b_aux1 = sum, dtype per format), over rows x Dv.
+ * max, b_aux1 = sum, dtype per format), over rows x Dv.  The b_* operands
+ * may be in pinned host memory (hipHostMalloc): the kernel reads them over
+ * the host link in place, so a host partial needs no copy to HBM first
+ * (the same holds for ws_merge_split and ws_mla_merge_split_uv).
  * Writes any non-null of out_bf16 [rows][Dv], out_f32 [rows][Dv], lse_out
  * [rows].  Empty + empty gives out 0, lse -inf.
  * Replaces _pairwise_merge + the final normalise

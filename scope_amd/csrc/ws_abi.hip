@@ -2,18 +2,11 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include <atomic>
-
-#include "ws_reduce.h"
+#include "ws_common.h"
 
 namespace ws {
 
 static thread_local char g_last_error[512] = "";
-static std::atomic<unsigned long long> g_epoch{1};
-
-unsigned long long next_epoch() {
-  return g_epoch.fetch_add(1, std::memory_order_relaxed) & ((1ull << 36) - 1);
-}
 
 int set_error(int code, const char* fmt, ...) {
   va_list ap;

@@ -63,13 +63,10 @@ struct GqaParams {
   int32_t* len_out;
   const uint16_t* k_new;  // [B][Hkv][1][DK] or nullptr (v_new [B][Hkv][1][D])
   const uint16_t* v_new;
-  float* out;          // final rows, fp32 (or nullptr when out_bf16 is given)
-  uint16_t* out_bf16;  // final rows, bf16 (or nullptr)
+  float* out;
   float* lse;
   SplitWorkspace ws;
   int B, Hkv, page_size, max_pages, num_pages, cap, n_splits;
-  int combine;  // the last split holding a piece of a shared row combines it here
-  unsigned long long epoch;  // this launch's arrival epoch (combine)
   float scale_log2;
 };
 
@@ -120,10 +117,7 @@ gqa_decode_kernel(
       if (s_pref[b + 1] != s_pref[b]) continue;
       const bool ok = len_ok(p.len_in[b], add, p.cap);
       const size_t q0 = (size_t)b * p.Hkv * G;
-      for (int idx = tid; idx < p.Hkv * G * D; idx += NT) {
-        if (p.out) p.out[q0 * D + idx] = ok ? 0.f : qnan();
-        if (p.out_bf16) p.out_bf16[q0 * D + idx] = ok ? (uint16_t)0 : (uint16_t)0x7fc0;
-      }
+      for (int idx = tid; idx < p.Hkv * G * D; idx += NT) p.out[q0 * D + idx] = ok ? 0.f : qnan();
       for (int idx = tid; idx < p.Hkv * G; idx += NT) p.lse[q0 + idx] = ok ? neg_inf() : qnan();
     }
   }
@@ -255,31 +249,19 @@ gqa_decode_kernel(
   // pool (read clamped), so the piece is NaN.
   // (The final partial goes to out / lse in fp32, a piece to its workspace
   // slot in bf16.)
-  int piece_row[2] = {-1, -1};  // rows this wave left a piece of (at most its first and last)
   auto flush = [&](int row, bool whole, bool bad) __attribute__((always_inline)) {
-    if (!whole) piece_row[piece_row[0] < 0 ? 0 : 1] = row;
     const float l_tot = wave_sum_xor16_32(l_run);
     if (head_ok) {
       const float inv = bad ? qnan() : 1.f / l_tot;
       const float lse_v = bad ? qnan() : (m_run + __log2f(l_tot)) * kLn2;
       if (whole) {
-        const size_t o0 = ((size_t)row * G + n16) * D + 32 * j;
-        if (p.out) {
-          float* o = p.out + o0;
+        float* o = p.out + ((size_t)row * G + n16) * D + 32 * j;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            ((float4*)(o + 8 * i))[0] = make_float4(acc[0][i] * inv, acc[1][i] * inv,
-                                                    acc[2][i] * inv, acc[3][i] * inv);
-            ((float4*)(o + 8 * i))[1] = make_float4(acc[4][i] * inv, acc[5][i] * inv,
-                                                    acc[6][i] * inv, acc[7][i] * inv);
-          }
-        }
-        if (p.out_bf16) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            store_piece8(p.out_bf16 + o0 + 8 * i, acc[0][i] * inv, acc[1][i] * inv,
-                         acc[2][i] * inv, acc[3][i] * inv, acc[4][i] * inv, acc[5][i] * inv,
-                         acc[6][i] * inv, acc[7][i] * inv);
+        for (int i = 0; i < 4; ++i) {
+          ((float4*)(o + 8 * i))[0] =
+              make_float4(acc[0][i] * inv, acc[1][i] * inv, acc[2][i] * inv, acc[3][i] * inv);
+          ((float4*)(o + 8 * i))[1] =
+              make_float4(acc[4][i] * inv, acc[5][i] * inv, acc[6][i] * inv, acc[7][i] * inv);
         }
         if (j == 0) p.lse[(size_t)row * G + n16] = lse_v;
       } else {
@@ -293,118 +275,6 @@ gqa_decode_kernel(
         if (j == 0) p.ws.part_lse[slot] = lse_v;
       }
     }
-  };
-
-  // Combine of a row spread over several splits, run by the last of them to
-  // arrive (one-launch entry points): the row's G x 128 outputs are 16G
-  // chunks of 8 columns of one head, chunk c = lane + 64 i (head c / 16); its
-  // pieces are read KB at a time (all their loads in flight together) and
-  // folded in by an online LSE combine.  NaN pieces stay NaN (max_nan).
-  auto combine_row = [&](int row, int w_first, int nseg) __attribute__((always_inline)) {
-    constexpr int NCH = 16 * G;
-    constexpr int CPL = (NCH + 63) / 64;
-    constexpr int KB = CPL >= 4 ? 4 : (CPL == 2 ? 8 : 16);
-    const size_t slot0 = (size_t)w_first + row;
-    int hh[CPL], cc[CPL];
-    float M[CPL], Ls[CPL], a[CPL][8];
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = min(lane + 64 * i, NCH - 1);
-      hh[i] = c >> 4;
-      cc[i] = (c & 15) * 8;
-      M[i] = neg_inf();
-      Ls[i] = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) a[i][e] = 0.f;
-    }
-    for (int s0 = 0; s0 < nseg; s0 += KB) {
-      float lv[KB][CPL];
-      u32x4 pv[KB][CPL];
-#pragma unroll
-      for (int k = 0; k < KB; ++k) {
-        const size_t slot = slot0 + min(s0 + k, nseg - 1);
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-          lv[k][i] = p.ws.part_lse[slot * G + hh[i]];
-          pv[k][i] = *(const u32x4*)(p.ws.part_out + (slot * G + hh[i]) * D + cc[i]);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        float mn = M[i];
-#pragma unroll
-        for (int k = 0; k < KB; ++k)
-          if (s0 + k < nseg) mn = max_nan(mn, lv[k][i]);
-        const float sc = M[i] == neg_inf() ? 0.f : __expf(M[i] - mn);
-        Ls[i] *= sc;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a[i][e] *= sc;
-#pragma unroll
-        for (int k = 0; k < KB; ++k) {
-          if (s0 + k >= nseg) continue;
-          const float w = __expf(lv[k][i] - mn);
-          Ls[i] += w;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t wd = pv[k][i][e];
-            a[i][2 * e] += w * __builtin_bit_cast(float, wd << 16);
-            a[i][2 * e + 1] += w * __builtin_bit_cast(float, wd & 0xffff0000u);
-          }
-        }
-        M[i] = mn;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      if (lane + 64 * i >= NCH) continue;
-      const float inv = 1.f / Ls[i];
-      const size_t o0 = ((size_t)row * G + hh[i]) * D + cc[i];
-      if (p.out) {
-        ((float4*)(p.out + o0))[0] = make_float4(a[i][0] * inv, a[i][1] * inv, a[i][2] * inv,
-                                                 a[i][3] * inv);
-        ((float4*)(p.out + o0))[1] = make_float4(a[i][4] * inv, a[i][5] * inv, a[i][6] * inv,
-                                                 a[i][7] * inv);
-      }
-      if (p.out_bf16)
-        store_piece8(p.out_bf16 + o0, a[i][0] * inv, a[i][1] * inv, a[i][2] * inv,
-                     a[i][3] * inv, a[i][4] * inv, a[i][5] * inv, a[i][6] * inv, a[i][7] * inv);
-      if (cc[i] == 0) p.lse[(size_t)row * G + hh[i]] = M[i] + __logf(Ls[i]);
-    }
-  };
-  // A wave's arrival at a row it left a piece of: the splits holding the
-  // row's blocks count in (a lock-free CAS on the row's counter word, at most
-  // one retry per other arrival), and the last one combines the row.
-  auto arrive = [&](int row) __attribute__((always_inline)) {
-    if (row < 0) return;
-    row = uniform(row);
-    const int b = uniform(row / p.Hkv);
-    const int kvh = row - b * p.Hkv;
-    const int nbb = (s_len[b] + 31) >> 5;
-    const int rs = s_pref[b] + kvh * nbb;
-    int w_first, nseg;
-    plan_row_splits(plan, b, rs, nbb, s_wpref, w_first, nseg);
-    __threadfence();  // this wave's piece is visible before its arrival
-    int idx = 0;
-    if (lane == 0) {
-      unsigned long long* ctr = p.ws.counters + row;
-      const unsigned long long key = arrival_key(p.epoch);
-      unsigned long long old = __hip_atomic_load(ctr, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-      while (true) {
-        const bool mine = (old >> 13) == key;
-        const unsigned long long nw = mine ? old + 1 : (key << 13) | 1ull;
-        const unsigned long long prev = atomicCAS(ctr, old, nw);
-        if (prev == old) {
-          idx = mine ? (int)(old & 0x1fffull) : 0;
-          break;
-        }
-        old = prev;
-      }
-    }
-    idx = __shfl(idx, 0);
-    if (idx != nseg - 1) return;
-    __threadfence();  // the other pieces are visible to the loads below
-    combine_row(row, w_first, nseg);
   };
 
   // Ring of S register stages: stage st holds the block k with k % S == st
@@ -474,10 +344,6 @@ gqa_decode_kernel(
     if (base + decltype(i)::value < nblk) step(i, base + decltype(i)::value);
   });
   flush(run_row, run_first && run_last, run_bad);
-  if (p.combine) {
-    arrive(piece_row[0]);
-    arrive(piece_row[1]);
-  }
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -488,13 +354,17 @@ using namespace ws;
 
 // Splits (waves) of a GQA call: n_splits when given, else two per CU (one
 // two-wave workgroup), at most what the blocks of the longest possible batch
-// can feed with 8 blocks each.  Measured on MI355X at 537 MB per launch: two
+// can feed with 2 blocks each.  Measured on MI355X at 537 MB per launch: two
 // long streams per CU beat four or eight shorter ones (79.7 us against 80.5
-// and 84.0), and a third register stage gains nothing.
+// and 84.0), and a third register stage gains nothing.  Small calls (split
+// step + merge, r = 1, us per layer): B1 Hkv4 L4096 (516 blocks) 14.4 at 8
+// blocks per split (71 splits), 12.5-12.8 at 2 (258); B1 Hkv8 L4096 16.2 ->
+// 11.9; B4 Hkv4 L4096 16.3 -> 13.3; one block per split makes the merge's
+// rows longer (128 pieces) and was slower again (14.0).
 static int gqa_splits(int n_splits, int rows_kv, int max_len) {
   if (n_splits > 0) return n_splits;
   const long long max_blocks = (long long)rows_kv * ((max_len + 31) / 32);
-  return choose_workgroups(0, kGqaSplitsPerCu, max_blocks, 8);
+  return choose_workgroups(0, kGqaSplitsPerCu, max_blocks, 2);
 }
 
 static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
@@ -504,10 +374,8 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
                       int n_splits, float scale, float* out, float* lse,
                       void* workspace, size_t workspace_bytes, void* stream,
                       bool combine, const char* name, uint16_t* out_bf16 = nullptr) {
-  if (!q || !k_pages || !v_pages || !page_table || !len_in || (!out && !out_bf16) || !lse)
+  if (!q || !k_pages || !v_pages || !page_table || !len_in || !out || !lse)
     return set_error(WS_EINVAL, "%s: null pointer", name);
-  if (!out && !combine)
-    return set_error(WS_EINVAL, "%s: a deferred-combine step needs the fp32 out", name);
   if (B < 0 || B > kMaxSeqs || Hkv <= 0 || Hq <= 0 || Hq % Hkv)
     return set_error(WS_EINVAL, "%s: bad batch/heads B=%d Hq=%d Hkv=%d (B <= %d)", name,
                      B, Hq, Hkv, kMaxSeqs);
@@ -531,7 +399,6 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
                      (long long)num_pages * Hkv * page_size);
   if (n_splits < 0) return set_error(WS_EINVAL, "%s: n_splits %d < 0", name, n_splits);
   if (!aligned16(q) || !aligned16(k_pages) || !aligned16(v_pages) || !aligned16(out) ||
-      !aligned16(out_bf16) ||
       (k_new && (!aligned16(k_new) || !aligned16(v_new))))
     return set_error(WS_EINVAL, "%s: buffers must be 16-byte aligned", name);
   if (k_new && !v_new) return set_error(WS_EINVAL, "%s: v_new is null", name);
@@ -564,14 +431,8 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   prm.k_new = k_new;
   prm.v_new = v_new;
   prm.out = out;
-  prm.out_bf16 = out_bf16;
   prm.lse = lse;
   prm.ws = carve_workspace(workspace, rows_kv, G, n);
-  // One-launch entry points: the rows several waves share are combined in
-  // the same launch by the last of those waves to finish (row counters in
-  // the workspace, tagged with this launch's epoch).
-  prm.combine = combine ? 1 : 0;
-  prm.epoch = combine ? next_epoch() : 0;
   prm.B = B;
   prm.Hkv = Hkv;
   prm.page_size = page_size;
@@ -601,7 +462,14 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
     switch (G) { WS_GQA_CASE(1, kGqaDk192) }
   }
 #undef WS_GQA_CASE
-  return check_launch(name);
+  int rc = check_launch(name);
+  if (rc != WS_OK || !combine) return rc;
+  // One-launch entry points: the rows held by several waves are combined by
+  // the split merge on the same stream, in place (D = 128: one column chunk
+  // per row, so each element is read and written by the same thread).
+  rc = merge_split_pieces(len_in, k_new ? 1 : 0, B, Hkv, G, D, prm.cap, n, out, lse, prm.ws,
+                          out, lse, out_bf16, s);
+  return rc != WS_OK ? rc : check_launch(name);
 }
 
 extern "C" int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
@@ -696,9 +564,12 @@ extern "C" int ws_gqa_append_decode_full(
     int B, int Hq, int Hkv, int D, int page_size, int max_pages, int num_pages, int max_len,
     int n_splits, float scale, uint16_t* out_bf16, float* out, float* lse, void* workspace,
     size_t workspace_bytes, void* stream) {
-  if (!k_new) return set_error(WS_EINVAL, "ws_gqa_append_decode_full: k_new is null");
+  static const char* name = "ws_gqa_append_decode_full";
+  if (!k_new) return set_error(WS_EINVAL, "%s: k_new is null", name);
+  if (!out_bf16) return set_error(WS_EINVAL, "%s: out_bf16 is null", name);
+  if (((uintptr_t)out_bf16 & 15u) != 0)
+    return set_error(WS_EINVAL, "%s: buffers must be 16-byte aligned", name);
   return gqa_launch(q, k_new, v_new, k_pages, v_pages, page_table, len_in, len_out, B, Hq,
                     Hkv, D, D, page_size, max_pages, num_pages, max_len, n_splits, scale, out,
-                    lse, workspace, workspace_bytes, stream, true, "ws_gqa_append_decode_full",
-                    out_bf16);
+                    lse, workspace, workspace_bytes, stream, true, name, out_bf16);
 }

@@ -376,6 +376,41 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
 }
 
 
+// Split combine without a host partial (the one-launch GQA entry points):
+// one 64-lane workgroup per output row, Dv <= 256 so a row is one column
+// chunk and out/lse may alias out_g/lse_g; out_bf16 (optional) receives the
+// same output rounded to bf16.
+int merge_split_pieces(const int32_t* len, int len_add, int B, int R, int heads, int Dv,
+                       int cap, int n, const float* out_g, const float* lse_g,
+                       const SplitWorkspace& w, float* out, float* lse, uint16_t* out_bf16,
+                       hipStream_t stream) {
+  if (Dv > 4 * kMergeChunk4)
+    return set_error(WS_EINVAL, "merge_split_pieces: Dv %d > %d", Dv, 4 * kMergeChunk4);
+  MergeSplitParams prm;
+  prm.gpu_len = len;
+  prm.B = B;
+  prm.ng = 1;
+  prm.R = R;
+  prm.heads = heads;
+  prm.Dv = Dv;
+  prm.cap = cap;
+  prm.grid = n;
+  prm.add = len_add;
+  prm.out_g = out_g;
+  prm.lse_g = lse_g;
+  prm.part_out = w.part_out;
+  prm.part_lse = w.part_lse;
+  prm.b_out = nullptr;
+  prm.b_aux0 = nullptr;
+  prm.b_aux1 = nullptr;
+  prm.out_bf16 = out_bf16;
+  prm.out_f32 = out;
+  prm.lse_out = lse;
+  hipLaunchKernelGGL(merge_split_kernel<-1>, dim3((unsigned)(B * R * heads)), dim3(64), 0,
+                     stream, prm);
+  return WS_OK;
+}
+
 }  // namespace ws
 
 using namespace ws;

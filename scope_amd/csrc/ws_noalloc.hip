@@ -9,8 +9,8 @@
 // device current) and only that address is passed to the kernels.  Every call
 // on one GPU shares the array, so calls that overlap on one GPU (different
 // streams, or threads without ordering) race; calls ordered on one stream do
-// not.  The array needs no initial contents: a call writes every slot it
-// reads back, and its row arrival counters carry a per-launch tag.
+// not.  The array needs no initial contents: a call writes every slot it or
+// its combine launch reads back.
 #include <mutex>
 
 #include "ws_reduce.h"

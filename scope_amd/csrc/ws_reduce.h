@@ -4,29 +4,19 @@
 // split that holds a whole row writes the row's final partial (out
 // normalised fp32, lse natural log) straight to the caller's out / lse; a
 // row spread over several splits leaves one piece per split in the
-// workspace, and either the last of those splits to finish combines them in
-// the same launch (the GQA one-launch entry points) or a later launch on the
-// same stream (merge_split_kernel, merge_split_uv_kernel, mla_reduce_kernel)
-// rebuilds the plan to find and LSE-combine them.
+// workspace, and a later launch on the same stream (merge_split_kernel,
+// merge_split_uv_kernel, mla_reduce_kernel) rebuilds the plan to find and
+// LSE-combine them.
 //
 // Workspace layout (ws_decode_plan), for a call over rows_kv rows of `heads`
 // output rows each, run by n splits:
-//   [row arrival counters int32 x rows_kv, padded to 256 B]
 //   [slot lse f32 x (n + rows_kv) x heads, padded to 256 B]
 //   [slot out bf16 x (n + rows_kv) x heads x Dv]
 // (slot = split + row, ws_plan.h).  Pieces are normalised and rounded to
 // bf16 (their weights stay fp32): a 32-token block carries 36 KB of latent
 // and an MLA piece 16 x 512 outputs, so at 256 splits fp32 pieces cost
 // 8 MB of writes and reads per call.  Every call writes the slots it reads
-// back.  The counters are used by the GQA kernel when it combines shared
-// rows itself (the one-launch entry points): each split that leaves a piece
-// of a row counts its arrival, and the last one combines the row.  A counter
-// word is tag (15 bits) | launch epoch (36 bits) | arrivals (13 bits): a
-// launch's first arrival finds no match there (an earlier launch's epoch, or
-// whatever data an earlier call of another shape left in those bytes) and
-// starts the count afresh, so the workspace still needs no initial contents.
-// Epochs come from a per-process sequence (next_epoch) that would take 2^36
-// launches to wrap.
+// back, so the workspace needs no initial contents.
 #pragma once
 
 #include "ws_common.h"
@@ -39,23 +29,13 @@ constexpr int kReduceMaxWeights = 4096;
 __host__ __device__ inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 struct SplitWorkspace {
-  unsigned long long* counters;  // [rows_kv] tag | epoch | arrivals per row (arrival_word)
   float* part_lse;
   uint16_t* part_out;  // bf16
 };
 
 __host__ __device__ inline size_t workspace_bytes(int rows_kv, int heads, int Dv, int n) {
   const size_t slots = (size_t)n + rows_kv;
-  return align256((size_t)rows_kv * 8) + align256(slots * heads * 4) + slots * heads * Dv * 2;
-}
-
-// The next launch epoch (1, 2, ...; thread-safe).
-unsigned long long next_epoch();
-
-// Arrival counter word: tag | epoch | count.
-constexpr unsigned long long kArrivalTag = 0x52c3;
-__host__ __device__ inline unsigned long long arrival_key(unsigned long long epoch) {
-  return (kArrivalTag << 36) | (epoch & ((1ull << 36) - 1));
+  return align256(slots * heads * 4) + slots * heads * Dv * 2;
 }
 
 __host__ __device__ inline SplitWorkspace carve_workspace(void* base, int rows_kv,
@@ -63,8 +43,6 @@ __host__ __device__ inline SplitWorkspace carve_workspace(void* base, int rows_k
   SplitWorkspace w;
   char* p = (char*)base;
   const size_t slots = (size_t)n + rows_kv;
-  w.counters = (unsigned long long*)p;
-  p += align256((size_t)rows_kv * 8);
   w.part_lse = (float*)p;
   p += align256(slots * heads * 4);
   w.part_out = (uint16_t*)p;
@@ -77,6 +55,15 @@ __host__ __device__ inline SplitWorkspace carve_workspace(void* base, int rows_k
 int choose_workgroups(int n_workgroups, int per_cu, long long max_blocks, int min_blocks);
 // Workgroups of an MLA call (ws_mla.hip).
 int mla_workgroups(int n_workgroups, int B, int max_len);
+// Combines the pieces of a split decode step with no host partial: rows held
+// by several splits are LSE-combined from the workspace, the others copied;
+// lengths are len[b] + len_add; out/lse may alias out_g/lse_g (Dv <= 256);
+// out_bf16, when not null, also receives the output in bf16.  Launches on
+// `stream`; returns WS_OK or an error code (ws_merge.hip).
+int merge_split_pieces(const int32_t* len, int len_add, int B, int R, int heads, int Dv,
+                       int cap, int n, const float* out_g, const float* lse_g,
+                       const SplitWorkspace& w, float* out, float* lse, uint16_t* out_bf16,
+                       hipStream_t stream);
 
 // Eight outputs of a piece, rounded to bf16, as one 16-byte store.
 __device__ __forceinline__ void store_piece8(uint16_t* dst, float a0, float a1, float a2,

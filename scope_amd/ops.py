@@ -41,6 +41,7 @@ EXPORTS = (
     "ws_lse_merge",
     "ws_attn_decode_partial",
     "ws_attn_append_decode_partial",
+    "ws_copy",
     "ws_noalloc_scratch_bytes",
     "ws_gqa_append_decode_partial_noalloc",
 )
@@ -125,6 +126,8 @@ def lib() -> ctypes.CDLL:
         L.ws_attn_append_decode_partial.restype = i32
         L.ws_attn_append_decode_partial.argtypes = [vp] * 8 + [i32] * 10 + [f32, vp, vp, vp,
                                                                              sz, vp]
+        L.ws_copy.restype = i32
+        L.ws_copy.argtypes = [vp, vp, sz, vp]
         L.ws_noalloc_scratch_bytes.restype = sz
         L.ws_noalloc_scratch_bytes.argtypes = []
         L.ws_gqa_append_decode_partial_noalloc.restype = i32
@@ -199,6 +202,32 @@ def decode_plan(kind: int, rows_kv: int, heads: int, max_len: int,
     _check(lib().ws_decode_plan(kind, rows_kv, heads, max_len, n_workgroups,
                                 ctypes.byref(n), ctypes.byref(wsb)), "ws_decode_plan")
     return n.value, wsb.value
+
+
+# ---------------------------------------------------------------------------
+# transfers
+
+
+def copy_(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+    """dst.copy_(src) by the library's copy kernel (ws_copy) on the current
+    stream of the GPU side: one of them on the GPU, the other on the GPU or in
+    pinned host memory.  Used for a layer's query to the host partial, where
+    a DMA copy's set-up latency sits on every layer's critical path."""
+    if dst.dtype != src.dtype or dst.numel() != src.numel():
+        raise ValueError("copy_: dst and src must have the same dtype and size")
+    gpu = dst if dst.is_cuda else src
+    if not gpu.is_cuda:
+        raise ValueError("copy_: one side must be on a GPU")
+    for t, n in ((dst, "dst"), (src, "src")):
+        if not t.is_contiguous():
+            raise ValueError(f"copy_: {n} must be contiguous")
+        if t.is_cuda and t.device != gpu.device:
+            raise ValueError("copy_: tensors on two GPUs")
+        if not t.is_cuda and not t.is_pinned():
+            raise ValueError(f"copy_: {n} must be on the GPU or in pinned host memory")
+    _check(lib().ws_copy(_ptr(dst), _ptr(src), dst.numel() * dst.element_size(),
+                         _stream(gpu.device)), "ws_copy")
+    return dst
 
 
 # ---------------------------------------------------------------------------
@@ -429,9 +458,10 @@ def gqa_append_decode_full(q, k_new, v_new, k_pages, v_pages, page_table, len_in
                            scale, max_len, n_workgroups=0, out_bf16=None, out=None, lse=None,
                            want_fp32=False):
     """The whole decode step of a partition that holds every token (no host
-    share), in one launch: gqa_append_decode_partial that also writes the
-    normalised output in bf16.  Returns (out_bf16 [B, Hq, D], lse [B, Hq])
-    or, with want_fp32 (or an `out` given), (out_bf16, out fp32, lse)."""
+    share): gqa_append_decode_partial that also writes the normalised output
+    in bf16 (the step launch and its combine launch).  Returns (out_bf16
+    [B, Hq, D], lse [B, Hq]) or, with want_fp32 (or an `out` given),
+    (out_bf16, out fp32, lse)."""
     dev = k_pages.device
     for t, n, dt, nd in ((q, "q", torch.bfloat16, 3), (k_new, "k_new", torch.bfloat16, 4),
                          (v_new, "v_new", torch.bfloat16, 4),
@@ -455,15 +485,14 @@ def gqa_append_decode_full(q, k_new, v_new, k_pages, v_pages, page_table, len_in
     if out_bf16 is None:
         out_bf16 = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=dev)
     _require(out_bf16, "out_bf16", torch.bfloat16, dev, 3)
-    if out is None and want_fp32:
+    give_fp32 = want_fp32 or out is not None
+    if out is None:  # the step's fp32 partial (finalised in place by the combine)
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=dev)
-    if out is not None:
-        _require(out, "out", torch.float32, dev, 3)
+    _require(out, "out", torch.float32, dev, 3)
     if lse is None:
         lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
     _require(lse, "lse", torch.float32, dev, 2)
-    if out_bf16.shape != q.shape or (out is not None and out.shape != q.shape) or \
-            lse.shape != (B, Hq):
+    if out_bf16.shape != q.shape or out.shape != q.shape or lse.shape != (B, Hq):
         raise ValueError("out_bf16/out must be [B, Hq, D] and lse [B, Hq]")
     nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
     ws = _workspace(dev, wsb)
@@ -472,7 +501,7 @@ def gqa_append_decode_full(q, k_new, v_new, k_pages, v_pages, page_table, len_in
         _ptr(len_in), _ptr(len_out), B, Hq, Hkv, D, PS, page_table.shape[1], P,
         int(max_len), nwg, float(scale), _ptr(out_bf16), _ptr(out), _ptr(lse), _ptr(ws), wsb,
         _stream(dev)), "ws_gqa_append_decode_full")
-    return (out_bf16, out, lse) if out is not None else (out_bf16, lse)
+    return (out_bf16, out, lse) if give_fp32 else (out_bf16, lse)
 
 
 def gqa_append_decode_partial_noalloc(q, k_new, v_new, k_pages, v_pages, page_table, len_in,
@@ -664,22 +693,7 @@ def merge_split(step: SplitStep, b=None, fmt=PARTIAL_LSE_F32, out_dtype=torch.bf
     step.check_workspace()
     dev = step.out_g.device
     rows = step.out_g.numel() // step.Dv
-    b_out = b_aux0 = b_aux1 = None
-    if b is not None:
-        if fmt == PARTIAL_LSE_F32:
-            b_out, b_aux0 = b
-            _require(b_out, "b.out", torch.float32, dev)
-            _require(b_aux0, "b.lse", torch.float32, dev)
-        else:
-            b_out, b_aux0, b_aux1 = b
-            dt = torch.bfloat16 if fmt == TRIPLE_NORM_BF16 else torch.float32
-            _require(b_out, "b.out", dt, dev)
-            _require(b_aux0, "b.max", dt, dev)
-            _require(b_aux1, "b.sum", dt, dev)
-            if b_aux1.numel() != rows:
-                raise ValueError("b.sum must have one value per row")
-        if b_out.numel() != rows * step.Dv or b_aux0.numel() != rows:
-            raise ValueError("host partial does not match the step's rows")
+    b_out, b_aux0, b_aux1 = _host_operand(b, fmt, rows, step.Dv, dev)
     if out is None:
         out = torch.empty((rows, step.Dv), dtype=out_dtype, device=dev)
     if want_lse and lse_out is None:
@@ -696,21 +710,39 @@ def merge_split(step: SplitStep, b=None, fmt=PARTIAL_LSE_F32, out_dtype=torch.bf
     return out, (lse_out if want_lse else None)
 
 
+def _require_operand(t, name, dtype, dev):
+    """A merge's host operand: a tensor on `dev`, or a pinned host tensor,
+    which the merge kernel reads in place over the host link."""
+    if isinstance(t, torch.Tensor) and not t.is_cuda:
+        if not t.is_pinned():
+            raise ValueError(f"{name} must be on {dev} or in pinned host memory")
+        if t.dtype != dtype:
+            raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        return
+    _require(t, name, dtype, dev)
+
+
 def _host_operand(b, fmt, rows, Dv, dev):
+    """Pointers of the host partial `b` in format fmt (None: no host partial),
+    validated against rows x Dv."""
     b_out = b_aux0 = b_aux1 = None
     if b is not None:
         if fmt == PARTIAL_LSE_F32:
             b_out, b_aux0 = b
-            _require(b_out, "b.out", torch.float32, dev)
-            _require(b_aux0, "b.lse", torch.float32, dev)
-        else:
+            _require_operand(b_out, "b.out", torch.float32, dev)
+            _require_operand(b_aux0, "b.lse", torch.float32, dev)
+        elif fmt in (TRIPLE_UNNORM_F32, TRIPLE_NORM_BF16, TRIPLE_NORM_F32):
             b_out, b_aux0, b_aux1 = b
             dt = torch.bfloat16 if fmt == TRIPLE_NORM_BF16 else torch.float32
-            _require(b_out, "b.out", dt, dev)
-            _require(b_aux0, "b.max", dt, dev)
-            _require(b_aux1, "b.sum", dt, dev)
+            _require_operand(b_out, "b.out", dt, dev)
+            _require_operand(b_aux0, "b.max", dt, dev)
+            _require_operand(b_aux1, "b.sum", dt, dev)
             if b_aux1.numel() != rows:
                 raise ValueError("b.sum must have one value per row")
+        else:
+            raise ValueError(f"unknown host-partial format {fmt}")
         if b_out.numel() != rows * Dv or b_aux0.numel() != rows:
             raise ValueError("host partial does not match the step's rows")
     return b_out, b_aux0, b_aux1
@@ -785,21 +817,9 @@ def lse_merge(out_g, lse_g, b, fmt=PARTIAL_LSE_F32, out_dtype=torch.bfloat16,
     rows = out_g.numel() // Dv
     if lse_g.numel() != rows:
         raise ValueError("lse_g must have one value per output row")
-    if fmt == PARTIAL_LSE_F32:
-        b_out, b_aux0 = b
-        b_aux1 = None
-        _require(b_out, "b.out", torch.float32, dev)
-        _require(b_aux0, "b.lse", torch.float32, dev)
-    else:
-        b_out, b_aux0, b_aux1 = b
-        dt = torch.bfloat16 if fmt == TRIPLE_NORM_BF16 else torch.float32
-        _require(b_out, "b.out", dt, dev)
-        _require(b_aux0, "b.max", dt, dev)
-        _require(b_aux1, "b.sum", dt, dev)
-        if b_aux1.numel() != rows:
-            raise ValueError("b.sum must have one value per row")
-    if b_out.numel() != rows * Dv or b_aux0.numel() != rows:
-        raise ValueError("second partial does not match the GPU partial's shape")
+    if b is None:
+        raise ValueError("lse_merge needs a second partial")
+    b_out, b_aux0, b_aux1 = _host_operand(b, fmt, rows, Dv, dev)
     if out is None:
         out = torch.empty(out_g.shape, dtype=out_dtype, device=dev)
     if want_lse and lse_out is None:

@@ -298,7 +298,7 @@ class _PagedTwoSided:
         """A pinned host buffer of the cache, allocated once per (name, shape).
         One buffer per role is enough: every host partial waits for the
         query copy of its own layer, which the stream orders after the
-        previous layer's partial -> GPU copy out of the same buffers."""
+        previous layer's merge, the last reader of the same buffers."""
         bufs = self.__dict__.setdefault("_pin_bufs", {})
         key = (name, tuple(shape), dtype)
         t = bufs.get(key)
@@ -308,10 +308,13 @@ class _PagedTwoSided:
         return t
 
     def _to_host(self, *ts):
+        """The query tensors in pinned host buffers, copied by the library's
+        copy kernel on the current stream (no DMA set-up latency on the
+        layer's critical path), and an event after the copies."""
         out = []
         for i, t in enumerate(ts):
             h = self._pinned(f"q{i}", t.shape, t.dtype)
-            h.copy_(t, non_blocking=True)
+            ops.copy_(h, t.contiguous())
             out.append(h)
         ev = self.__dict__.get("_q_event")
         if ev is None:
@@ -360,7 +363,9 @@ class _PagedTwoSided:
                         time.perf_counter() - t0)
 
     def _merge(self, step, part, dev, w_uv=None, return_lse=False):
-        b = None if part is None else tuple(x.to(dev, non_blocking=True) for x in part)
+        # the host partial stays in its pinned buffers: the merge reads it in
+        # place over the host link
+        b = part
         if w_uv is not None:
             out_v, _, lse = ops.merge_split_uv(step, w_uv, b, ops.PARTIAL_LSE_F32,
                                                want_lse=return_lse)

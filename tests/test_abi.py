@@ -36,17 +36,16 @@ def test_version_and_plan():
     L = ops.lib()
     assert L.ws_version().decode().startswith("wsgpu")
     pad = lambda n: -(-n // 256) * 256
-    # explicit split counts are kept; workspace = row arrival counters + lse
-    # slots + bf16 piece slots
+    # explicit split counts are kept; workspace = lse slots + bf16 piece slots
     n, wsb = ops.decode_plan(0, 16, 8, 32768, 100)
-    assert n == 100 and wsb == pad(16 * 8) + pad((100 + 16) * 8 * 4) + (100 + 16) * 8 * 128 * 2
+    assert n == 100 and wsb == pad((100 + 16) * 8 * 4) + (100 + 16) * 8 * 128 * 2
     n, wsb = ops.decode_plan(1, 8, 16, 16384, 64)
-    assert n == 64 and wsb == pad(8 * 8) + pad((64 + 8) * 16 * 4) + (64 + 8) * 16 * 512 * 2
-    # the library's choice never exceeds the blocks available (8 per GQA
+    assert n == 64 and wsb == pad((64 + 8) * 16 * 4) + (64 + 8) * 16 * 512 * 2
+    # the library's choice never exceeds the blocks available (2 per GQA
     # split, i.e. per wave) nor the merge's 4096 splits
     for rows, G, L in ((128, 4, 15773), (16, 8, 131072), (4, 8, 4096), (1, 1, 1), (2, 16, 1 << 20)):
         n, _ = ops.decode_plan(0, rows, G, L, 0)
-        assert 1 <= n <= max(1, -(-rows * -(-L // 32) // 8)) and n <= 4096
+        assert 1 <= n <= max(1, -(-rows * -(-L // 32) // 2)) and n <= 4096
     n, _ = ops.decode_plan(1, 8, 16, 8192, 0)
     assert 1 <= n <= 8 * 256 // 4
     with pytest.raises(ops.WsError):
@@ -98,3 +97,15 @@ def test_host_side_argument_checks():
     assert rc == -1 and b"b_aux1" in L.ws_last_error()
     rc = L.ws_lse_merge(fake, fake, fake, fake, None, 9, None, fake, None, 4, 128, None)
     assert rc == -1 and b"format" in L.ws_last_error()
+    # ws_copy: alignment, size and overlap are checked before any launch
+    rc = L.ws_copy(fake, ctypes.c_void_p(0x2008), 64, None)
+    assert rc == -1 and b"aligned" in L.ws_last_error()
+    rc = L.ws_copy(fake, ctypes.c_void_p(0x2000), 66, None)
+    assert rc == -1 and b"multiple of 4" in L.ws_last_error()
+    rc = L.ws_copy(fake, ctypes.c_void_p(0x1010), 64, None)
+    assert rc == -1 and b"overlap" in L.ws_last_error()
+    assert L.ws_copy(None, None, 0, None) == 0  # nothing to copy
+    rc = L.ws_copy(None, fake, 16, None)
+    assert rc == -1 and b"null" in L.ws_last_error()
+    with pytest.raises(ValueError, match="one side must be on a GPU"):
+        ops.copy_(torch.zeros(4), torch.zeros(4))
