@@ -82,6 +82,25 @@ const char* ws_version(void);
 int ws_copy(void* dst, const void* src, size_t bytes, void* stream);
 
 /*
+ * Page copies of a boundary move, every layer at once: for l < n_layers and
+ * i < n_pages, page dst_ids[i] of dst + l * dst_layer_stride = page
+ * src_ids[i] of src + l * src_layer_stride (pages of page_bytes, a multiple
+ * of 16; strides in bytes).  Either pool may be HBM or pinned host memory:
+ * the kernel reads and writes across the host link itself, with no host-side
+ * gather and no staging copy.  dst_ids / src_ids: n_pages int32 each in
+ * device-accessible memory, inside [0, dst_num_pages) / [0, src_num_pages)
+ * (an id outside moves nothing).  Replaces the reference's movement of
+ * tokens across the split: the host-segment tokens past the GPU share that
+ * every step copies to the GPU (system/deepseek.py:368-371) and the GPU
+ * segment's .to(device) (system/mixoffload.py:1369-1370); here a share change
+ * moves whole pages once.
+ */
+int ws_copy_pages(void* dst, long long dst_layer_stride, const int32_t* dst_ids,
+                  int dst_num_pages, const void* src, long long src_layer_stride,
+                  const int32_t* src_ids, int src_num_pages, int n_pages, int n_layers,
+                  long long page_bytes, void* stream);
+
+/*
  * Append n_new tokens per sequence to the GQA pools at positions
  * gpu_len[b] .. gpu_len[b] + n_new - 1, then (if update_len) gpu_len[b] += n_new.
  * k_new, v_new: [B][Hkv][n_new][D] bf16 (the reference's k4d/v4d layout).

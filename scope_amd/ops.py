@@ -16,6 +16,7 @@ from __future__ import annotations
 import ctypes
 import os
 
+import numpy as np
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -42,6 +43,7 @@ EXPORTS = (
     "ws_attn_decode_partial",
     "ws_attn_append_decode_partial",
     "ws_copy",
+    "ws_copy_pages",
     "ws_noalloc_scratch_bytes",
     "ws_gqa_append_decode_partial_noalloc",
 )
@@ -128,6 +130,8 @@ def lib() -> ctypes.CDLL:
                                                                              sz, vp]
         L.ws_copy.restype = i32
         L.ws_copy.argtypes = [vp, vp, sz, vp]
+        L.ws_copy_pages.restype = i32
+        L.ws_copy_pages.argtypes = [vp, i64, vp, i32, vp, i64, vp, i32, i32, i32, i64, vp]
         L.ws_noalloc_scratch_bytes.restype = sz
         L.ws_noalloc_scratch_bytes.argtypes = []
         L.ws_gqa_append_decode_partial_noalloc.restype = i32
@@ -228,6 +232,43 @@ def copy_(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
     _check(lib().ws_copy(_ptr(dst), _ptr(src), dst.numel() * dst.element_size(),
                          _stream(gpu.device)), "ws_copy")
     return dst
+
+
+def copy_pages(dst_pool: torch.Tensor, dst_ids, src_pool: torch.Tensor, src_ids) -> None:
+    """dst_pool[:, dst_ids[i]] = src_pool[:, src_ids[i]] for every layer, by
+    the library's page-copy kernel (ws_copy_pages) on the current stream of
+    the GPU side.  Pools are [layers, num_pages, *page] of one dtype; one of
+    them on the GPU, the other on the same GPU or in pinned host memory (the
+    kernel crosses the host link itself: no host gather, no staging)."""
+    if dst_pool.dtype != src_pool.dtype or dst_pool.dim() < 2 or \
+            dst_pool.shape[0] != src_pool.shape[0] or dst_pool.shape[2:] != src_pool.shape[2:]:
+        raise ValueError("copy_pages: pools must match in dtype, layers and page shape")
+    gpu = dst_pool if dst_pool.is_cuda else src_pool
+    if not gpu.is_cuda:
+        raise ValueError("copy_pages: one pool must be on a GPU")
+    for t, n in ((dst_pool, "dst_pool"), (src_pool, "src_pool")):
+        if not t.is_contiguous():
+            raise ValueError(f"copy_pages: {n} must be contiguous")
+        if t.is_cuda and t.device != gpu.device:
+            raise ValueError("copy_pages: pools on two GPUs")
+        if not t.is_cuda and not t.is_pinned():
+            raise ValueError(f"copy_pages: {n} must be on the GPU or in pinned host memory")
+    di = np.asarray(dst_ids, np.int64).reshape(-1)
+    si = np.asarray(src_ids, np.int64).reshape(-1)
+    if di.shape != si.shape:
+        raise ValueError("copy_pages: dst_ids and src_ids differ in length")
+    if di.size == 0:
+        return
+    for ids, pool, n in ((di, dst_pool, "dst_ids"), (si, src_pool, "src_ids")):
+        if ids.min() < 0 or ids.max() >= pool.shape[1]:
+            raise ValueError(f"copy_pages: {n} outside [0, {pool.shape[1]})")
+    ids = torch.from_numpy(np.stack([di, si]).astype(np.int32)).to(gpu.device)
+    page_bytes = dst_pool[0, 0].numel() * dst_pool.element_size()
+    _check(lib().ws_copy_pages(
+        _ptr(dst_pool), dst_pool.stride(0) * dst_pool.element_size(), _ptr(ids[0]),
+        dst_pool.shape[1], _ptr(src_pool), src_pool.stride(0) * src_pool.element_size(),
+        _ptr(ids[1]), src_pool.shape[1], int(di.size), dst_pool.shape[0], page_bytes,
+        _stream(gpu.device)), "ws_copy_pages")
 
 
 # ---------------------------------------------------------------------------

@@ -148,10 +148,10 @@ class _PagedTwoSided:
 
     def set_boundaries(self, targets) -> None:
         """Move every sequence's boundary to targets[b] host tokens in one
-        batch: one gather, one transfer and one scatter per direction and
-        payload, all layers at once, through pinned staging.  New pages are
-        taken before any page is given back, so no page is both read and
-        written within a batch.  Returns when the copies are done."""
+        batch: one page-copy launch per direction and payload, all layers at
+        once (pinned host pools; unpinned ones go through pinned staging).
+        New pages are taken before any page is given back, so no page is both
+        read and written within a batch.  Returns when the copies are done."""
         ps = self.page_size
         g = self.gpu
         if len(targets) != self.batch:
@@ -256,8 +256,14 @@ class _PagedTwoSided:
             self._stage_ev[k] = ev
 
     def _pages_to_gpu(self, gp, hp, pids_g, pids_h):
-        """gp[:, pids_g] = hp[:, pids_h] for every layer."""
+        """gp[:, pids_g] = hp[:, pids_h] for every layer: from pinned host
+        pools by the library's page-copy kernel (it reads across the host
+        link itself), else through pinned staging."""
         dev = self.gpu.device
+        if dev.type == "cuda" and hp.is_pinned():
+            ops.copy_pages(gp, pids_g, hp, pids_h)
+            torch.cuda.synchronize(dev)
+            return
         self._stages()
         ig = torch.tensor(pids_g, dtype=torch.int64, device=dev)
         ih = torch.tensor(pids_h, dtype=torch.int64)
@@ -272,8 +278,13 @@ class _PagedTwoSided:
             self._wait_stage(k)
 
     def _pages_to_host(self, gp, hp, pids_g, pids_h):
-        """hp[:, pids_h] = gp[:, pids_g] for every layer."""
+        """hp[:, pids_h] = gp[:, pids_g] for every layer (to pinned host pools
+        by the page-copy kernel, else through pinned staging)."""
         dev = self.gpu.device
+        if dev.type == "cuda" and hp.is_pinned():
+            ops.copy_pages(hp, pids_h, gp, pids_g)
+            torch.cuda.synchronize(dev)
+            return
         self._stages()
         ig = torch.tensor(pids_g, dtype=torch.int64, device=dev)
         ih = torch.tensor(pids_h, dtype=torch.int64)

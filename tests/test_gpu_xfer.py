@@ -66,3 +66,39 @@ def test_merges_read_pinned_host_operands_in_place(fmt):
                                  out_dtype=torch.float32)
         torch.cuda.synchronize()
         assert torch.equal(got, want) and torch.equal(gl, wl), rep
+
+
+@pytest.mark.parametrize("page_shape", [(64, 576), (8, 64, 128), (3, 16)])
+def test_copy_pages_both_directions_every_layer(page_shape):
+    _say(f"ws_copy_pages page {page_shape}")
+    layers, n_host, n_gpu = 3, 40, 33
+    g = torch.Generator().manual_seed(11)
+    host = torch.randn((layers, n_host, *page_shape), generator=g).to(torch.bfloat16)
+    host = host.pin_memory()
+    gpu = torch.randn((layers, n_gpu, *page_shape), generator=g).to(torch.bfloat16).to(DEV)
+    rng = torch.Generator().manual_seed(12)
+    src = torch.randperm(n_host, generator=rng)[:17].tolist()
+    dst = torch.randperm(n_gpu, generator=rng)[:17].tolist()
+    want = gpu.clone()
+    want[:, dst] = host[:, src].to(DEV)
+    ops.copy_pages(gpu, dst, host, src)  # host -> HBM
+    torch.cuda.synchronize()
+    assert torch.equal(gpu, want)
+    back_src = torch.randperm(n_gpu, generator=rng)[:9].tolist()
+    back_dst = torch.randperm(n_host, generator=rng)[:9].tolist()
+    want_h = host.clone()
+    want_h[:, back_dst] = gpu[:, back_src].cpu()
+    ops.copy_pages(host, back_dst, gpu, back_src)  # HBM -> host
+    torch.cuda.synchronize()
+    assert torch.equal(host, want_h)
+
+
+def test_copy_pages_rejects_ids_outside_the_pools():
+    host = torch.zeros((1, 4, 64, 576), dtype=torch.bfloat16).pin_memory()
+    gpu = torch.zeros((1, 3, 64, 576), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="dst_ids"):
+        ops.copy_pages(gpu, [3], host, [0])
+    with pytest.raises(ValueError, match="src_ids"):
+        ops.copy_pages(gpu, [0], host, [-1])
+    with pytest.raises(ValueError, match="pinned"):
+        ops.copy_pages(gpu, [0], torch.zeros((1, 4, 64, 576), dtype=torch.bfloat16), [0])
