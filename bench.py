@@ -679,8 +679,9 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
     out = torch.empty((rows, 512), dtype=torch.bfloat16, device=dev)
     q_h = torch.empty((rows * 576,), dtype=torch.bfloat16, pin_memory=True)
     qn_h, qp_h = q_h[:rows * 512].view(rows, 512), q_h[rows * 512:].view(rows, 64)
-    part_h = torch.empty((rows * 513,), dtype=torch.float32, pin_memory=True)
-    oc_h, lc_h = part_h[:rows * 512].view(rows, 512), part_h[rows * 512:]
+    # the host partial: bf16 out (wh_mla_partial_bf16) and fp32 lse, pinned
+    oc_h = torch.empty((rows, 512), dtype=torch.bfloat16, pin_memory=True)
+    lc_h = torch.empty((rows,), dtype=torch.float32, pin_memory=True)
     h_lens = torch.from_numpy(h_tok.astype(np.int32))
     h_tab = torch.from_numpy(h_table)
     with_host = bool(h_tok.sum() > 0)
@@ -722,7 +723,7 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
                 # the merge reads the host partial in place (pinned memory)
                 rc |= f_merge(lo, B, 1, H, 512, cap, nwg, p(out_g), p(lse_g), p(ws),
                               ctypes.c_size_t(wsb), p(oc_h), p(lc_h), None,
-                              ops.PARTIAL_LSE_F32, p(out), None, None, stream)
+                              ops.PARTIAL_LSE_BF16, p(out), None, None, stream)
             else:
                 rc |= f_merge(lo, B, 1, H, 512, cap, nwg, p(out_g), p(lse_g), p(ws),
                               ctypes.c_size_t(wsb), None, None, None, 0, p(out), None, None,

@@ -65,6 +65,10 @@ extern "C" {
                                      bf16 path of fused_cpu_attn                 */
 #define WS_TRIPLE_NORM_F32 3      /* (out normalised fp32, max fp32, sum fp32):
                                      fp32 path of fused_cpu_attn                 */
+#define WS_PARTIAL_LSE_BF16 4     /* (out normalised bf16, lse fp32): the native
+                                     host partial's bf16 output (wshost.h
+                                     wh_*_partial_bf16), half the bytes for a
+                                     merge that reads it across the host link */
 
 const char* ws_last_error(void);
 const char* ws_version(void);
@@ -395,8 +399,8 @@ int ws_split_reduce(const float* part_out, const float* part_lse,
 
 /*
  * Merge the GPU partial (out_g, lse_g) with a second partial in format fmt_b
- * (WS_PARTIAL_LSE_F32: b_out fp32, b_aux0 = lse fp32; WS_TRIPLE_*: b_aux0 =
- * max, b_aux1 = sum, dtype per format), over rows x Dv.  The b_* operands
+ * (WS_PARTIAL_LSE_F32 / _BF16: b_out fp32 / bf16, b_aux0 = lse fp32;
+ * WS_TRIPLE_*: b_aux0 = max, b_aux1 = sum, dtype per format), over rows x Dv.  The b_* operands
  * may be in pinned host memory (hipHostMalloc): the kernel reads them over
  * the host link in place, so a host partial needs no copy to HBM first
  * (the same holds for ws_merge_split and ws_mla_merge_split_uv).

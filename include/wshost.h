@@ -69,6 +69,16 @@ int wh_gqa_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v
                    int D, int page_size, int max_pages, int num_pages, float scale,
                    float* out, float* lse, int n_threads);
 
+/* wh_gqa_partial writing out as bf16 (rounded to nearest even), lse fp32:
+ * the (out, lse) pair the GPU merges take as WS_PARTIAL_LSE_BF16, half the
+ * bytes of the fp32 out for a merge that reads it across the host link.
+ * (fused_cpu_attn's own bf16 path, kernel/cpu_attn.cpp:631-634, rounds max
+ * and sum to bf16 as well; here the lse stays fp32.) */
+int wh_gqa_partial_bf16(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                        const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                        int D, int page_size, int max_pages, int num_pages, float scale,
+                        uint16_t* out, float* lse, int n_threads);
+
 /* wh_gqa_partial with separate key and value widths: q [B, Hq, Dk],
  * k_pages [num_pages, Hkv, page_size, Dk], v_pages [num_pages, Hkv,
  * page_size, Dv], out [B, Hq, Dv].  (Dk, Dv): equal multiples of 32 up to 256,
@@ -103,6 +113,14 @@ int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t*
                    const int32_t* page_table, const int32_t* lens, int B, int H, int page_size,
                    int max_pages, int num_pages, float scale, float* out, float* lse,
                    int n_threads);
+
+/* wh_mla_partial writing out as bf16 (rounded to nearest even), lse fp32
+ * (WS_PARTIAL_LSE_BF16 for the GPU merges). */
+int wh_mla_partial_bf16(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
+                        int c_stride, const uint16_t* pe_pages, int pe_stride,
+                        const int32_t* page_table, const int32_t* lens, int B, int H,
+                        int page_size, int max_pages, int num_pages, float scale,
+                        uint16_t* out, float* lse, int n_threads);
 
 /* Streaming read bandwidth of the host memory in GB/s (the host side's
  * roofline for the share scheduler): n_threads OpenMP threads (<= 0: the

@@ -162,20 +162,32 @@ Plan make_plan(const int32_t* row_len, int R) {
   return P;
 }
 
+// An output value as stored: fp32 as is, or bf16 rounded to nearest even
+// (a NaN stays a quiet NaN).
+inline float to_out(float v, float*) { return v; }
+inline uint16_t to_out(float v, uint16_t*) {
+  uint32_t u;
+  std::memcpy(&u, &v, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
 // Final (out, lse) of H heads from a state; o_at(h, s) reads o in staging
-// order, out_row(h) is head h's output row (Dv floats).
-template <class OAt, class OutRow>
+// order, out_row(h) is head h's output row (Dv values of OutT: fp32, or bf16
+// as uint16_t).
+template <class OutT, class OAt, class OutRow>
 void write_final(const float* base, int H, int Dv, float* lse, OAt o_at, OutRow out_row) {
   for (int h = 0; h < H; ++h) {
     const float l = base[H + h];
-    float* dst = out_row(h);
+    OutT* dst = out_row(h);
     if (!(l > 0.f)) {
-      std::memset(dst, 0, sizeof(float) * Dv);
+      std::memset(dst, 0, sizeof(OutT) * Dv);
       lse[h] = -INFINITY;
       continue;
     }
     const float inv = 1.f / l;
-    for (int s = 0; s < Dv; ++s) dst[wh::stage_col(s)] = o_at(h, s) * inv;
+    for (int s = 0; s < Dv; ++s) dst[wh::stage_col(s)] = to_out(o_at(h, s) * inv, dst);
     lse[h] = (base[h] + std::log2(l)) * kLn2;
   }
 }
@@ -223,10 +235,11 @@ void for_pages(const int32_t* table_row, int page_size, int t0, int t1, F f) {
 
 namespace {
 
+template <class OutT>
 int attn_partial(const char* fn, const uint16_t* q, const uint16_t* k_pages,
                  const uint16_t* v_pages, const int32_t* page_table, const int32_t* lens, int B,
                  int Hq, int Hkv, int Dk, int D, int page_size, int max_pages, int num_pages,
-                 float scale, float* out, float* lse, int n_threads) {
+                 float scale, OutT* out, float* lse, int n_threads) {
   g_err[0] = '\0';
   if (!isa_ok()) return fail(WH_ENOTSUP, "%s: this CPU lacks AVX-512 F/BW/BF16", fn);
   if (B < 0 || Hkv < 1 || Hq < 1 || Hq % Hkv != 0)
@@ -258,12 +271,12 @@ int attn_partial(const char* fn, const uint16_t* q, const uint16_t* k_pages,
               });
   };
   auto fin = [&](int r, const float* st) {
-    write_final(
+    write_final<OutT>(
         st, G, D, lse + (size_t)r * G, [&](int h, int s) { return st[2 * G + h * D + s]; },
         [&](int h) { return out + ((size_t)r * G + h) * D; });
   };
   auto empty = [&](int r) {
-    std::memset(out + (size_t)r * G * D, 0, sizeof(float) * G * D);
+    std::memset(out + (size_t)r * G * D, 0, sizeof(OutT) * G * D);
     for (int h = 0; h < G; ++h) lse[(size_t)r * G + h] = -INFINITY;
   };
   run_plan(P, R, G, D, n_threads, row_len.data(), seg, fin, empty,
@@ -271,50 +284,25 @@ int attn_partial(const char* fn, const uint16_t* q, const uint16_t* k_pages,
   return WH_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-const char* wh_last_error(void) { return g_err; }
-
-const char* wh_version(void) { return "wshost 0.1 avx512bf16"; }
-
-int wh_isa_supported(void) { return isa_ok() ? 1 : 0; }
-
-int wh_gqa_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
-                   const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
-                   int D, int page_size, int max_pages, int num_pages, float scale,
-                   float* out, float* lse, int n_threads) {
-  return attn_partial("wh_gqa_partial", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv, D,
-                      D, page_size, max_pages, num_pages, scale, out, lse, n_threads);
-}
-
-int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
-                    const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
-                    int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
-                    float* out, float* lse, int n_threads) {
-  return attn_partial("wh_attn_partial", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv, Dk,
-                      Dv, page_size, max_pages, num_pages, scale, out, lse, n_threads);
-}
-
-int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
-                   int c_stride, const uint16_t* pe_pages, int pe_stride,
-                   const int32_t* page_table, const int32_t* lens, int B, int H, int page_size,
-                   int max_pages, int num_pages, float scale, float* out, float* lse,
-                   int n_threads) {
+template <class OutT>
+int mla_partial(const char* fn, const uint16_t* q_nope, const uint16_t* q_pe,
+                const uint16_t* c_pages, int c_stride, const uint16_t* pe_pages, int pe_stride,
+                const int32_t* page_table, const int32_t* lens, int B, int H, int page_size,
+                int max_pages, int num_pages, float scale, OutT* out, float* lse,
+                int n_threads) {
   using namespace wh;
   g_err[0] = '\0';
-  if (!isa_ok()) return fail(WH_ENOTSUP, "wh_mla_partial: this CPU lacks AVX-512 F/BW/BF16");
-  if (B < 0) return fail(WH_EINVAL, "wh_mla_partial: bad batch %d", B);
+  if (!isa_ok()) return fail(WH_ENOTSUP, "%s: this CPU lacks AVX-512 F/BW/BF16", fn);
+  if (B < 0) return fail(WH_EINVAL, "%s: bad batch %d", fn, B);
   if (H < kMlaHeads || H % kMlaHeads)
-    return fail(WH_EINVAL, "wh_mla_partial: %d heads is not a multiple of %d", H, kMlaHeads);
+    return fail(WH_EINVAL, "%s: %d heads is not a multiple of %d", fn, H, kMlaHeads);
   if (c_stride < kMlaC || pe_stride < kMlaPe)
-    return fail(WH_EINVAL, "wh_mla_partial: token strides %d / %d below 512 / 64", c_stride,
-                pe_stride);
+    return fail(WH_EINVAL, "%s: token strides %d / %d below 512 / 64", fn,
+                c_stride, pe_stride);
   if (B == 0) return WH_OK;
   if (!q_nope || !q_pe || !c_pages || !pe_pages || !page_table || !lens || !out || !lse)
-    return fail(WH_EINVAL, "wh_mla_partial: null pointer");
-  if (int rc = check_pages("wh_mla_partial", page_table, lens, B, page_size, max_pages,
+    return fail(WH_EINVAL, "%s: null pointer", fn);
+  if (int rc = check_pages(fn, page_table, lens, B, page_size, max_pages,
                            num_pages))
     return rc;
   // Rows of the plan: (sequence b, 16-head group g), v = b * ng + g, whose
@@ -345,17 +333,71 @@ int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t*
               });
   };
   auto fin = [&](int v, const float* st) {
-    write_final(
+    write_final<OutT>(
         st, Hg, Dv, lse + (size_t)v * Hg, [&](int h, int s) { return st[2 * Hg + s * Hg + h]; },
         [&](int h) { return out + ((size_t)v * Hg + h) * Dv; });
   };
   auto empty = [&](int v) {
-    std::memset(out + (size_t)v * Hg * Dv, 0, sizeof(float) * Hg * Dv);
+    std::memset(out + (size_t)v * Hg * Dv, 0, sizeof(OutT) * Hg * Dv);
     for (int h = 0; h < Hg; ++h) lse[(size_t)v * Hg + h] = -INFINITY;
   };
   run_plan(P, R, Hg, Dv, n_threads, row_len.data(), seg, fin, empty,
            [](size_t i) { return (int)(i % kMlaHeads); });
   return WH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* wh_last_error(void) { return g_err; }
+
+const char* wh_version(void) { return "wshost 0.1 avx512bf16"; }
+
+int wh_isa_supported(void) { return isa_ok() ? 1 : 0; }
+
+int wh_gqa_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                   const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                   int D, int page_size, int max_pages, int num_pages, float scale,
+                   float* out, float* lse, int n_threads) {
+  return attn_partial("wh_gqa_partial", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv, D,
+                      D, page_size, max_pages, num_pages, scale, out, lse, n_threads);
+}
+
+int wh_gqa_partial_bf16(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                        const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                        int D, int page_size, int max_pages, int num_pages, float scale,
+                        uint16_t* out, float* lse, int n_threads) {
+  return attn_partial("wh_gqa_partial_bf16", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv,
+                      D, D, page_size, max_pages, num_pages, scale, out, lse, n_threads);
+}
+
+int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                    const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                    int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
+                    float* out, float* lse, int n_threads) {
+  return attn_partial("wh_attn_partial", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv, Dk,
+                      Dv, page_size, max_pages, num_pages, scale, out, lse, n_threads);
+}
+
+int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
+                   int c_stride, const uint16_t* pe_pages, int pe_stride,
+                   const int32_t* page_table, const int32_t* lens, int B, int H, int page_size,
+                   int max_pages, int num_pages, float scale, float* out, float* lse,
+                   int n_threads) {
+  return mla_partial("wh_mla_partial", q_nope, q_pe, c_pages, c_stride, pe_pages, pe_stride,
+                     page_table, lens, B, H, page_size, max_pages, num_pages, scale, out, lse,
+                     n_threads);
+}
+
+int wh_mla_partial_bf16(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
+                        int c_stride, const uint16_t* pe_pages, int pe_stride,
+                        const int32_t* page_table, const int32_t* lens, int B, int H,
+                        int page_size, int max_pages, int num_pages, float scale,
+                        uint16_t* out, float* lse, int n_threads) {
+  return mla_partial("wh_mla_partial_bf16", q_nope, q_pe, c_pages, c_stride, pe_pages,
+                     pe_stride, page_table, lens, B, H, page_size, max_pages, num_pages, scale,
+                     out, lse, n_threads);
 }
 
 double wh_host_read_gbs(size_t bytes, int n_threads, int reps) {

@@ -17,6 +17,11 @@ __device__ __forceinline__ void load_b(const void* b_out, const void* aux0,
   if (FMT == WS_PARTIAL_LSE_F32) {
     lse_b = ((const float*)aux0)[row];
     o_b = ((const float4*)((const float*)b_out + (size_t)row * Dv))[c];
+  } else if (FMT == WS_PARTIAL_LSE_BF16) {
+    lse_b = ((const float*)aux0)[row];
+    const uint2 raw = ((const uint2*)((const uint16_t*)b_out + (size_t)row * Dv))[c];
+    o_b = make_float4(bf16_to_f32(raw.x & 0xffffu), bf16_to_f32(raw.x >> 16),
+                      bf16_to_f32(raw.y & 0xffffu), bf16_to_f32(raw.y >> 16));
   } else if (FMT == WS_TRIPLE_UNNORM_F32 || FMT == WS_TRIPLE_NORM_F32) {
     const float m = ((const float*)aux0)[row];
     const float s = ((const float*)aux1)[row];
@@ -411,6 +416,14 @@ int merge_split_pieces(const int32_t* len, int len_add, int B, int R, int heads,
   return WS_OK;
 }
 
+// The host-partial formats: whether a format is known, and whether it needs
+// b_aux1 (the triples' sum).
+static bool fmt_known(int f) {
+  return f == WS_PARTIAL_LSE_F32 || f == WS_TRIPLE_UNNORM_F32 || f == WS_TRIPLE_NORM_BF16 ||
+         f == WS_TRIPLE_NORM_F32 || f == WS_PARTIAL_LSE_BF16;
+}
+static bool fmt_has_sum(int f) { return f != WS_PARTIAL_LSE_F32 && f != WS_PARTIAL_LSE_BF16; }
+
 }  // namespace ws
 
 using namespace ws;
@@ -435,10 +448,9 @@ extern "C" int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, i
     return set_error(WS_EINVAL, "ws_merge_split: bad sizes");
   const int Bp = B * ng;      // plan sequences
   heads /= ng;                // heads per plan row
-  if (b_out && (!b_aux0 || (fmt_b != WS_PARTIAL_LSE_F32 && !b_aux1)))
+  if (b_out && (!b_aux0 || (fmt_has_sum(fmt_b) && !b_aux1)))
     return set_error(WS_EINVAL, "ws_merge_split: host partial without its lse / max / sum");
-  if (b_out && fmt_b != WS_PARTIAL_LSE_F32 && fmt_b != WS_TRIPLE_UNNORM_F32 &&
-      fmt_b != WS_TRIPLE_NORM_BF16 && fmt_b != WS_TRIPLE_NORM_F32)
+  if (b_out && !fmt_known(fmt_b))
     return set_error(WS_EINVAL, "ws_merge_split: unknown format %d", fmt_b);
   if (n_workgroups > kReduceMaxWeights)
     return set_error(WS_EINVAL, "ws_merge_split: %d workgroups exceed %d", n_workgroups,
@@ -491,6 +503,9 @@ extern "C" int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, i
       case WS_TRIPLE_NORM_BF16:
         hipLaunchKernelGGL(merge_split_kernel<WS_TRIPLE_NORM_BF16>, grid, block, 0, s, prm);
         break;
+      case WS_PARTIAL_LSE_BF16:
+        hipLaunchKernelGGL(merge_split_kernel<WS_PARTIAL_LSE_BF16>, grid, block, 0, s, prm);
+        break;
       default:
         hipLaunchKernelGGL(merge_split_kernel<WS_TRIPLE_NORM_F32>, grid, block, 0, s, prm);
         break;
@@ -506,7 +521,9 @@ extern "C" int ws_lse_merge(const float* out_g, const float* lse_g,
                             void* stream) {
   if (!out_g || !lse_g || !b_out || !b_aux0)
     return set_error(WS_EINVAL, "ws_lse_merge: null input pointer");
-  if (fmt_b != WS_PARTIAL_LSE_F32 && !b_aux1)
+  if (!fmt_known(fmt_b))
+    return set_error(WS_EINVAL, "ws_lse_merge: unknown format %d", fmt_b);
+  if (fmt_has_sum(fmt_b) && !b_aux1)
     return set_error(WS_EINVAL, "ws_lse_merge: triple format needs b_aux1 (sum)");
   if (rows < 0 || Dv <= 0 || Dv % 4 || Dv > 512)
     return set_error(WS_EINVAL, "ws_lse_merge: bad sizes rows=%d Dv=%d", rows, Dv);
@@ -527,6 +544,7 @@ extern "C" int ws_lse_merge(const float* out_g, const float* lse_g,
     WS_MERGE_CASE(WS_TRIPLE_UNNORM_F32)
     WS_MERGE_CASE(WS_TRIPLE_NORM_BF16)
     WS_MERGE_CASE(WS_TRIPLE_NORM_F32)
+    WS_MERGE_CASE(WS_PARTIAL_LSE_BF16)
 #undef WS_MERGE_CASE
     default:
       return set_error(WS_EINVAL, "ws_lse_merge: unknown format %d", fmt_b);
@@ -550,10 +568,9 @@ extern "C" int ws_mla_merge_split_uv(const int32_t* gpu_len, int B, int heads,
                      heads, Dout);
   const int ng = heads / 16;
   const int Bp = B * ng;  // plan sequences (sequence, 16-head group)
-  if (b_out && (!b_aux0 || (fmt_b != WS_PARTIAL_LSE_F32 && !b_aux1)))
+  if (b_out && (!b_aux0 || (fmt_has_sum(fmt_b) && !b_aux1)))
     return set_error(WS_EINVAL, "ws_mla_merge_split_uv: host partial without its lse / max / sum");
-  if (b_out && fmt_b != WS_PARTIAL_LSE_F32 && fmt_b != WS_TRIPLE_UNNORM_F32 &&
-      fmt_b != WS_TRIPLE_NORM_BF16 && fmt_b != WS_TRIPLE_NORM_F32)
+  if (b_out && !fmt_known(fmt_b))
     return set_error(WS_EINVAL, "ws_mla_merge_split_uv: unknown format %d", fmt_b);
   if (n_workgroups > kReduceMaxWeights)
     return set_error(WS_EINVAL, "ws_mla_merge_split_uv: %d workgroups exceed %d", n_workgroups,
@@ -605,6 +622,10 @@ extern "C" int ws_mla_merge_split_uv(const int32_t* gpu_len, int B, int heads,
         break;
       case WS_TRIPLE_NORM_BF16:
         hipLaunchKernelGGL(merge_split_uv_kernel<WS_TRIPLE_NORM_BF16>, grid, block, 0, s, prm,
+                           w_uv, Dout, out_v);
+        break;
+      case WS_PARTIAL_LSE_BF16:
+        hipLaunchKernelGGL(merge_split_uv_kernel<WS_PARTIAL_LSE_BF16>, grid, block, 0, s, prm,
                            w_uv, Dout, out_v);
         break;
       default:

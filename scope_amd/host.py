@@ -17,7 +17,8 @@ take the reference's dense host arrays (one page per sequence):
   MLA  q_nope [B*16, 512], q_pe [B*16, 64] bf16; latent_pages
        [num_pages, page_size, 576] bf16 (dense: c [B, cap, 512], pe [B, cap, 64])
   page_table [B, max_pages] int32, lens [B] int32 host tokens
-  out  fp32 [B, Hq, D] / [B*16, 512]; lse fp32 [B, Hq] / [B*16]
+  out  fp32 (or bf16: the *_bf16 entry points) [B, Hq, D] / [B*16, 512];
+       lse fp32 [B, Hq] / [B*16]
 There is no fallback: a missing library or a CPU without AVX-512 BF16 raises.
 """
 from __future__ import annotations
@@ -32,8 +33,8 @@ LIB_PATH = os.path.join(_HERE, "lib", "libwshost.so")
 
 # Entry points declared in include/wshost.h.
 EXPORTS = ("wh_last_error", "wh_version", "wh_isa_supported", "wh_gqa_partial",
-           "wh_attn_partial", "wh_host_read_gbs",
-           "wh_mla_partial")
+           "wh_gqa_partial_bf16", "wh_attn_partial", "wh_host_read_gbs",
+           "wh_mla_partial", "wh_mla_partial_bf16")
 
 MLA_HEADS = 16
 MLA_C = 512
@@ -69,9 +70,13 @@ def lib() -> ctypes.CDLL:
         L.wh_attn_partial.argtypes = [vp, vp, vp, vp, vp] + [i32] * 8 + [f32, vp, vp, i32]
         L.wh_host_read_gbs.restype = ctypes.c_double
         L.wh_host_read_gbs.argtypes = [ctypes.c_size_t, i32, i32]
+        L.wh_gqa_partial_bf16.restype = i32
+        L.wh_gqa_partial_bf16.argtypes = L.wh_gqa_partial.argtypes
         L.wh_mla_partial.restype = i32
         L.wh_mla_partial.argtypes = [vp, vp, vp, i32, vp, i32, vp, vp] + [i32] * 5 + [f32, vp,
                                                                                      vp, i32]
+        L.wh_mla_partial_bf16.restype = i32
+        L.wh_mla_partial_bf16.argtypes = L.wh_mla_partial.argtypes
         _lib = L
     return _lib
 
@@ -120,12 +125,16 @@ def _table(page_table, B):
     return page_table.contiguous()
 
 
-def _outputs(out, lse, out_shape, lse_shape):
+def _outputs(out, lse, out_shape, lse_shape, out_dtype=torch.float32):
+    """The output buffers: out fp32, or bf16 (the *_bf16 entry points), as
+    given or allocated in out_dtype; lse fp32."""
     if out is None:
-        out = torch.empty(out_shape, dtype=torch.float32)
+        out = torch.empty(out_shape, dtype=out_dtype)
     if lse is None:
         lse = torch.empty(lse_shape, dtype=torch.float32)
-    _cpu(out, torch.float32, "out")
+    if out.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"out must be float32 or bfloat16 (got {out.dtype})")
+    _cpu(out, out.dtype, "out")
     _cpu(lse, torch.float32, "lse")
     if tuple(out.shape) != tuple(out_shape) or tuple(lse.shape) != tuple(lse_shape):
         raise ValueError(f"out/lse must be {tuple(out_shape)} / {tuple(lse_shape)}")
@@ -152,9 +161,11 @@ class Prepared:
 
 def gqa_partial(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, page_table,
                 lens, scale: float, threads: int = 0, out: torch.Tensor | None = None,
-                lse: torch.Tensor | None = None, prepare: bool = False):
-    """(out fp32 [B, Hq, D], lse fp32 [B, Hq]) over paged host KV pools
-    k_pages / v_pages [num_pages, Hkv, page_size, D] (the GPU pool layout).
+                lse: torch.Tensor | None = None, prepare: bool = False,
+                out_dtype=torch.float32):
+    """(out [B, Hq, D], lse fp32 [B, Hq]) over paged host KV pools
+    k_pages / v_pages [num_pages, Hkv, page_size, D] (the GPU pool layout);
+    out fp32, or bf16 (wh_gqa_partial_bf16) when out / out_dtype is bf16.
     prepare=True returns a Prepared call instead of running it."""
     B, Hq, D = q.shape
     _cpu(q, torch.bfloat16, "q")
@@ -166,8 +177,9 @@ def gqa_partial(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, p
     num_pages, Hkv, ps, _ = k_pages.shape
     table = _table(page_table, B)
     lens = _lens(lens, B)
-    out, lse = _outputs(out, lse, (B, Hq, D), (B, Hq))
-    call = Prepared(lib().wh_gqa_partial,
+    out, lse = _outputs(out, lse, (B, Hq, D), (B, Hq), out_dtype)
+    fn = lib().wh_gqa_partial_bf16 if out.dtype == torch.bfloat16 else lib().wh_gqa_partial
+    call = Prepared(fn,
                     (_p(q), _p(k_pages), _p(v_pages), _p(table), _p(lens), B, Hq, Hkv, D, ps,
                      table.shape[1], num_pages, ctypes.c_float(scale), _p(out), _p(lse),
                      int(threads)),
@@ -198,6 +210,8 @@ def attn_partial(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, 
     table = _table(page_table, B)
     lens = _lens(lens, B)
     out, lse = _outputs(out, lse, (B, Hq, Dv), (B, Hq))
+    if out.dtype != torch.float32:
+        raise TypeError("attn_partial writes a float32 out")
     _check(lib().wh_attn_partial(_p(q), _p(k_pages), _p(v_pages), _p(table), _p(lens), B, Hq,
                                  Hkv, Dk, Dv, ps, table.shape[1], num_pages,
                                  ctypes.c_float(scale), _p(out), _p(lse), int(threads)))
@@ -221,10 +235,11 @@ def gqa_partial_dense(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens, s
 
 def mla_partial(q_nope: torch.Tensor, q_pe: torch.Tensor, latent_pages: torch.Tensor,
                 page_table, lens, scale: float, threads: int = 0, out=None, lse=None,
-                prepare: bool = False):
-    """(out fp32 [B*16, 512], lse fp32 [B*16]) over a paged host latent pool
+                prepare: bool = False, out_dtype=torch.float32):
+    """(out [B*H, 512], lse fp32 [B*H]) over a paged host latent pool
     latent_pages [num_pages, page_size, 576] (the GPU pool layout: 512 latent
-    then 64 rope per token).  prepare=True returns a Prepared call."""
+    then 64 rope per token); out fp32, or bf16 (wh_mla_partial_bf16) when
+    out / out_dtype is bf16.  prepare=True returns a Prepared call."""
     _cpu(latent_pages, torch.bfloat16, "latent_pages")
     if latent_pages.dim() != 3 or latent_pages.shape[2] != MLA_C + MLA_PE:
         raise ValueError(f"latent_pages must be [num_pages, page_size, 576], got "
@@ -232,7 +247,7 @@ def mla_partial(q_nope: torch.Tensor, q_pe: torch.Tensor, latent_pages: torch.Te
     num_pages, ps, W = latent_pages.shape
     pe_view = latent_pages.view(-1)[MLA_C:]
     return _mla_call(q_nope, q_pe, latent_pages, W, pe_view, W, page_table, lens, ps,
-                     num_pages, scale, threads, out, lse, prepare)
+                     num_pages, scale, threads, out, lse, prepare, out_dtype)
 
 
 def mla_partial_dense(q_nope: torch.Tensor, q_pe: torch.Tensor, c: torch.Tensor,
@@ -253,7 +268,7 @@ def mla_partial_dense(q_nope: torch.Tensor, q_pe: torch.Tensor, c: torch.Tensor,
 
 
 def _mla_call(q_nope, q_pe, c, c_stride, pe, pe_stride, page_table, lens, page_size,
-              num_pages, scale, threads, out, lse, prepare=False):
+              num_pages, scale, threads, out, lse, prepare=False, out_dtype=torch.float32):
     _cpu(q_nope, torch.bfloat16, "q_nope")
     _cpu(q_pe, torch.bfloat16, "q_pe")
     rows = q_nope.shape[0]
@@ -268,8 +283,9 @@ def _mla_call(q_nope, q_pe, c, c_stride, pe, pe_stride, page_table, lens, page_s
     H = rows // B
     table = _table(page_table, B)
     lens = _lens(lens, B)
-    out, lse = _outputs(out, lse, (rows, MLA_C), (rows,))
-    call = Prepared(lib().wh_mla_partial,
+    out, lse = _outputs(out, lse, (rows, MLA_C), (rows,), out_dtype)
+    fn = lib().wh_mla_partial_bf16 if out.dtype == torch.bfloat16 else lib().wh_mla_partial
+    call = Prepared(fn,
                     (_p(q_nope), _p(q_pe), _p(c), int(c_stride), _p(pe), int(pe_stride),
                      _p(table), _p(lens), B, H, int(page_size), table.shape[1], int(num_pages),
                      ctypes.c_float(scale), _p(out), _p(lse), int(threads)),

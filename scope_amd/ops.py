@@ -53,6 +53,7 @@ PARTIAL_LSE_F32 = 0
 TRIPLE_UNNORM_F32 = 1
 TRIPLE_NORM_BF16 = 2
 TRIPLE_NORM_F32 = 3
+PARTIAL_LSE_BF16 = 4
 
 MLA_LATENT = 576
 MLA_C = 512
@@ -770,9 +771,10 @@ def _host_operand(b, fmt, rows, Dv, dev):
     validated against rows x Dv."""
     b_out = b_aux0 = b_aux1 = None
     if b is not None:
-        if fmt == PARTIAL_LSE_F32:
+        if fmt in (PARTIAL_LSE_F32, PARTIAL_LSE_BF16):
             b_out, b_aux0 = b
-            _require_operand(b_out, "b.out", torch.float32, dev)
+            _require_operand(b_out, "b.out",
+                             torch.float32 if fmt == PARTIAL_LSE_F32 else torch.bfloat16, dev)
             _require_operand(b_aux0, "b.lse", torch.float32, dev)
         elif fmt in (TRIPLE_UNNORM_F32, TRIPLE_NORM_BF16, TRIPLE_NORM_F32):
             b_out, b_aux0, b_aux1 = b
@@ -850,6 +852,7 @@ def lse_merge(out_g, lse_g, b, fmt=PARTIAL_LSE_F32, out_dtype=torch.bfloat16,
       fmt TRIPLE_UNNORM_F32 b = (o unnormalised fp32, max fp32, sum fp32)
       fmt TRIPLE_NORM_BF16  b = (out bf16 normalised, max bf16, sum bf16)
       fmt TRIPLE_NORM_F32   b = (out fp32 normalised, max fp32, sum fp32)
+      fmt PARTIAL_LSE_BF16  b = (out bf16 normalised, lse fp32)
     Returns (merged out in out_dtype (bf16 or fp32), lse fp32 or None)."""
     dev = out_g.device
     _require(out_g, "out_g", torch.float32, dev)

@@ -374,14 +374,15 @@ class _PagedTwoSided:
                         time.perf_counter() - t0)
 
     def _merge(self, step, part, dev, w_uv=None, return_lse=False):
-        # the host partial stays in its pinned buffers: the merge reads it in
-        # place over the host link
+        # the host partial (bf16 out, fp32 lse) stays in its pinned buffers:
+        # the merge reads it in place over the host link
         b = part
+        fmt = ops.PARTIAL_LSE_BF16 if part is not None and part[0].dtype == torch.bfloat16 \
+            else ops.PARTIAL_LSE_F32
         if w_uv is not None:
-            out_v, _, lse = ops.merge_split_uv(step, w_uv, b, ops.PARTIAL_LSE_F32,
-                                               want_lse=return_lse)
+            out_v, _, lse = ops.merge_split_uv(step, w_uv, b, fmt, want_lse=return_lse)
             return (out_v, lse) if return_lse else out_v
-        out, lse = ops.merge_split(step, b, ops.PARTIAL_LSE_F32, want_lse=return_lse)
+        out, lse = ops.merge_split(step, b, fmt, want_lse=return_lse)
         return (out, lse) if return_lse else out
 
 
@@ -453,7 +454,7 @@ class PagedMlaCache(_PagedTwoSided):
             t0 = time.perf_counter()
             part = host.mla_partial(
                 qn_h, qp_h, self.host.data[0][layer], self.host.table_t, self.host.lens_t,
-                scale, host_threads, self._pinned("out", (rows, ops.MLA_C), torch.float32),
+                scale, host_threads, self._pinned("out", (rows, ops.MLA_C), torch.bfloat16),
                 self._pinned("lse", (rows,), torch.float32))
             host_s = time.perf_counter() - t0
         res = self._merge(step, part, dev, w_uv, return_lse)
@@ -530,7 +531,7 @@ class PagedKVCache(_PagedTwoSided):
             part = host.gqa_partial(
                 q_h, self.host.data[0][layer], self.host.data[1][layer], self.host.table_t,
                 self.host.lens_t, scale, host_threads,
-                self._pinned("out", (B, Hq, D), torch.float32),
+                self._pinned("out", (B, Hq, D), torch.bfloat16),
                 self._pinned("lse", (B, Hq), torch.float32))
             host_s = time.perf_counter() - t0
         out, lse = self._merge(step, part, dev, return_lse=True)

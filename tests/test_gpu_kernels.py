@@ -276,7 +276,8 @@ def test_split_reduce_merges_valid_splits():
 
 
 @pytest.mark.parametrize("fmt", [ops.PARTIAL_LSE_F32, ops.TRIPLE_UNNORM_F32,
-                                 ops.TRIPLE_NORM_BF16, ops.TRIPLE_NORM_F32])
+                                 ops.TRIPLE_NORM_BF16, ops.TRIPLE_NORM_F32,
+                                 ops.PARTIAL_LSE_BF16])
 @pytest.mark.parametrize("Dv", [128, 512])
 def test_lse_merge_formats(fmt, Dv):
     _say(f"lse_merge fmt={fmt} Dv={Dv}")
@@ -302,6 +303,12 @@ def test_lse_merge_formats(fmt, Dv):
     elif fmt == ops.TRIPLE_NORM_F32:
         b = tuple(torch.from_numpy(x).to(DEV) for x in (ob, mb, sb))
         ob_n, lb_n = O.triple_to_partial(ob, mb, sb, normalized=True)
+    elif fmt == ops.PARTIAL_LSE_BF16:  # bf16 out, fp32 lse
+        lb = np.where(sb > 0, mb + np.log(np.where(sb > 0, sb, 1)), -np.inf).astype(np.float32)
+        ob16 = torch.from_numpy(np.where(sb[:, None] > 0, ob, 0).astype(np.float32)).to(
+            torch.bfloat16)
+        b = (ob16.to(DEV), torch.from_numpy(lb).to(DEV))
+        ob_n, lb_n = ob16.float().numpy(), lb
     else:
         ob16, mb16, sb16 = (torch.from_numpy(x).to(torch.bfloat16) for x in (ob, mb, sb))
         b = tuple(x.to(DEV) for x in (ob16, mb16, sb16))

@@ -44,7 +44,8 @@ def test_copy_rejects_bad_arguments():
         ops.copy_(a[4:36], a[0:32])
 
 
-@pytest.mark.parametrize("fmt", [ops.PARTIAL_LSE_F32, ops.TRIPLE_NORM_BF16])
+@pytest.mark.parametrize("fmt", [ops.PARTIAL_LSE_F32, ops.TRIPLE_NORM_BF16,
+                                 ops.PARTIAL_LSE_BF16])
 def test_merges_read_pinned_host_operands_in_place(fmt):
     _say(f"lse_merge with a pinned host operand fmt={fmt}")
     rows, Dv = 300, 128
@@ -53,8 +54,9 @@ def test_merges_read_pinned_host_operands_in_place(fmt):
     lse_g = (torch.randn(rows, generator=g) + 3).to(DEV)
     dt = torch.float32 if fmt == ops.PARTIAL_LSE_F32 else torch.bfloat16
     hb = [torch.empty((rows, Dv), dtype=dt, pin_memory=True),
-          torch.empty(rows, dtype=dt, pin_memory=True)]
-    if fmt != ops.PARTIAL_LSE_F32:
+          torch.empty(rows, dtype=torch.float32 if fmt == ops.PARTIAL_LSE_BF16 else dt,
+                      pin_memory=True)]
+    if fmt == ops.TRIPLE_NORM_BF16:
         hb.append(torch.empty(rows, dtype=dt, pin_memory=True))
     for rep in range(4):  # the host rewrites the same pinned buffers each call
         hb[0].copy_(torch.randn((rows, Dv), generator=g))

@@ -351,3 +351,50 @@ def test_mla_partial_any_multiple_of_16_heads(H, lens, threads):
         assert_close(lse[h].numpy(), lw, LSE_ATOL, LSE_RTOL, f"H={H} lse b={b}")
     with pytest.raises(ValueError, match="multiple"):
         host.mla_partial_dense(qn[:B * 24], qp[:B * 24], c, pe, lens, scale, threads)
+
+
+def _bf16_rne_np(x):
+    """float32 array -> its bf16 bit patterns, round to nearest even (the
+    rounding torch's .to(torch.bfloat16) also uses)."""
+    return bits(torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16))
+
+
+@needs_isa
+@pytest.mark.parametrize("threads", [1, 5])
+def test_bf16_outputs_are_the_fp32_outputs_rounded(threads):
+    """wh_gqa_partial_bf16 / wh_mla_partial_bf16 compute exactly what the fp32
+    entry points do and round out to bf16 (nearest even); lse is identical."""
+    rng = np.random.default_rng(40 + threads)
+    ps = 64
+    lens = [ps * 3 + 5, 0, 1, 200]
+    B = len(lens)
+    table, num_pages = _paged(rng, lens, ps)
+    Hkv, G, D = 2, 4, 128
+    q = bf16_randn((B, Hkv * G, D), 41)
+    kp = bf16_randn((num_pages, Hkv, ps, D), 42)
+    vp = bf16_randn((num_pages, Hkv, ps, D), 43)
+    o32, l32 = host.gqa_partial(q, kp, vp, table, lens, D ** -0.5, threads)
+    o16, l16 = host.gqa_partial(q, kp, vp, table, lens, D ** -0.5, threads,
+                                out_dtype=torch.bfloat16)
+    assert o16.dtype == torch.bfloat16
+    assert np.array_equal(bits(o16), _bf16_rne_np(o32.numpy()))
+    assert torch.equal(l16, l32)
+    qn = bf16_randn((B * 32, 512), 44, 0.5)  # 32 heads: two 16-head groups
+    qp = bf16_randn((B * 32, 64), 45, 0.5)
+    pool = bf16_randn((num_pages, ps, 576), 46, 0.5)
+    m32, n32 = host.mla_partial(qn, qp, pool, table, lens, 192 ** -0.5, threads)
+    out = torch.empty((B * 32, 512), dtype=torch.bfloat16)
+    m16, n16 = host.mla_partial(qn, qp, pool, table, lens, 192 ** -0.5, threads, out=out)
+    assert m16.data_ptr() == out.data_ptr()
+    assert np.array_equal(bits(m16), _bf16_rne_np(m32.numpy()))
+    assert torch.equal(n16, n32)
+
+
+@needs_isa
+def test_fp32_only_entry_rejects_bf16_out():
+    q = bf16_randn((1, 16, 192), 50)
+    kp = bf16_randn((1, 16, 64, 192), 51)
+    vp = bf16_randn((1, 16, 64, 128), 52)
+    with pytest.raises(TypeError, match="float32"):
+        host.attn_partial(q, kp, vp, torch.zeros((1, 1), dtype=torch.int32), [10], 0.1,
+                          out=torch.empty((1, 16, 128), dtype=torch.bfloat16))
