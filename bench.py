@@ -411,7 +411,9 @@ def mla_step_bench(*, B, H, lens, share, steps, warmup, seed, dev, label, wg=0):
         "partial_gbs": round(kernel_bytes / part_us / 1e3, 1),
         "partial_frac": round(kernel_bytes / part_us / 1e3 / HBM_PEAK_GBS, 4),
         "partial_tflops": round(flops / part_us / 1e6, 2),
-        "mfma_frac_bf16_dense": round(flops / part_us / 1e6 / 2500.0, 4),
+        # algorithmic flops / event time against the 2.5 PFLOP/s dense bf16
+        # peak; the counter-based figures are in "counters" when committed
+        "flops_frac_bf16_dense": round(flops / part_us / 1e6 / 2500.0, 4),
         "partial_bytes": int(kernel_bytes),
         "partial_flops": int(flops),
         "step_bytes": int(step_bytes),
@@ -982,6 +984,29 @@ EXTRA_WORKLOADS = ("mla32k",)
 HEAD_KERNEL = "ws::gqa_decode_kernel<4, 128, true>"
 
 
+MLA_KERNEL = "ws::mla_decode_kernel<true>"
+
+
+def committed_counters(workload_key, kernel):
+    """The committed rocprofv3 counter summary of a workload's kernel from
+    profiles/traffic.json (HBM traffic over algorithmic bytes, MFMA
+    utilisation, LDS bank-conflict share), or None when none is committed for
+    this kernel."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            ent = json.load(f).get(workload_key)
+    except (OSError, ValueError):
+        return None
+    if ent is None or ent.get("kernel") != kernel:
+        return None
+    keep = ("traffic_over_algorithmic", "traffic_bytes_per_launch", "mfma_util",
+            "mfma_busy_cycles_per_dispatch", "lds_bank_conflict_frac", "kernel_trace_mean_us")
+    out = {k: ent[k] for k in keep if k in ent}
+    out["source"] = f"profiles/traffic.json[{workload_key}] ({kernel})"
+    return out
+
+
 def committed_traffic(workload_key, kernel=HEAD_KERNEL):
     """HBM bytes per launch of the GQA partial kernel from profiles/, if a
     FETCH_SIZE/WRITE_SIZE summary for this workload and this kernel is
@@ -1133,6 +1158,7 @@ def main():
         mla = mla_step_bench(B=8, H=16, lens=[16384] * 8, share=0.5, steps=args.steps,
                              warmup=args.warmup, seed=args.seed + 3, dev=dev,
                              label="dsv2lite_mla_b8_L16384")
+        mla["counters"] = committed_counters("dsv2lite_mla_b8_L16384_r0.5", MLA_KERNEL)
         extra["mla"] = mla
         log(f"mla: {mla['us_per_layer']} us/layer, partial {mla['partial_us']} us = "
             f"{mla['partial_gbs']} GB/s, {mla['partial_tflops']} TFLOP/s")
@@ -1140,6 +1166,7 @@ def main():
         res = mla_step_bench(B=8, H=16, lens=[32768] * 8, share=1.0,
                              steps=max(10, args.steps // 2), warmup=args.warmup,
                              seed=args.seed + 7 + 32768, dev=dev, label="dsv2lite_mla_b8_L32768")
+        res["counters"] = committed_counters("dsv2lite_mla_b8_L32768_r1", MLA_KERNEL)
         extra["mla32k"] = res
         log(f"mla B8 L=32768: {res['us_per_layer']} us/layer, partial {res['partial_us']} us "
             f"= {res['partial_gbs']} GB/s")
@@ -1149,6 +1176,8 @@ def main():
             res = mla_step_bench(B=8, H=16, lens=[Lm] * 8, share=1.0,
                                  steps=max(10, args.steps // 2), warmup=args.warmup,
                                  seed=args.seed + 7 + Lm, dev=dev, label=f"dsv2lite_mla_b8_L{Lm}")
+            if Lm == 32768:
+                res["counters"] = committed_counters("dsv2lite_mla_b8_L32768_r1", MLA_KERNEL)
             msweep.append(res)
             log(f"mla B8 L={Lm}: {res['us_per_layer']} us/layer, partial {res['partial_us']} us "
                 f"= {res['partial_gbs']} GB/s")
