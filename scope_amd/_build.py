@@ -107,6 +107,36 @@ def build_host(verbose: bool = False) -> str:
     return HOST_LIB
 
 
+# ---------------------------------------------------------------------------
+# Layer driver: scope_amd/lib/libwslayer.so, host code (hipcc, no kernels) over
+# the two libraries above, found next to it at run time.
+
+LAYER_LIB = os.path.join(LIBDIR, "libwslayer.so")
+
+
+def build_layer(verbose: bool = False) -> str:
+    """Compile the two-sided layer driver and link libwslayer.so against
+    libwsgpu.so and libwshost.so (build those first); returns its path."""
+    os.makedirs(OBJDIR, exist_ok=True)
+    obj = os.path.join(OBJDIR, "wl_layer.o")
+    cmd = [HIPCC, "-O3", "-std=c++17", "-fPIC", "-Wall", "-c",
+           os.path.join(CSRC, "wl_layer.cpp"), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for wl_layer.cpp:\n{r.stdout}\n{r.stderr}")
+    tmp = LAYER_LIB + ".tmp"
+    cmd = [HIPCC, "-shared", "-fPIC", obj, "-L", LIBDIR, "-lwsgpu", "-lwshost",
+           "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, LAYER_LIB)
+    if verbose:
+        print(f"built {LAYER_LIB}", file=sys.stderr)
+    return LAYER_LIB
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
     print(build_host(verbose=True))
+    print(build_layer(verbose=True))

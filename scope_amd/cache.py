@@ -92,6 +92,25 @@ class _PagedBase:
         self.page_table[b, have:need].copy_(
             torch.from_numpy(self.host_table[b, have:need].copy()), non_blocking=False)
 
+    def _reserve_next(self, layer: int, n: int) -> None:
+        """reserve() for every sequence of `layer` about to grow by n tokens,
+        touching only the sequences that need a new page."""
+        need = (self.lens[layer] + n + self.page_size - 1) // self.page_size
+        for b in np.nonzero(need > self._pages_held)[0]:
+            self.reserve(int(b), int(self.lens[layer, b]) + n)
+
+    def _partial_bufs(self, rows: int, Dv: int):
+        """The split step's (out fp32 [rows, Dv], lse fp32 [rows]) buffers,
+        reused step after step: like the workspace, they belong to the latest
+        split step (its merge runs before the next step on the stream, and the
+        workspace generation guard refuses an older step's merge)."""
+        bufs = getattr(self, "_pbufs", None)
+        if bufs is None or bufs[0].shape != (rows, Dv):
+            bufs = (torch.empty((rows, Dv), dtype=torch.float32, device=self.device),
+                    torch.empty((rows,), dtype=torch.float32, device=self.device))
+            self._pbufs = bufs
+        return bufs
+
     def reserve_all(self, n_tokens_per_seq) -> None:
         for b, n in enumerate(n_tokens_per_seq):
             self.reserve(b, int(n))
@@ -111,6 +130,11 @@ class _PagedBase:
     def _split_workspace(self, kind: int, rows_kv: int, heads: int, max_len: int,
                          n_workgroups: int) -> torch.Tensor:
         _, wsb = ops.decode_plan(kind, rows_kv, heads, max_len, n_workgroups)
+        return self._split_workspace_bytes(wsb)
+
+    def _split_workspace_bytes(self, wsb: int) -> torch.Tensor:
+        """The workspace for a split step of wsb bytes, under a new generation
+        (an older split step's merge is refused from now on)."""
         self._ws_gen = getattr(self, "_ws_gen", 0) + 1
         return self.workspace(wsb)
 
@@ -186,22 +210,54 @@ class GqaGpuPartition(_PagedBase):
         self.lens[layer] += 1
         return out
 
+    def check_step_inputs(self, q: torch.Tensor, k_new: torch.Tensor,
+                          v_new: torch.Tensor):
+        """The decode step's own inputs, checked (the pools, page table,
+        lengths and buffers are the partition's).  Returns contiguous
+        (k_new, v_new)."""
+        B, Hkv, D = self.batch, self.num_kv_heads, self.head_dim
+        k_new, v_new = k_new.contiguous(), v_new.contiguous()
+        dev = self.page_table.device  # with its index
+        for t, n in ((q, "q"), (k_new, "k_new"), (v_new, "v_new")):
+            if t.device != dev or t.dtype != torch.bfloat16:
+                raise ValueError(f"{n} must be bf16 on {dev}")
+        if q.dim() != 3 or q.shape[0] != B or q.shape[2] != D or q.shape[1] % Hkv or \
+                not q.is_contiguous():
+            raise ValueError(f"q must be a contiguous [{B}, Hq, {D}] with Hq a multiple of {Hkv}")
+        if k_new.shape != (B, Hkv, 1, D) or v_new.shape != k_new.shape:
+            raise ValueError(f"k_new/v_new must be [B, Hkv, 1, D] = {(B, Hkv, 1, D)}")
+        return k_new, v_new
+
+    def prepare_split(self, layer: int, Hq: int, n_workgroups: int = 0):
+        """Pages for the step's new token, and (max_len, n_splits, workspace,
+        out fp32 [B*Hq, D], lse fp32 [B*Hq]) of a split step of `layer` under
+        a new workspace generation."""
+        B, Hkv, D = self.batch, self.num_kv_heads, self.head_dim
+        self._reserve_next(layer, 1)
+        max_len = self.max_len(layer) + 1
+        nwg, wsb = ops.decode_plan(0, B * Hkv, Hq // Hkv, max_len, n_workgroups)
+        ws = self._split_workspace_bytes(wsb)
+        out, lse = self._partial_bufs(B * Hq, D)
+        return max_len, nwg, ws, out, lse
+
+    def advance(self, layer: int) -> None:
+        """Bookkeeping after a fused step of `layer` was launched: the device
+        lengths moved to the other array, one token more."""
+        self._flip(layer)
+        self.lens[layer] += 1
+
     def step_split(self, layer: int, q: torch.Tensor, k_new: torch.Tensor,
                    v_new: torch.Tensor, scale: float, n_workgroups=0) -> "ops.SplitStep":
         """step() with the combine of rows shared by several splits (one wave
         each) left to ops.merge_split, which does it in the same launch as the
         merge with the host partial.  Returns the ops.SplitStep to finish."""
-        for b in range(self.batch):
-            self.reserve(b, int(self.lens[layer, b]) + 1)
-        max_len = self.max_len(layer) + 1
-        G = q.shape[1] // self.num_kv_heads
-        ws = self._split_workspace(0, self.batch * self.num_kv_heads, G, max_len, n_workgroups)
-        st = ops.gqa_append_decode_split(
-            q, k_new.contiguous(), v_new.contiguous(), self.k[layer], self.v[layer],
-            self.page_table, self.len_dev(layer), self._len_next(layer), scale, max_len,
-            n_workgroups, ws)
-        self._flip(layer)
-        self.lens[layer] += 1
+        k_new, v_new = self.check_step_inputs(q, k_new, v_new)
+        B, Hq, D = q.shape
+        max_len, nwg, ws, out, lse = self.prepare_split(layer, Hq, n_workgroups)
+        st = ops._gqa_split_launch(q, k_new, v_new, self.k[layer], self.v[layer],
+                                   self.page_table, self.len_dev(layer), self._len_next(layer),
+                                   scale, max_len, nwg, out.view(B, Hq, D), lse.view(B, Hq), ws)
+        self.advance(layer)
         return self._own(st)
 
 
@@ -254,21 +310,55 @@ class MlaGpuPartition(_PagedBase):
         self.lens[layer] += 1
         return out
 
+    def check_step_inputs(self, q_nope: torch.Tensor, q_pe: torch.Tensor,
+                          c_new: torch.Tensor, pe_new: torch.Tensor) -> int:
+        """The decode step's own inputs, checked (the pool, page table, lengths
+        and buffers are the partition's).  Returns the head count H."""
+        B = self.batch
+        rows = q_nope.shape[0] if q_nope.dim() == 2 else -1
+        dev = self.page_table.device  # with its index
+        for t, n in ((q_nope, "q_nope"), (q_pe, "q_pe"), (c_new, "c_new"), (pe_new, "pe_new")):
+            if t.device != dev or t.dtype != torch.bfloat16:
+                raise ValueError(f"{n} must be bf16 on {dev}")
+        if rows <= 0 or rows % (16 * B) or q_nope.shape[1] != ops.MLA_C or \
+                q_pe.shape != (rows, ops.MLA_PE) or not q_nope.is_contiguous() or \
+                not q_pe.is_contiguous():
+            raise ValueError(f"q_nope / q_pe must be contiguous [B*H, 512] / [B*H, 64], "
+                             f"H a multiple of 16, B = {B}")
+        for t, n, w in ((c_new, "c_new", ops.MLA_C), (pe_new, "pe_new", ops.MLA_PE)):
+            if t.shape != (B, 1, w) or t.stride(2) != 1:
+                raise ValueError(f"{n} must be [B, 1, {w}] with unit last stride")
+        return rows // B
+
+    def prepare_split(self, layer: int, H: int, n_workgroups: int = 0):
+        """Pages for the step's new token, and (max_len, n_splits, workspace,
+        out fp32 [B*H, 512], lse fp32 [B*H]) of a split step of `layer` under
+        a new workspace generation."""
+        B = self.batch
+        self._reserve_next(layer, 1)
+        max_len = self.max_len(layer) + 1
+        nwg, wsb = ops.decode_plan(1, B, H, max_len, n_workgroups)
+        ws = self._split_workspace_bytes(wsb)
+        out, lse = self._partial_bufs(B * H, ops.MLA_C)
+        return max_len, nwg, ws, out, lse
+
+    def advance(self, layer: int) -> None:
+        """Bookkeeping after a fused step of `layer` was launched: the device
+        lengths moved to the other array, one token more."""
+        self._flip(layer)
+        self.lens[layer] += 1
+
     def step_split(self, layer: int, q_nope: torch.Tensor, q_pe: torch.Tensor,
                    c_new: torch.Tensor, pe_new: torch.Tensor, scale: float,
                    n_workgroups=0) -> "ops.SplitStep":
         """step() with the combine of sequences held by several workgroups left
         to ops.merge_split / ops.merge_split_uv.  Returns the ops.SplitStep."""
-        for b in range(self.batch):
-            self.reserve(b, int(self.lens[layer, b]) + 1)
-        max_len = self.max_len(layer) + 1
-        H = q_nope.shape[0] // self.batch
-        ws = self._split_workspace(1, self.batch, H, max_len, n_workgroups)
-        st = ops.mla_append_decode_split(
-            q_nope, q_pe, c_new, pe_new, self.latent[layer], self.page_table,
-            self.len_dev(layer), self._len_next(layer), scale, max_len, n_workgroups, ws)
-        self._flip(layer)
-        self.lens[layer] += 1
+        H = self.check_step_inputs(q_nope, q_pe, c_new, pe_new)
+        max_len, nwg, ws, out, lse = self.prepare_split(layer, H, n_workgroups)
+        st = ops._mla_split_launch(q_nope, q_pe, c_new, pe_new, self.latent[layer],
+                                   self.page_table, self.len_dev(layer), self._len_next(layer),
+                                   scale, max_len, nwg, out, lse, ws)
+        self.advance(layer)
         return self._own(st)
 
 

@@ -155,7 +155,9 @@ def _ptr(t):
 
 
 def _stream(device: torch.device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """The current HIP stream of `device` (the raw handle torch launches on)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(idx))
 
 
 def _require(t: torch.Tensor, name: str, dtype: torch.dtype, device=None,
@@ -188,12 +190,15 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     queued on this stream keeps its memory until it ran).  Each call writes
     the slots it reads back, so no initial contents are needed."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (idx, torch.cuda.current_stream(idx).cuda_stream)
+    key = (idx, torch._C._cuda_getCurrentRawStream(idx))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
+
+
+_plans: dict = {}
 
 
 def decode_plan(kind: int, rows_kv: int, heads: int, max_len: int,
@@ -203,9 +208,19 @@ def decode_plan(kind: int, rows_kv: int, heads: int, max_len: int,
     A split is one wave for GQA and one workgroup for MLA; the keyword keeps
     the name n_workgroups.  0 lets the library choose for the current
     device."""
+    # the answer depends on the arguments and the current device only (a
+    # decode loop asks the same question for every layer of a step)
+    key = (kind, rows_kv, heads, max_len, n_workgroups,
+           torch.cuda.current_device() if torch.cuda.is_initialized() else -1)
+    hit = _plans.get(key)
+    if hit is not None:
+        return hit
     n, wsb = ctypes.c_int(0), ctypes.c_size_t(0)
     _check(lib().ws_decode_plan(kind, rows_kv, heads, max_len, n_workgroups,
                                 ctypes.byref(n), ctypes.byref(wsb)), "ws_decode_plan")
+    if len(_plans) > 4096:
+        _plans.clear()
+    _plans[key] = (n.value, wsb.value)
     return n.value, wsb.value
 
 
@@ -674,11 +689,22 @@ def gqa_append_decode_split(q, k_new, v_new, k_pages, v_pages, page_table, len_i
         workspace = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
     elif workspace.numel() * workspace.element_size() < wsb:
         raise ValueError(f"workspace needs {wsb} bytes")
+    return _gqa_split_launch(q, k_new, v_new, k_pages, v_pages, page_table, len_in, len_out,
+                             scale, max_len, nwg, out, lse, workspace)
+
+
+def _gqa_split_launch(q, k_new, v_new, k_pages, v_pages, page_table, len_in, len_out, scale,
+                      max_len, nwg, out, lse, workspace) -> SplitStep:
+    """The ws_gqa_append_decode_split launch on arguments already checked
+    (gqa_append_decode_split, or a cache that owns the pools, page table,
+    lengths, partial buffers and workspace); returns the SplitStep."""
+    B, Hq, D = q.shape
+    P, Hkv, PS, _ = k_pages.shape
     _check(lib().ws_gqa_append_decode_split(
         _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
         _ptr(len_in), _ptr(len_out), B, Hq, Hkv, D, PS, page_table.shape[1], P,
         int(max_len), nwg, float(scale), _ptr(out), _ptr(lse), _ptr(workspace),
-        workspace.numel() * workspace.element_size(), _stream(dev)),
+        workspace.numel() * workspace.element_size(), _stream(k_pages.device)),
         "ws_gqa_append_decode_split")
     return SplitStep(len_out, B, Hkv, Hq // Hkv, D, PS * page_table.shape[1], nwg, out, lse,
                      workspace)
@@ -717,12 +743,24 @@ def mla_append_decode_split(q_nope, q_pe, c_new, pe_new, latent_pages, page_tabl
         workspace = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
     elif workspace.numel() * workspace.element_size() < wsb:
         raise ValueError(f"workspace needs {wsb} bytes")
+    return _mla_split_launch(q_nope, q_pe, c_new, pe_new, latent_pages, page_table, len_in,
+                             len_out, scale, max_len, nwg, out, lse, workspace)
+
+
+def _mla_split_launch(q_nope, q_pe, c_new, pe_new, latent_pages, page_table, len_in, len_out,
+                      scale, max_len, nwg, out, lse, workspace) -> SplitStep:
+    """The ws_mla_append_decode_split launch on arguments already checked
+    (mla_append_decode_split, or a cache that owns the pools, page table,
+    lengths, partial buffers and workspace); returns the SplitStep."""
+    B = page_table.shape[0]
+    P, PS, _ = latent_pages.shape
+    H = q_nope.shape[0] // B
     _check(lib().ws_mla_append_decode_split(
         _ptr(q_nope), _ptr(q_pe), _ptr(c_new), c_new.stride(0), _ptr(pe_new),
         pe_new.stride(0), _ptr(latent_pages), _ptr(page_table), _ptr(len_in),
         _ptr(len_out), B, H, PS, page_table.shape[1], P, int(max_len), nwg, float(scale),
         _ptr(out), _ptr(lse), _ptr(workspace), workspace.numel() * workspace.element_size(),
-        _stream(dev)), "ws_mla_append_decode_split")
+        _stream(latent_pages.device)), "ws_mla_append_decode_split")
     return SplitStep(len_out, B, 1, H, MLA_C, PS * page_table.shape[1], nwg, out, lse,
                      workspace)
 

@@ -15,11 +15,13 @@ h_b is always a multiple of the page size: a host page is full, and decode
 appends go to the GPU side only (the new token is at position L_b >= h_b), as
 in the reference's boundary split (system/deepseek.py:181-188).
 
-A decode step per layer: q to pinned host memory; the GPU split step
-(append + partial over the HBM pages); the native host partial over the host
-pages in the calling thread while the GPU runs; its (out, lse) to the GPU;
-ws_merge_split.  Lengths are the same in every layer between steps; migrate
-only then.
+A decode step per layer is one call of the native layer driver
+(scope_amd/layer.py, libwslayer.so), with the GIL released: q to pinned host
+memory by a copy kernel; the GPU split step (append + partial over the HBM
+pages); the native host partial over the host pages in the calling thread
+while the GPU runs (bf16 out, fp32 lse, pinned); the merge, which reads it in
+place (ws_merge_split, or ws_mla_merge_split_uv with the W_UV epilogue).
+Lengths are the same in every layer between steps; migrate only then.
 """
 from __future__ import annotations
 
@@ -28,7 +30,10 @@ import time
 import numpy as np
 import torch
 
-from . import host, ops
+from . import ops
+from .layer import WlError, WlGqaLayer, WlMlaLayer
+from .layer import lib as layer_lib
+from .layer import run as run_layer
 from .cache import GqaGpuPartition, MlaGpuPartition, PagePool
 from .partition import pages_for
 
@@ -318,20 +323,51 @@ class _PagedTwoSided:
             bufs[key] = t
         return t
 
-    def _to_host(self, *ts):
-        """The query tensors in pinned host buffers, copied by the library's
-        copy kernel on the current stream (no DMA set-up latency on the
-        layer's critical path), and an event after the copies."""
-        out = []
-        for i, t in enumerate(ts):
-            h = self._pinned(f"q{i}", t.shape, t.dtype)
-            ops.copy_(h, t.contiguous())
-            out.append(h)
-        ev = self.__dict__.get("_q_event")
-        if ev is None:
-            ev = self._q_event = torch.cuda.Event()
-        ev.record()
-        return out, ev
+    def _layer_args(self, layer: int, cls):
+        """The layer driver's argument structure of this cache (one, reused:
+        a call fills every field it reads)."""
+        a = self.__dict__.get("_wl_args")
+        if a is None or not isinstance(a, cls):
+            a = self._wl_args = cls()
+        a.ev_step_begin = a.ev_step_end = None
+        if self.controller is not None:
+            e0, e1 = self._timing[layer]
+            a.ev_step_begin, a.ev_step_end = e0.cuda_event, e1.cuda_event
+        return a
+
+    def _host_args(self, a, layer: int, rows: int, threads: int, q_bufs, out_shape) -> None:
+        """The host side of the driver's arguments: pinned query copies, the
+        host pools, page table and lengths, and the pinned bf16 / fp32 host
+        partial."""
+        for name, shape in q_bufs:
+            setattr(a, name, self._pinned(name, shape, torch.bfloat16).data_ptr())
+        data = self.host.data
+        if len(data) == 1:  # MLA: one latent pool
+            a.host_latent = data[0][layer].data_ptr()
+        else:  # GQA: K and V pools
+            a.host_k, a.host_v = data[0][layer].data_ptr(), data[1][layer].data_ptr()
+        a.host_table = self.host.table_t.data_ptr()
+        a.host_lens = self.host.lens_t.data_ptr()
+        a.host_page_size = self.page_size
+        a.host_max_pages = self.host.table.shape[1]
+        a.host_num_pages = self.host.num_pages
+        a.host_threads = int(threads)
+        a.out_h = self._pinned("out", out_shape, torch.bfloat16).data_ptr()
+        a.lse_h = self._pinned("lse", (rows,), torch.float32).data_ptr()
+
+    def _run_layer(self, layer: int, fn, a, dev) -> None:
+        """Runs the layer driver; the device lengths advanced as soon as the
+        split step was launched, so the host bookkeeping follows them even
+        when a later stage fails."""
+        try:
+            run_layer(fn, a, ops._stream(dev))
+        except WlError as e:
+            if e.stage >= 1:
+                self.gpu.advance(layer)
+            raise
+        self.gpu.advance(layer)
+        if self.controller is not None:
+            self._layer_done(layer, a.host_seconds)
 
     # -- online share control --------------------------------------------------
 
@@ -343,6 +379,9 @@ class _PagedTwoSided:
         self.controller = controller
         self._timing = [(torch.cuda.Event(enable_timing=True),
                          torch.cuda.Event(enable_timing=True)) for _ in range(self.num_layers)]
+        for e0, e1 in self._timing:  # create the events (the layer driver records them)
+            e0.record()
+            e1.record()
         self._layer_log = []
 
     def _layer_done(self, layer: int, host_s: float) -> None:
@@ -372,18 +411,6 @@ class _PagedTwoSided:
         pages = sum(abs(t - h) for t, h in zip(targets, host_now)) // self.page_size
         ctl.record_move(ctl.share_of(lens, host_now), ctl.share_of(lens, targets), pages,
                         time.perf_counter() - t0)
-
-    def _merge(self, step, part, dev, w_uv=None, return_lse=False):
-        # the host partial (bf16 out, fp32 lse) stays in its pinned buffers:
-        # the merge reads it in place over the host link
-        b = part
-        fmt = ops.PARTIAL_LSE_BF16 if part is not None and part[0].dtype == torch.bfloat16 \
-            else ops.PARTIAL_LSE_F32
-        if w_uv is not None:
-            out_v, _, lse = ops.merge_split_uv(step, w_uv, b, fmt, want_lse=return_lse)
-            return (out_v, lse) if return_lse else out_v
-        out, lse = ops.merge_split(step, b, fmt, want_lse=return_lse)
-        return (out, lse) if return_lse else out
 
 
 class PagedMlaCache(_PagedTwoSided):
@@ -436,31 +463,43 @@ class PagedMlaCache(_PagedTwoSided):
         W_UV epilogue in one launch), ready for o_proj.  With return_lse, a
         pair (that output, merged lse [B*16] fp32)."""
         g = self.gpu
+        H = g.check_step_inputs(q_nope, q_pe, c_new, pe_new)
+        B = self.batch
+        rows = B * H
         dev = q_nope.device
-        with_host = bool(self.host.lens.any())
-        if with_host:
-            (qn_h, qp_h), ev = self._to_host(q_nope, q_pe)
-        timing = self._timing[layer] if self.controller is not None else None
-        if timing:
-            timing[0].record()
-        step = g.step_split(layer, q_nope, q_pe, c_new, pe_new, scale, n_workgroups)
-        if timing:
-            timing[1].record()
-        part = None
-        host_s = 0.0
-        if with_host:
-            ev.synchronize()
-            rows = q_nope.shape[0]
-            t0 = time.perf_counter()
-            part = host.mla_partial(
-                qn_h, qp_h, self.host.data[0][layer], self.host.table_t, self.host.lens_t,
-                scale, host_threads, self._pinned("out", (rows, ops.MLA_C), torch.bfloat16),
-                self._pinned("lse", (rows,), torch.float32))
-            host_s = time.perf_counter() - t0
-        res = self._merge(step, part, dev, w_uv, return_lse)
-        if timing:
-            self._layer_done(layer, host_s)
-        return res
+        if w_uv is not None:
+            if w_uv.dtype != torch.bfloat16 or w_uv.device != dev or w_uv.dim() != 3 or \
+                    w_uv.shape[0] != H or w_uv.shape[2] != ops.MLA_C or \
+                    not w_uv.is_contiguous() or w_uv.shape[1] % 32 or w_uv.shape[1] > 512:
+                raise ValueError(f"w_uv must be a contiguous bf16 [{H}, Dout, 512] on {dev}, "
+                                 "Dout a multiple of 32 up to 512")
+        max_len, nwg, ws, out_g, lse_g = g.prepare_split(layer, H, n_workgroups)
+        a = self._layer_args(layer, WlMlaLayer)
+        a.q_nope, a.q_pe = q_nope.data_ptr(), q_pe.data_ptr()
+        a.c_new, a.c_stride = c_new.data_ptr(), c_new.stride(0)
+        a.pe_new, a.pe_stride = pe_new.data_ptr(), pe_new.stride(0)
+        a.latent_pages = g.latent[layer].data_ptr()
+        a.page_table = g.page_table.data_ptr()
+        a.len_in, a.len_out = g.len_dev(layer).data_ptr(), g._len_next(layer).data_ptr()
+        a.B, a.H, a.page_size = B, H, g.page_size
+        a.max_pages, a.num_pages = g.page_table.shape[1], g.num_pages
+        a.max_len, a.n_splits, a.scale = max_len, nwg, float(scale)
+        a.out_g, a.lse_g = out_g.data_ptr(), lse_g.data_ptr()
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        self._host_args(a, layer, rows, host_threads,
+                        q_bufs=(("q_nope_h", (rows, ops.MLA_C)), ("q_pe_h", (rows, ops.MLA_PE))),
+                        out_shape=(rows, ops.MLA_C))
+        lse_out = torch.empty((rows,), dtype=torch.float32, device=dev) if return_lse else None
+        a.lse_out = lse_out.data_ptr() if return_lse else None
+        if w_uv is None:
+            res = torch.empty((rows, ops.MLA_C), dtype=torch.bfloat16, device=dev)
+            a.out, a.w_uv, a.Dout, a.out_v = res.data_ptr(), None, 0, None
+        else:
+            Dout = w_uv.shape[1]
+            res = torch.empty((B, H * Dout), dtype=torch.bfloat16, device=dev)
+            a.out, a.w_uv, a.Dout, a.out_v = None, w_uv.data_ptr(), Dout, res.data_ptr()
+        self._run_layer(layer, layer_lib().wl_mla_layer, a, dev)
+        return (res, lse_out) if return_lse else res
 
 
 class PagedKVCache(_PagedTwoSided):
@@ -512,34 +551,27 @@ class PagedKVCache(_PagedTwoSided):
         Returns [B, Hq, D] bf16; with return_lse, a pair (that output,
         merged lse [B, Hq] fp32)."""
         g = self.gpu
+        k_new, v_new = g.check_step_inputs(q, k_new, v_new)
+        B, Hq, D = q.shape
         dev = q.device
-        with_host = bool(self.host.lens.any())
-        if with_host:
-            (q_h,), ev = self._to_host(q)
-        timing = self._timing[layer] if self.controller is not None else None
-        if timing:
-            timing[0].record()
-        step = g.step_split(layer, q, k_new, v_new, scale, n_workgroups)
-        if timing:
-            timing[1].record()
-        part = None
-        host_s = 0.0
-        if with_host:
-            ev.synchronize()
-            B, Hq, D = q.shape
-            t0 = time.perf_counter()
-            part = host.gqa_partial(
-                q_h, self.host.data[0][layer], self.host.data[1][layer], self.host.table_t,
-                self.host.lens_t, scale, host_threads,
-                self._pinned("out", (B, Hq, D), torch.bfloat16),
-                self._pinned("lse", (B, Hq), torch.float32))
-            host_s = time.perf_counter() - t0
-        out, lse = self._merge(step, part, dev, return_lse=True)
-        if timing:
-            self._layer_done(layer, host_s)
-        if return_lse:
-            return out.view(q.shape), lse.view(q.shape[:2])
-        return out.view(q.shape)
+        max_len, nwg, ws, out_g, lse_g = g.prepare_split(layer, Hq, n_workgroups)
+        a = self._layer_args(layer, WlGqaLayer)
+        a.q, a.k_new, a.v_new = q.data_ptr(), k_new.data_ptr(), v_new.data_ptr()
+        a.k_pages, a.v_pages = g.k[layer].data_ptr(), g.v[layer].data_ptr()
+        a.page_table = g.page_table.data_ptr()
+        a.len_in, a.len_out = g.len_dev(layer).data_ptr(), g._len_next(layer).data_ptr()
+        a.B, a.Hq, a.Hkv, a.D, a.page_size = B, Hq, g.num_kv_heads, D, g.page_size
+        a.max_pages, a.num_pages = g.page_table.shape[1], g.num_pages
+        a.max_len, a.n_splits, a.scale = max_len, nwg, float(scale)
+        a.out_g, a.lse_g = out_g.data_ptr(), lse_g.data_ptr()
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        self._host_args(a, layer, B * Hq, host_threads, q_bufs=(("q_h", (B, Hq, D)),),
+                        out_shape=(B, Hq, D))
+        res = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=dev)
+        lse_out = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
+        a.out, a.lse_out = res.data_ptr(), (lse_out.data_ptr() if return_lse else None)
+        self._run_layer(layer, layer_lib().wl_gqa_layer, a, dev)
+        return (res, lse_out) if return_lse else res
 
 
 def absorb_q(q_nope: torch.Tensor, w_uk: torch.Tensor) -> torch.Tensor:
