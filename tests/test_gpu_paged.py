@@ -122,3 +122,44 @@ def test_paged_mla_step_with_uv_epilogue_and_absorbed_query():
                                       full[None, :, 512:], scale)
         want = np.einsum("hk,hvk->hv", m_o, O.as_f64(bits(w_uv))).reshape(H * Dout)
         assert_close(got[b], want, OUT_ATOL, OUT_RTOL, f"out_v b={b}")
+
+
+def test_layer_driver_failure_after_the_step_keeps_lengths_consistent():
+    """A host-side failure after the split step was launched (here: a host
+    length past the host page table) raises with stage 1; the cache counts
+    the token the step appended, and the next step attends over it."""
+    from scope_amd.layer import WlError
+
+    B, H, layers = 2, 16, 1
+    lens = [300, 129]
+    hosts = [128, 64]
+    scale = 192 ** -0.5
+    cache = PagedMlaCache(layers, B, max_tokens=512, page_size=PS, device=DEV)
+    lat = [torch.cat([bf16_randn((L + 2, 512), 70 + b, 0.5), bf16_randn((L + 2, 64), 75 + b, 0.5)],
+                     dim=1) for b, L in enumerate(lens)]
+    for b, (L, h) in enumerate(zip(lens, hosts)):
+        cache.load(0, b, lat[b][:L, :512].contiguous(), lat[b][:L, 512:].contiguous(), h)
+    cap = cache.host.table.shape[1] * PS
+    good = int(cache.host.lens[1])
+    cache.host.lens[1] = cap + PS  # the host partial refuses it, after the GPU step
+    new = torch.stack([lat[b][lens[b]] for b in range(B)]).view(B, 1, 576).to(DEV)
+    qn = bf16_randn((B * H, 512), 80, 0.5).to(DEV)
+    qp = bf16_randn((B * H, 64), 81, 0.5).to(DEV)
+    with pytest.raises(WlError) as err:
+        cache.step(0, qn, qp, new[..., :512].contiguous(), new[..., 512:].contiguous(), scale,
+                   host_threads=2)
+    assert err.value.stage == 1
+    cache.host.lens[1] = good
+    torch.cuda.synchronize()
+    assert [cache.seq_len(b) for b in range(B)] == [L + 1 for L in lens]
+    new2 = torch.stack([lat[b][lens[b] + 1] for b in range(B)]).view(B, 1, 576).to(DEV)
+    out = cache.step(0, qn, qp, new2[..., :512].contiguous(), new2[..., 512:].contiguous(),
+                     scale, host_threads=2)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    for b in range(B):
+        full = bits(lat[b][:lens[b] + 2])
+        hh = slice(b * H, (b + 1) * H)
+        want, _ = O.mla_attention_fp64(bits(qn[hh]), bits(qp[hh]), full[None, :, :512],
+                                       full[None, :, 512:], scale)
+        assert_close(got[hh], want, OUT_ATOL, OUT_RTOL, f"b={b} after the failed step")
