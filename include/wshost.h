@@ -92,6 +92,18 @@ int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* 
                     int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
                     float* out, float* lse, int n_threads);
 
+/* wh_attn_partial over fp32 q and K / V pools (same shapes, float), fp32
+ * FMAs with fp32 probabilities.  (Dk, Dv): equal multiples of 16 up to 256,
+ * or (192, 128).
+ * Replaces the float32 path of fused_cpu_attn (kernel/cpu_attn.cpp:572-636,
+ * whose fp32 case returns the unnormalised (out, max, sum) triple) and
+ * fused_cpu_attn_fp32 (kernel/cpu_attn.cpp:817-848, normalised), returning
+ * (out, lse). */
+int wh_attn_partial_f32(const float* q, const float* k_pages, const float* v_pages,
+                        const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                        int Dk, int Dv, int page_size, int max_pages, int num_pages,
+                        float scale, float* out, float* lse, int n_threads);
+
 /* Absorbed-MLA host partial (H heads, a multiple of 16: 16 for
  * DeepSeek-V2-Lite, 128 for DeepSeek-V2; 512-wide latent + 64-wide rope key).
  * Replaces fused_cpu_attn_mla_compressed (kernel/cpu_attn.cpp:852-1022, nH =

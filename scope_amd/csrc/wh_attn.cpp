@@ -19,6 +19,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/wshost.h"
@@ -174,9 +175,9 @@ inline uint16_t to_out(float v, uint16_t*) {
 }
 
 // Final (out, lse) of H heads from a state; o_at(h, s) reads o in staging
-// order, out_row(h) is head h's output row (Dv values of OutT: fp32, or bf16
-// as uint16_t).
-template <class OutT, class OAt, class OutRow>
+// order (kStaged) or in column order, out_row(h) is head h's output row (Dv
+// values of OutT: fp32, or bf16 as uint16_t).
+template <class OutT, bool kStaged = true, class OAt, class OutRow>
 void write_final(const float* base, int H, int Dv, float* lse, OAt o_at, OutRow out_row) {
   for (int h = 0; h < H; ++h) {
     const float l = base[H + h];
@@ -187,7 +188,8 @@ void write_final(const float* base, int H, int Dv, float* lse, OAt o_at, OutRow 
       continue;
     }
     const float inv = 1.f / l;
-    for (int s = 0; s < Dv; ++s) dst[wh::stage_col(s)] = to_out(o_at(h, s) * inv, dst);
+    for (int s = 0; s < Dv; ++s)
+      dst[kStaged ? wh::stage_col(s) : s] = to_out(o_at(h, s) * inv, dst);
     lse[h] = (base[h] + std::log2(l)) * kLn2;
   }
 }
@@ -235,22 +237,25 @@ void for_pages(const int32_t* table_row, int page_size, int t0, int t1, F f) {
 
 namespace {
 
-template <class OutT>
-int attn_partial(const char* fn, const uint16_t* q, const uint16_t* k_pages,
-                 const uint16_t* v_pages, const int32_t* page_table, const int32_t* lens, int B,
-                 int Hq, int Hkv, int Dk, int D, int page_size, int max_pages, int num_pages,
-                 float scale, OutT* out, float* lse, int n_threads) {
+// InT: uint16_t (bf16 inputs, the AVX-512 BF16 kernels) or float (fp32
+// inputs, fp32 FMAs).
+template <class InT, class OutT>
+int attn_partial(const char* fn, const InT* q, const InT* k_pages, const InT* v_pages,
+                 const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv, int Dk,
+                 int D, int page_size, int max_pages, int num_pages, float scale, OutT* out,
+                 float* lse, int n_threads) {
+  constexpr bool kF32 = std::is_same_v<InT, float>;
   g_err[0] = '\0';
   if (!isa_ok()) return fail(WH_ENOTSUP, "%s: this CPU lacks AVX-512 F/BW/BF16", fn);
   if (B < 0 || Hkv < 1 || Hq < 1 || Hq % Hkv != 0)
     return fail(WH_EINVAL, "%s: bad shape B=%d Hq=%d Hkv=%d", fn, B, Hq, Hkv);
   const int G = Hq / Hkv;
   if (G > 16) return fail(WH_EINVAL, "%s: group size %d > 16", fn, G);
-  if (!wh::gqa_dims_supported(Dk, D))
+  if (kF32 ? !wh::gqa_f32_dims_supported(Dk, D) : !wh::gqa_dims_supported(Dk, D))
     return fail(WH_EINVAL,
-                "%s: head_dim Dk=%d Dv=%d unsupported (equal multiples of 32 in [32, 256], "
+                "%s: head_dim Dk=%d Dv=%d unsupported (equal multiples of %d in [%d, 256], "
                 "or 192 / 128)",
-                fn, Dk, D);
+                fn, Dk, D, kF32 ? 16 : 32, kF32 ? 16 : 32);
   if (B == 0) return WH_OK;
   if (!q || !k_pages || !v_pages || !page_table || !lens || !out || !lse)
     return fail(WH_EINVAL, "%s: null pointer", fn);
@@ -266,12 +271,16 @@ int attn_partial(const char* fn, const uint16_t* q, const uint16_t* k_pages,
     for_pages(page_table + (size_t)b * max_pages, page_size, t0, t1,
               [&](int pid, int a, int e) {
                 const size_t head = ((size_t)pid * Hkv + kvh) * page_size;  // first token
-                wh::gqa_attend(q + (size_t)r * G * Dk, k_pages + head * Dk, v_pages + head * D,
-                               G, Dk, D, a, e, sl2, s.m, s.l, s.o);
+                if constexpr (kF32)
+                  wh::gqa_attend_f32(q + (size_t)r * G * Dk, k_pages + head * Dk,
+                                     v_pages + head * D, G, Dk, D, a, e, sl2, s.m, s.l, s.o);
+                else
+                  wh::gqa_attend(q + (size_t)r * G * Dk, k_pages + head * Dk,
+                                 v_pages + head * D, G, Dk, D, a, e, sl2, s.m, s.l, s.o);
               });
   };
   auto fin = [&](int r, const float* st) {
-    write_final<OutT>(
+    write_final<OutT, !kF32>(
         st, G, D, lse + (size_t)r * G, [&](int h, int s) { return st[2 * G + h * D + s]; },
         [&](int h) { return out + ((size_t)r * G + h) * D; });
   };
@@ -378,6 +387,14 @@ int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* 
                     float* out, float* lse, int n_threads) {
   return attn_partial("wh_attn_partial", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv, Dk,
                       Dv, page_size, max_pages, num_pages, scale, out, lse, n_threads);
+}
+
+int wh_attn_partial_f32(const float* q, const float* k_pages, const float* v_pages,
+                        const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                        int Dk, int Dv, int page_size, int max_pages, int num_pages,
+                        float scale, float* out, float* lse, int n_threads) {
+  return attn_partial("wh_attn_partial_f32", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv,
+                      Dk, Dv, page_size, max_pages, num_pages, scale, out, lse, n_threads);
 }
 
 int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,

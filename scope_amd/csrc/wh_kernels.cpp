@@ -17,6 +17,8 @@
 //   (p_t, p_t+1) per head, broadcast (c_t[d], c_t+1[d])).
 // Probabilities enter PV rounded to bf16 (as on the GPU path); the running
 // sum l adds the fp32 probabilities.
+// GQA over fp32 inputs: the same blocks with fp32 FMAs (scores through the
+// same transpose-add tree), value rows read as they are, probabilities fp32.
 #include "wh_kernels.h"
 
 #include <immintrin.h>
@@ -208,6 +210,113 @@ void gqa_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G, 
     case 256: return gqa_attend_d<256, 256>(q, k, v, G, t0, t1, sl2, m, l, o);
     default: return;  // rejected by the caller
   }
+}
+
+// ---------------------------------------------------------------------------
+// GQA, fp32 inputs
+
+namespace {
+
+// Scores of the 16 fp32 tokens at k (token j at k + j*DK) against one head.
+template <int DK>
+inline __m512 gqa_scores16_f32(const float* qg, const float* k) {
+  __m512 acc[16];
+#pragma GCC unroll 16
+  for (int j = 0; j < 16; ++j) acc[j] = _mm512_setzero_ps();
+#pragma GCC unroll 16
+  for (int c = 0; c < DK / 16; ++c) {
+    const __m512 qv = _mm512_loadu_ps(qg + 16 * c);
+#pragma GCC unroll 16
+    for (int j = 0; j < 16; ++j)
+      acc[j] = _mm512_fmadd_ps(qv, _mm512_loadu_ps(k + j * DK + 16 * c), acc[j]);
+  }
+  return reduce16(acc);
+}
+
+// DK: key width, D: value width (both multiples of 16).  Per 32-token
+// block: the scores of all heads, then per head the online-softmax update
+// and o = o * corr + sum_t p_t v_t with fp32 FMAs.
+template <int DK, int D>
+void gqa_attend_f32_d(const float* q, const float* k, const float* v, int G, int t0, int t1,
+                      float sl2, float* m, float* l, float* o) {
+  constexpr int NZ = D / 16;  // zmm per value row
+  alignas(64) float sc[16][32];
+  alignas(64) float pt[32];
+  alignas(64) float tile[16 * DK];
+  const __m512 ninf = _mm512_set1_ps(-INFINITY);
+  const __m512 vsl2 = _mm512_set1_ps(sl2);
+  for (int tb = t0; tb < t1; tb += 32) {
+    const int n = t1 - tb < 32 ? t1 - tb : 32;
+    for (int half = 0; half < 2; ++half) {
+      const int valid = n - 16 * half;
+      if (valid <= 0) {
+        for (int g = 0; g < G; ++g) _mm512_store_ps(sc[g] + 16 * half, ninf);
+        continue;
+      }
+      const float* kb = k + (size_t)(tb + 16 * half) * DK;
+      if (valid < 16) {  // copy the tail into a zeroed tile: no read past the range
+        std::memset(tile, 0, sizeof(tile));
+        std::memcpy(tile, kb, sizeof(float) * valid * DK);
+        kb = tile;
+      }
+      const __mmask16 vm = valid < 16 ? (__mmask16)((1u << valid) - 1) : (__mmask16)0xFFFF;
+      for (int g = 0; g < G; ++g) {
+        const __m512 s = _mm512_mul_ps(gqa_scores16_f32<DK>(q + (size_t)g * DK, kb), vsl2);
+        _mm512_store_ps(sc[g] + 16 * half, _mm512_mask_blend_ps(vm, ninf, s));
+      }
+    }
+    const float* vb = v + (size_t)tb * D;
+    for (int g = 0; g < G; ++g) {
+      const __m512 s0 = _mm512_load_ps(sc[g]), s1 = _mm512_load_ps(sc[g] + 16);
+      const float mx = _mm512_reduce_max_ps(_mm512_max_ps(s0, s1));
+      const float mo = m[g];
+      const float mn = mo > mx ? mo : mx;
+      const float corr = std::exp2(mo - mn);  // 0 when the state is empty
+      const __m512 mnv = _mm512_set1_ps(mn);
+      const __m512 p0 = exp2v(_mm512_sub_ps(s0, mnv)), p1 = exp2v(_mm512_sub_ps(s1, mnv));
+      l[g] = l[g] * corr + _mm512_reduce_add_ps(_mm512_add_ps(p0, p1));
+      m[g] = mn;
+      _mm512_store_ps(pt, p0);
+      _mm512_store_ps(pt + 16, p1);
+      float* og = o + (size_t)g * D;
+      const __m512 cv = _mm512_set1_ps(corr);
+      __m512 acc[NZ];
+#pragma GCC unroll 16
+      for (int r = 0; r < NZ; ++r) acc[r] = _mm512_mul_ps(_mm512_loadu_ps(og + 16 * r), cv);
+      for (int t = 0; t < n; ++t) {
+        const __m512 pv = _mm512_set1_ps(pt[t]);
+        const float* vr = vb + (size_t)t * D;
+#pragma GCC unroll 16
+        for (int r = 0; r < NZ; ++r)
+          acc[r] = _mm512_fmadd_ps(pv, _mm512_loadu_ps(vr + 16 * r), acc[r]);
+      }
+#pragma GCC unroll 16
+      for (int r = 0; r < NZ; ++r) _mm512_storeu_ps(og + 16 * r, acc[r]);
+    }
+  }
+}
+
+}  // namespace
+
+bool gqa_f32_dims_supported(int Dk, int Dv) {
+  return (Dk == Dv && Dk >= 16 && Dk <= 256 && Dk % 16 == 0) || (Dk == 192 && Dv == 128);
+}
+
+void gqa_attend_f32(const float* q, const float* k, const float* v, int G, int Dk, int Dv,
+                    int t0, int t1, float sl2, float* m, float* l, float* o) {
+  if (Dk == 192 && Dv == 128)
+    return gqa_attend_f32_d<192, 128>(q, k, v, G, t0, t1, sl2, m, l, o);
+  if (Dk != Dv) return;  // rejected by the caller
+#define WH_F32_CASE(DD) \
+  case DD: return gqa_attend_f32_d<DD, DD>(q, k, v, G, t0, t1, sl2, m, l, o);
+  switch (Dk) {
+    WH_F32_CASE(16) WH_F32_CASE(32) WH_F32_CASE(48) WH_F32_CASE(64)
+    WH_F32_CASE(80) WH_F32_CASE(96) WH_F32_CASE(112) WH_F32_CASE(128)
+    WH_F32_CASE(144) WH_F32_CASE(160) WH_F32_CASE(176) WH_F32_CASE(192)
+    WH_F32_CASE(208) WH_F32_CASE(224) WH_F32_CASE(240) WH_F32_CASE(256)
+    default: return;  // rejected by the caller
+  }
+#undef WH_F32_CASE
 }
 
 // ---------------------------------------------------------------------------

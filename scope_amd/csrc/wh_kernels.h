@@ -36,6 +36,15 @@ bool gqa_dims_supported(int Dk, int Dv);
 void gqa_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G, int Dk,
                 int Dv, int t0, int t1, float scale_log2, float* m, float* l, float* o);
 
+// GQA over fp32 q / K / V (the float32 inputs the reference CPU kernel also
+// takes): the same layout as gqa_attend with floats; (Dk, Dv): Dk == Dv a
+// multiple of 16 up to 256, or (192, 128) (gqa_f32_dims_supported); G at
+// most 16.  o: G*Dv floats in natural column order (no staging); the
+// probabilities enter PV in fp32.
+bool gqa_f32_dims_supported(int Dk, int Dv);
+void gqa_attend_f32(const float* q, const float* k, const float* v, int G, int Dk, int Dv,
+                    int t0, int t1, float scale_log2, float* m, float* l, float* o);
+
 // MLA (absorbed, 16 heads): qt is the query in pair-transposed form
 // (mla_prepare_q); token t's latent is c + t*c_tok (512 bf16, also the value)
 // and pe + t*pe_tok (64 bf16).  m, l: 16 floats; o: 512*16 floats, slot-major

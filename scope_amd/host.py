@@ -33,7 +33,7 @@ LIB_PATH = os.path.join(_HERE, "lib", "libwshost.so")
 
 # Entry points declared in include/wshost.h.
 EXPORTS = ("wh_last_error", "wh_version", "wh_isa_supported", "wh_gqa_partial",
-           "wh_gqa_partial_bf16", "wh_attn_partial", "wh_host_read_gbs",
+           "wh_gqa_partial_bf16", "wh_attn_partial", "wh_attn_partial_f32", "wh_host_read_gbs",
            "wh_mla_partial", "wh_mla_partial_bf16")
 
 MLA_HEADS = 16
@@ -68,6 +68,8 @@ def lib() -> ctypes.CDLL:
                                      vp, vp, i32]
         L.wh_attn_partial.restype = i32
         L.wh_attn_partial.argtypes = [vp, vp, vp, vp, vp] + [i32] * 8 + [f32, vp, vp, i32]
+        L.wh_attn_partial_f32.restype = i32
+        L.wh_attn_partial_f32.argtypes = L.wh_attn_partial.argtypes
         L.wh_host_read_gbs.restype = ctypes.c_double
         L.wh_host_read_gbs.argtypes = [ctypes.c_size_t, i32, i32]
         L.wh_gqa_partial_bf16.restype = i32
@@ -196,11 +198,14 @@ def attn_partial(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, 
     """gqa_partial with separate key / value widths (wh_attn_partial):
     q [B, Hq, Dk], k_pages [num_pages, Hkv, page_size, Dk], v_pages
     [num_pages, Hkv, page_size, Dv] -> (out fp32 [B, Hq, Dv], lse fp32
-    [B, Hq]).  (Dk, Dv): equal, or (192, 128)."""
+    [B, Hq]).  (Dk, Dv): equal, or (192, 128).  bf16 inputs, or float32 ones
+    (wh_attn_partial_f32: fp32 FMAs and probabilities, widths multiples of
+    16)."""
     B, Hq, Dk = q.shape
-    _cpu(q, torch.bfloat16, "q")
-    _cpu(k_pages, torch.bfloat16, "k_pages")
-    _cpu(v_pages, torch.bfloat16, "v_pages")
+    dt = q.dtype if q.dtype in (torch.bfloat16, torch.float32) else torch.bfloat16
+    _cpu(q, dt, "q")
+    _cpu(k_pages, dt, "k_pages")
+    _cpu(v_pages, dt, "v_pages")
     if k_pages.dim() != 4 or v_pages.dim() != 4 or k_pages.shape[:3] != v_pages.shape[:3] \
             or k_pages.shape[3] != Dk:
         raise ValueError(f"pools must be [num_pages, Hkv, page_size, Dk / Dv], got "
@@ -212,9 +217,10 @@ def attn_partial(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, 
     out, lse = _outputs(out, lse, (B, Hq, Dv), (B, Hq))
     if out.dtype != torch.float32:
         raise TypeError("attn_partial writes a float32 out")
-    _check(lib().wh_attn_partial(_p(q), _p(k_pages), _p(v_pages), _p(table), _p(lens), B, Hq,
-                                 Hkv, Dk, Dv, ps, table.shape[1], num_pages,
-                                 ctypes.c_float(scale), _p(out), _p(lse), int(threads)))
+    fn = lib().wh_attn_partial_f32 if dt == torch.float32 else lib().wh_attn_partial
+    _check(fn(_p(q), _p(k_pages), _p(v_pages), _p(table), _p(lens), B, Hq, Hkv, Dk, Dv, ps,
+              table.shape[1], num_pages, ctypes.c_float(scale), _p(out), _p(lse),
+              int(threads)))
     return out, lse
 
 

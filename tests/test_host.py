@@ -320,6 +320,84 @@ def test_attn_partial_separate_key_value_widths(Hkv, G, Dk, Dv, page_size, threa
                          LSE_RTOL, f"lse vs C port b={b}")
 
 
+def _randn_f32(shape, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32)
+
+
+# fp32 inputs, fp32 arithmetic: within 1e-4 of the fp64 closed form
+F32_ATOL = F32_RTOL = 1e-4
+
+
+@needs_isa
+@pytest.mark.parametrize("Hkv,G,Dk,Dv,page_size,threads,lens", [
+    (8, 4, 128, 128, 64, 7, [200, 1, 0, 333]),    # Mixtral grouping, ragged, one empty
+    (2, 16, 256, 256, 32, 3, [65, 97]),
+    (3, 1, 16, 16, 32, 2, [40, 7, 0]),
+    (16, 1, 192, 128, 64, 5, [129, 64]),          # decompressed DeepSeek-V2 widths
+    (1, 3, 48, 48, 64, 1, [1000]),
+    (2, 2, 128, 128, 64, 4, [0, 0]),              # all empty: the merge identity
+])
+def test_attn_partial_fp32_inputs(Hkv, G, Dk, Dv, page_size, threads, lens):
+    """wh_attn_partial_f32 (fused_cpu_attn on float32 inputs,
+    kernel/cpu_attn.cpp:572-636, and fused_cpu_attn_fp32, :817-848) against the
+    fp64 closed form and the oracle's C restatement run on the same floats."""
+    from oracle import port
+    rng = np.random.default_rng(Dk + G)
+    B = len(lens)
+    table, num_pages = _paged(rng, lens, page_size)
+    q = _randn_f32((B, Hkv * G, Dk), 21)
+    kp = _randn_f32((num_pages, Hkv, page_size, Dk), 22)
+    vp = _randn_f32((num_pages, Hkv, page_size, Dv), 23)
+    scale = Dk ** -0.5
+    out, lse = host.attn_partial(q, kp, vp, table, lens, scale, threads)
+    assert out.dtype == torch.float32 and tuple(out.shape) == (B, Hkv * G, Dv)
+    tb = table.numpy()
+    for b, L in enumerate(lens):
+        k = _gather(kp.numpy(), tb, b, L, page_size)
+        v = _gather(vp.numpy(), tb, b, L, page_size)
+        qb = q[b].numpy().reshape(Hkv, G, Dk)
+        ow, lw = O.gqa_attention_fp64(qb, k, v, scale)
+        assert_close(out[b].numpy().reshape(Hkv, G, Dv), ow, F32_ATOL, F32_RTOL, f"out b={b}")
+        assert_close(lse[b].numpy().reshape(Hkv, G), lw, F32_ATOL, F32_RTOL, f"lse b={b}")
+        if L == 0:
+            assert np.all(out[b].numpy() == 0) and np.all(np.isneginf(lse[b].numpy()))
+            continue
+        po, pm, ps = port.cpu_attn(qb, np.ascontiguousarray(k), np.ascontiguousarray(v), scale,
+                                   normalize=False, n_threads=2)
+        assert_close(out[b].numpy().reshape(Hkv, G, Dv), po / ps, F32_ATOL, F32_RTOL,
+                     f"vs C port b={b}")
+
+
+@needs_isa
+def test_attn_partial_fp32_independent_of_thread_split():
+    """fp32 probabilities: a different thread split changes only the fp32
+    summation order."""
+    rng = np.random.default_rng(5)
+    lens = [1999, 31, 1000, 64]
+    table, num_pages = _paged(rng, lens, 64)
+    q = _randn_f32((4, 8, 128), 31)
+    kp = _randn_f32((num_pages, 2, 64, 128), 32)
+    vp = _randn_f32((num_pages, 2, 64, 128), 33)
+    ref_o, ref_l = host.attn_partial(q, kp, vp, table, lens, 0.09, 1)
+    for th in (2, 7, 64):
+        o, l = host.attn_partial(q, kp, vp, table, lens, 0.09, th)
+        np.testing.assert_allclose(o.numpy(), ref_o.numpy(), atol=1e-5, rtol=1e-5)
+        np.testing.assert_allclose(l.numpy(), ref_l.numpy(), atol=1e-6, rtol=1e-6)
+
+
+@needs_isa
+def test_attn_partial_fp32_argument_errors():
+    kp = _randn_f32((1, 1, 32, 40), 2)
+    with pytest.raises(host.WhError, match="multiples of 16"):
+        host.attn_partial(_randn_f32((1, 2, 40), 1), kp, kp,
+                          torch.zeros((1, 1), dtype=torch.int32), [5], 0.1, 1)
+    kp = _randn_f32((1, 1, 32, 64), 2)
+    with pytest.raises(ValueError):  # mixed input dtypes
+        host.attn_partial(bf16_randn((1, 2, 64), 1), kp, kp,
+                          torch.zeros((1, 1), dtype=torch.int32), [5], 0.1, 1)
+
+
 @needs_isa
 def test_attn_partial_rejects_other_width_pairs():
     q = bf16_randn((1, 2, 192), 1)
