@@ -30,14 +30,28 @@ int gpu_fail(int rc, const char* what) {
   return fail(rc, "%s: %s", what, ws_last_error());
 }
 
-// The event the host waits on for the query copy: one per thread, created
-// on first use.  It keeps the default system-scope release, so the copy's
-// writes to host memory are visible once it has completed.
-int query_event(hipEvent_t* ev) {
-  thread_local hipEvent_t e = nullptr;
-  if (!e && hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess)
-    return fail(WS_ELAUNCH, "wl: hipEventCreateWithFlags failed");
-  *ev = e;
+// The event the host waits on for the query copy: one per thread and
+// device, created on first use (an event records only on streams of the
+// device it was created on).  It keeps the default system-scope release, so
+// the copy's writes to host memory are visible once it has completed.
+constexpr int kMaxDevices = 64;
+
+int query_event(hipStream_t s, hipEvent_t* ev) {
+  thread_local hipEvent_t e[kMaxDevices] = {};
+  int dev = 0, cur = 0;
+  if (hipStreamGetDevice(s, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(WS_ELAUNCH, "wl: the stream's device is unknown");
+  if (!e[dev]) {
+    if (hipGetDevice(&cur) != hipSuccess || hipSetDevice(dev) != hipSuccess)
+      return fail(WS_ELAUNCH, "wl: cannot select device %d", dev);
+    const hipError_t rc = hipEventCreateWithFlags(&e[dev], hipEventDisableTiming);
+    hipSetDevice(cur);
+    if (rc != hipSuccess) {
+      e[dev] = nullptr;
+      return fail(WS_ELAUNCH, "wl: hipEventCreateWithFlags failed");
+    }
+  }
+  *ev = e[dev];
   return WS_OK;
 }
 
@@ -59,7 +73,7 @@ int query_to_host(void* const* dst, const void* const* src, const size_t* bytes,
                   hipStream_t s, hipEvent_t* ev) {
   for (int i = 0; i < n; ++i)
     if (int rc = ws_copy(dst[i], src[i], bytes[i], s)) return gpu_fail(rc, "wl: query copy");
-  if (int rc = query_event(ev)) return rc;
+  if (int rc = query_event(s, ev)) return rc;
   if (hipEventRecord(*ev, s) != hipSuccess) return fail(WS_ELAUNCH, "wl: hipEventRecord failed");
   return WS_OK;
 }
