@@ -62,8 +62,9 @@ constexpr int kPageChunk = kXferThreads * 8 * 16;  // bytes of a page one workgr
 // page i, dst page dst_ids[i] of layer l = src page src_ids[i] of layer l,
 // in chunks of kPageChunk bytes (blockIdx.x = i * chunks + chunk).  Each
 // thread moves eight 16-byte units, all loads in flight before the stores.
-// Ids outside [0, num_pages) were refused on the host; a listed id that is
-// out of range anyway moves nothing.
+// The ids live in device memory, so the launcher cannot check them: a listed
+// id outside [0, num_pages) moves nothing (scope_amd/ops.py copy_pages
+// refuses such ids before the launch).
 __global__ __launch_bounds__(kXferThreads) void copy_pages_kernel(
     char* __restrict__ dst, long long dst_layer_stride, const int32_t* __restrict__ dst_ids,
     int dst_num_pages, const char* __restrict__ src, long long src_layer_stride,
