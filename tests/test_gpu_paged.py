@@ -163,3 +163,35 @@ def test_layer_driver_failure_after_the_step_keeps_lengths_consistent():
         want, _ = O.mla_attention_fp64(bits(qn[hh]), bits(qp[hh]), full[None, :, :512],
                                        full[None, :, 512:], scale)
         assert_close(got[hh], want, OUT_ATOL, OUT_RTOL, f"b={b} after the failed step")
+
+
+def test_paged_gqa_step_on_a_side_stream_matches_the_default_stream():
+    """The layer driver runs on the caller's current stream (its query-copy
+    event is created on that stream's device): two caches with the same data,
+    one stepped on a side stream, give bit-identical outputs."""
+    B, Hkv, G, D = 2, 4, 4, 128
+    lens, hosts = [200, 77], [128, 64]
+    scale = D ** -0.5
+    caches = [PagedKVCache(1, B, Hkv, D, max_tokens=max(lens) + PS, page_size=PS, device=DEV)
+              for _ in range(2)]
+    ks = [bf16_randn((Hkv, L + 1, D), 600 + b) for b, L in enumerate(lens)]
+    vs = [bf16_randn((Hkv, L + 1, D), 610 + b) for b, L in enumerate(lens)]
+    for c in caches:
+        for b, (L, h) in enumerate(zip(lens, hosts)):
+            c.load(0, b, ks[b][:, :L].contiguous(), vs[b][:, :L].contiguous(), h)
+    k_new = torch.stack([ks[b][:, lens[b]:lens[b] + 1] for b in range(B)]).to(DEV)
+    v_new = torch.stack([vs[b][:, lens[b]:lens[b] + 1] for b in range(B)]).to(DEV)
+    q = bf16_randn((B, Hkv * G, D), 620).to(DEV)
+    out0 = caches[0].step(0, q, k_new, v_new, scale, host_threads=2)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out1 = caches[1].step(0, q, k_new, v_new, scale, host_threads=2)
+    side.synchronize()
+    assert np.array_equal(bits(out0), bits(out1))
+    qb = bits(q.cpu()).reshape(B, Hkv, G, D)
+    got = out1.float().cpu().numpy()
+    for b in range(B):
+        want, _ = O.gqa_attention_fp64(qb[b], bits(ks[b]), bits(vs[b]), scale)
+        assert_close(got[b].reshape(Hkv, G, D), want, OUT_ATOL, OUT_RTOL, f"b={b}")
