@@ -1,0 +1,163 @@
+"""The reference CPU extension's Python surface on libwshost.so.
+
+kernel/cpu_attn.cpp:1024-1054 binds fused_cpu_attn, fused_cpu_attn_fp32,
+fused_cpu_attn_mla, fused_cpu_attn_mla_compressed, set_num_threads and
+get_num_threads; the runtimes call them through an extension handle
+(system/mixoffload.py:1333, system/qwenoffload.py:1085,1412,
+system/deepseek.py:355, roofline/bench_resident_kv.py:129-133).  This module
+has the same names, arguments and output shapes, so it can stand in for that
+handle (`self._cpu_attn_ext = scope_amd.cpu_attn`), and runs this package's
+host kernels (AVX-512 BF16, or fp32 FMAs for float32 inputs).
+
+Outputs are the reference's triples in an equivalent form: with the natural-
+log LSE of a row, max = LSE and sum = 1 (bf16 outputs: max = LSE rounded to
+bf16, sum = exp(LSE - max) rounded to bf16, which keeps the LSE to about 4e-3
+where a bf16 LSE alone would lose up to 6e-2).  Every consumer in the
+reference uses (max, sum) only through exp(max - M) * sum and out * sum
+(system/mixoffload.py:1334, 1452-1464; system/deepseek.py:394-402;
+roofline/bench_resident_kv.py:141-148), so merges and normalisations give
+the results of the true (max, sum).  The unnormalised outputs
+(fused_cpu_attn_mla, fused_cpu_attn_mla_compressed) are out * sum = out.
+
+Differences from the reference: an empty sequence (S == 0) gives out = 0,
+max = -inf, sum = 0 (the merge identity) where the reference divides by zero;
+bf16 head widths are multiples of 32 up to 256 or 192 / 128 (float32: multiples
+of 16), where the reference takes any multiple of 16.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+from . import host
+
+_threads = 0  # 0: the OpenMP default
+
+
+def set_num_threads(n: int) -> None:
+    """Threads of the following calls (kernel/cpu_attn.cpp:1046-1050)."""
+    global _threads
+    _threads = max(1, int(n))
+
+
+def get_num_threads() -> int:
+    """Threads a call uses (kernel/cpu_attn.cpp:1051-1053)."""
+    if _threads > 0:
+        return _threads
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return omp if omp > 0 else len(os.sched_getaffinity(0))
+
+
+def _bf16_pair(lse: torch.Tensor):
+    """(max, sum) in bf16 with max + log(sum) = lse to within bf16's rounding of sum."""
+    m = lse.to(torch.bfloat16)
+    mf = m.float()
+    s = torch.where(torch.isneginf(lse), torch.zeros_like(lse), torch.exp(lse - mf))
+    return m, s.to(torch.bfloat16)
+
+
+def _rows(t: torch.Tensor, name: str, width: int):
+    """A [N, S, width] K or V view as paged-pool arguments: (tensor whose
+    data_ptr is row 0, token stride of a row in tokens).  Rows may be strided
+    (dims 0-1, as the reference honours them, kernel/cpu_attn.cpp:598-601);
+    a layout a page cannot express is copied first."""
+    if t.dim() != 3 or t.shape[2] != width:
+        raise ValueError(f"{name} must be [N, S, {width}], got {tuple(t.shape)}")
+    N, S, _ = t.shape
+    if t.stride(2) != 1 or t.stride(1) != width or (N > 1 and t.stride(0) % width) or \
+            (N > 1 and t.stride(0) < S * width):
+        t = t.contiguous()
+    row = t.stride(0) // width if N > 1 else max(S, 1)
+    return t, max(row, 1)
+
+
+def _attn(q, k, v, scale, threads):
+    """(out [N, G, Dv] fp32 normalised, lse [N, G]) over dense rows k, v [N, S, D]."""
+    if not q.is_contiguous():
+        raise ValueError("q must be contiguous")
+    N, G, Dk = q.shape
+    Dv = v.shape[2]
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("k and v must have q's dtype")
+    if k.shape[:2] != v.shape[:2] or k.shape[0] != N:
+        raise ValueError(f"k {tuple(k.shape)} / v {tuple(v.shape)} do not match q "
+                         f"{tuple(q.shape)}")
+    S = k.shape[1]
+    k, pk = _rows(k, "k", Dk)
+    v, pv = _rows(v, "v", Dv)
+    if pk != pv:  # one page size for both pools
+        k, v = k.contiguous(), v.contiguous()
+        pk = pv = max(S, 1)
+    table = torch.arange(N, dtype=torch.int32).view(N, 1)
+    lens = torch.full((N,), S, dtype=torch.int32)
+    if N == 0 or S == 0:  # nothing to attend: the merge identity
+        return (torch.zeros((N, G, Dv), dtype=torch.float32),
+                torch.full((N, G), float("-inf"), dtype=torch.float32))
+    out = torch.empty((N, G, Dv), dtype=torch.float32)
+    lse = torch.empty((N, G), dtype=torch.float32)
+    L = host.lib()
+    fn = L.wh_attn_partial_f32 if q.dtype == torch.float32 else L.wh_attn_partial
+    host._check(fn(host._p(q), host._p(k), host._p(v), host._p(table), host._p(lens), N, G, 1,
+                   Dk, Dv, pk, 1, N, ctypes.c_float(scale), host._p(out), host._p(lse),
+                   int(threads)))
+    return out, lse
+
+
+def fused_cpu_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float):
+    """kernel/cpu_attn.cpp:572-636: q [B_kv, G, D], k / v [B_kv, S, D], bf16 or
+    float32.  Returns the normalised out and (max, sum) [B_kv, G, 1], all bf16
+    for bf16 inputs, float32 for float32 inputs."""
+    if q.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("q must be float32 or bfloat16")
+    out, lse = _attn(q, k, v, scale, get_num_threads())
+    if q.dtype == torch.bfloat16:
+        m, s = _bf16_pair(lse)
+        return out.to(torch.bfloat16), m.unsqueeze(-1), s.unsqueeze(-1)
+    return out, lse.unsqueeze(-1), _unit_sum(lse).unsqueeze(-1)
+
+
+def fused_cpu_attn_fp32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float):
+    """kernel/cpu_attn.cpp:817-848: float32 inputs; normalised out, max, sum
+    (float32)."""
+    if q.dtype != torch.float32 or k.dtype != torch.float32 or v.dtype != torch.float32:
+        raise ValueError("fused_cpu_attn_fp32 requires float32 inputs")
+    out, lse = _attn(q, k, v, scale, get_num_threads())
+    return out, lse.unsqueeze(-1), _unit_sum(lse).unsqueeze(-1)
+
+
+def fused_cpu_attn_mla(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float):
+    """kernel/cpu_attn.cpp:638-672: bf16 q [B_kv, G, Dk], k [B_kv, S, Dk],
+    v [B_kv, S, Dv] (Dk may differ from Dv); unnormalised float32 out and
+    float32 (max, sum)."""
+    if q.dtype != torch.bfloat16:
+        raise ValueError("fused_cpu_attn_mla requires bf16 inputs")
+    out, lse = _attn(q, k, v, scale, get_num_threads())
+    return out, lse.unsqueeze(-1), _unit_sum(lse).unsqueeze(-1)
+
+
+def fused_cpu_attn_mla_compressed(q_proj: torch.Tensor, q_pe: torch.Tensor,
+                                  c_kv: torch.Tensor, k_pe: torch.Tensor, scale: float):
+    """kernel/cpu_attn.cpp:852-1022: q_proj [B*H, 512], q_pe [B*H, 64],
+    c_kv [B, S, 512], k_pe [B, S, 64] bf16 (H = q rows / B, a multiple of 16
+    here); unnormalised float32 out [B*H, 512], max [B*H], sum [B*H]."""
+    if not (q_proj.is_contiguous() and c_kv.is_contiguous()):
+        raise ValueError("q_proj and c_kv must be contiguous")
+    B, S = c_kv.shape[0], c_kv.shape[1]
+    if B == 0 or c_kv.dim() != 3 or c_kv.shape[2] != host.MLA_C or \
+            tuple(k_pe.shape) != (B, S, host.MLA_PE):
+        raise ValueError(f"c_kv must be [B, S, 512] and k_pe [B, S, 64], got "
+                         f"{tuple(c_kv.shape)} / {tuple(k_pe.shape)}")
+    if S == 0:  # nothing to attend: the merge identity
+        rows = q_proj.shape[0]
+        lse = torch.full((rows,), float("-inf"), dtype=torch.float32)
+        return torch.zeros((rows, host.MLA_C), dtype=torch.float32), lse, _unit_sum(lse)
+    out, lse = host.mla_partial_dense(q_proj.contiguous(), q_pe.contiguous(), c_kv,
+                                      k_pe.contiguous(), [S] * B, scale, get_num_threads())
+    return out, lse, _unit_sum(lse)
+
+
+def _unit_sum(lse: torch.Tensor) -> torch.Tensor:
+    """sum = 1 beside max = lse (0 for an empty row, whose lse is -inf)."""
+    return torch.where(torch.isneginf(lse), torch.zeros_like(lse), torch.ones_like(lse))
