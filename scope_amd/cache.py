@@ -66,6 +66,27 @@ class _PagedBase:
                                      device=self.device)
         self._cur = np.zeros(num_layers, np.int64)
         self._pages_held = np.zeros(batch, np.int64)
+        # addresses of the two length arrays of every layer (the step entry
+        # points take raw pointers; indexing the tensor would build a view)
+        lp = self._len_bufs.data_ptr()
+        self._len_ptr = [[lp + 4 * batch * (k * num_layers + l) for l in range(num_layers)]
+                         for k in range(2)]
+        pd = self.page_table.device  # with its index
+        self._dev_index = pd.index if pd.type != "cpu" else -1
+
+    def len_ptrs(self, layer: int):
+        """(address of the current device lengths of `layer`, address of the
+        other array, which a fused step writes)."""
+        c = int(self._cur[layer])
+        return self._len_ptr[c][layer], self._len_ptr[1 - c][layer]
+
+    def on_device(self, t: torch.Tensor) -> bool:
+        """Whether t is a bf16 tensor on this partition's device."""
+        if t.dtype is not torch.bfloat16:
+            return False
+        if self._dev_index < 0:
+            return not t.is_cuda
+        return t.is_cuda and t.get_device() == self._dev_index
 
     def len_dev(self, layer: int) -> torch.Tensor:
         """Device lengths [B] of `layer` (the current one of its two arrays)."""
@@ -217,10 +238,9 @@ class GqaGpuPartition(_PagedBase):
         (k_new, v_new)."""
         B, Hkv, D = self.batch, self.num_kv_heads, self.head_dim
         k_new, v_new = k_new.contiguous(), v_new.contiguous()
-        dev = self.page_table.device  # with its index
         for t, n in ((q, "q"), (k_new, "k_new"), (v_new, "v_new")):
-            if t.device != dev or t.dtype != torch.bfloat16:
-                raise ValueError(f"{n} must be bf16 on {dev}")
+            if not self.on_device(t):
+                raise ValueError(f"{n} must be bf16 on {self.page_table.device}")
         if q.dim() != 3 or q.shape[0] != B or q.shape[2] != D or q.shape[1] % Hkv or \
                 not q.is_contiguous():
             raise ValueError(f"q must be a contiguous [{B}, Hq, {D}] with Hq a multiple of {Hkv}")
@@ -316,10 +336,9 @@ class MlaGpuPartition(_PagedBase):
         and buffers are the partition's).  Returns the head count H."""
         B = self.batch
         rows = q_nope.shape[0] if q_nope.dim() == 2 else -1
-        dev = self.page_table.device  # with its index
         for t, n in ((q_nope, "q_nope"), (q_pe, "q_pe"), (c_new, "c_new"), (pe_new, "pe_new")):
-            if t.device != dev or t.dtype != torch.bfloat16:
-                raise ValueError(f"{n} must be bf16 on {dev}")
+            if not self.on_device(t):
+                raise ValueError(f"{n} must be bf16 on {self.page_table.device}")
         if rows <= 0 or rows % (16 * B) or q_nope.shape[1] != ops.MLA_C or \
                 q_pe.shape != (rows, ops.MLA_PE) or not q_nope.is_contiguous() or \
                 not q_pe.is_contiguous():

@@ -324,33 +324,51 @@ class _PagedTwoSided:
         return t
 
     def _layer_args(self, layer: int, cls):
-        """The layer driver's argument structure of this cache (one, reused:
-        a call fills every field it reads)."""
-        a = self.__dict__.get("_wl_args")
-        if a is None or not isinstance(a, cls):
-            a = self._wl_args = cls()
-        a.ev_step_begin = a.ev_step_end = None
+        """The layer driver's argument structure of `layer`, one per layer and
+        reused step after step: the fields no step changes (the pools, page
+        tables and paging of both sides, all allocated once with the cache)
+        are set when it is built, and a step writes the others."""
+        wl = self.__dict__.setdefault("_wl_args", {})
+        a = wl.get(layer)
+        if a is None:
+            a = wl[layer] = cls()
+            data = self.host.data
+            if len(data) == 1:  # MLA: one latent pool
+                a.host_latent = data[0][layer].data_ptr()
+            else:  # GQA: K and V pools
+                a.host_k, a.host_v = data[0][layer].data_ptr(), data[1][layer].data_ptr()
+            a.host_table = self.host.table_t.data_ptr()
+            a.host_lens = self.host.lens_t.data_ptr()
+            a.host_page_size = self.page_size
+            a.host_max_pages = self.host.table.shape[1]
+            a.host_num_pages = self.host.num_pages
+            g = self.gpu
+            a.page_table = g.page_table.data_ptr()
+            a.B, a.page_size = self.batch, g.page_size
+            a.max_pages, a.num_pages = g.page_table.shape[1], g.num_pages
+            self._gpu_static_args(a, layer)
         if self.controller is not None:
             e0, e1 = self._timing[layer]
             a.ev_step_begin, a.ev_step_end = e0.cuda_event, e1.cuda_event
+        elif a.ev_step_begin:
+            a.ev_step_begin = a.ev_step_end = None
         return a
 
-    def _host_args(self, a, layer: int, rows: int, threads: int, q_bufs, out_shape) -> None:
-        """The host side of the driver's arguments: pinned query copies, the
-        host pools, page table and lengths, and the pinned bf16 / fp32 host
-        partial."""
+    def _gpu_static_args(self, a, layer: int) -> None:
+        """The GPU pools of `layer` in its driver structure (per subclass)."""
+        raise NotImplementedError
+
+    def _step_args(self, a, layer: int, rows: int, threads: int, max_len: int, nwg: int,
+                   ws, out_g, lse_g, q_bufs, out_shape) -> None:
+        """The fields of the driver structure a step sets: lengths, plan,
+        workspace and split partials, the pinned query copies and the pinned
+        bf16 / fp32 host partial (pinned buffers are allocated once per shape)."""
+        a.len_in, a.len_out = self.gpu.len_ptrs(layer)
+        a.max_len, a.n_splits = max_len, nwg
+        a.out_g, a.lse_g = out_g.data_ptr(), lse_g.data_ptr()
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
         for name, shape in q_bufs:
             setattr(a, name, self._pinned(name, shape, torch.bfloat16).data_ptr())
-        data = self.host.data
-        if len(data) == 1:  # MLA: one latent pool
-            a.host_latent = data[0][layer].data_ptr()
-        else:  # GQA: K and V pools
-            a.host_k, a.host_v = data[0][layer].data_ptr(), data[1][layer].data_ptr()
-        a.host_table = self.host.table_t.data_ptr()
-        a.host_lens = self.host.lens_t.data_ptr()
-        a.host_page_size = self.page_size
-        a.host_max_pages = self.host.table.shape[1]
-        a.host_num_pages = self.host.num_pages
         a.host_threads = int(threads)
         a.out_h = self._pinned("out", out_shape, torch.bfloat16).data_ptr()
         a.lse_h = self._pinned("lse", (rows,), torch.float32).data_ptr()
@@ -428,6 +446,9 @@ class PagedMlaCache(_PagedTwoSided):
     def _gpu_payload(self):
         return [self.gpu.latent]
 
+    def _gpu_static_args(self, a, layer: int) -> None:
+        a.latent_pages = self.gpu.latent[layer].data_ptr()
+
     def load(self, layer: int, b: int, c_kv: torch.Tensor, k_pe: torch.Tensor,
              host_tokens: int) -> None:
         """Prefill sequence b of `layer` with c_kv [L, 512], k_pe [L, 64] (CPU
@@ -478,15 +499,8 @@ class PagedMlaCache(_PagedTwoSided):
         a.q_nope, a.q_pe = q_nope.data_ptr(), q_pe.data_ptr()
         a.c_new, a.c_stride = c_new.data_ptr(), c_new.stride(0)
         a.pe_new, a.pe_stride = pe_new.data_ptr(), pe_new.stride(0)
-        a.latent_pages = g.latent[layer].data_ptr()
-        a.page_table = g.page_table.data_ptr()
-        a.len_in, a.len_out = g.len_dev(layer).data_ptr(), g._len_next(layer).data_ptr()
-        a.B, a.H, a.page_size = B, H, g.page_size
-        a.max_pages, a.num_pages = g.page_table.shape[1], g.num_pages
-        a.max_len, a.n_splits, a.scale = max_len, nwg, float(scale)
-        a.out_g, a.lse_g = out_g.data_ptr(), lse_g.data_ptr()
-        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-        self._host_args(a, layer, rows, host_threads,
+        a.H, a.scale = H, float(scale)
+        self._step_args(a, layer, rows, host_threads, max_len, nwg, ws, out_g, lse_g,
                         q_bufs=(("q_nope_h", (rows, ops.MLA_C)), ("q_pe_h", (rows, ops.MLA_PE))),
                         out_shape=(rows, ops.MLA_C))
         lse_out = torch.empty((rows,), dtype=torch.float32, device=dev) if return_lse else None
@@ -519,6 +533,10 @@ class PagedKVCache(_PagedTwoSided):
 
     def _gpu_payload(self):
         return [self.gpu.k, self.gpu.v]
+
+    def _gpu_static_args(self, a, layer: int) -> None:
+        a.k_pages, a.v_pages = self.gpu.k[layer].data_ptr(), self.gpu.v[layer].data_ptr()
+        a.Hkv, a.D = self.num_kv_heads, self.head_dim
 
     def load(self, layer: int, b: int, k: torch.Tensor, v: torch.Tensor,
              host_tokens: int) -> None:
@@ -557,16 +575,9 @@ class PagedKVCache(_PagedTwoSided):
         max_len, nwg, ws, out_g, lse_g = g.prepare_split(layer, Hq, n_workgroups)
         a = self._layer_args(layer, WlGqaLayer)
         a.q, a.k_new, a.v_new = q.data_ptr(), k_new.data_ptr(), v_new.data_ptr()
-        a.k_pages, a.v_pages = g.k[layer].data_ptr(), g.v[layer].data_ptr()
-        a.page_table = g.page_table.data_ptr()
-        a.len_in, a.len_out = g.len_dev(layer).data_ptr(), g._len_next(layer).data_ptr()
-        a.B, a.Hq, a.Hkv, a.D, a.page_size = B, Hq, g.num_kv_heads, D, g.page_size
-        a.max_pages, a.num_pages = g.page_table.shape[1], g.num_pages
-        a.max_len, a.n_splits, a.scale = max_len, nwg, float(scale)
-        a.out_g, a.lse_g = out_g.data_ptr(), lse_g.data_ptr()
-        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-        self._host_args(a, layer, B * Hq, host_threads, q_bufs=(("q_h", (B, Hq, D)),),
-                        out_shape=(B, Hq, D))
+        a.Hq, a.scale = Hq, float(scale)
+        self._step_args(a, layer, B * Hq, host_threads, max_len, nwg, ws, out_g, lse_g,
+                        q_bufs=(("q_h", (B, Hq, D)),), out_shape=(B, Hq, D))
         res = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=dev)
         lse_out = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
         a.out, a.lse_out = res.data_ptr(), (lse_out.data_ptr() if return_lse else None)
