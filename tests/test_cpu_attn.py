@@ -166,3 +166,31 @@ def test_empty_range_is_the_merge_identity_and_threads():
         X.fused_cpu_attn_fp32(q, k, k, 0.1)      # bf16 into the fp32 entry
     with pytest.raises(ValueError):
         X.fused_cpu_attn_mla(q.float(), k.float(), k.float(), 0.1)
+
+
+def test_reference_self_test_shape_fp32():
+    """The reference's own check of fused_cpu_attn's float32 path
+    (kernel/build.py:28-64: seed 42, B_kv 512, G 4, D 128, S 3072, against a
+    1024-token blocked online softmax in torch), at its full shape, through
+    this module.  The reference prints the differences without a threshold;
+    here out is within 1e-4 and the LSE carried by (max, sum) within 1e-5."""
+    torch.manual_seed(42)
+    B, G, D, S = 512, 4, 128, 3072
+    q = torch.randn(B, G, D); k = torch.randn(B, S, D); v = torch.randn(B, S, D)
+    scale = D ** -0.5
+    out_acc = torch.zeros(B, G, D); m_acc = torch.full((B, G, 1), float("-inf"))
+    s_acc = torch.zeros(B, G, 1)
+    for s0 in range(0, S, 1024):
+        sc = torch.bmm(q, k[:, s0:s0 + 1024].transpose(-2, -1)) * scale
+        mb = sc.amax(-1, keepdim=True)
+        eb = torch.exp(sc - mb)
+        mn = torch.max(m_acc, mb)
+        wo, wn = torch.exp(m_acc - mn), torch.exp(mb - mn)
+        s_acc = wo * s_acc + wn * eb.sum(-1, keepdim=True)
+        out_acc = wo * out_acc + wn * torch.bmm(eb, v[:, s0:s0 + 1024])
+        m_acc = mn
+    ref_out = (out_acc / s_acc).numpy()
+    ref_lse = (m_acc + torch.log(s_acc)).numpy()
+    o, m, s = X.fused_cpu_attn(q, k, v, scale)
+    np.testing.assert_allclose(o.numpy(), ref_out, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(_lse(m, s), ref_lse, rtol=0, atol=1e-5)
