@@ -152,6 +152,40 @@ def test_reference_api_local_bmm_softmax_and_merge():
     assert_close(m2[..., 0].cpu().numpy(), wl, LSE_ATOL, LSE_RTOL, "merged lse")
 
 
+def test_reference_flow_with_the_cpu_extension_drop_in():
+    """run_kvlen_resident's three ranges (roofline/bench_resident_kv.py:314-352)
+    with every partial behind a reference signature: the CPU range through
+    scope_amd.cpu_attn.fused_cpu_attn (bf16 normalised triple, un-normalised
+    as system/mixoffload.py:1334 does), the resident range through
+    resident_layer, the streamed range through local_bmm_softmax, merged by
+    pairwise_merge; against fp64 over the whole range."""
+    from scope_amd import cpu_attn
+    N, kv, G, D = 8, 3000, 4, 128
+    q = bf16_randn((N, G, D), 91)
+    k = bf16_randn((N, kv + 1, D), 92)
+    v = bf16_randn((N, kv + 1, D), 93)
+    scale = D ** -0.5
+    cpu_end, res_end = 1100, 2100          # CPU [0, 1100), resident [1100, 2100] + new token
+    oc, mc, sc = cpu_attn.fused_cpu_attn(q, k[:, :cpu_end], v[:, :cpu_end], scale)
+    oc = (oc.float() * sc.float()).to(DEV)
+    mc, sc = mc.float().to(DEV), sc.float().to(DEV)
+    qd = q.to(DEV)
+    kr = k[:, cpu_end:res_end + 1].contiguous().to(DEV)
+    vr = v[:, cpu_end:res_end + 1].contiguous().to(DEV)
+    new_k, new_v = kr[:, -1:].clone(), vr[:, -1:].clone()
+    kr[:, -1:] = 0
+    vr[:, -1:] = 0
+    parts = [reference_api.resident_layer(qd, kr, vr, new_k, new_v, scale),
+             reference_api.local_bmm_softmax(qd, k[:, res_end + 1:].contiguous().to(DEV),
+                                             v[:, res_end + 1:].contiguous().to(DEV), scale)]
+    o1, m1, s1 = reference_api.pairwise_merge(oc, mc, sc, *parts[0])
+    o2, m2, s2 = reference_api.pairwise_merge(o1, m1, s1, *parts[1])
+    got = (o2 / s2.clamp(min=1e-6)).to(torch.bfloat16).float().cpu().numpy()
+    want, wl = O.gqa_attention_fp64(bits(q), bits(k), bits(v), scale)
+    assert_close(got, want, OUT_ATOL, OUT_RTOL, "three ranges")
+    assert_close(m2[..., 0].cpu().numpy(), wl, 1e-2, 1e-2, "merged lse (bf16 CPU triple)")
+
+
 def test_reference_api_resident_layer():
     N, cap, G, D = 8, 513, 4, 128
     k = bf16_randn((N, cap, D), 81).to(DEV)
