@@ -195,3 +195,33 @@ def test_paged_gqa_step_on_a_side_stream_matches_the_default_stream():
     for b in range(B):
         want, _ = O.gqa_attention_fp64(qb[b], bits(ks[b]), bits(vs[b]), scale)
         assert_close(got[b].reshape(Hkv, G, D), want, OUT_ATOL, OUT_RTOL, f"b={b}")
+
+
+def test_paged_mla_step_with_more_sequences_than_one_wave_plans():
+    """B = 70 sequences (past the 64 a single wave plans): the step falls back
+    to the workgroup-wide plan, ragged lengths, a host share on some
+    sequences; against fp64 over every sequence."""
+    B, H = 70, 16
+    rng = np.random.default_rng(70)
+    lens = [int(x) for x in rng.integers(1, 300, B)]
+    hosts = [PS * int(rng.integers(0, 3)) if L > 2 * PS else 0 for L in lens]
+    hosts = [min(h, (L // PS) * PS) for h, L in zip(hosts, lens)]
+    scale = 192 ** -0.5
+    cache = PagedMlaCache(1, B, max_tokens=max(lens) + PS, page_size=PS, device=DEV)
+    lat = [torch.cat([bf16_randn((L + 1, 512), 1000 + b, 0.5),
+                      bf16_randn((L + 1, 64), 2000 + b, 0.5)], dim=1) for b, L in enumerate(lens)]
+    for b, (L, h) in enumerate(zip(lens, hosts)):
+        cache.load(0, b, lat[b][:L, :512].contiguous(), lat[b][:L, 512:].contiguous(), h)
+    new = torch.stack([lat[b][lens[b]] for b in range(B)]).view(B, 1, 576).to(DEV)
+    qn = bf16_randn((B * H, 512), 3000, 0.5)
+    qp = bf16_randn((B * H, 64), 3001, 0.5)
+    out = cache.step(0, qn.to(DEV), qp.to(DEV), new[..., :512].contiguous(),
+                     new[..., 512:].contiguous(), scale, host_threads=4)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    for b in range(B):
+        full = bits(lat[b][:lens[b] + 1])
+        hh = slice(b * H, (b + 1) * H)
+        want, _ = O.mla_attention_fp64(bits(qn[hh]), bits(qp[hh]), full[None, :, :512],
+                                       full[None, :, 512:], scale)
+        assert_close(got[hh], want, OUT_ATOL, OUT_RTOL, f"b={b} (L={lens[b]}, host={hosts[b]})")
