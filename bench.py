@@ -966,12 +966,12 @@ def cpu_baseline(data, Hkv, G, budget_s, threads):
 
 # Workloads timed beside the headline (all by default; --workloads picks some):
 #   shares     headline shape at r = 0.25, 0.75
-#   qwen3      Qwen3 B4 length sweep 8k..128k (config 4)
-#   single     Qwen3 B1 L4096 in one partition (config 1)
-#   mla        DeepSeek-V2-Lite B8 L16384 r 0.5 (config 3)
+#   qwen3      Qwen3 B4 length sweep 8k..128k, r = 1
+#   single     Qwen3 B1 L4096 in one partition
+#   mla        DeepSeek-V2-Lite B8 L16384 r 0.5
 #   mla_sweep  DeepSeek-V2-Lite B8 length sweep 8k..128k
 #   host       native host partial rates and the host read bandwidth
-#   model      27-layer DeepSeek-V2-Lite decode, B32 lognormal, every share (config 5)
+#   model      27-layer DeepSeek-V2-Lite decode, B32 lognormal, every share
 #   migrate    boundary movement of a paged two-sided MLA cache (4 layers, B32)
 #   epilogue   MLA merge + W_UV: fused kernel against merge then bmm
 WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "host", "model", "migrate",
