@@ -331,10 +331,12 @@ def test_lse_merge_formats(fmt, Dv):
 # fused append + partial (one launch per decode step)
 
 
-@pytest.mark.parametrize("Hkv,G,wg", [(8, 4, 0), (8, 4, 5), (4, 8, 64), (2, 16, 3)])
-def test_gqa_append_decode_fused_steps(Hkv, G, wg):
-    _say(f"gqa fused append+decode Hkv={Hkv} G={G} wg={wg}")
-    D, PS = 128, 64
+@pytest.mark.parametrize("Hkv,G,wg,PS", [(8, 4, 0, 64), (8, 4, 5, 64), (4, 8, 64, 64),
+                                         (2, 16, 3, 64), (8, 4, 5, 32), (4, 8, 0, 96)])
+def test_gqa_append_decode_fused_steps(Hkv, G, wg, PS):
+    # page sizes 32 and 96 (not a power of two): appends across page ends
+    _say(f"gqa fused append+decode Hkv={Hkv} G={G} wg={wg} PS={PS}")
+    D = 128
     lens = [0, 1, 63, 64, 200, 777]
     B, steps = len(lens), 3
     total = [L + steps for L in lens]
@@ -473,13 +475,14 @@ def test_gqa_split_capacity_error():
         ops.gqa_decode_partial(q, k_pages, v_pages, pt, gl, 0.1, 64, n_workgroups=5000)
 
 
-@pytest.mark.parametrize("wg,lens", [(0, [0, 5, 64, 300]), (3, [0, 5, 64, 300]),
-                                     (1, [0, 5, 300, 4200])])
-def test_mla_append_decode_fused_steps(wg, lens):
+@pytest.mark.parametrize("wg,lens,PS", [(0, [0, 5, 64, 300], 64), (3, [0, 5, 64, 300], 64),
+                                        (1, [0, 5, 300, 4200], 64), (3, [0, 95, 96, 300], 96),
+                                        (2, [0, 31, 32, 700], 32)])
+def test_mla_append_decode_fused_steps(wg, lens, PS):
     # wg 1 with 4200 tokens: the new token's segment ends two page-id
-    # windows past its start
-    _say(f"mla fused append+decode wg={wg} lens={lens}")
-    H, PS = 16, 64
+    # windows past its start; page sizes 96 and 32: appends across page ends
+    _say(f"mla fused append+decode wg={wg} lens={lens} PS={PS}")
+    H = 16
     B, steps = len(lens), 2
     total = [L + steps for L in lens]
     lat, pt, gl, cs, pes = mla_pool(total, PS, seed=44)
