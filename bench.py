@@ -765,12 +765,14 @@ def mla_model_bench(*, B, layers, lens, share, steps, warmup, seed, dev, threads
 
 
 def share_control_bench(*, B, layers, lens, start_share, budget_frac, steps, seed, dev, threads,
-                        label):
+                        label, async_moves=False):
     """The share controller driving a two-sided paged MLA cache
     (scope_amd.paged.PagedMlaCache + scheduler.ShareController) through
     `steps` decode steps of a `layers`-layer model, with an HBM budget of
     budget_frac of the cache's bytes, starting from share start_share.
-    Returns the per-step share, wall time per layer and the moves."""
+    With async_moves the page copies of a move run under the following
+    steps (side stream) instead of between them.  Returns the per-step
+    share, wall time per layer and the moves."""
     import torch
 
     from scope_amd.paged import PagedMlaCache
@@ -799,33 +801,43 @@ def share_control_bench(*, B, layers, lens, start_share, budget_frac, steps, see
     qn = [_randn_bf16((rows, 512), gen, 0.5, dev) for _ in range(layers)]
     qp = [_randn_bf16((rows, 64), gen, 0.5, dev) for _ in range(layers)]
     kv_new = _randn_bf16((layers, B, 1, 576), gen, 0.5, dev)
-    cache.attach(ctl)
+    cache.attach(ctl, async_moves=async_moves)
     scale = 192 ** -0.5
     per_step = []
+    cur = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
     for i in range(steps):
-        torch.cuda.synchronize()
+        # a decode loop waits for its own stream (the step's outputs), not for
+        # the side stream of a move's copies
+        cur.synchronize()
         t0 = time.perf_counter()
         for l in range(layers):
             cache.step(l, qn[l], qp[l], kv_new[l, :, :, :512], kv_new[l, :, :, 512:], scale,
                        host_threads=threads)
-        torch.cuda.synchronize()
+        cur.synchronize()
         dt = time.perf_counter() - t0
-        moved = [m for m in ctl.moves if m.step == i + 1]
-        per_step.append({
-            "step": i, "share_after": round(ctl.shares[-1], 4),
-            "ms": round(dt * 1e3, 2),
-            "us_per_layer_excl_move": round((dt - sum(m.seconds for m in moved)) / layers * 1e6,
-                                            1),
-            "move_ms": round(sum(m.seconds for m in moved) * 1e3, 1),
-            "move_pages_per_layer": sum(m.pages for m in moved)})
+        per_step.append({"step": i, "share_after": round(ctl.shares[-1], 4),
+                         "moving": cache.moving, "ms": round(dt * 1e3, 2)})
         log(f"share control step {i}: share {per_step[-1]['share_after']}, "
-            f"{per_step[-1]['us_per_layer_excl_move']} us/layer, move "
-            f"{per_step[-1]['move_ms']} ms")
+            f"{per_step[-1]['ms']} ms" + (", a move in flight" if cache.moving else ""))
+    cache.finish_boundaries()
+    # a move's stall (the copies when waited for; else only their issue and
+    # the switch) is counted at the step that started it
+    for i, st in enumerate(per_step):
+        moved = [m for m in ctl.moves if m.step == i + 1]
+        stall = sum(m.stall_seconds for m in moved)
+        st["us_per_layer_excl_move"] = round((st["ms"] * 1e-3 - stall) / layers * 1e6, 1)
+        st["move_stall_ms"] = round(stall * 1e3, 2)
+        st["move_pages_per_layer"] = sum(m.pages for m in moved)
     moves = [{"step": m.step, "from": round(m.share_from, 4), "to": round(m.share_to, 4),
               "pages_per_layer": m.pages, "ms": round(m.seconds * 1e3, 1),
-              "gbs": round(m.pages * PAGE * bpt * layers / m.seconds / 1e9, 1)}
+              "stall_ms": round(m.stall_seconds * 1e3, 2),
+              "copy_ms": round(m.copy_seconds * 1e3, 1),
+              "gbs": round(m.pages * PAGE * bpt * layers / m.copy_seconds / 1e9, 1)}
              for m in ctl.moves]
     return {"label": label, "batch": B, "layers": layers, "start_share": start_share,
+            "async_moves": async_moves,
+            "total_ms": round(sum(p["ms"] for p in per_step), 1),
             "hbm_budget_frac": budget_frac, "host_threads": threads,
             "capacity_share_start": round(sched.capacity_share(sum(lens) * bpt, layers), 4),
             "chosen": [round(r, 4) for r in ctl.chosen], "steps": per_step, "moves": moves,
@@ -1223,6 +1235,14 @@ def main():
                                  budget_frac=0.5, steps=10, seed=args.seed + 23, dev=dev,
                                  threads=th, label="dsv2lite_mla_b32_share_control")
         extra["mla_model"]["share_control"] = sc
+        torch.cuda.empty_cache()
+        sa = share_control_bench(B=32, layers=args.model_layers, lens=m_lens, start_share=0.1,
+                                 budget_frac=0.5, steps=10, seed=args.seed + 23, dev=dev,
+                                 threads=th, label="dsv2lite_mla_b32_share_control_async",
+                                 async_moves=True)
+        extra["mla_model"]["share_control_async"] = sa
+        log(f"share control: {sc['total_ms']} ms over 10 steps waiting for the moves, "
+            f"{sa['total_ms']} ms with the copies under the steps")
         torch.cuda.empty_cache()
         sm = extra["mla_model"]["scheduler"]
         log(f"share model: gpu {sm['gpu_fit']}, host {sm['host_fit']}, r_balance "

@@ -97,12 +97,15 @@ int ws_copy(void* dst, const void* src, size_t bytes, void* stream);
  * tokens across the split: the host-segment tokens past the GPU share that
  * every step copies to the GPU (system/deepseek.py:368-371) and the GPU
  * segment's .to(device) (system/mixoffload.py:1369-1370); here a share change
- * moves whole pages once.
+ * moves whole pages once.  max_workgroups bounds the grid (0: a default of
+ * 2048); a copy across the host link is bound by the link, and a few dozen
+ * workgroups keep it busy while leaving the CUs to kernels that run beside
+ * it on another stream.
  */
 int ws_copy_pages(void* dst, long long dst_layer_stride, const int32_t* dst_ids,
                   int dst_num_pages, const void* src, long long src_layer_stride,
                   const int32_t* src_ids, int src_num_pages, int n_pages, int n_layers,
-                  long long page_bytes, void* stream);
+                  long long page_bytes, int max_workgroups, void* stream);
 
 /*
  * Append n_new tokens per sequence to the GQA pools at positions

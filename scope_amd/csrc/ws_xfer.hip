@@ -57,38 +57,47 @@ extern "C" int ws_copy(void* dst, const void* src, size_t bytes, void* stream) {
 namespace ws {
 
 constexpr int kPageChunk = kXferThreads * 8 * 16;  // bytes of a page one workgroup moves
+// Default bound of a page copy's grid: eight workgroups per CU keep an
+// HBM-to-HBM copy at the memory rate; each loops over the units beyond it.
+constexpr int kCopyPagesMaxBlocks = 2048;
 
-// Page copies of a boundary move: for every layer l (blockIdx.y) and listed
-// page i, dst page dst_ids[i] of layer l = src page src_ids[i] of layer l,
-// in chunks of kPageChunk bytes (blockIdx.x = i * chunks + chunk).  Each
-// thread moves eight 16-byte units, all loads in flight before the stores.
-// The ids live in device memory, so the launcher cannot check them: a listed
-// id outside [0, num_pages) moves nothing (scope_amd/ops.py copy_pages
-// refuses such ids before the launch).
+// Page copies of a boundary move: for every layer l and listed page i,
+// dst page dst_ids[i] of layer l = src page src_ids[i] of layer l, in units
+// of one kPageChunk-byte chunk of one page of one layer (unit u: layer
+// u / (n_pages * chunks), then page, then chunk), the grid striding over
+// the units.  Each thread moves eight 16-byte units of a chunk, all loads in
+// flight before the stores.  The ids live in device memory, so the launcher
+// cannot check them: a listed id outside [0, num_pages) moves nothing
+// (scope_amd/ops.py copy_pages refuses such ids before the launch).
 __global__ __launch_bounds__(kXferThreads) void copy_pages_kernel(
     char* __restrict__ dst, long long dst_layer_stride, const int32_t* __restrict__ dst_ids,
     int dst_num_pages, const char* __restrict__ src, long long src_layer_stride,
-    const int32_t* __restrict__ src_ids, int src_num_pages, int chunks, long long page_bytes) {
-  const int i = blockIdx.x / chunks;
-  const int c = blockIdx.x - i * chunks;
-  const int d = dst_ids[i];
-  const int s = src_ids[i];
-  if (d < 0 || d >= dst_num_pages || s < 0 || s >= src_num_pages) return;
-  const long long l = blockIdx.y;
-  const long long off = (long long)c * kPageChunk;
-  const u32x4* sp = (const u32x4*)(src + l * src_layer_stride + s * page_bytes + off);
-  u32x4* dp = (u32x4*)(dst + l * dst_layer_stride + d * page_bytes + off);
-  const int n16 = (int)(std::min<long long>(kPageChunk, page_bytes - off) / 16);
-  u32x4 v[8];
+    const int32_t* __restrict__ src_ids, int src_num_pages, int n_pages, int chunks,
+    long long page_bytes, long long units) {
+  const long long per_layer = (long long)n_pages * chunks;
+  for (long long u = blockIdx.x; u < units; u += gridDim.x) {
+    const long long l = u / per_layer;
+    const int r = (int)(u - l * per_layer);
+    const int i = r / chunks;
+    const int c = r - i * chunks;
+    const int d = dst_ids[i];
+    const int s = src_ids[i];
+    if (d < 0 || d >= dst_num_pages || s < 0 || s >= src_num_pages) continue;
+    const long long off = (long long)c * kPageChunk;
+    const u32x4* sp = (const u32x4*)(src + l * src_layer_stride + s * page_bytes + off);
+    u32x4* dp = (u32x4*)(dst + l * dst_layer_stride + d * page_bytes + off);
+    const int n16 = (int)(std::min<long long>(kPageChunk, page_bytes - off) / 16);
+    u32x4 v[8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int k = u * kXferThreads + threadIdx.x;
-    if (k < n16) v[u] = sp[k];
-  }
+    for (int k8 = 0; k8 < 8; ++k8) {
+      const int k = k8 * kXferThreads + threadIdx.x;
+      if (k < n16) v[k8] = sp[k];
+    }
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int k = u * kXferThreads + threadIdx.x;
-    if (k < n16) dp[k] = v[u];
+    for (int k8 = 0; k8 < 8; ++k8) {
+      const int k = k8 * kXferThreads + threadIdx.x;
+      if (k < n16) dp[k] = v[k8];
+    }
   }
 }
 
@@ -97,25 +106,30 @@ __global__ __launch_bounds__(kXferThreads) void copy_pages_kernel(
 extern "C" int ws_copy_pages(void* dst, long long dst_layer_stride, const int32_t* dst_ids,
                              int dst_num_pages, const void* src, long long src_layer_stride,
                              const int32_t* src_ids, int src_num_pages, int n_pages,
-                             int n_layers, long long page_bytes, void* stream) {
+                             int n_layers, long long page_bytes, int max_workgroups,
+                             void* stream) {
   static const char* name = "ws_copy_pages";
   if (n_pages == 0 || n_layers == 0) return WS_OK;
   if (!dst || !src || !dst_ids || !src_ids)
     return set_error(WS_EINVAL, "%s: null pointer", name);
-  if (n_pages < 0 || n_layers < 0 || n_layers > 65535 || page_bytes <= 0 ||
-      page_bytes % 16 || dst_num_pages <= 0 || src_num_pages <= 0)
-    return set_error(WS_EINVAL, "%s: bad sizes n_pages=%d n_layers=%d page_bytes=%lld", name,
-                     n_pages, n_layers, page_bytes);
+  if (n_pages < 0 || n_layers < 0 || page_bytes <= 0 || page_bytes % 16 ||
+      dst_num_pages <= 0 || src_num_pages <= 0 || max_workgroups < 0)
+    return set_error(WS_EINVAL,
+                     "%s: bad sizes n_pages=%d n_layers=%d page_bytes=%lld max_workgroups=%d",
+                     name, n_pages, n_layers, page_bytes, max_workgroups);
   if (((uintptr_t)dst & 15u) || ((uintptr_t)src & 15u) || dst_layer_stride % 16 ||
       src_layer_stride % 16)
     return set_error(WS_EINVAL, "%s: pools and layer strides must be 16-byte aligned", name);
   const long long chunks = (page_bytes + kPageChunk - 1) / kPageChunk;
   if ((long long)n_pages * chunks > 0x7fffffffLL)
-    return set_error(WS_EINVAL, "%s: %d pages of %lld bytes exceed the grid", name, n_pages,
-                     page_bytes);
-  hipLaunchKernelGGL(copy_pages_kernel, dim3((unsigned)(n_pages * chunks), (unsigned)n_layers),
-                     dim3(kXferThreads), 0, (hipStream_t)stream, (char*)dst, dst_layer_stride,
-                     dst_ids, dst_num_pages, (const char*)src, src_layer_stride, src_ids,
-                     src_num_pages, (int)chunks, page_bytes);
+    return set_error(WS_EINVAL, "%s: %d pages of %lld bytes exceed the chunk index range", name,
+                     n_pages, page_bytes);
+  const long long units = (long long)n_pages * chunks * n_layers;
+  const int cap = max_workgroups > 0 ? max_workgroups : kCopyPagesMaxBlocks;
+  const int grid = (int)std::min<long long>(units, cap);
+  hipLaunchKernelGGL(copy_pages_kernel, dim3(grid), dim3(kXferThreads), 0, (hipStream_t)stream,
+                     (char*)dst, dst_layer_stride, dst_ids, dst_num_pages, (const char*)src,
+                     src_layer_stride, src_ids, src_num_pages, n_pages, (int)chunks, page_bytes,
+                     units);
   return check_launch(name);
 }

@@ -132,7 +132,7 @@ def lib() -> ctypes.CDLL:
         L.ws_copy.restype = i32
         L.ws_copy.argtypes = [vp, vp, sz, vp]
         L.ws_copy_pages.restype = i32
-        L.ws_copy_pages.argtypes = [vp, i64, vp, i32, vp, i64, vp, i32, i32, i32, i64, vp]
+        L.ws_copy_pages.argtypes = [vp, i64, vp, i32, vp, i64, vp, i32, i32, i32, i64, i32, vp]
         L.ws_noalloc_scratch_bytes.restype = sz
         L.ws_noalloc_scratch_bytes.argtypes = []
         L.ws_gqa_append_decode_partial_noalloc.restype = i32
@@ -250,12 +250,14 @@ def copy_(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
     return dst
 
 
-def copy_pages(dst_pool: torch.Tensor, dst_ids, src_pool: torch.Tensor, src_ids) -> None:
+def copy_pages(dst_pool: torch.Tensor, dst_ids, src_pool: torch.Tensor, src_ids,
+               max_workgroups: int = 0) -> None:
     """dst_pool[:, dst_ids[i]] = src_pool[:, src_ids[i]] for every layer, by
     the library's page-copy kernel (ws_copy_pages) on the current stream of
     the GPU side.  Pools are [layers, num_pages, *page] of one dtype; one of
     them on the GPU, the other on the same GPU or in pinned host memory (the
-    kernel crosses the host link itself: no host gather, no staging)."""
+    kernel crosses the host link itself: no host gather, no staging).
+    max_workgroups bounds the kernel's grid (0: the library's default)."""
     if dst_pool.dtype != src_pool.dtype or dst_pool.dim() < 2 or \
             dst_pool.shape[0] != src_pool.shape[0] or dst_pool.shape[2:] != src_pool.shape[2:]:
         raise ValueError("copy_pages: pools must match in dtype, layers and page shape")
@@ -284,7 +286,7 @@ def copy_pages(dst_pool: torch.Tensor, dst_ids, src_pool: torch.Tensor, src_ids)
         _ptr(dst_pool), dst_pool.stride(0) * dst_pool.element_size(), _ptr(ids[0]),
         dst_pool.shape[1], _ptr(src_pool), src_pool.stride(0) * src_pool.element_size(),
         _ptr(ids[1]), src_pool.shape[1], int(di.size), dst_pool.shape[0], page_bytes,
-        _stream(gpu.device)), "ws_copy_pages")
+        int(max_workgroups), _stream(gpu.device)), "ws_copy_pages")
 
 
 # ---------------------------------------------------------------------------

@@ -22,6 +22,10 @@ pages); the native host partial over the host pages in the calling thread
 while the GPU runs (bf16 out, fp32 lse, pinned); the merge, which reads it in
 place (ws_merge_split, or ws_mla_merge_split_uv with the W_UV epilogue).
 Lengths are the same in every layer between steps; migrate only then.
+set_boundaries() waits for a move's page copies; begin_boundaries() lets
+them run on a side stream under the following steps, which keep the
+current boundaries until poll_boundaries() / finish_boundaries() switches
+both sides over.
 """
 from __future__ import annotations
 
@@ -54,6 +58,19 @@ class _HostPages:
         self.lens_t = torch.from_numpy(self.lens)
 
 
+class _Move:
+    """A boundary move whose page copies have been issued: per sequence
+    (b, h, h_new, k, GPU page ids, host page ids), for moves toward the host
+    (`downs`) and toward the GPU (`ups`); `event` follows the copies on the
+    GPU's side stream (None: they are done)."""
+
+    def __init__(self):
+        self.downs, self.ups, self.kept = [], [], []
+        self.event = self.start = None
+        self.pages = 0
+        self.info = None  # the controller's record of the move
+
+
 class _PagedTwoSided:
     """Shared bookkeeping of the two-sided caches; subclasses name the
     payload tensors of each side and the decode step."""
@@ -69,6 +86,16 @@ class _PagedTwoSided:
             host_pages = batch * self.max_pages
         self.host = _HostPages(num_layers, batch, self.max_pages, host_pages,
                                self._page_shapes(), pin)
+        # the side stream of boundary moves (default priority), used once here
+        # so that its first-use costs (its queue, the allocator's first block
+        # for it) are not paid by the first move
+        dev = self.gpu.device
+        self._move_stream = None
+        if dev.type == "cuda":
+            self._move_stream = torch.cuda.Stream(device=dev)
+            with torch.cuda.stream(self._move_stream):
+                torch.zeros(1, dtype=torch.int32, device=dev)
+            self._move_stream.synchronize()
 
     # -- payload access (per subclass) -------------------------------------
 
@@ -156,7 +183,43 @@ class _PagedTwoSided:
         batch: one page-copy launch per direction and payload, all layers at
         once (pinned host pools; unpinned ones go through pinned staging).
         New pages are taken before any page is given back, so no page is both
-        read and written within a batch.  Returns when the copies are done."""
+        read and written within a batch.  Returns when the copies are done and
+        both sides use the new boundaries (a move in flight is finished
+        first)."""
+        self.finish_boundaries()
+        if self.begin_boundaries(targets):
+            self.finish_boundaries()
+
+    _move = None  # the boundary move in flight (_Move), or None
+    last_kept: list = []  # sequences the last switch left at their boundary
+    last_copy_seconds = None  # GPU time of the last switched move's copies (side stream)
+
+    @property
+    def moving(self) -> bool:
+        """A boundary move has been started and not yet switched to."""
+        return self._move is not None
+
+    # Grid of a move's page copies: the host link bounds them, and a few dozen
+    # workgroups keep it busy while the decode kernels of a begun move, which
+    # want a whole CU per workgroup, still find room beside them.
+    MOVE_WORKGROUPS = 64
+
+    def begin_boundaries(self, targets) -> bool:
+        """Start moving every sequence's boundary to targets[b] host tokens
+        and return without waiting for the copies.  The destination pages are
+        taken from the pools now; with pinned host pools on a GPU the page
+        copies queue on a side stream behind the work already queued on the
+        current one (otherwise they run here, through pinned staging).
+        Decode steps go on over the current boundaries meanwhile: the copies
+        read full pages that decode appends never write (the host's trailing
+        pages, or the GPU's leading pages below its newest token) and write
+        pages that no table holds yet.  poll_boundaries() or
+        finish_boundaries() switches both sides to the new boundaries, with
+        the lengths of that moment.  One move at a time.  Returns False when
+        no boundary moves."""
+        if self._move is not None:
+            raise RuntimeError("a boundary move is in flight: poll_boundaries() or "
+                               "finish_boundaries() first")
         ps = self.page_size
         g = self.gpu
         if len(targets) != self.batch:
@@ -170,58 +233,121 @@ class _PagedTwoSided:
                                  f"in [0, {L}]")
             h = int(self.host.lens[b])
             if h_new != h:
-                plan.append((b, h, h_new, L))
+                plan.append((b, h, h_new))
         if not plan:
-            return
-        need_g = sum((h - hn) // ps for _, h, hn, _ in plan if hn < h)
-        need_h = sum((hn - h) // ps for _, h, hn, _ in plan if hn > h)
+            return False
+        need_g = sum((h - hn) // ps for _, h, hn in plan if hn < h)
+        need_h = sum((hn - h) // ps for _, h, hn in plan if hn > h)
         if need_g > g.pool.free or need_h > self.host.pool.free:
             raise MemoryError(f"boundary move needs {need_g} GPU / {need_h} host free pages, "
                               f"{g.pool.free} / {self.host.pool.free} available")
-        for b, h, hn, _ in plan:
+        for b, h, hn in plan:
             if hn < h and int(g._pages_held[b]) + (h - hn) // ps > g.max_pages:
                 raise ValueError(f"sequence {b}: GPU partition capacity exceeded")
-        down_g, down_h, up_h, up_g = [], [], [], []  # page ids, in move order
-        release_g, release_h = [], []
-        for b, h, h_new, L in plan:
+        m = _Move()
+        for b, h, h_new in plan:
             k = abs(h_new - h) // ps
-            gpu_tok = L - h
-            held_g = int(g._pages_held[b])
             if h_new > h:  # GPU's leading k pages -> new host pages
-                pids_g = g.host_table[b, :k].copy()
-                hp0 = int(self.host.held[b])
-                self._host_reserve(b, h_new)
-                down_g.extend(int(x) for x in pids_g)
-                down_h.extend(int(x) for x in self.host.table[b, hp0:hp0 + k])
-                g.host_table[b, :held_g - k] = g.host_table[b, k:held_g].copy()
-                g.host_table[b, held_g - k:held_g] = -1
-                g._pages_held[b] = held_g - k
-                release_g.extend(int(x) for x in pids_g)
-                self._set_gpu_lens(b, gpu_tok - k * ps)
+                pids_g = [int(x) for x in g.host_table[b, :k]]
+                pids_h = [self.host.pool.alloc() for _ in range(k)]
+                m.downs.append((b, h, h_new, k, pids_g, pids_h))
             else:  # host's trailing k pages -> new GPU pages
                 hp1 = h // ps
-                pids_h = self.host.table[b, hp1 - k:hp1].copy()
+                pids_h = [int(x) for x in self.host.table[b, hp1 - k:hp1]]
                 pids_g = [g.pool.alloc() for _ in range(k)]
-                up_h.extend(int(x) for x in pids_h)
-                up_g.extend(pids_g)
-                g.host_table[b, k:held_g + k] = g.host_table[b, :held_g].copy()
-                g.host_table[b, :k] = pids_g
-                g._pages_held[b] = held_g + k
-                self.host.table[b, hp1 - k:hp1] = 0
-                self.host.held[b] = hp1 - k
-                release_h.extend(int(x) for x in pids_h)
-                self._set_gpu_lens(b, gpu_tok + k * ps)
+                m.ups.append((b, h, h_new, k, pids_g, pids_h))
+        down_g = [x for e in m.downs for x in e[4]]
+        down_h = [x for e in m.downs for x in e[5]]
+        up_g = [x for e in m.ups for x in e[4]]
+        up_h = [x for e in m.ups for x in e[5]]
+        m.pages = len(down_g) + len(up_g)
+        dev = g.device
+        side = dev.type == "cuda" and all(hp.is_pinned() for hp in self.host.data)
+        if side:
+            ms = self._move_stream
+            ms.wait_stream(torch.cuda.current_stream(dev))
+            m.start = torch.cuda.Event(enable_timing=True)
+            m.start.record(ms)
+            with torch.cuda.stream(ms):
+                wg = self.MOVE_WORKGROUPS
+                for gp, hp in zip(self._gpu_payload(), self.host.data):  # all layers at once
+                    if down_g:
+                        ops.copy_pages(hp, down_h, gp, down_g, wg)
+                    if up_g:
+                        ops.copy_pages(gp, up_g, hp, up_h, wg)
+                m.event = torch.cuda.Event(enable_timing=True)
+                m.event.record(ms)
+        else:
+            for gp, hp in zip(self._gpu_payload(), self.host.data):
+                if down_g:
+                    self._pages_to_host(gp, hp, down_g, down_h)
+                if up_g:
+                    self._pages_to_gpu(gp, hp, up_g, up_h)
+        self._move = m
+        return True
+
+    def poll_boundaries(self) -> bool:
+        """Between decode steps: if the copies of the move in flight are done,
+        switch both sides to its boundaries and return True; else False."""
+        m = self._move
+        if m is None or (m.event is not None and not m.event.query()):
+            return False
+        self._switch(m)
+        return True
+
+    def finish_boundaries(self) -> None:
+        """Between decode steps: wait for the copies of the move in flight (if
+        any) and switch both sides to its boundaries."""
+        m = self._move
+        if m is None:
+            return
+        if m.event is not None:
+            m.event.synchronize()
+        self._switch(m)
+
+    def _switch(self, m) -> None:
+        """The tables and lengths of both sides after the copies of move m,
+        with the GPU lengths of now (decode appends may have added tokens
+        since the move began).  A sequence whose GPU side can no longer take
+        its new leading pages (appends filled the partition meanwhile) keeps
+        its boundary; its pages go back to the pool (listed in last_kept)."""
+        ps = self.page_size
+        g = self.gpu
+        self._move = None
+        self.last_kept = m.kept
+        self.last_copy_seconds = m.start.elapsed_time(m.event) * 1e-3 if m.event else None
+        for b, h, h_new, k, pids_g, pids_h in m.downs:
+            L = self.seq_len(b)
+            held_g = int(g._pages_held[b])
+            g.host_table[b, :held_g - k] = g.host_table[b, k:held_g].copy()
+            g.host_table[b, held_g - k:held_g] = -1
+            g._pages_held[b] = held_g - k
+            hp0 = h // ps
+            self.host.table[b, hp0:hp0 + k] = pids_h
+            self.host.held[b] = hp0 + k
             self.host.lens[b] = h_new
-        for gp, hp in zip(self._gpu_payload(), self.host.data):  # all layers at once
-            if down_g:
-                self._pages_to_host(gp, hp, down_g, down_h)
-            if up_g:
-                self._pages_to_gpu(gp, hp, up_g, up_h)
-        for pid in release_g:
-            g.pool.release(pid)
-        for pid in release_h:
-            self.host.pool.release(pid)
-        for b, _, _, _ in plan:
+            self._set_gpu_lens(b, L - h - k * ps)
+            for pid in pids_g:
+                g.pool.release(pid)
+        for b, h, h_new, k, pids_g, pids_h in m.ups:
+            L = self.seq_len(b)
+            held_g = int(g._pages_held[b])
+            if held_g + k > g.max_pages:
+                m.kept.append(b)
+                for pid in pids_g:
+                    g.pool.release(pid)
+                continue
+            g.host_table[b, k:held_g + k] = g.host_table[b, :held_g].copy()
+            g.host_table[b, :k] = pids_g
+            g._pages_held[b] = held_g + k
+            hp1 = h // ps
+            self.host.table[b, hp1 - k:hp1] = 0
+            self.host.held[b] = hp1 - k
+            self.host.lens[b] = h_new
+            self._set_gpu_lens(b, L - h + k * ps)
+            for pid in pids_h:
+                self.host.pool.release(pid)
+        for b in sorted({e[0] for e in m.downs + m.ups}):
             self._write_gpu_row(b)
 
     # -- page copies through pinned staging ------------------------------------
@@ -261,14 +387,10 @@ class _PagedTwoSided:
             self._stage_ev[k] = ev
 
     def _pages_to_gpu(self, gp, hp, pids_g, pids_h):
-        """gp[:, pids_g] = hp[:, pids_h] for every layer: from pinned host
-        pools by the library's page-copy kernel (it reads across the host
-        link itself), else through pinned staging."""
+        """gp[:, pids_g] = hp[:, pids_h] for every layer through pinned staging
+        (an unpinned host pool; pinned pools are copied by the library's
+        page-copy kernel in begin_boundaries)."""
         dev = self.gpu.device
-        if dev.type == "cuda" and hp.is_pinned():
-            ops.copy_pages(gp, pids_g, hp, pids_h)
-            torch.cuda.synchronize(dev)
-            return
         self._stages()
         ig = torch.tensor(pids_g, dtype=torch.int64, device=dev)
         ih = torch.tensor(pids_h, dtype=torch.int64)
@@ -283,13 +405,9 @@ class _PagedTwoSided:
             self._wait_stage(k)
 
     def _pages_to_host(self, gp, hp, pids_g, pids_h):
-        """hp[:, pids_h] = gp[:, pids_g] for every layer (to pinned host pools
-        by the page-copy kernel, else through pinned staging)."""
+        """hp[:, pids_h] = gp[:, pids_g] for every layer through pinned staging
+        (an unpinned host pool)."""
         dev = self.gpu.device
-        if dev.type == "cuda" and hp.is_pinned():
-            ops.copy_pages(hp, pids_h, gp, pids_g)
-            torch.cuda.synchronize(dev)
-            return
         self._stages()
         ig = torch.tensor(pids_g, dtype=torch.int64, device=dev)
         ih = torch.tensor(pids_h, dtype=torch.int64)
@@ -391,10 +509,17 @@ class _PagedTwoSided:
 
     controller = None  # a scheduler.ShareController, or None
 
-    def attach(self, controller) -> None:
+    async_moves = False  # controller moves: begin_boundaries (True) or set_boundaries
+
+    def attach(self, controller, async_moves: bool = False) -> None:
         """Let `controller` (scheduler.ShareController) move the boundary after
-        every decode step, from the per-layer times this cache measures."""
+        every decode step, from the per-layer times this cache measures.
+        With async_moves, a move's page copies run under the following decode
+        steps (begin_boundaries) and the cache switches to the new boundaries
+        after the first step that ends with them done; otherwise the decode
+        loop waits for the copies (set_boundaries)."""
         self.controller = controller
+        self.async_moves = async_moves
         self._timing = [(torch.cuda.Event(enable_timing=True),
                          torch.cuda.Event(enable_timing=True)) for _ in range(self.num_layers)]
         for e0, e1 in self._timing:  # create the events (the layer driver records them)
@@ -418,17 +543,30 @@ class _PagedTwoSided:
             e.synchronize()
             ctl.observe_layer(g_tok * bpt, a.elapsed_time(e) * 1e-3, h_tok * bpt, h_s)
         self._layer_log = []
+        m = self._move
+        if m is not None:
+            t0 = time.perf_counter()
+            if self.poll_boundaries() and m.info is not None:
+                step, r0, r1, t_begin, stall = m.info
+                t1 = time.perf_counter()
+                ctl.record_move(r0, r1, m.pages, t1 - t_begin, stall + t1 - t0, step=step,
+                                copy_seconds=self.last_copy_seconds)
         lens = [self.seq_len(b) for b in range(self.batch)]
         host_now = [int(x) for x in self.host.lens]
-        targets = ctl.decide(lens, host_now)
+        targets = ctl.decide(lens, host_now, moving=self._move is not None)
         if targets is None:
+            return
+        r0, r1 = ctl.share_of(lens, host_now), ctl.share_of(lens, targets)
+        if self.async_moves:
+            t0 = time.perf_counter()
+            if self.begin_boundaries(targets):
+                self._move.info = (ctl.steps, r0, r1, t0, time.perf_counter() - t0)
             return
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         self.set_boundaries(targets)
         pages = sum(abs(t - h) for t, h in zip(targets, host_now)) // self.page_size
-        ctl.record_move(ctl.share_of(lens, host_now), ctl.share_of(lens, targets), pages,
-                        time.perf_counter() - t0)
+        ctl.record_move(r0, r1, pages, time.perf_counter() - t0)
 
 
 class PagedMlaCache(_PagedTwoSided):

@@ -147,7 +147,12 @@ class ShareMove:
     share_from: float
     share_to: float
     pages: int          # pages moved, summed over sequences (per layer)
-    seconds: float      # wall time of the move (all layers)
+    seconds: float      # wall time of the move (all layers), from its start to the switch
+    # time the decode loop spent on it: all of `seconds` when the loop waits
+    # for the copies, only the issue and the switch when they run under the
+    # following steps
+    stall_seconds: float = 0.0
+    copy_seconds: float = 0.0  # the page copies alone
 
 
 class ShareController:
@@ -213,11 +218,13 @@ class ShareController:
             out.append(min(-(-h // ps) * ps, (L // ps) * ps) if round_up else (h // ps) * ps)
         return out
 
-    def decide(self, lens, host_tokens):
+    def decide(self, lens, host_tokens, moving: bool = False):
         """After a decode step: host-token targets per sequence if the chosen
         share moves the boundary by at least min_move_pages pages per
         sequence, or if the GPU side has outgrown the HBM budget (decode
-        appends land on the GPU side); else None."""
+        appends land on the GPU side); else None.  With moving (a move of
+        the cache is still in flight), the choice is recorded and None
+        returned."""
         self.steps += 1
         W = float(sum(int(x) for x in lens)) * self.bytes_per_token
         r = self.sched.choose(W, self.layers, self.granularity)
@@ -230,12 +237,20 @@ class ShareController:
         over = budget is not None and gpu_bytes > budget
         moved = sum(abs(t - int(h)) for t, h in zip(targets, host_tokens)) // self.page_size
         same = all(t == int(h) for t, h in zip(targets, host_tokens))
-        if same or (moved < self.min_move_pages * max(1, len(lens)) and not over):
+        if moving or same or (moved < self.min_move_pages * max(1, len(lens)) and not over):
             self.shares.append(self.share_of(lens, host_tokens))
             return None
         self.shares.append(self.share_of(lens, targets))
         return targets
 
     def record_move(self, share_from: float, share_to: float, pages: int,
-                    seconds: float) -> None:
-        self.moves.append(ShareMove(self.steps, share_from, share_to, pages, seconds))
+                    seconds: float, stall_seconds: float | None = None,
+                    step: int | None = None, copy_seconds: float | None = None) -> None:
+        """A move the cache made: started after decode step `step` (default:
+        the last decided), `seconds` to its switch, `stall_seconds` of them
+        spent by the decode loop and `copy_seconds` by its page copies
+        (default: all)."""
+        self.moves.append(ShareMove(self.steps if step is None else step, share_from,
+                                    share_to, pages, seconds,
+                                    seconds if stall_seconds is None else stall_seconds,
+                                    seconds if copy_seconds is None else copy_seconds))

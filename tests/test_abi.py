@@ -110,10 +110,12 @@ def test_host_side_argument_checks():
     with pytest.raises(ValueError, match="one side must be on a GPU"):
         ops.copy_(torch.zeros(4), torch.zeros(4))
     # ws_copy_pages: sizes and alignment are checked before any launch
-    rc = L.ws_copy_pages(fake, 0, fake, 4, fake, 0, fake, 4, 1, 1, 72, None)
+    rc = L.ws_copy_pages(fake, 0, fake, 4, fake, 0, fake, 4, 1, 1, 72, 0, None)
     assert rc == -1 and b"bad sizes" in L.ws_last_error()
-    rc = L.ws_copy_pages(fake, 8, fake, 4, fake, 0, fake, 4, 1, 1, 64, None)
+    rc = L.ws_copy_pages(fake, 8, fake, 4, fake, 0, fake, 4, 1, 1, 64, 0, None)
     assert rc == -1 and b"aligned" in L.ws_last_error()
-    rc = L.ws_copy_pages(None, 0, fake, 4, fake, 0, fake, 4, 1, 1, 64, None)
+    rc = L.ws_copy_pages(None, 0, fake, 4, fake, 0, fake, 4, 1, 1, 64, 0, None)
     assert rc == -1 and b"null" in L.ws_last_error()
-    assert L.ws_copy_pages(None, 0, None, 0, None, 0, None, 0, 0, 1, 64, None) == 0
+    assert L.ws_copy_pages(None, 0, None, 0, None, 0, None, 0, 0, 1, 64, 0, None) == 0
+    rc = L.ws_copy_pages(fake, 0, fake, 4, fake, 0, fake, 4, 1, 1, 64, -1, None)
+    assert rc == -1 and b"max_workgroups" in L.ws_last_error()

@@ -58,6 +58,86 @@ def test_paged_mla_steps_across_boundary_moves():
         assert cache.seq_len(b) == lens[b] + steps
 
 
+def test_paged_mla_steps_while_begun_boundary_moves_copy():
+    """Decode steps queued while a begun move's page copies run on the side
+    stream use the current boundaries; after the switch, the new ones."""
+    B, H, layers = 3, 16, 2
+    lens = [900, 300, 64]
+    hosts = [256, 0, 0]
+    scale = 192 ** -0.5
+    steps = 6
+    cache = PagedMlaCache(layers, B, max_tokens=max(lens) + steps + PS, page_size=PS, device=DEV)
+    lat = {}
+    for layer in range(layers):
+        for b, (L, h) in enumerate(zip(lens, hosts)):
+            lat[layer, b] = bf16_randn((L + steps, 576), 70 + 10 * layer + b, 0.5)
+            x = lat[layer, b]
+            cache.load(layer, b, x[:L, :512].contiguous(), x[:L, 512:].contiguous(), h)
+    # (boundaries to begin before the step, poll / finish after it)
+    plan = [(None, None), ([768, 256, 0], "poll"), (None, "finish"), ([0, 0, 64], None),
+            (None, "poll"), (None, "finish")]
+    for s, (targets, after) in enumerate(plan):
+        if targets is not None:
+            assert cache.begin_boundaries(targets)
+        _say(f"paged mla step {s} begin={targets} moving={cache.moving} "
+             f"host={[cache.host_tokens(b) for b in range(B)]}")
+        for layer in range(layers):
+            pos = [lens[b] + s for b in range(B)]
+            new = torch.stack([lat[layer, b][pos[b]] for b in range(B)]).view(B, 1, 576)
+            qn = bf16_randn((B * H, 512), 600 + 10 * s + layer, 0.5)
+            qp = bf16_randn((B * H, 64), 650 + 10 * s + layer, 0.5)
+            out = cache.step(layer, qn.to(DEV), qp.to(DEV), new[..., :512].contiguous().to(DEV),
+                             new[..., 512:].contiguous().to(DEV), scale, host_threads=3)
+            got = out.float().cpu().numpy()
+            for b in range(B):
+                full = bits(lat[layer, b][:pos[b] + 1])
+                hh = slice(b * H, (b + 1) * H)
+                want, _ = O.mla_attention_fp64(bits(qn[hh]), bits(qp[hh]), full[None, :, :512],
+                                               full[None, :, 512:], scale)
+                assert_close(got[hh], want, OUT_ATOL, OUT_RTOL, f"step {s} layer {layer} b={b}")
+        if after == "poll":
+            cache.poll_boundaries()
+        elif after == "finish":
+            cache.finish_boundaries()
+            assert not cache.moving and cache.last_kept == []
+    assert [cache.host_tokens(b) for b in range(B)] == [0, 0, 64]
+    for b in range(B):
+        assert cache.seq_len(b) == lens[b] + steps
+
+
+def test_paged_gqa_steps_while_a_begun_boundary_move_copies():
+    B, Hkv, G, D = 2, 8, 4, 128
+    lens = [900, 200]
+    hosts = [448, 0]
+    scale = D ** -0.5
+    steps = 3
+    cache = PagedKVCache(1, B, Hkv, D, max_tokens=max(lens) + steps + PS, page_size=PS,
+                         device=DEV)
+    ks = [bf16_randn((Hkv, L + steps, D), 310 + b) for b, L in enumerate(lens)]
+    vs = [bf16_randn((Hkv, L + steps, D), 410 + b) for b, L in enumerate(lens)]
+    for b, (L, h) in enumerate(zip(lens, hosts)):
+        cache.load(0, b, ks[b][:, :L].contiguous(), vs[b][:, :L].contiguous(), h)
+    for s, targets in enumerate([[64, 128], None, None]):
+        if targets is not None:
+            assert cache.begin_boundaries(targets)   # seq 0 to the GPU, seq 1 to the host
+        _say(f"paged gqa step {s} moving={cache.moving} "
+             f"host={[cache.host_tokens(b) for b in range(B)]}")
+        pos = [lens[b] + s for b in range(B)]
+        k_new = torch.stack([ks[b][:, pos[b]:pos[b] + 1] for b in range(B)]).to(DEV)
+        v_new = torch.stack([vs[b][:, pos[b]:pos[b] + 1] for b in range(B)]).to(DEV)
+        q = bf16_randn((B, Hkv * G, D), 510 + s)
+        out = cache.step(0, q.to(DEV), k_new, v_new, scale, host_threads=3)
+        got = out.float().cpu().numpy()
+        qb = bits(q).reshape(B, Hkv, G, D)
+        for b in range(B):
+            want, _ = O.gqa_attention_fp64(qb[b], bits(ks[b][:, :pos[b] + 1]),
+                                           bits(vs[b][:, :pos[b] + 1]), scale)
+            assert_close(got[b].reshape(Hkv, G, D), want, OUT_ATOL, OUT_RTOL, f"step {s} b={b}")
+        if s == 1:
+            cache.finish_boundaries()
+    assert [cache.host_tokens(b) for b in range(B)] == [64, 128]
+
+
 def test_paged_gqa_steps_across_boundary_moves():
     B, Hkv, G, D, layers = 2, 8, 4, 128, 1
     lens = [900, 200]

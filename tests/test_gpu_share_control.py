@@ -23,7 +23,10 @@ H = 16
 SCALE = 192 ** -0.5
 
 
-def test_controller_moves_a_paged_mla_cache_to_its_hbm_budget():
+@pytest.mark.parametrize("async_moves", [False, True])
+def test_controller_moves_a_paged_mla_cache_to_its_hbm_budget(async_moves):
+    # async_moves: the move's copies run under the next steps, which use the
+    # old boundaries until the switch
     layers, steps = 3, 4
     lens = [3000, 1500, 800, 5000]
     B = len(lens)
@@ -38,7 +41,7 @@ def test_controller_moves_a_paged_mla_cache_to_its_hbm_budget():
     for l in range(layers):
         for b, L in enumerate(lens):
             cache.load(l, b, lat[l][b][:L, :512], lat[l][b][:L, 512:], host0[b])
-    cache.attach(ctl)
+    cache.attach(ctl, async_moves=async_moves)
     for s in range(steps):
         for l in range(layers):
             qn = bf16_randn((B * H, 512), 50 + 10 * s + l, 0.5).to(DEV)
@@ -57,6 +60,7 @@ def test_controller_moves_a_paged_mla_cache_to_its_hbm_budget():
                 assert_close(got[rows], want, OUT_ATOL, OUT_RTOL, what)
                 assert_close(got_l[rows], wl, LSE_ATOL, LSE_RTOL, what + " lse")
     print(f"moves {ctl.moves}, shares {ctl.shares}, chosen {ctl.chosen}", flush=True)
+    cache.finish_boundaries()
     assert ctl.steps == steps
     assert ctl.moves and ctl.moves[0].step == 1
     assert ctl.moves[0].share_from < 0.15 and abs(ctl.moves[0].share_to - 0.5) < 0.03

@@ -70,9 +70,11 @@ def test_merges_read_pinned_host_operands_in_place(fmt):
         assert torch.equal(got, want) and torch.equal(gl, wl), rep
 
 
-@pytest.mark.parametrize("page_shape", [(64, 576), (8, 64, 128), (3, 16)])
-def test_copy_pages_both_directions_every_layer(page_shape):
-    _say(f"ws_copy_pages page {page_shape}")
+@pytest.mark.parametrize("page_shape,wg", [((64, 576), 0), ((8, 64, 128), 0), ((3, 16), 0),
+                                           ((64, 576), 5), ((8, 64, 128), 1)])
+def test_copy_pages_both_directions_every_layer(page_shape, wg):
+    # wg: a bounded grid that strides over the (layer, page, chunk) units
+    _say(f"ws_copy_pages page {page_shape} max_workgroups {wg}")
     layers, n_host, n_gpu = 3, 40, 33
     g = torch.Generator().manual_seed(11)
     host = torch.randn((layers, n_host, *page_shape), generator=g).to(torch.bfloat16)
@@ -83,14 +85,14 @@ def test_copy_pages_both_directions_every_layer(page_shape):
     dst = torch.randperm(n_gpu, generator=rng)[:17].tolist()
     want = gpu.clone()
     want[:, dst] = host[:, src].to(DEV)
-    ops.copy_pages(gpu, dst, host, src)  # host -> HBM
+    ops.copy_pages(gpu, dst, host, src, wg)  # host -> HBM
     torch.cuda.synchronize()
     assert torch.equal(gpu, want)
     back_src = torch.randperm(n_gpu, generator=rng)[:9].tolist()
     back_dst = torch.randperm(n_host, generator=rng)[:9].tolist()
     want_h = host.clone()
     want_h[:, back_dst] = gpu[:, back_src].cpu()
-    ops.copy_pages(host, back_dst, gpu, back_src)  # HBM -> host
+    ops.copy_pages(host, back_dst, gpu, back_src, wg)  # HBM -> host
     torch.cuda.synchronize()
     assert torch.equal(host, want_h)
 

@@ -178,3 +178,77 @@ def test_mixed_direction_batch_and_pool_exhaustion():
         cache.set_boundaries([4 * PS, 3 * PS, 2 * PS])
     _check_accounting(cache)                  # a refused move changes nothing
     assert [cache.host_tokens(b) for b in range(B)] == [2 * PS, PS, 0]
+
+
+def _mla_cache_with(lens, hosts, layers, max_tokens, **kw):
+    cache = PagedMlaCache(layers, len(lens), max_tokens=max_tokens, page_size=PS, device="cpu",
+                          pin=False, **kw)
+    data = {}
+    for layer in range(layers):
+        for b, (L, h) in enumerate(zip(lens, hosts)):
+            data[layer, b] = bf16_randn((L, 576), 300 + 10 * layer + b)
+            if layer == 0:
+                cache._host_reserve(b, h)
+                cache.host.lens[b] = h
+            for p in range(h // PS):
+                cache.host.data[0][layer, int(cache.host.table[b, p])] = \
+                    data[layer, b][p * PS:(p + 1) * PS]
+            _fill_gpu(cache.gpu, layer, b, [data[layer, b][h:]])
+    return cache, data
+
+
+def _append_all(cache, data, n, seed):
+    """n decode appends to every sequence of every layer (GPU side)."""
+    for (layer, b), rows in list(data.items()):
+        new = bf16_randn((n, 576), seed + 10 * layer + b)
+        _fill_gpu(cache.gpu, layer, b, [new])
+        data[layer, b] = torch.cat([rows, new])
+
+
+def _check_tokens(cache, data):
+    for (layer, b), rows in data.items():
+        (got,) = _gather(cache, layer, b)
+        assert np.array_equal(bits(got), bits(rows)), (layer, b)
+
+
+def test_begun_move_keeps_the_boundaries_until_the_switch():
+    """begin_boundaries copies the pages but leaves both sides' tables and
+    lengths alone; decode appends meanwhile; the switch uses the lengths of
+    its own moment."""
+    layers = 2
+    lens, hosts = [5 * PS + 7, 3 * PS + 2, 2 * PS + 1], [2 * PS, 0, 2 * PS]
+    cache, data = _mla_cache_with(lens, hosts, layers, max_tokens=9 * PS)
+    targets = [4 * PS, 2 * PS, 0]            # seqs 0 and 1 toward the host, seq 2 to the GPU
+    assert cache.begin_boundaries(targets) and cache.moving
+    assert [cache.host_tokens(b) for b in range(3)] == hosts
+    _check_tokens(cache, data)
+    _append_all(cache, data, PS + 3, 900)    # steps go on over the current boundaries
+    _check_tokens(cache, data)
+    with pytest.raises(RuntimeError):
+        cache.begin_boundaries(hosts)        # one move at a time
+    assert cache.poll_boundaries() and not cache.moving
+    assert [cache.host_tokens(b) for b in range(3)] == targets and cache.last_kept == []
+    _check_accounting(cache)
+    _check_tokens(cache, data)
+    assert not cache.poll_boundaries()       # nothing in flight
+    assert not cache.begin_boundaries(targets)
+    # set_boundaries finishes a begun move first
+    cache.begin_boundaries([0, 0, 2 * PS])
+    cache.set_boundaries([PS, 0, 0])
+    assert [cache.host_tokens(b) for b in range(3)] == [PS, 0, 0]
+    _check_accounting(cache)
+    _check_tokens(cache, data)
+
+
+def test_begun_move_to_the_gpu_is_kept_when_appends_fill_the_partition():
+    layers = 1
+    cache, data = _mla_cache_with([3 * PS], [2 * PS], layers, max_tokens=4 * PS, gpu_pages=8)
+    free_g = cache.gpu.pool.free
+    assert cache.begin_boundaries([0])       # 1 + 2 GPU pages fit in 4
+    assert cache.gpu.pool.free == free_g - 2
+    _append_all(cache, data, 2 * PS, 700)    # now 3 GPU pages: 3 + 2 > 4
+    cache.finish_boundaries()
+    assert cache.last_kept == [0] and cache.host_tokens(0) == 2 * PS
+    assert cache.gpu.pool.free == free_g - 2  # the two appended pages; the move's came back
+    _check_accounting(cache)
+    _check_tokens(cache, data)
