@@ -313,11 +313,14 @@ class _PagedTwoSided:
         its boundary; its pages go back to the pool (listed in last_kept)."""
         ps = self.page_size
         g = self.gpu
+        # lengths first: between steps they agree across layers (else this
+        # raises and the move stays in flight)
+        lens = {e[0]: self.seq_len(e[0]) for e in m.downs + m.ups}
         self._move = None
         self.last_kept = m.kept
         self.last_copy_seconds = m.start.elapsed_time(m.event) * 1e-3 if m.event else None
         for b, h, h_new, k, pids_g, pids_h in m.downs:
-            L = self.seq_len(b)
+            L = lens[b]
             held_g = int(g._pages_held[b])
             g.host_table[b, :held_g - k] = g.host_table[b, k:held_g].copy()
             g.host_table[b, held_g - k:held_g] = -1
@@ -330,7 +333,7 @@ class _PagedTwoSided:
             for pid in pids_g:
                 g.pool.release(pid)
         for b, h, h_new, k, pids_g, pids_h in m.ups:
-            L = self.seq_len(b)
+            L = lens[b]
             held_g = int(g._pages_held[b])
             if held_g + k > g.max_pages:
                 m.kept.append(b)

@@ -226,6 +226,11 @@ def test_begun_move_keeps_the_boundaries_until_the_switch():
     _check_tokens(cache, data)
     with pytest.raises(RuntimeError):
         cache.begin_boundaries(hosts)        # one move at a time
+    cache.gpu.lens[1, 0] += 1                # layer 1 mid-step: no switch, the move stays
+    with pytest.raises(RuntimeError, match="mid-step"):
+        cache.poll_boundaries()
+    assert cache.moving
+    cache.gpu.lens[1, 0] -= 1
     assert cache.poll_boundaries() and not cache.moving
     assert [cache.host_tokens(b) for b in range(3)] == targets and cache.last_kept == []
     _check_accounting(cache)
