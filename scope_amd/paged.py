@@ -67,7 +67,8 @@ class _Move:
     def __init__(self):
         self.downs, self.ups, self.kept = [], [], []
         self.event = self.start = None
-        self.pages = 0
+        self.pages = self.bytes = 0
+        self.t_begin = 0.0
         self.info = None  # the controller's record of the move
 
 
@@ -199,10 +200,18 @@ class _PagedTwoSided:
         """A boundary move has been started and not yet switched to."""
         return self._move is not None
 
-    # Grid of a move's page copies: the host link bounds them, and a few dozen
-    # workgroups keep it busy while the decode kernels of a begun move, which
-    # want a whole CU per workgroup, still find room beside them.
-    MOVE_WORKGROUPS = 64
+    # Grid of a move's page copies: the host link bounds them, and 16
+    # workgroups (256 KB of loads in flight) keep it as busy as 64 do, while
+    # the decode kernels that run beside a begun move's copies are slowed far
+    # less (their own loads wait behind fewer outstanding host-link reads).
+    MOVE_WORKGROUPS = 16
+    # At the end of a step, wait for a begun move's copies when they are
+    # expected to end within this fraction of a step (at the copy rate last
+    # measured in this process, _move_rate bytes/s; before any, a PCIe Gen5
+    # x16 link's usual rate), instead of running one more step at the old
+    # boundaries.
+    MOVE_WAIT_FRACTION = 0.25
+    _move_rate = 50e9
 
     def begin_boundaries(self, targets) -> bool:
         """Start moving every sequence's boundary to targets[b] host tokens
@@ -261,6 +270,9 @@ class _PagedTwoSided:
         up_g = [x for e in m.ups for x in e[4]]
         up_h = [x for e in m.ups for x in e[5]]
         m.pages = len(down_g) + len(up_g)
+        m.bytes = m.pages * sum(p[0, 0].numel() * p.element_size() * p.shape[0]
+                                for p in self._gpu_payload())
+        m.t_begin = time.perf_counter()
         dev = g.device
         side = dev.type == "cuda" and all(hp.is_pinned() for hp in self.host.data)
         if side:
@@ -319,6 +331,8 @@ class _PagedTwoSided:
         self._move = None
         self.last_kept = m.kept
         self.last_copy_seconds = m.start.elapsed_time(m.event) * 1e-3 if m.event else None
+        if self.last_copy_seconds and m.bytes:  # the host link's rate, for every cache
+            _PagedTwoSided._move_rate = m.bytes / self.last_copy_seconds
         for b, h, h_new, k, pids_g, pids_h in m.downs:
             L = lens[b]
             held_g = int(g._pages_held[b])
@@ -511,6 +525,7 @@ class _PagedTwoSided:
     # -- online share control --------------------------------------------------
 
     controller = None  # a scheduler.ShareController, or None
+    _step_end = None  # perf_counter at the end of the last step's bookkeeping
 
     async_moves = False  # controller moves: begin_boundaries (True) or set_boundaries
 
@@ -539,6 +554,13 @@ class _PagedTwoSided:
                                 host_s))
         if layer != self.num_layers - 1:
             return
+        try:
+            self._step_done()
+        finally:
+            self._step_end = time.perf_counter()
+
+    def _step_done(self) -> None:
+        """After the last layer of a decode step: the controller's part."""
         ctl = self.controller
         bpt = ctl.bytes_per_token
         for l, g_tok, h_tok, h_s in self._layer_log:
@@ -546,10 +568,20 @@ class _PagedTwoSided:
             e.synchronize()
             ctl.observe_layer(g_tok * bpt, a.elapsed_time(e) * 1e-3, h_tok * bpt, h_s)
         self._layer_log = []
+        now = time.perf_counter()
+        step_s = now - self._step_end if self._step_end is not None else None
         m = self._move
         if m is not None:
-            t0 = time.perf_counter()
-            if self.poll_boundaries() and m.info is not None:
+            t0 = now
+            done = self.poll_boundaries()
+            if not done and step_s is not None:
+                # copies expected to end within a small part of a step: wait
+                # for them rather than run one more step at the old share
+                left = m.bytes / self._move_rate - (now - m.t_begin)
+                if left < self.MOVE_WAIT_FRACTION * step_s:
+                    self.finish_boundaries()
+                    done = True
+            if done and m.info is not None:
                 step, r0, r1, t_begin, stall = m.info
                 t1 = time.perf_counter()
                 ctl.record_move(r0, r1, m.pages, t1 - t_begin, stall + t1 - t0, step=step,
