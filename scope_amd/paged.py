@@ -145,6 +145,7 @@ class _PagedTwoSided:
         g = self.gpu
         if len(lens) != self.batch or len(host_tokens) != self.batch:
             raise ValueError(f"need {self.batch} lengths and host token counts")
+        self._check_no_move("reserve_layout")
         if self.host.lens.any() or g.lens.any():
             raise RuntimeError("reserve_layout needs an empty cache")
         for b, (L, h) in enumerate(zip(lens, host_tokens)):
@@ -200,8 +201,12 @@ class _PagedTwoSided:
         """A boundary move has been started and not yet switched to."""
         return self._move is not None
 
+    def _check_no_move(self, what: str) -> None:
+        if self._move is not None:
+            raise RuntimeError(f"{what} during a boundary move: finish_boundaries() first")
+
     # Grid of a move's page copies: the host link bounds them, and 16
-    # workgroups (256 KB of loads in flight) keep it as busy as 64 do, while
+    # workgroups (512 KB of loads in flight) keep it as busy as 64 do, while
     # the decode kernels that run beside a begun move's copies are slowed far
     # less (their own loads wait behind fewer outstanding host-link reads).
     MOVE_WORKGROUPS = 16
@@ -629,6 +634,7 @@ class PagedMlaCache(_PagedTwoSided):
         the layers of a sequence with the same split."""
         ps = self.page_size
         L = c_kv.shape[0]
+        self._check_no_move("load")
         if host_tokens % ps or not 0 <= host_tokens <= L:
             raise ValueError(f"host_tokens must be a page multiple in [0, {L}]")
         if layer == 0:
@@ -717,6 +723,7 @@ class PagedKVCache(_PagedTwoSided):
         tokens [0, host_tokens) to host pages, the rest to HBM."""
         ps = self.page_size
         L = k.shape[1]
+        self._check_no_move("load")
         if host_tokens % ps or not 0 <= host_tokens <= L:
             raise ValueError(f"host_tokens must be a page multiple in [0, {L}]")
         if layer == 0:

@@ -226,6 +226,8 @@ def test_begun_move_keeps_the_boundaries_until_the_switch():
     _check_tokens(cache, data)
     with pytest.raises(RuntimeError):
         cache.begin_boundaries(hosts)        # one move at a time
+    with pytest.raises(RuntimeError, match="boundary move"):
+        cache.load(0, 0, data[0, 0][:, :512], data[0, 0][:, 512:], 0)
     cache.gpu.lens[1, 0] += 1                # layer 1 mid-step: no switch, the move stays
     with pytest.raises(RuntimeError, match="mid-step"):
         cache.poll_boundaries()
