@@ -152,3 +152,21 @@ def test_controller_hysteresis_ignores_sub_page_moves():
     lens2 = [L + 3 for L in lens]
     t = ctl.decide(lens2, host)
     assert t == [2112] * 8 and ctl.shares[-1] <= 0.5
+
+
+def test_controller_records_but_does_not_move_while_a_move_is_in_flight():
+    lens = [3000, 5000, 700]
+    sched = ShareScheduler(gpu=Side(10e-6, 6e12), host=Side(10e-6, 100e9))
+    ctl = ShareController(sched, 4096, 32, 64)
+    host = ctl.targets_for(0.25, lens)
+    assert ctl.decide(lens, host, moving=True) is None     # would move to r = 1 otherwise
+    assert ctl.steps == 1 and ctl.chosen == [1.0]
+    assert ctl.shares == [ctl.share_of(lens, host)]       # the current boundaries
+    assert ctl.decide(lens, host) == [0, 0, 0]
+    # a move the cache ran under later steps: its own step, wall and stall times
+    ctl.record_move(0.25, 1.0, 40, 0.07, stall_seconds=0.008, step=1, copy_seconds=0.056)
+    m = ctl.moves[-1]
+    assert (m.step, m.seconds, m.stall_seconds, m.copy_seconds) == (1, 0.07, 0.008, 0.056)
+    ctl.record_move(1.0, 0.5, 10, 0.02)                   # waited for: all of it is stall
+    m = ctl.moves[-1]
+    assert m.step == 2 and m.stall_seconds == m.copy_seconds == 0.02
