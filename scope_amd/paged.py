@@ -280,26 +280,35 @@ class _PagedTwoSided:
         m.t_begin = time.perf_counter()
         dev = g.device
         side = dev.type == "cuda" and all(hp.is_pinned() for hp in self.host.data)
-        if side:
-            ms = self._move_stream
-            ms.wait_stream(torch.cuda.current_stream(dev))
-            m.start = torch.cuda.Event(enable_timing=True)
-            m.start.record(ms)
-            with torch.cuda.stream(ms):
-                wg = self.MOVE_WORKGROUPS
-                for gp, hp in zip(self._gpu_payload(), self.host.data):  # all layers at once
+        try:
+            if side:
+                ms = self._move_stream
+                ms.wait_stream(torch.cuda.current_stream(dev))
+                m.start = torch.cuda.Event(enable_timing=True)
+                m.start.record(ms)
+                with torch.cuda.stream(ms):
+                    wg = self.MOVE_WORKGROUPS
+                    for gp, hp in zip(self._gpu_payload(), self.host.data):  # all layers at once
+                        if down_g:
+                            ops.copy_pages(hp, down_h, gp, down_g, wg)
+                        if up_g:
+                            ops.copy_pages(gp, up_g, hp, up_h, wg)
+                    m.event = torch.cuda.Event(enable_timing=True)
+                    m.event.record(ms)
+            else:
+                for gp, hp in zip(self._gpu_payload(), self.host.data):
                     if down_g:
-                        ops.copy_pages(hp, down_h, gp, down_g, wg)
+                        self._pages_to_host(gp, hp, down_g, down_h)
                     if up_g:
-                        ops.copy_pages(gp, up_g, hp, up_h, wg)
-                m.event = torch.cuda.Event(enable_timing=True)
-                m.event.record(ms)
-        else:
-            for gp, hp in zip(self._gpu_payload(), self.host.data):
-                if down_g:
-                    self._pages_to_host(gp, hp, down_g, down_h)
-                if up_g:
-                    self._pages_to_gpu(gp, hp, up_g, up_h)
+                        self._pages_to_gpu(gp, hp, up_g, up_h)
+        except BaseException:
+            if side:
+                self._move_stream.synchronize()  # copies already queued end first
+            for pid in down_h:
+                self.host.pool.release(pid)
+            for pid in up_g:
+                g.pool.release(pid)
+            raise
         self._move = m
         return True
 

@@ -259,3 +259,17 @@ def test_begun_move_to_the_gpu_is_kept_when_appends_fill_the_partition():
     assert cache.gpu.pool.free == free_g - 2  # the two appended pages; the move's came back
     _check_accounting(cache)
     _check_tokens(cache, data)
+
+
+def test_a_move_whose_copies_fail_gives_its_pages_back():
+    cache, data = _mla_cache_with([3 * PS + 5, 2 * PS], [PS, 2 * PS], 1, max_tokens=6 * PS)
+    free = (cache.gpu.pool.free, cache.host.pool.free)
+
+    def fail(*a):
+        raise RuntimeError("copy failed")
+    cache._pages_to_host = cache._pages_to_gpu = fail
+    with pytest.raises(RuntimeError, match="copy failed"):
+        cache.begin_boundaries([2 * PS, 0])
+    assert not cache.moving and (cache.gpu.pool.free, cache.host.pool.free) == free
+    _check_accounting(cache)
+    _check_tokens(cache, data)
