@@ -95,14 +95,32 @@ int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* 
 /* wh_attn_partial over fp32 q and K / V pools (same shapes, float), fp32
  * FMAs with fp32 probabilities.  (Dk, Dv): equal multiples of 16 up to 256,
  * or (192, 128).
- * Replaces the float32 path of fused_cpu_attn (kernel/cpu_attn.cpp:572-636,
- * whose fp32 case returns the unnormalised (out, max, sum) triple) and
- * fused_cpu_attn_fp32 (kernel/cpu_attn.cpp:817-848, normalised), returning
- * (out, lse). */
+ * Replaces the float32 path of fused_cpu_attn (kernel/cpu_attn.cpp:572-636)
+ * and fused_cpu_attn_fp32 (kernel/cpu_attn.cpp:817-848), both of which
+ * return the normalised out with (max, sum); returns (out, lse). */
 int wh_attn_partial_f32(const float* q, const float* k_pages, const float* v_pages,
                         const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
                         int Dk, int Dv, int page_size, int max_pages, int num_pages,
                         float scale, float* out, float* lse, int n_threads);
+
+/* The reference CPU kernel's own triple: wh_attn_partial / _f32 returning
+ * fp32 (out [B, Hq, Dv], row_max [B, Hq], row_sum [B, Hq]) instead of
+ * (out, lse).  row_max is the largest scaled score q.k * scale of the row,
+ * row_sum the sum of exp(q.k * scale - row_max), and out is divided by
+ * row_sum when `normalize` is nonzero, else left as the weighted sum.  These
+ * are the outputs of fused_cpu_attn (normalised; kernel/cpu_attn.cpp:540-567,
+ * 628-635), fused_cpu_attn_fp32 (normalised; :817-848) and
+ * fused_cpu_attn_mla (unnormalised; :638-672).  An empty row gives out = 0,
+ * row_max = -inf, row_sum = 0. */
+int wh_attn_triple(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                   const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                   int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
+                   int normalize, float* out, float* row_max, float* row_sum, int n_threads);
+int wh_attn_triple_f32(const float* q, const float* k_pages, const float* v_pages,
+                       const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                       int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
+                       int normalize, float* out, float* row_max, float* row_sum,
+                       int n_threads);
 
 /* Absorbed-MLA host partial (H heads, a multiple of 16: 16 for
  * DeepSeek-V2-Lite, 128 for DeepSeek-V2; 512-wide latent + 64-wide rope key).
@@ -133,6 +151,16 @@ int wh_mla_partial_bf16(const uint16_t* q_nope, const uint16_t* q_pe, const uint
                         const int32_t* page_table, const int32_t* lens, int B, int H,
                         int page_size, int max_pages, int num_pages, float scale,
                         uint16_t* out, float* lse, int n_threads);
+
+/* wh_mla_partial returning the reference's triple: fp32 out [B*H, 512]
+ * (unnormalised unless `normalize`), row_max [B*H] and row_sum [B*H] as for
+ * wh_attn_triple.  Replaces fused_cpu_attn_mla_compressed's outputs
+ * (kernel/cpu_attn.cpp:1001-1021: unnormalised out, max, sum). */
+int wh_mla_triple(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
+                  int c_stride, const uint16_t* pe_pages, int pe_stride,
+                  const int32_t* page_table, const int32_t* lens, int B, int H, int page_size,
+                  int max_pages, int num_pages, float scale, int normalize, float* out,
+                  float* row_max, float* row_sum, int n_threads);
 
 /* Streaming read bandwidth of the host memory in GB/s (the host side's
  * roofline for the share scheduler): n_threads OpenMP threads (<= 0: the

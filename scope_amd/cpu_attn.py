@@ -9,15 +9,14 @@ has the same names, arguments and output shapes, so it can stand in for that
 handle (`self._cpu_attn_ext = scope_amd.cpu_attn`), and runs this package's
 host kernels (AVX-512 BF16, or fp32 FMAs for float32 inputs).
 
-Outputs are the reference's triples in an equivalent form: with the natural-
-log LSE of a row, max = LSE and sum = 1 (bf16 outputs: max = LSE rounded to
-bf16, sum = exp(LSE - max) rounded to bf16, which keeps the LSE to about 4e-3
-where a bf16 LSE alone would lose up to 6e-2).  Every consumer in the
-reference uses (max, sum) only through exp(max - M) * sum and out * sum
-(system/mixoffload.py:1334, 1452-1464; system/deepseek.py:394-402;
-roofline/bench_resident_kv.py:141-148), so merges and normalisations give
-the results of the true (max, sum).  The unnormalised outputs
-(fused_cpu_attn_mla, fused_cpu_attn_mla_compressed) are out * sum = out.
+Outputs are the reference's own triples: max is the row's largest scaled
+score q.k * scale, sum the sum of exp(q.k * scale - max), both fp32 and rounded
+to bf16 only where the reference rounds them (fused_cpu_attn on bf16 inputs,
+kernel/cpu_attn.cpp:631-634); out is normalised (fused_cpu_attn,
+fused_cpu_attn_fp32) or not (fused_cpu_attn_mla, _mla_compressed) as there.
+The host kernels carry exactly this running max and sum (log2-domain scores,
+so sum is the same number), and return them through wh_attn_triple /
+wh_mla_triple.
 
 Differences from the reference: an empty sequence (S == 0) gives out = 0,
 max = -inf, sum = 0 (the merge identity) where the reference divides by zero;
@@ -27,7 +26,6 @@ share a KV row (G <= 16), and absorbed MLA takes H a multiple of 16.
 """
 from __future__ import annotations
 
-import ctypes
 import os
 
 import torch
@@ -51,14 +49,6 @@ def get_num_threads() -> int:
     return omp if omp > 0 else len(os.sched_getaffinity(0))
 
 
-def _bf16_pair(lse: torch.Tensor):
-    """(max, sum) in bf16 with max + log(sum) = lse to within bf16's rounding of sum."""
-    m = lse.to(torch.bfloat16)
-    mf = m.float()
-    s = torch.where(torch.isneginf(lse), torch.zeros_like(lse), torch.exp(lse - mf))
-    return m, s.to(torch.bfloat16)
-
-
 def _rows(t: torch.Tensor, name: str, width: int):
     """A [N, S, width] K or V view as paged-pool arguments: (tensor whose
     data_ptr is row 0, token stride of a row in tokens).  Rows may be strided
@@ -74,8 +64,9 @@ def _rows(t: torch.Tensor, name: str, width: int):
     return t, max(row, 1)
 
 
-def _attn(q, k, v, scale, threads):
-    """(out [N, G, Dv] fp32 normalised, lse [N, G]) over dense rows k, v [N, S, D]."""
+def _triple(q, k, v, scale, normalize, threads):
+    """fp32 (out [N, G, Dv], max [N, G], sum [N, G]) over dense rows k, v
+    [N, S, D], out normalised when `normalize`."""
     if not q.is_contiguous():
         raise ValueError("q must be contiguous")
     N, G, Dk = q.shape
@@ -86,6 +77,10 @@ def _attn(q, k, v, scale, threads):
         raise ValueError(f"k {tuple(k.shape)} / v {tuple(v.shape)} do not match q "
                          f"{tuple(q.shape)}")
     S = k.shape[1]
+    if N == 0 or S == 0:  # nothing to attend: the merge identity
+        return (torch.zeros((N, G, Dv), dtype=torch.float32),
+                torch.full((N, G), float("-inf"), dtype=torch.float32),
+                torch.zeros((N, G), dtype=torch.float32))
     k, pk = _rows(k, "k", Dk)
     v, pv = _rows(v, "v", Dv)
     if pk != pv:  # one page size for both pools
@@ -93,30 +88,28 @@ def _attn(q, k, v, scale, threads):
         pk = pv = max(S, 1)
     table = torch.arange(N, dtype=torch.int32).view(N, 1)
     lens = torch.full((N,), S, dtype=torch.int32)
-    if N == 0 or S == 0:  # nothing to attend: the merge identity
-        return (torch.zeros((N, G, Dv), dtype=torch.float32),
-                torch.full((N, G), float("-inf"), dtype=torch.float32))
-    out = torch.empty((N, G, Dv), dtype=torch.float32)
-    lse = torch.empty((N, G), dtype=torch.float32)
-    L = host.lib()
-    fn = L.wh_attn_partial_f32 if q.dtype == torch.float32 else L.wh_attn_partial
-    host._check(fn(host._p(q), host._p(k), host._p(v), host._p(table), host._p(lens), N, G, 1,
-                   Dk, Dv, pk, 1, N, ctypes.c_float(scale), host._p(out), host._p(lse),
-                   int(threads)))
-    return out, lse
+    # row n of k / v is page n of a pool with one KV head and pk tokens per page
+    try:
+        kp = torch.as_strided(k, (N, 1, pk, Dk), (pk * Dk, pk * Dk, Dk, 1))
+        vp = torch.as_strided(v, (N, 1, pk, Dv), (pk * Dv, pk * Dv, Dv, 1))
+    except RuntimeError:  # the last row's page would run past the storage
+        kp = k.contiguous().view(N, 1, S, Dk)
+        vp = v.contiguous().view(N, 1, S, Dv)
+    return host.attn_triple(q, kp, vp, table, lens, scale, normalize, threads)
 
 
 def fused_cpu_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float):
     """kernel/cpu_attn.cpp:572-636: q [B_kv, G, D], k / v [B_kv, S, D], bf16 or
     float32.  Returns the normalised out and (max, sum) [B_kv, G, 1], all bf16
-    for bf16 inputs, float32 for float32 inputs."""
+    for bf16 inputs (each rounded from its fp32 value), float32 for float32
+    inputs."""
     if q.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("q must be float32 or bfloat16")
-    out, lse = _attn(q, k, v, scale, get_num_threads())
+    out, m, s = _triple(q, k, v, scale, True, get_num_threads())
+    m, s = m.unsqueeze(-1), s.unsqueeze(-1)
     if q.dtype == torch.bfloat16:
-        m, s = _bf16_pair(lse)
-        return out.to(torch.bfloat16), m.unsqueeze(-1), s.unsqueeze(-1)
-    return out, lse.unsqueeze(-1), _unit_sum(lse).unsqueeze(-1)
+        return out.to(torch.bfloat16), m.to(torch.bfloat16), s.to(torch.bfloat16)
+    return out, m, s
 
 
 def fused_cpu_attn_fp32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float):
@@ -124,8 +117,8 @@ def fused_cpu_attn_fp32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale
     (float32)."""
     if q.dtype != torch.float32 or k.dtype != torch.float32 or v.dtype != torch.float32:
         raise ValueError("fused_cpu_attn_fp32 requires float32 inputs")
-    out, lse = _attn(q, k, v, scale, get_num_threads())
-    return out, lse.unsqueeze(-1), _unit_sum(lse).unsqueeze(-1)
+    out, m, s = _triple(q, k, v, scale, True, get_num_threads())
+    return out, m.unsqueeze(-1), s.unsqueeze(-1)
 
 
 def fused_cpu_attn_mla(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float):
@@ -134,8 +127,8 @@ def fused_cpu_attn_mla(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale:
     float32 (max, sum)."""
     if q.dtype != torch.bfloat16:
         raise ValueError("fused_cpu_attn_mla requires bf16 inputs")
-    out, lse = _attn(q, k, v, scale, get_num_threads())
-    return out, lse.unsqueeze(-1), _unit_sum(lse).unsqueeze(-1)
+    out, m, s = _triple(q, k, v, scale, False, get_num_threads())
+    return out, m.unsqueeze(-1), s.unsqueeze(-1)
 
 
 def fused_cpu_attn_mla_compressed(q_proj: torch.Tensor, q_pe: torch.Tensor,
@@ -152,13 +145,8 @@ def fused_cpu_attn_mla_compressed(q_proj: torch.Tensor, q_pe: torch.Tensor,
                          f"{tuple(c_kv.shape)} / {tuple(k_pe.shape)}")
     if S == 0:  # nothing to attend: the merge identity
         rows = q_proj.shape[0]
-        lse = torch.full((rows,), float("-inf"), dtype=torch.float32)
-        return torch.zeros((rows, host.MLA_C), dtype=torch.float32), lse, _unit_sum(lse)
-    out, lse = host.mla_partial_dense(q_proj.contiguous(), q_pe.contiguous(), c_kv,
-                                      k_pe.contiguous(), [S] * B, scale, get_num_threads())
-    return out, lse, _unit_sum(lse)
-
-
-def _unit_sum(lse: torch.Tensor) -> torch.Tensor:
-    """sum = 1 beside max = lse (0 for an empty row, whose lse is -inf)."""
-    return torch.where(torch.isneginf(lse), torch.zeros_like(lse), torch.ones_like(lse))
+        return (torch.zeros((rows, host.MLA_C), dtype=torch.float32),
+                torch.full((rows,), float("-inf"), dtype=torch.float32),
+                torch.zeros((rows,), dtype=torch.float32))
+    return host.mla_triple_dense(q_proj.contiguous(), q_pe.contiguous(), c_kv,
+                                 k_pe.contiguous(), [S] * B, scale, False, get_num_threads())

@@ -174,23 +174,58 @@ inline uint16_t to_out(float v, uint16_t*) {
   return (uint16_t)(u >> 16);
 }
 
-// Final (out, lse) of H heads from a state; o_at(h, s) reads o in staging
-// order (kStaged) or in column order, out_row(h) is head h's output row (Dv
-// values of OutT: fp32, or bf16 as uint16_t).
-template <class OutT, bool kStaged = true, class OAt, class OutRow>
-void write_final(const float* base, int H, int Dv, float* lse, OAt o_at, OutRow out_row) {
+// Where a call's rows go: the (out, lse) form, or the reference CPU kernel's
+// triple (out, max, sum) (kernel/cpu_attn.cpp:540-567): max the row's largest
+// scaled score in natural-log units, sum the sum of exp(score - max), out
+// divided by sum when `normalize` (fused_cpu_attn) or not (fused_cpu_attn_mla,
+// _mla_compressed).  Output row i of a call is out + i * Dv, lse[i] / mx[i] /
+// sm[i].
+template <class OutT>
+struct Sink {
+  OutT* out;
+  float* lse;      // (out, lse) form; nullptr selects the triple form
+  float* mx;       // triple form
+  float* sm;
+  bool normalize;  // triple form: out / sum
+  bool ok() const { return out && (lse || (mx && sm)); }
+};
+
+template <class OutT>
+void write_empty(const Sink<OutT>& k, size_t row0, int H, int Dv) {
+  std::memset(k.out + row0 * Dv, 0, sizeof(OutT) * H * Dv);
   for (int h = 0; h < H; ++h) {
+    if (k.lse) {
+      k.lse[row0 + h] = -INFINITY;
+    } else {
+      k.mx[row0 + h] = -INFINITY;
+      k.sm[row0 + h] = 0.f;
+    }
+  }
+}
+
+// Final rows row0 .. row0 + H - 1 of H heads from a state; o_at(h, s) reads o
+// in staging order (kStaged) or in column order.  The state's m is the row
+// max in log2 units (scores scaled by scale * log2(e)) and l the sum of
+// 2^(score - m), which is the sum of exp(natural score - natural max).
+template <class OutT, bool kStaged = true, class OAt>
+void write_final(const float* base, int H, int Dv, const Sink<OutT>& k, size_t row0, OAt o_at) {
+  for (int h = 0; h < H; ++h) {
+    const size_t r = row0 + h;
     const float l = base[H + h];
-    OutT* dst = out_row(h);
+    OutT* dst = k.out + r * Dv;
     if (!(l > 0.f)) {
-      std::memset(dst, 0, sizeof(OutT) * Dv);
-      lse[h] = -INFINITY;
+      write_empty(k, r, 1, Dv);
       continue;
     }
-    const float inv = 1.f / l;
+    const float inv = (k.lse || k.normalize) ? 1.f / l : 1.f;
     for (int s = 0; s < Dv; ++s)
       dst[kStaged ? wh::stage_col(s) : s] = to_out(o_at(h, s) * inv, dst);
-    lse[h] = (base[h] + std::log2(l)) * kLn2;
+    if (k.lse) {
+      k.lse[r] = (base[h] + std::log2(l)) * kLn2;
+    } else {
+      k.mx[r] = base[h] * kLn2;
+      k.sm[r] = l;
+    }
   }
 }
 
@@ -242,8 +277,8 @@ namespace {
 template <class InT, class OutT>
 int attn_partial(const char* fn, const InT* q, const InT* k_pages, const InT* v_pages,
                  const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv, int Dk,
-                 int D, int page_size, int max_pages, int num_pages, float scale, OutT* out,
-                 float* lse, int n_threads) {
+                 int D, int page_size, int max_pages, int num_pages, float scale,
+                 const Sink<OutT>& sink, int n_threads) {
   constexpr bool kF32 = std::is_same_v<InT, float>;
   g_err[0] = '\0';
   if (!isa_ok()) return fail(WH_ENOTSUP, "%s: this CPU lacks AVX-512 F/BW/BF16", fn);
@@ -257,7 +292,7 @@ int attn_partial(const char* fn, const InT* q, const InT* k_pages, const InT* v_
                 "or 192 / 128)",
                 fn, Dk, D, kF32 ? 16 : 32, kF32 ? 16 : 32);
   if (B == 0) return WH_OK;
-  if (!q || !k_pages || !v_pages || !page_table || !lens || !out || !lse)
+  if (!q || !k_pages || !v_pages || !page_table || !lens || !sink.ok())
     return fail(WH_EINVAL, "%s: null pointer", fn);
   if (int rc = check_pages(fn, page_table, lens, B, page_size, max_pages, num_pages)) return rc;
   const int R = B * Hkv;
@@ -280,14 +315,10 @@ int attn_partial(const char* fn, const InT* q, const InT* k_pages, const InT* v_
               });
   };
   auto fin = [&](int r, const float* st) {
-    write_final<OutT, !kF32>(
-        st, G, D, lse + (size_t)r * G, [&](int h, int s) { return st[2 * G + h * D + s]; },
-        [&](int h) { return out + ((size_t)r * G + h) * D; });
+    write_final<OutT, !kF32>(st, G, D, sink, (size_t)r * G,
+                             [&](int h, int s) { return st[2 * G + h * D + s]; });
   };
-  auto empty = [&](int r) {
-    std::memset(out + (size_t)r * G * D, 0, sizeof(OutT) * G * D);
-    for (int h = 0; h < G; ++h) lse[(size_t)r * G + h] = -INFINITY;
-  };
+  auto empty = [&](int r) { write_empty(sink, (size_t)r * G, G, D); };
   run_plan(P, R, G, D, n_threads, row_len.data(), seg, fin, empty,
            [D](size_t i) { return (int)(i / D); });
   return WH_OK;
@@ -297,7 +328,7 @@ template <class OutT>
 int mla_partial(const char* fn, const uint16_t* q_nope, const uint16_t* q_pe,
                 const uint16_t* c_pages, int c_stride, const uint16_t* pe_pages, int pe_stride,
                 const int32_t* page_table, const int32_t* lens, int B, int H, int page_size,
-                int max_pages, int num_pages, float scale, OutT* out, float* lse,
+                int max_pages, int num_pages, float scale, const Sink<OutT>& sink,
                 int n_threads) {
   using namespace wh;
   g_err[0] = '\0';
@@ -309,7 +340,7 @@ int mla_partial(const char* fn, const uint16_t* q_nope, const uint16_t* q_pe,
     return fail(WH_EINVAL, "%s: token strides %d / %d below 512 / 64", fn,
                 c_stride, pe_stride);
   if (B == 0) return WH_OK;
-  if (!q_nope || !q_pe || !c_pages || !pe_pages || !page_table || !lens || !out || !lse)
+  if (!q_nope || !q_pe || !c_pages || !pe_pages || !page_table || !lens || !sink.ok())
     return fail(WH_EINVAL, "%s: null pointer", fn);
   if (int rc = check_pages(fn, page_table, lens, B, page_size, max_pages,
                            num_pages))
@@ -342,14 +373,10 @@ int mla_partial(const char* fn, const uint16_t* q_nope, const uint16_t* q_pe,
               });
   };
   auto fin = [&](int v, const float* st) {
-    write_final<OutT>(
-        st, Hg, Dv, lse + (size_t)v * Hg, [&](int h, int s) { return st[2 * Hg + s * Hg + h]; },
-        [&](int h) { return out + ((size_t)v * Hg + h) * Dv; });
+    write_final<OutT>(st, Hg, Dv, sink, (size_t)v * Hg,
+                      [&](int h, int s) { return st[2 * Hg + s * Hg + h]; });
   };
-  auto empty = [&](int v) {
-    std::memset(out + (size_t)v * Hg * Dv, 0, sizeof(OutT) * Hg * Dv);
-    for (int h = 0; h < Hg; ++h) lse[(size_t)v * Hg + h] = -INFINITY;
-  };
+  auto empty = [&](int v) { write_empty(sink, (size_t)v * Hg, Hg, Dv); };
   run_plan(P, R, Hg, Dv, n_threads, row_len.data(), seg, fin, empty,
            [](size_t i) { return (int)(i % kMlaHeads); });
   return WH_OK;
@@ -361,7 +388,7 @@ extern "C" {
 
 const char* wh_last_error(void) { return g_err; }
 
-const char* wh_version(void) { return "wshost 0.1 avx512bf16"; }
+const char* wh_version(void) { return "wshost 0.2 avx512bf16"; }
 
 int wh_isa_supported(void) { return isa_ok() ? 1 : 0; }
 
@@ -370,7 +397,8 @@ int wh_gqa_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v
                    int D, int page_size, int max_pages, int num_pages, float scale,
                    float* out, float* lse, int n_threads) {
   return attn_partial("wh_gqa_partial", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv, D,
-                      D, page_size, max_pages, num_pages, scale, out, lse, n_threads);
+                      D, page_size, max_pages, num_pages, scale,
+                      Sink<float>{out, lse, nullptr, nullptr, true}, n_threads);
 }
 
 int wh_gqa_partial_bf16(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
@@ -378,7 +406,8 @@ int wh_gqa_partial_bf16(const uint16_t* q, const uint16_t* k_pages, const uint16
                         int D, int page_size, int max_pages, int num_pages, float scale,
                         uint16_t* out, float* lse, int n_threads) {
   return attn_partial("wh_gqa_partial_bf16", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv,
-                      D, D, page_size, max_pages, num_pages, scale, out, lse, n_threads);
+                      D, D, page_size, max_pages, num_pages, scale,
+                      Sink<uint16_t>{out, lse, nullptr, nullptr, true}, n_threads);
 }
 
 int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
@@ -386,7 +415,8 @@ int wh_attn_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* 
                     int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
                     float* out, float* lse, int n_threads) {
   return attn_partial("wh_attn_partial", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv, Dk,
-                      Dv, page_size, max_pages, num_pages, scale, out, lse, n_threads);
+                      Dv, page_size, max_pages, num_pages, scale,
+                      Sink<float>{out, lse, nullptr, nullptr, true}, n_threads);
 }
 
 int wh_attn_partial_f32(const float* q, const float* k_pages, const float* v_pages,
@@ -394,7 +424,27 @@ int wh_attn_partial_f32(const float* q, const float* k_pages, const float* v_pag
                         int Dk, int Dv, int page_size, int max_pages, int num_pages,
                         float scale, float* out, float* lse, int n_threads) {
   return attn_partial("wh_attn_partial_f32", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv,
-                      Dk, Dv, page_size, max_pages, num_pages, scale, out, lse, n_threads);
+                      Dk, Dv, page_size, max_pages, num_pages, scale,
+                      Sink<float>{out, lse, nullptr, nullptr, true}, n_threads);
+}
+
+int wh_attn_triple(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                   const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                   int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
+                   int normalize, float* out, float* row_max, float* row_sum, int n_threads) {
+  return attn_partial("wh_attn_triple", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv, Dk,
+                      Dv, page_size, max_pages, num_pages, scale,
+                      Sink<float>{out, nullptr, row_max, row_sum, normalize != 0}, n_threads);
+}
+
+int wh_attn_triple_f32(const float* q, const float* k_pages, const float* v_pages,
+                       const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
+                       int Dk, int Dv, int page_size, int max_pages, int num_pages, float scale,
+                       int normalize, float* out, float* row_max, float* row_sum,
+                       int n_threads) {
+  return attn_partial("wh_attn_triple_f32", q, k_pages, v_pages, page_table, lens, B, Hq, Hkv,
+                      Dk, Dv, page_size, max_pages, num_pages, scale,
+                      Sink<float>{out, nullptr, row_max, row_sum, normalize != 0}, n_threads);
 }
 
 int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
@@ -403,8 +453,8 @@ int wh_mla_partial(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t*
                    int max_pages, int num_pages, float scale, float* out, float* lse,
                    int n_threads) {
   return mla_partial("wh_mla_partial", q_nope, q_pe, c_pages, c_stride, pe_pages, pe_stride,
-                     page_table, lens, B, H, page_size, max_pages, num_pages, scale, out, lse,
-                     n_threads);
+                     page_table, lens, B, H, page_size, max_pages, num_pages, scale,
+                     Sink<float>{out, lse, nullptr, nullptr, true}, n_threads);
 }
 
 int wh_mla_partial_bf16(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
@@ -414,7 +464,17 @@ int wh_mla_partial_bf16(const uint16_t* q_nope, const uint16_t* q_pe, const uint
                         uint16_t* out, float* lse, int n_threads) {
   return mla_partial("wh_mla_partial_bf16", q_nope, q_pe, c_pages, c_stride, pe_pages,
                      pe_stride, page_table, lens, B, H, page_size, max_pages, num_pages, scale,
-                     out, lse, n_threads);
+                     Sink<uint16_t>{out, lse, nullptr, nullptr, true}, n_threads);
+}
+
+int wh_mla_triple(const uint16_t* q_nope, const uint16_t* q_pe, const uint16_t* c_pages,
+                  int c_stride, const uint16_t* pe_pages, int pe_stride,
+                  const int32_t* page_table, const int32_t* lens, int B, int H, int page_size,
+                  int max_pages, int num_pages, float scale, int normalize, float* out,
+                  float* row_max, float* row_sum, int n_threads) {
+  return mla_partial("wh_mla_triple", q_nope, q_pe, c_pages, c_stride, pe_pages, pe_stride,
+                     page_table, lens, B, H, page_size, max_pages, num_pages, scale,
+                     Sink<float>{out, nullptr, row_max, row_sum, normalize != 0}, n_threads);
 }
 
 double wh_host_read_gbs(size_t bytes, int n_threads, int reps) {

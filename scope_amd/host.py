@@ -34,7 +34,8 @@ LIB_PATH = os.path.join(_HERE, "lib", "libwshost.so")
 # Entry points declared in include/wshost.h.
 EXPORTS = ("wh_last_error", "wh_version", "wh_isa_supported", "wh_gqa_partial",
            "wh_gqa_partial_bf16", "wh_attn_partial", "wh_attn_partial_f32", "wh_host_read_gbs",
-           "wh_mla_partial", "wh_mla_partial_bf16")
+           "wh_mla_partial", "wh_mla_partial_bf16", "wh_attn_triple", "wh_attn_triple_f32",
+           "wh_mla_triple")
 
 MLA_HEADS = 16
 MLA_C = 512
@@ -79,6 +80,13 @@ def lib() -> ctypes.CDLL:
                                                                                      vp, i32]
         L.wh_mla_partial_bf16.restype = i32
         L.wh_mla_partial_bf16.argtypes = L.wh_mla_partial.argtypes
+        for name in ("wh_attn_triple", "wh_attn_triple_f32"):
+            getattr(L, name).restype = i32
+            getattr(L, name).argtypes = [vp, vp, vp, vp, vp] + [i32] * 8 + [f32, i32, vp, vp,
+                                                                             vp, i32]
+        L.wh_mla_triple.restype = i32
+        L.wh_mla_triple.argtypes = [vp, vp, vp, i32, vp, i32, vp, vp] + [i32] * 5 + [
+            f32, i32, vp, vp, vp, i32]
         _lib = L
     return _lib
 
@@ -222,6 +230,65 @@ def attn_partial(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, 
               table.shape[1], num_pages, ctypes.c_float(scale), _p(out), _p(lse),
               int(threads)))
     return out, lse
+
+
+def attn_triple(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, page_table,
+                lens, scale: float, normalize: bool, threads: int = 0):
+    """The reference CPU kernel's triple over paged pools (wh_attn_triple /
+    _f32): fp32 (out [B, Hq, Dv], row_max [B, Hq], row_sum [B, Hq]) with
+    row_max the largest scaled score, row_sum the sum of exp(score - row_max)
+    and out divided by row_sum when `normalize`.  Shapes and dtypes as
+    attn_partial."""
+    B, Hq, Dk = q.shape
+    dt = q.dtype if q.dtype in (torch.bfloat16, torch.float32) else torch.bfloat16
+    _cpu(q, dt, "q")
+    _cpu(k_pages, dt, "k_pages")
+    _cpu(v_pages, dt, "v_pages")
+    if k_pages.dim() != 4 or v_pages.dim() != 4 or k_pages.shape[:3] != v_pages.shape[:3] \
+            or k_pages.shape[3] != Dk:
+        raise ValueError(f"pools must be [num_pages, Hkv, page_size, Dk / Dv], got "
+                         f"{tuple(k_pages.shape)} / {tuple(v_pages.shape)}")
+    num_pages, Hkv, ps, _ = k_pages.shape
+    Dv = v_pages.shape[3]
+    table = _table(page_table, B)
+    lens = _lens(lens, B)
+    out = torch.empty((B, Hq, Dv), dtype=torch.float32)
+    mx = torch.empty((B, Hq), dtype=torch.float32)
+    sm = torch.empty((B, Hq), dtype=torch.float32)
+    fn = lib().wh_attn_triple_f32 if dt == torch.float32 else lib().wh_attn_triple
+    _check(fn(_p(q), _p(k_pages), _p(v_pages), _p(table), _p(lens), B, Hq, Hkv, Dk, Dv, ps,
+              table.shape[1], num_pages, ctypes.c_float(scale), int(bool(normalize)), _p(out),
+              _p(mx), _p(sm), int(threads)))
+    return out, mx, sm
+
+
+def mla_triple_dense(q_nope: torch.Tensor, q_pe: torch.Tensor, c: torch.Tensor,
+                     pe: torch.Tensor, lens, scale: float, normalize: bool, threads: int = 0):
+    """The reference's MLA triple (wh_mla_triple) over the dense host arrays
+    c [B, cap, 512], pe [B, cap, 64]: fp32 (out [B*H, 512], row_max [B*H],
+    row_sum [B*H]), out unnormalised unless `normalize`."""
+    B, cap, Dc = c.shape
+    _cpu(c, torch.bfloat16, "c")
+    _cpu(pe, torch.bfloat16, "pe")
+    _cpu(q_nope, torch.bfloat16, "q_nope")
+    _cpu(q_pe, torch.bfloat16, "q_pe")
+    rows = q_nope.shape[0]
+    if Dc != MLA_C or tuple(pe.shape) != (B, cap, MLA_PE) or B == 0 or \
+            rows % (B * MLA_HEADS) or tuple(q_nope.shape) != (rows, MLA_C) or \
+            tuple(q_pe.shape) != (rows, MLA_PE):
+        raise ValueError(f"q_nope [B*H, 512], q_pe [B*H, 64], c [B, cap, 512], pe "
+                         f"[B, cap, 64] with H a multiple of 16; got {tuple(q_nope.shape)}, "
+                         f"{tuple(q_pe.shape)}, {tuple(c.shape)}, {tuple(pe.shape)}")
+    table = torch.arange(B, dtype=torch.int32).view(B, 1)
+    lens = _lens(lens, B)
+    out = torch.empty((rows, MLA_C), dtype=torch.float32)
+    mx = torch.empty((rows,), dtype=torch.float32)
+    sm = torch.empty((rows,), dtype=torch.float32)
+    _check(lib().wh_mla_triple(_p(q_nope), _p(q_pe), _p(c), MLA_C, _p(pe), MLA_PE, _p(table),
+                               _p(lens), B, rows // B, max(cap, 1), 1, B,
+                               ctypes.c_float(scale), int(bool(normalize)), _p(out), _p(mx),
+                               _p(sm), int(threads)))
+    return out, mx, sm
 
 
 def gqa_partial_dense(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens, scale: float,

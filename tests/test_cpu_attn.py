@@ -5,7 +5,8 @@ reference kernel, in the reference's own output conventions.
 Bars: float32 outputs within 2e-2 (bf16 inputs) or 1e-4 (float32 inputs) of
 the fp64 closed form; the LSE carried by (max, sum) within 1e-3, or 1e-2
 when max and sum are bf16 (the reference's bf16 triple carries about that
-much itself).  The key property is the drop-in one: triples of two halves of
+much itself); max and sum themselves within 1e-5 / 1e-4 relative of the C
+restatement's and of fp64 brute force (one bf16 step when they are bf16).  The key property is the drop-in one: triples of two halves of
 a sequence, merged by the reference's _pairwise_merge formula and
 normalised, equal attention over the whole sequence.
 """
@@ -95,6 +96,105 @@ def test_fused_cpu_attn_mla_compressed():
                                       bits(pe[b:b + 1]), scale)
         assert_close((o[h] / s[h, None]).numpy(), ow, OUT_ATOL, OUT_RTOL, f"out b={b}")
         assert_close(_lse(m[h], s[h]), lw, LSE_ATOL, LSE_RTOL, f"lse b={b}")
+
+
+def _bf16_round(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def _max_sum_fp64(qf, kf, scale):
+    """Brute-force row max of q.k * scale and sum of exp(score - max), fp64:
+    q [N, G, D], k [N, S, D]."""
+    sc = np.einsum("ngd,nsd->ngs", qf.astype(np.float64), kf.astype(np.float64)) * scale
+    mx = sc.max(-1)
+    return mx, np.exp(sc - mx[..., None]).sum(-1)
+
+
+@pytest.mark.parametrize("entry", ["fused_cpu_attn_bf16", "fused_cpu_attn_f32",
+                                   "fused_cpu_attn_fp32", "fused_cpu_attn_mla",
+                                   "fused_cpu_attn_mla_192"])
+def test_max_and_sum_are_the_reference_kernels(entry):
+    """The (max, sum) of every dense entry point are the reference kernel's
+    own values (kernel/cpu_attn.cpp:540-567, 628-635), not an equivalent
+    pair: against the oracle's C restatement of that kernel on the same
+    inputs, and against fp64 brute force.  fp32 outputs: max to 1e-5 and sum
+    to 1e-4 relative; bf16 outputs (fused_cpu_attn on bf16 inputs): each the
+    C restatement's fp32 value rounded to bf16, within one bf16 step (the two
+    fp32 values may straddle a rounding boundary).  The unnormalised out of
+    fused_cpu_attn_mla is within the output bar of the C restatement's."""
+    from oracle import port
+    N, G, S = 5, 4, 613
+    Dk, Dv = (192, 128) if entry == "fused_cpu_attn_mla_192" else (128, 128)
+    f32 = entry in ("fused_cpu_attn_f32", "fused_cpu_attn_fp32")
+    if f32:
+        q, k, v = _f32((N, G, Dk), 50), _f32((N, S, Dk), 51), _f32((N, S, Dv), 52)
+    else:
+        q, k, v = bf16_randn((N, G, Dk), 50), bf16_randn((N, S, Dk), 51), bf16_randn((N, S, Dv), 52)
+    scale = Dk ** -0.5
+    normalize = entry.startswith("fused_cpu_attn_f") or entry == "fused_cpu_attn_bf16"
+    fn = getattr(X, "fused_cpu_attn_mla" if entry.startswith("fused_cpu_attn_mla")
+                 else ("fused_cpu_attn_fp32" if entry == "fused_cpu_attn_fp32"
+                       else "fused_cpu_attn"))
+    o, m, s = fn(q, k, v, scale)
+    po, pm, ps = port.cpu_attn(_np(q), _np(k), _np(v), scale, normalize=normalize,
+                               n_threads=3)
+    qf = q.float().numpy()
+    kf = k.float().numpy()
+    bm, bs = _max_sum_fp64(qf, kf, scale)
+    if entry == "fused_cpu_attn_bf16":
+        assert m.dtype == s.dtype == torch.bfloat16
+        for got, want, what in ((m, pm, "max"), (s, ps, "sum")):
+            got = got.float().numpy()
+            step = np.abs(_bf16_round(want)) * 2.0 ** -7
+            assert np.all(np.abs(got - _bf16_round(want)) <= step), what
+            assert np.mean(got == _bf16_round(want)) > 0.9, what
+        assert_close(m.float().numpy()[..., 0], bm, 0, 2.0 ** -8, "max vs fp64")
+        assert_close(s.float().numpy()[..., 0], bs, 0, 2.0 ** -7, "sum vs fp64")
+        return
+    assert m.dtype == s.dtype == torch.float32
+    assert_close(m.numpy(), pm, 1e-5, 1e-5, "max vs C restatement")
+    assert_close(s.numpy(), ps, 0, 1e-4, "sum vs C restatement")
+    assert_close(m.numpy()[..., 0], bm, 1e-5, 1e-5, "max vs fp64")
+    assert_close(s.numpy()[..., 0], bs, 0, 1e-4, "sum vs fp64")
+    tol = 1e-4 if f32 else OUT_ATOL
+    scale_o = 1.0 if normalize else np.abs(po).max()
+    assert_close(o.numpy() / scale_o, po / scale_o, tol, tol, "out vs C restatement")
+
+
+def test_max_and_sum_of_mla_compressed_are_the_reference_kernels():
+    """fused_cpu_attn_mla_compressed's (max, sum) (kernel/cpu_attn.cpp:1001-1021)
+    against the C restatement and fp64 brute force over the 576-wide score;
+    the unnormalised out against the C restatement's."""
+    from oracle import port
+    B, H, S = 3, 16, 517
+    qp_, qr = bf16_randn((B * H, 512), 60, 0.5), bf16_randn((B * H, 64), 61, 0.5)
+    c, pe = bf16_randn((B, S, 512), 62, 0.5), bf16_randn((B, S, 64), 63, 0.5)
+    scale = 192 ** -0.5
+    o, m, s = X.fused_cpu_attn_mla_compressed(qp_, qr, c, pe, scale)
+    po, pm, ps = port.cpu_attn_mla_compressed(bits(qp_), bits(qr), bits(c), bits(pe), scale,
+                                              n_threads=3)
+    assert_close(m.numpy(), pm, 1e-5, 1e-5, "max vs C restatement")
+    assert_close(s.numpy(), ps, 0, 1e-4, "sum vs C restatement")
+    qf = torch.cat([qp_, qr], 1).float().numpy().reshape(B, H, 576)
+    kf = torch.cat([c, pe], 2).float().numpy()
+    bm, bs = _max_sum_fp64(qf, kf, scale)
+    assert_close(m.numpy(), bm.reshape(-1), 1e-5, 1e-5, "max vs fp64")
+    assert_close(s.numpy(), bs.reshape(-1), 0, 1e-4, "sum vs fp64")
+    mag = np.abs(po).max()
+    assert_close(o.numpy() / mag, po / mag, OUT_ATOL, OUT_RTOL, "out vs C restatement")
+
+
+def test_max_and_sum_planted_mistakes_fail():
+    """The checks above catch a max kept in log2 units and a sum taken
+    relative to a stale max: both planted in the oracle's brute force, on the
+    CPU."""
+    q, k = bf16_randn((2, 4, 128), 70), bf16_randn((2, 90, 128), 71)
+    _, m, s = X.fused_cpu_attn_mla(q, k, k, 0.1)
+    bm, bs = _max_sum_fp64(q.float().numpy(), k.float().numpy(), 0.1)
+    with pytest.raises(AssertionError):
+        assert_close(m.numpy()[..., 0], bm * 1.4426950408889634, 1e-5, 1e-5, "log2 max")
+    with pytest.raises(AssertionError):
+        assert_close(s.numpy()[..., 0], bs * np.exp(bm - (bm - 0.5)), 0, 1e-4, "stale max")
 
 
 @pytest.mark.parametrize("fn", ["fused_cpu_attn", "fused_cpu_attn_mla", "compressed"])

@@ -128,7 +128,7 @@ def dsv2_batch():
     return lens, lat, qs, ref
 
 
-@pytest.mark.parametrize("r", [0.1, 0.5, 0.9])
+@pytest.mark.parametrize("r", [0.1, 0.3, 0.5, 0.7, 0.9])
 def test_dsv2lite_b32_lognormal_decode_loop(dsv2_batch, r):
     lens, lat, qs, ref = dsv2_batch
     B, H = len(lens), MLA_H

@@ -5,14 +5,16 @@ partition boundary lies: the GPU partial over the trailing floor(r L) tokens
 merged with the host partial over the rest is the same softmax for every r.
 Each case builds the partitioned cache at three shares (data drawn on the
 GPU for speed), runs the fused append + split step, the native host partial
-and the merge, and checks (a) the shares agree with each other, (b) sampled
-rows against fp64 attention over the whole sequence.
+and the merge, and checks (a) the shares agree with each other, outputs and
+merged LSE, (b) every row's output and LSE against the oracle's C restatement
+of the reference CPU kernel over the whole sequence, and sampled rows against
+fp64 attention.
 """
 import numpy as np
 import pytest
 import torch
 
-from helpers import OUT_ATOL, OUT_RTOL, assert_close, bits
+from helpers import LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, assert_close, bits
 from oracle import attn_np as O
 from oracle import port
 from scope_amd import host, ops
@@ -43,7 +45,7 @@ def test_mixtral_b16_full_size_share_invariance():
     q = _randn_bf16((B, Hkv * G, D), gen)
     k_new = torch.stack([x[:, -1:] for x in k])
     v_new = torch.stack([x[:, -1:] for x in v])
-    outs = {}
+    outs, lses = {}, {}
     for r in (0.25, 0.5, 0.75):
         g = [int(np.floor(r * int(L))) for L in lens]
         h = [int(L) - gg for L, gg in zip(lens, g)]
@@ -58,29 +60,35 @@ def test_mixtral_b16_full_size_share_invariance():
             hv[b * Hkv:(b + 1) * Hkv, :h[b]] = v[b][:, :h[b]].cpu()
         st = part.step_split(0, q, k_new, v_new, scale)
         ho, hl = host.gqa_partial_dense(q.cpu(), hk, hv, h, scale, 16)
-        out, _ = ops.merge_split(st, (ho.to(DEV), hl.to(DEV)), ops.PARTIAL_LSE_F32,
-                                 out_dtype=torch.float32)
+        out, lse = ops.merge_split(st, (ho.to(DEV), hl.to(DEV)), ops.PARTIAL_LSE_F32,
+                                   out_dtype=torch.float32)
         torch.cuda.synchronize()
         outs[r] = out.cpu().numpy().reshape(B, Hkv, G, D)
+        lses[r] = lse.cpu().numpy().reshape(B, Hkv, G)
         assert part.lens[0].tolist() == [gg + 1 for gg in g]
     # (a) the boundary does not change the attention
     for r in (0.5, 0.75):
         assert_close(outs[r], outs[0.25], 5e-3, 5e-3, f"share {r} vs 0.25")
+        assert_close(lses[r], lses[0.25], LSE_ATOL, LSE_RTOL, f"share {r} vs 0.25 lse")
     # (b) every row against the oracle's C restatement of the reference CPU
     # kernel (pinned to fp64), sampled rows against fp64, over the whole
     # sequence
     qb = bits(q).reshape(B, Hkv, G, D)
     for b in range(B):
-        po, _, _ = port.cpu_attn(qb[b], bits(k[b]), bits(v[b]), scale, normalize=True,
-                                 n_threads=16)
-        for r, o in outs.items():
-            assert_close(o[b], po, OUT_ATOL, OUT_RTOL, f"r={r} b={b} vs C port")
+        po, pm, ps = port.cpu_attn(qb[b], bits(k[b]), bits(v[b]), scale, normalize=True,
+                                   n_threads=16)
+        pl = (pm + np.log(ps))[..., 0]
+        for r in outs:
+            assert_close(outs[r][b], po, OUT_ATOL, OUT_RTOL, f"r={r} b={b} vs C port")
+            assert_close(lses[r][b], pl, LSE_ATOL, LSE_RTOL, f"r={r} b={b} lse vs C port")
     for b in (0, 5, 13):
         for kvh in (0, 7):
-            want, _ = O.gqa_attention_fp64(qb[b, kvh][None], bits(k[b][kvh:kvh + 1]),
-                                           bits(v[b][kvh:kvh + 1]), scale)
-            for r, o in outs.items():
-                assert_close(o[b, kvh], want[0], OUT_ATOL, OUT_RTOL, f"r={r} b={b} kvh={kvh}")
+            want, wl = O.gqa_attention_fp64(qb[b, kvh][None], bits(k[b][kvh:kvh + 1]),
+                                            bits(v[b][kvh:kvh + 1]), scale)
+            for r in outs:
+                what = f"r={r} b={b} kvh={kvh}"
+                assert_close(outs[r][b, kvh], want[0], OUT_ATOL, OUT_RTOL, what)
+                assert_close(lses[r][b, kvh], wl[0], LSE_ATOL, LSE_RTOL, what + " lse")
 
 
 def test_dsv2lite_mla_b8_full_size_share_invariance():
@@ -92,7 +100,7 @@ def test_dsv2lite_mla_b8_full_size_share_invariance():
     qn = _randn_bf16((B * H, 512), gen, 0.5)
     qp = _randn_bf16((B * H, 64), gen, 0.5)
     new = torch.stack([x[-1:] for x in lat])
-    outs = {}
+    outs, lses = {}, {}
     for r in (0.25, 0.5, 1.0):
         g = int(np.floor(r * L))
         h = L - g
@@ -107,18 +115,33 @@ def test_dsv2lite_mla_b8_full_size_share_invariance():
             hc = torch.stack([x[:h, :512].cpu() for x in lat]).contiguous()
             hpe = torch.stack([x[:h, 512:].cpu() for x in lat]).contiguous()
             ho, hl = host.mla_partial_dense(qn.cpu(), qp.cpu(), hc, hpe, [h] * B, scale, 16)
-            out, _ = ops.merge_split(st, (ho.to(DEV), hl.to(DEV)), ops.PARTIAL_LSE_F32,
-                                     out_dtype=torch.float32)
+            out, lse = ops.merge_split(st, (ho.to(DEV), hl.to(DEV)), ops.PARTIAL_LSE_F32,
+                                       out_dtype=torch.float32)
         else:
-            out, _ = ops.merge_split(st, None, out_dtype=torch.float32)
+            out, lse = ops.merge_split(st, None, out_dtype=torch.float32)
         torch.cuda.synchronize()
         outs[r] = out.cpu().numpy()
+        lses[r] = lse.cpu().numpy()
     for r in (0.5, 1.0):
         assert_close(outs[r], outs[0.25], 5e-3, 5e-3, f"share {r} vs 0.25")
+        assert_close(lses[r], lses[0.25], LSE_ATOL, LSE_RTOL, f"share {r} vs 0.25 lse")
+    # every sequence against the C restatement of fused_cpu_attn_mla_compressed
+    # over all L + 1 tokens (unnormalised out, max, sum -> out / sum, lse)
+    full = np.stack([bits(x) for x in lat])
+    po, pm, ps = port.cpu_attn_mla_compressed(bits(qn), bits(qp), full[:, :, :512],
+                                              full[:, :, 512:], scale, n_threads=16)
+    pl = pm + np.log(ps)
+    po = po / ps[:, None]
+    for r in outs:
+        for b in range(B):
+            rows = slice(b * H, (b + 1) * H)
+            assert_close(outs[r][rows], po[rows], OUT_ATOL, OUT_RTOL, f"r={r} b={b} vs C port")
+            assert_close(lses[r][rows], pl[rows], LSE_ATOL, LSE_RTOL,
+                         f"r={r} b={b} lse vs C port")
     for b in (0, 7):
-        full = bits(lat[b])
         rows = slice(b * H, (b + 1) * H)
-        want, _ = O.mla_attention_fp64(bits(qn[rows]), bits(qp[rows]), full[None, :, :512],
-                                       full[None, :, 512:], scale)
-        for r, o in outs.items():
-            assert_close(o[rows], want, OUT_ATOL, OUT_RTOL, f"r={r} b={b}")
+        want, wl = O.mla_attention_fp64(bits(qn[rows]), bits(qp[rows]), full[b:b + 1, :, :512],
+                                        full[b:b + 1, :, 512:], scale)
+        for r in outs:
+            assert_close(outs[r][rows], want, OUT_ATOL, OUT_RTOL, f"r={r} b={b}")
+            assert_close(lses[r][rows], wl, LSE_ATOL, LSE_RTOL, f"r={r} b={b} lse")
