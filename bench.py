@@ -19,8 +19,9 @@ Reported on one JSON line (stdout):
              (hipEventDisableSystemFence) around every launch of the timed
              region, against the 8 TB/s HBM peak; traffic from the committed rocprofv3
              FETCH_SIZE / WRITE_SIZE summary when one exists for this workload
-  cpu_baseline  the oracle's C restatement of the reference CPU kernel over a
-             bounded sample of the same GPU-share tokens, on the host cores
+  cpu_baseline  the clean-room AVX-512 BF16 host kernel (libwshost.so
+             wh_gqa_partial, the reference CPU kernel's contract) over the same
+             GPU-share tokens, one call per sequence, on pinned host cores
   by_share, kv_len_sweep, mla, mla_kv_len_sweep, single_partition
              the other shares, the Qwen3 length sweep (batch 4, r = 1), the
              absorbed-MLA layer (DeepSeek-V2-Lite, batch 8, L 16384, r 0.5),
@@ -592,25 +593,48 @@ def epilogue_bench(*, B, L, steps, seed, dev, label):
     return res
 
 
-def host_read_gbs(threads, nbytes=1 << 30, reps=5):
+_HOST_BW = {}
+
+
+def host_read_gbs(threads, nbytes=1 << 30, reps=3, probes=5):
     """Host DRAM streaming read bandwidth (wh_host_read_gbs: `threads` OpenMP
-    threads summing a buffer they first touched with 512-bit loads), best of
-    `reps` passes."""
+    threads summing a buffer they first touched with 512-bit loads): the
+    median of `probes` probes, each the best of `reps` passes, measured once
+    per thread count in a run so that every figure of the run is compared
+    with the same number (single probes on these virtual hosts have ranged
+    over 2x within one run)."""
     from scope_amd import host
 
-    return round(host.host_read_gbs(nbytes, threads, reps), 1)
+    if threads not in _HOST_BW:
+        vals = sorted(round(host.host_read_gbs(nbytes, threads, reps), 1)
+                      for _ in range(probes))
+        _HOST_BW[threads] = (float(np.median(vals)), vals)
+    return _HOST_BW[threads][0]
 
 
-def share_model(rows):
+def host_read_probes(threads):
+    """The probes behind host_read_gbs(threads) (after it has run)."""
+    return _HOST_BW.get(threads, (None, []))[1]
+
+
+def share_model(rows, host_bw_gbs=None):
     """Calibrates the share scheduler's roofline model from a share sweep of
     the multi-layer MLA run and compares its per-layer predictions with the
-    measured ones."""
-    from scope_amd.scheduler import ShareScheduler, fit_side
+    measured ones.  Each side is fitted from its own partial's times,
+    bounded by its physical rate (the HBM peak; the host read bandwidth of
+    the run) and with single outlying points left out (a point more than 15%
+    off the fit of the others, e.g. a GPU partial slowed by clocks that
+    dropped while the GPU waited milliseconds for the host side); the
+    residuals and the points left out are reported."""
+    from scope_amd.scheduler import ShareScheduler, fit_side_report
 
     gpts = [(r["gpu_tokens"] * 1152.0, r["gpu_partial_us_per_layer"] * 1e-6) for r in rows]
     hpts = [(r["host_tokens"] * 1152.0, r["host_partial_us_per_layer"] * 1e-6) for r in rows
             if r["host_tokens"] > 0]
-    gpu, hst = fit_side(gpts), fit_side(hpts)
+    gfit = fit_side_report(gpts, max_rate_bps=HBM_PEAK_GBS * 1e9, reject_rel=0.15)
+    hfit = fit_side_report(hpts, max_rate_bps=host_bw_gbs * 1e9 if host_bw_gbs else None,
+                           reject_rel=0.15)
+    gpu, hst = gfit.side, hfit.side
     mixed = [r for r in rows if r["host_tokens"] > 0]
     resid = [r["us_per_layer"] - max(r["gpu_partial_us_per_layer"],
                                      r["host_partial_us_per_layer"]) for r in mixed]
@@ -621,17 +645,25 @@ def share_model(rows):
                            merge_gpu_only_s=(float(np.median(gpu_only_resid)) * 1e-6
                                              if only else 0.0))
     W = rows[0]["layer_bytes"]
+    pred = [sched.predict(r["share"], W)["layer"] * 1e6 for r in rows]
+    share_of = {r["gpu_tokens"] * 1152.0: r["share"] for r in rows}
+    share_of_h = {r["host_tokens"] * 1152.0: r["share"] for r in rows}
     return {
         "gpu_fit": {"fixed_us": round(gpu.fixed_s * 1e6, 1),
-                    "gbs": round(gpu.rate_bps / 1e9, 1)},
+                    "gbs": round(gpu.rate_bps / 1e9, 1),
+                    "bound_gbs": HBM_PEAK_GBS, "rate_capped": gfit.rate_capped,
+                    "shares_left_out": [share_of[b] for b, _ in gfit.rejected]},
         "host_fit": {"fixed_us": round(hst.fixed_s * 1e6, 1),
-                     "gbs": round(hst.rate_bps / 1e9, 1)},
+                     "gbs": round(hst.rate_bps / 1e9, 1),
+                     "bound_gbs": host_bw_gbs, "rate_capped": hfit.rate_capped,
+                     "shares_left_out": [share_of_h[b] for b, _ in hfit.rejected]},
         "xfer_merge_us": round(sched.xfer_s * 1e6, 1),
         "r_balance": round(sched.balance_share(W), 4),
         "r_choice_unbounded": sched.choose(W),
         "shares": [r["share"] for r in rows],
-        "predicted_us": [round(sched.predict(r["share"], W)["layer"] * 1e6, 1) for r in rows],
+        "predicted_us": [round(x, 1) for x in pred],
         "measured_us": [r["us_per_layer"] for r in rows],
+        "rel_error": [round(x / r["us_per_layer"] - 1.0, 3) for x, r in zip(pred, rows)],
     }
 
 
@@ -782,8 +814,9 @@ def share_control_bench(*, B, layers, lens, start_share, budget_frac, steps, see
     lens = [int(x) for x in lens]
     bpt = 1152
     total = sum(lens) * bpt * layers
-    sched = ShareScheduler(gpu=Side(15e-6, 5e12), host=Side(40e-6, 50e9), xfer_s=60e-6,
-                           hbm_budget_bytes=budget_frac * total)
+    sched = ShareScheduler(gpu=Side(15e-6, 5e12, max_rate_bps=HBM_PEAK_GBS * 1e9),
+                           host=Side(40e-6, 50e9, max_rate_bps=host_read_gbs(threads) * 1e9),
+                           xfer_s=60e-6, hbm_budget_bytes=budget_frac * total)
     ctl = ShareController(sched, bpt, layers, PAGE)
     host0 = ctl.targets_for(start_share, lens)
     need_h = sum(-(-L // PAGE) for L in lens) + B  # host pages for any share
@@ -846,7 +879,8 @@ def share_control_bench(*, B, layers, lens, start_share, budget_frac, steps, see
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle's C restatement of the reference CPU kernel
+# CPU baseline: the clean-room AVX-512 BF16 host kernel (libwshost.so), with
+# the oracle's scalar C restatement of the reference CPU kernel beside it
 
 
 def _host_info():
@@ -954,7 +988,7 @@ def cpu_baseline(data, Hkv, G, budget_s, threads):
         "value": round(gbs, 2),
         "unit": "GB/s",
         "cores": threads,
-        "kind": "port",
+        "kind": "clean-room",
         "kernel": ("wh_gqa_partial: clean-room AVX-512 BF16 / OpenMP implementation of the "
                    "reference CPU kernel's contract (fused_cpu_attn, kernel/cpu_attn.cpp:"
                    "572-636), libwshost.so"),
@@ -965,6 +999,7 @@ def cpu_baseline(data, Hkv, G, budget_s, threads):
                    f"of {len(passes)} passes after 3 warm-up passes"),
         "us_per_layer_equiv": round(t * 1e6, 1),
         "host_read_gbs": bw,
+        "host_read_probes_gbs": host_read_probes(threads),
         "frac_of_host_read": round(gbs / bw, 3) if bw else None,
         "oracle_port_gbs": round(port_bytes / port_s / 1e9, 2) if port_s > 0 else None,
         "oracle_port_sample": f"{n_port} calls of the oracle's scalar C restatement, "
@@ -1208,6 +1243,7 @@ def main():
         for r in hp:
             r.update(hinfo)
             r["host_read_gbs"] = bw
+            r["host_read_probes_gbs"] = host_read_probes(th)
             r["frac_of_host_read"] = round(r["gbs"] / bw, 3)
             log(f"host partial {r['label']}: {r['us']} us = {r['gbs']} GB/s on {th} threads "
                 f"({r['frac_of_host_read']:.0%} of the {bw} GB/s host read bandwidth)")
@@ -1230,7 +1266,7 @@ def main():
         extra["mla_model"] = {"lens_seed": args.seed + 5, "lens": m_lens.tolist(),
                               "length_model": "lognormal(ln 4096, 1.0) clipped [256, 65536]",
                               "by_share": rows,
-                              "scheduler": share_model(rows)}
+                              "scheduler": share_model(rows, host_read_gbs(th))}
         sc = share_control_bench(B=32, layers=args.model_layers, lens=m_lens, start_share=0.1,
                                  budget_frac=0.5, steps=10, seed=args.seed + 23, dev=dev,
                                  threads=th, label="dsv2lite_mla_b32_share_control")
@@ -1247,7 +1283,8 @@ def main():
         sm = extra["mla_model"]["scheduler"]
         log(f"share model: gpu {sm['gpu_fit']}, host {sm['host_fit']}, r_balance "
             f"{sm['r_balance']}, predicted/measured us per layer "
-            f"{list(zip(sm['predicted_us'], sm['measured_us']))}")
+            f"{list(zip(sm['predicted_us'], sm['measured_us']))}, relative error "
+            f"{sm['rel_error']}")
 
     if "epilogue" in W:
         ep = [epilogue_bench(B=8, L=8192, steps=args.steps, seed=args.seed + 19, dev=dev,

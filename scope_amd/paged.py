@@ -459,13 +459,16 @@ class _PagedTwoSided:
 
     # -- decode-step plumbing -----------------------------------------------
 
-    def _pinned(self, name, shape, dtype):
-        """A pinned host buffer of the cache, allocated once per (name, shape).
-        One buffer per role is enough: every host partial waits for the
-        query copy of its own layer, which the stream orders after the
-        previous layer's merge, the last reader of the same buffers."""
+    def _pinned(self, name, shape, dtype, stream=0):
+        """A pinned host buffer of the cache, allocated once per (name, shape,
+        stream).  One buffer per role and stream is enough: every host
+        partial waits for the query copy of its own layer, which its stream
+        orders after the previous layer's merge on that stream, the last
+        reader of the same buffers.  Layers run on different streams get
+        different buffers, since nothing orders one stream's merge before
+        another stream's next host partial."""
         bufs = self.__dict__.setdefault("_pin_bufs", {})
-        key = (name, tuple(shape), dtype)
+        key = (name, tuple(shape), dtype, stream)
         t = bufs.get(key)
         if t is None:
             t = torch.empty(shape, dtype=dtype, pin_memory=True)
@@ -516,11 +519,13 @@ class _PagedTwoSided:
         a.max_len, a.n_splits = max_len, nwg
         a.out_g, a.lse_g = out_g.data_ptr(), lse_g.data_ptr()
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        dev = self.gpu.device
+        sk = torch.cuda.current_stream(dev).cuda_stream if dev.type == "cuda" else 0
         for name, shape in q_bufs:
-            setattr(a, name, self._pinned(name, shape, torch.bfloat16).data_ptr())
+            setattr(a, name, self._pinned(name, shape, torch.bfloat16, sk).data_ptr())
         a.host_threads = int(threads)
-        a.out_h = self._pinned("out", out_shape, torch.bfloat16).data_ptr()
-        a.lse_h = self._pinned("lse", (rows,), torch.float32).data_ptr()
+        a.out_h = self._pinned("out", out_shape, torch.bfloat16, sk).data_ptr()
+        a.lse_h = self._pinned("lse", (rows,), torch.float32, sk).data_ptr()
 
     def _run_layer(self, layer: int, fn, a, dev) -> None:
         """Runs the layer driver; the device lengths advanced as soon as the
@@ -605,17 +610,59 @@ class _PagedTwoSided:
         targets = ctl.decide(lens, host_now, moving=self._move is not None)
         if targets is None:
             return
-        r0, r1 = ctl.share_of(lens, host_now), ctl.share_of(lens, targets)
-        if self.async_moves:
-            t0 = time.perf_counter()
-            if self.begin_boundaries(targets):
-                self._move.info = (ctl.steps, r0, r1, t0, time.perf_counter() - t0)
+        r0, want = ctl.share_of(lens, host_now), ctl.share_of(lens, targets)
+        # what the pools and the partition can take now, one GPU page per
+        # sequence kept free for the appends of the next steps
+        targets = self.feasible_targets(targets, gpu_reserve=self.batch)
+        r1 = ctl.share_of(lens, targets)
+        if r1 != want:
+            ctl.amend_last_share(r1)
+        if targets == host_now:
+            ctl.record_skip(r0, want, "no free pages for the move")
             return
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        self.set_boundaries(targets)
+        # the step's outputs are already queued: a move that cannot start is
+        # recorded and skipped, never raised out of the step
+        try:
+            if self.async_moves:
+                t0 = time.perf_counter()
+                if self.begin_boundaries(targets):
+                    self._move.info = (ctl.steps, r0, r1, t0, time.perf_counter() - t0)
+                return
+            if self.gpu.device.type == "cuda":
+                torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            self.set_boundaries(targets)
+        except (MemoryError, ValueError) as e:
+            ctl.amend_last_share(r0)
+            ctl.record_skip(r0, r1, str(e))
+            return
         pages = sum(abs(t - h) for t, h in zip(targets, host_now)) // self.page_size
         ctl.record_move(r0, r1, pages, time.perf_counter() - t0)
+
+    def feasible_targets(self, targets, gpu_reserve: int = 0) -> list:
+        """targets[b] host tokens, each move cut down to what can start now:
+        a move toward the GPU by the free GPU pages (less gpu_reserve) and the
+        sequence's partition capacity, a move toward the host by the free host
+        pages, sequence by sequence in order.  (Pages a move frees come back
+        only at its switch, so they do not count.)"""
+        ps = self.page_size
+        g = self.gpu
+        free_g = g.pool.free - gpu_reserve
+        free_h = self.host.pool.free
+        out = []
+        for b, hn in enumerate(targets):
+            h, hn = int(self.host.lens[b]), int(hn)
+            if hn < h:
+                k = min((h - hn) // ps, max(0, free_g), g.max_pages - int(g._pages_held[b]))
+                k = max(0, k)
+                free_g -= k
+                hn = h - k * ps
+            elif hn > h:
+                k = min((hn - h) // ps, max(0, free_h))
+                free_h -= k
+                hn = h + k * ps
+            out.append(hn)
+        return out
 
 
 class PagedMlaCache(_PagedTwoSided):

@@ -34,12 +34,20 @@ from dataclasses import dataclass, field
 
 @dataclass
 class Side:
-    """Affine time model of one partial: seconds = fixed + bytes / rate."""
+    """Affine time model of one partial: seconds = fixed + bytes / rate.
+
+    max_rate_bps, when set, is the side's physical bound (the HBM peak for
+    the GPU partial, the measured host read bandwidth for the host partial):
+    no fit or online update takes the rate above it."""
     fixed_s: float
     rate_bps: float
+    max_rate_bps: float | None = None
 
     def time(self, nbytes: float) -> float:
         return self.fixed_s + nbytes / self.rate_bps
+
+    def bounded(self, rate_bps: float) -> float:
+        return rate_bps if self.max_rate_bps is None else min(rate_bps, self.max_rate_bps)
 
 
 @dataclass
@@ -115,25 +123,93 @@ class ShareScheduler:
         if nbytes <= 0 or eff <= 0:
             return
         w = self.ema_weight
-        s.rate_bps = (1.0 - w) * s.rate_bps + w * (nbytes / eff)
+        s.rate_bps = s.bounded((1.0 - w) * s.rate_bps + w * s.bounded(nbytes / eff))
         self.history.append((side, nbytes, seconds))
 
 
-def fit_side(points) -> Side:
-    """Least-squares affine fit seconds = fixed + bytes / rate over
-    (bytes, seconds) points (at least two distinct byte counts)."""
-    pts = [(float(b), float(t)) for b, t in points if b > 0]
-    if len(pts) < 2 or len({b for b, _ in pts}) < 2:
-        raise ValueError("need two or more distinct byte counts to fit a side")
+@dataclass
+class SideFit:
+    """A fitted side with the points it kept and the ones it left out."""
+    side: Side
+    used: list            # (bytes, seconds) points of the final fit
+    rejected: list        # points dropped as outliers
+    rate_capped: bool     # the least-squares rate exceeded max_rate_bps
+
+
+def _affine(pts, max_rate_bps, min_fixed_s):
+    """seconds = fixed + bytes / rate over pts by least squares, the rate
+    capped at max_rate_bps (the intercept then refitted as the median
+    residual) and the intercept floored at min_fixed_s (the slope then
+    refitted through it)."""
     n = len(pts)
     mb = sum(b for b, _ in pts) / n
     mt = sum(t for _, t in pts) / n
     sbb = sum((b - mb) ** 2 for b, _ in pts)
-    sbt = sum((b - mb) * (t - mt) for b, t in pts)
-    slope = sbt / sbb
+    slope = sum((b - mb) * (t - mt) for b, t in pts) / sbb
     if slope <= 0:
         raise ValueError("time does not grow with bytes; cannot fit a rate")
-    return Side(fixed_s=max(0.0, mt - slope * mb), rate_bps=1.0 / slope)
+    fixed = mt - slope * mb
+    capped = max_rate_bps is not None and 1.0 / slope > max_rate_bps
+    if capped:
+        slope = 1.0 / max_rate_bps
+        res = sorted(t - b * slope for b, t in pts)
+        fixed = 0.5 * (res[(n - 1) // 2] + res[n // 2])
+    if fixed < min_fixed_s:
+        fixed = min_fixed_s
+        slope = sum(b * (t - fixed) for b, t in pts) / sum(b * b for b, _ in pts)
+        if slope <= 0:
+            raise ValueError("time does not grow with bytes; cannot fit a rate")
+        if max_rate_bps is not None and 1.0 / slope > max_rate_bps:
+            slope, capped = 1.0 / max_rate_bps, True
+    return Side(fixed_s=fixed, rate_bps=1.0 / slope, max_rate_bps=max_rate_bps), capped
+
+
+def fit_side_report(points, max_rate_bps: float | None = None, min_fixed_s: float = 0.0,
+                    reject_rel: float | None = None) -> SideFit:
+    """Affine fit seconds = fixed + bytes / rate over (bytes, seconds) points,
+    physically bounded and robust to single bad points.
+
+    max_rate_bps caps the rate (a slope flatter than the hardware allows is a
+    measurement artefact, e.g. a short partial slowed by idle clocks making a
+    long one look fast); min_fixed_s floors the intercept (the launch floor).
+    With reject_rel, one point at a time is left out while more than three
+    remain: the one whose removal lets the fit explain the others best
+    (smallest largest relative error), if the fit of the others misses it by
+    more than reject_rel of its own time.  Judging each point by a fit that
+    excludes it keeps a single bad point from dragging the line towards
+    itself and getting good points rejected instead."""
+    pts = [(float(b), float(t)) for b, t in points if b > 0]
+    if len(pts) < 2 or len({b for b, _ in pts}) < 2:
+        raise ValueError("need two or more distinct byte counts to fit a side")
+    rejected = []
+    side, capped = _affine(pts, max_rate_bps, min_fixed_s)
+    while reject_rel is not None and len(pts) > 3:
+        best = None
+        for i in range(len(pts)):
+            rest = pts[:i] + pts[i + 1:]
+            if len({b for b, _ in rest}) < 2:
+                continue
+            try:
+                s_i, c_i = _affine(rest, max_rate_bps, min_fixed_s)
+            except ValueError:
+                continue
+            fit_err = max(abs(t - s_i.time(b)) / t for b, t in rest)
+            b_i, t_i = pts[i]
+            cand = (fit_err, i, s_i, c_i, abs(t_i - s_i.time(b_i)) / t_i)
+            if best is None or cand[0] < best[0]:
+                best = cand
+        if best is None or best[4] <= reject_rel:
+            break
+        rejected.append(pts.pop(best[1]))
+        side, capped = best[2], best[3]
+    return SideFit(side, pts, rejected, capped)
+
+
+def fit_side(points, max_rate_bps: float | None = None, min_fixed_s: float = 0.0,
+             reject_rel: float | None = None) -> Side:
+    """The side of fit_side_report: least squares by default, bounded and
+    outlier-robust when asked."""
+    return fit_side_report(points, max_rate_bps, min_fixed_s, reject_rel).side
 
 
 # --------------------------------------------------------------------------
@@ -191,6 +267,8 @@ class ShareController:
         self.moves: list[ShareMove] = []
         self.shares: list[float] = []   # share after each decide()
         self.chosen: list[float] = []   # the scheduler's choice at each decide()
+        # moves decided but not made: (step, share_from, share_wanted, reason)
+        self.skipped: list[tuple] = []
 
     def observe_layer(self, gpu_bytes: float, gpu_s: float, host_bytes: float,
                       host_s: float) -> None:
@@ -242,6 +320,17 @@ class ShareController:
             return None
         self.shares.append(self.share_of(lens, targets))
         return targets
+
+    def amend_last_share(self, r: float) -> None:
+        """The share the last decide() led to, when the cache could make only
+        part of the move (or none of it)."""
+        if self.shares:
+            self.shares[-1] = r
+
+    def record_skip(self, share_from: float, share_wanted: float, reason: str) -> None:
+        """A move decided after step self.steps that the cache could not start
+        (pools or partition full); the decode step itself went on."""
+        self.skipped.append((self.steps, share_from, share_wanted, reason))
 
     def record_move(self, share_from: float, share_to: float, pages: int,
                     seconds: float, stall_seconds: float | None = None,

@@ -273,3 +273,71 @@ def test_a_move_whose_copies_fail_gives_its_pages_back():
     assert not cache.moving and (cache.gpu.pool.free, cache.host.pool.free) == free
     _check_accounting(cache)
     _check_tokens(cache, data)
+
+
+def _controlled(cache, budget_bytes=None):
+    """A share controller on `cache` with the per-layer timing left out (no
+    GPU here): _step_done() is the controller's part of a decode step."""
+    from scope_amd.scheduler import ShareController, ShareScheduler, Side
+
+    sched = ShareScheduler(gpu=Side(1e-6, 6e12, max_rate_bps=8e12), host=Side(1e-6, 1e11),
+                           hbm_budget_bytes=budget_bytes)
+    ctl = ShareController(sched, 1152, cache.num_layers, cache.page_size)
+    cache.controller, cache.async_moves = ctl, False
+    cache._layer_log, cache._step_end = [], None
+    return ctl
+
+
+def test_controller_moves_are_cut_to_the_free_pages_and_never_raise():
+    """GPU pool sized exactly to the loaded layout plus 4 pages: the scheduler
+    wants everything in HBM (no budget, a fast GPU), which needs 9 more GPU
+    pages.  The move is cut to the free pages less one page per sequence
+    kept for appends, the tokens survive bit for bit, and the controller
+    records the share actually reached; with no page to spare the move is
+    skipped and recorded, and a move that fails to start is recorded too,
+    without raising out of the step."""
+    layers = 2
+    lens, hosts = [4 * PS + 3, 3 * PS + 5, 2 * PS], [3 * PS, 3 * PS, 2 * PS]
+    gpu_need = sum(-(-(L - h) // PS) for L, h in zip(lens, hosts))
+    cache, data = _mla_cache_with(lens, hosts, layers, 6 * PS, gpu_pages=gpu_need + 4)
+    ctl = _controlled(cache)
+    cache._step_done()
+    # 4 free GPU pages, 3 kept for appends: one page moves up (sequence 0's)
+    assert [cache.host_tokens(b) for b in range(3)] == [2 * PS, 3 * PS, 2 * PS]
+    assert cache.gpu.pool.free == 3
+    assert len(ctl.moves) == 1 and ctl.moves[0].pages == 1
+    assert ctl.shares[-1] == pytest.approx(ctl.share_of(lens, [2 * PS, 3 * PS, 2 * PS]))
+    _check_accounting(cache)
+    _check_tokens(cache, data)
+    # no GPU page to spare: skipped, recorded, nothing moves
+    cache._step_done()
+    assert [cache.host_tokens(b) for b in range(3)] == [2 * PS, 3 * PS, 2 * PS]
+    assert len(ctl.moves) == 1 and len(ctl.skipped) == 1
+    assert ctl.shares[-1] == pytest.approx(ctl.share_of(lens, [2 * PS, 3 * PS, 2 * PS]))
+    # a move that fails to start is recorded as skipped, not raised
+    cache.feasible_targets = lambda t, gpu_reserve=0: [PS, 3 * PS, 2 * PS]
+
+    def refuse(targets):
+        raise MemoryError("pool exhausted")
+    cache.set_boundaries = refuse
+    cache._step_done()
+    assert len(ctl.skipped) == 2 and "pool exhausted" in ctl.skipped[-1][3]
+    assert ctl.shares[-1] == pytest.approx(ctl.share_of(lens, [2 * PS, 3 * PS, 2 * PS]))
+    _check_accounting(cache)
+    _check_tokens(cache, data)
+
+
+def test_feasible_targets_respect_capacity_and_host_pool():
+    layers = 1
+    lens, hosts = [5 * PS, 2 * PS], [4 * PS, 0]
+    cache, _ = _mla_cache_with(lens, hosts, layers, 5 * PS, host_pages=5, gpu_pages=20)
+    # sequence 0 can take 4 pages up; sequence 1 wants 2 pages down but the
+    # host pool has 1 free page
+    assert cache.feasible_targets([0, 2 * PS]) == [0, PS]
+    # the partition capacity (5 pages per sequence) caps a move up
+    cache.gpu.max_pages = 3
+    assert cache.feasible_targets([0, 0], gpu_reserve=0) == [2 * PS, 0]
+    # the GPU reserve leaves pages free
+    cache.gpu.max_pages = 5
+    free = cache.gpu.pool.free
+    assert cache.feasible_targets([0, 0], gpu_reserve=free - 1) == [3 * PS, 0]

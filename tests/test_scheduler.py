@@ -4,7 +4,8 @@ r and against closed forms."""
 import numpy as np
 import pytest
 
-from scope_amd.scheduler import ShareController, ShareScheduler, Side, fit_side
+from scope_amd.scheduler import (ShareController, ShareScheduler, Side, fit_side,
+                                 fit_side_report)
 
 
 def _sched(**kw):
@@ -55,6 +56,68 @@ def test_granularity_rounds_down_within_capacity():
     assert r <= s.capacity_share(1e9, 4)
     s = _sched(hbm_budget_bytes=3e9)     # capacity share 0.75 is on the grid
     assert s.choose(1e9, 4, granularity=0.125) == pytest.approx(0.75)
+
+
+# A measured share sweep of the 27-layer DeepSeek-V2-Lite decode (B 32,
+# lognormal lengths, 16 host threads) on one MI355X box: tokens on each side
+# and the per-layer times of each partial and of the whole layer, at shares
+# 0.1, 0.3, 0.5, 0.7, 0.9 and 1.0.  Its r = 0.1 point is slow on both sides:
+# the GPU partial (30 MB in 37.9 us, 790 GB/s) ran on clocks that dropped
+# while the GPU waited ~3 ms per layer for the host, and the host partial ran
+# at 94 GB/s against 139-151 GB/s at the neighbouring shares.
+SWEEP_GPU_TOKENS = [26008, 78052, 130105, 182142, 234186, 260221]
+SWEEP_GPU_US = [37.9, 26.9, 36.2, 45.8, 54.9, 59.5]
+SWEEP_HOST_TOKENS = [234213, 182169, 130116, 78079, 26035]
+SWEEP_HOST_US = [2876.2, 1393.6, 1019.2, 647.7, 276.1]
+SWEEP_LAYER_US = [3129.4, 1455.4, 1075.7, 698.6, 325.8, 68.7]
+SWEEP_SHARES = [0.1, 0.3, 0.5, 0.7, 0.9, 1.0]
+SWEEP_HOST_READ_GBS = 202.2
+
+
+def test_bounded_fit_of_a_measured_sweep_stays_physical():
+    """The plain least-squares fit of the sweep's GPU points gives a rate
+    above the 8 TB/s HBM peak (9.8 TB/s); the bounded, outlier-robust fit
+    leaves the r = 0.1 points out, keeps both rates below their physical
+    bounds and predicts every other share's layer time within 10%."""
+    gpts = [(t * 1152.0, u * 1e-6) for t, u in zip(SWEEP_GPU_TOKENS, SWEEP_GPU_US)]
+    hpts = [(t * 1152.0, u * 1e-6) for t, u in zip(SWEEP_HOST_TOKENS, SWEEP_HOST_US)]
+    assert fit_side(gpts).rate_bps > 8e12  # the unbounded fit is unphysical
+    g = fit_side_report(gpts, max_rate_bps=8e12, reject_rel=0.15)
+    h = fit_side_report(hpts, max_rate_bps=SWEEP_HOST_READ_GBS * 1e9, reject_rel=0.15)
+    assert g.side.rate_bps <= 8e12 and h.side.rate_bps <= SWEEP_HOST_READ_GBS * 1e9
+    assert g.rejected == [gpts[0]] and h.rejected == [hpts[0]]
+    assert 6.0e12 < g.side.rate_bps < 7.0e12 and 150e9 < h.side.rate_bps < 170e9
+    resid = [m - max(a, b) for m, a, b in zip(SWEEP_LAYER_US, SWEEP_GPU_US, SWEEP_HOST_US)]
+    sched = ShareScheduler(gpu=g.side, host=h.side, xfer_s=float(np.median(resid)) * 1e-6,
+                           merge_s=0.0,
+                           merge_gpu_only_s=(SWEEP_LAYER_US[-1] - SWEEP_GPU_US[-1]) * 1e-6)
+    W = sum(SWEEP_GPU_TOKENS[-1:]) * 1152.0
+    for r, m in zip(SWEEP_SHARES[1:], SWEEP_LAYER_US[1:]):
+        assert abs(sched.predict(r, W)["layer"] * 1e6 / m - 1.0) < 0.10, r
+
+
+def test_bounded_fit_caps_the_rate_and_floors_the_intercept():
+    # points on a line steeper than the cap: the rate is the cap, the
+    # intercept the median residual
+    true = Side(5e-6, 10e12)
+    pts = [(b, true.time(b)) for b in (1e8, 2e8, 4e8, 8e8)]
+    r = fit_side_report(pts, max_rate_bps=8e12)
+    assert r.rate_capped and r.side.rate_bps == pytest.approx(8e12)
+    assert r.side.max_rate_bps == 8e12
+    # a negative least-squares intercept is floored and the slope refitted
+    pts = [(1e8, 10e-6), (2e8, 30e-6), (3e8, 50e-6)]
+    r = fit_side_report(pts, min_fixed_s=2e-6)
+    assert r.side.fixed_s == pytest.approx(2e-6)
+    assert r.side.time(2e8) == pytest.approx(30e-6, rel=0.15)
+    # an online update cannot take a bounded side above its bound
+    s = ShareScheduler(gpu=Side(0.0, 6e12, max_rate_bps=8e12), host=Side(0, 1e11))
+    for _ in range(50):
+        s.observe("gpu", 1e9, 1e9 / 20e12)
+    assert s.gpu.rate_bps <= 8e12
+    # with three points nothing is rejected; clean points are all kept
+    clean = [(b, Side(1e-5, 5e12).time(b)) for b in (1e8, 2e8, 3e8, 5e8, 8e8)]
+    assert fit_side_report(clean, reject_rel=0.05).rejected == []
+    assert fit_side_report(pts, reject_rel=0.01).rejected == []
 
 
 def test_fit_recovers_affine_sides_and_ema_tracks_rate():
