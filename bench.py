@@ -1021,8 +1021,9 @@ def cpu_baseline(data, Hkv, G, budget_s, threads):
 #   model      27-layer DeepSeek-V2-Lite decode, B32 lognormal, every share
 #   migrate    boundary movement of a paged two-sided MLA cache (4 layers, B32)
 #   epilogue   MLA merge + W_UV: fused kernel against merge then bmm
-WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "host", "model", "migrate",
-             "epilogue")
+#   mla128     DeepSeek-V2 (128 heads) B4 L32768, r = 1
+WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "mla128", "host", "model",
+             "migrate", "epilogue")
 # Extra workloads for profiling runs (not in the default set): the MLA layer at
 # B8 L32768, r = 1, on its own.
 EXTRA_WORKLOADS = ("mla32k",)
@@ -1229,6 +1230,20 @@ def main():
             log(f"mla B8 L={Lm}: {res['us_per_layer']} us/layer, partial {res['partial_us']} us "
                 f"= {res['partial_gbs']} GB/s")
         extra["mla_kv_len_sweep"] = msweep
+
+    if "mla128" in W:
+        # DeepSeek-V2 absorbed MLA, 128 heads over the shared latent: the
+        # one-pass HBM time of the latent is the bound the step is compared to
+        res = mla_step_bench(B=4, H=128, lens=[32768] * 4, share=1.0,
+                             steps=max(10, args.steps // 2), warmup=args.warmup,
+                             seed=args.seed + 128, dev=dev, label="dsv2_mla_h128_b4_L32768")
+        one_pass = 4 * 32768 * 1152 / (HBM_PEAK_GBS * 1e3)
+        res["one_pass_hbm_us"] = round(one_pass, 2)
+        res["partial_over_one_pass"] = round(res["partial_us"] / one_pass, 2)
+        extra["mla128"] = res
+        log(f"mla H128 B4 L=32768: {res['us_per_layer']} us/layer, partial {res['partial_us']} "
+            f"us = {res['partial_over_one_pass']}x the one-pass HBM time, "
+            f"{res.get('partial_tflops')} TFLOP/s")
 
     th = _host_threads()
     if "host" in W:

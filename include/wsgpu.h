@@ -139,7 +139,8 @@ int ws_latent_append(const uint16_t* c_new, int64_t c_stride,
 
 /*
  * Plan of a decode call: kind 0 (GQA: rows_kv = B * Hkv, heads = the group
- * size G) or 1 (MLA: rows_kv = B, heads = H, a multiple of 16), over sequences of at most
+ * size G) or 1 (MLA: rows_kv = B, heads = H, a multiple of 16; H = 128 with B <= 64
+ * plans sequences with 128-head pieces, other H 16-head groups), over sequences of at most
  * max_len tokens.  n_splits is the number of pieces the call cuts its work
  * into: one per wave for GQA (two per workgroup, each streaming on its
  * own), one per workgroup for MLA.  0 = the library's choice for the current
@@ -284,8 +285,10 @@ int ws_attn_append_decode_partial(const uint16_t* q, const uint16_t* k_new,
  * score = (q_nope . c + q_pe . pe) * scale over the shared 576-wide latent,
  * out = softmax . c (512-wide).  H: any multiple of 16 (16 for
  * DeepSeek-V2-Lite, 128 for DeepSeek-V2; nH = q rows / B as in
- * kernel/cpu_attn.cpp:860); each group of 16 heads is planned as a sequence of
- * its own over the shared latent, and a sequence's new latent is written once.
+ * kernel/cpu_attn.cpp:860).  H = 128 with B <= 64 runs one pass over each
+ * latent block for all 128 heads (a workgroup of four 32-head waves, pieces of
+ * 128 heads); other H plan each group of 16 heads as a sequence of its own
+ * over the shared latent.  A sequence's new latent is written once.
  * Outputs out: [B*H][512] fp32 normalised, lse: [B*H] fp32.
  * Replaces the GPU partial of _mla_compressed_forward
  * (system/deepseek.py:364-392; also roofline/bench_rstar_revalidate_ds2.py:74-86).

@@ -483,10 +483,10 @@ extern "C" int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
   if (kind == 0) {
     n = gqa_splits(n_workgroups, rows_kv, max_len);
     bytes = ws::workspace_bytes(rows_kv, heads, kGqaD, n);
-  } else {  // one plan sequence per (sequence, 16-head group)
-    const int rows = rows_kv * (heads / 16);
-    n = mla_workgroups(n_workgroups, rows, max_len);
-    bytes = ws::workspace_bytes(rows, 16, 512, n);
+  } else {  // one plan sequence per (sequence, 16-head group), or per sequence (wide)
+    const MlaLayout lay = mla_layout(rows_kv, heads);
+    n = mla_workgroups(n_workgroups, lay.plan_seqs, max_len);
+    bytes = ws::workspace_bytes(lay.plan_seqs, lay.piece_heads, 512, n);
   }
   if (n_workgroups_out) *n_workgroups_out = n;
   if (workspace_bytes_out) *workspace_bytes_out = bytes;

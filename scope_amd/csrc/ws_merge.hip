@@ -244,8 +244,9 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
   const int t = threadIdx.x;
   const int b = qrow / p.heads;
   const int h = qrow - b * p.heads;
-  const int pv_seq = qrow >> 4;  // plan sequence (b, 16-head group) and head in it
-  const int h16 = qrow & 15;
+  const int hp = p.heads / p.ng;  // heads of a piece: 16, or 128 (wide layout)
+  const int pv_seq = qrow / hp;   // plan sequence (b, head group) and head in it
+  const int h16 = qrow - pv_seq * hp;
   // The W_UV rows of the first kUvGroup passes do not depend on the merge:
   // their loads go out first and land while the plan and the merge run.
   const int lane8 = t & 7;
@@ -278,13 +279,13 @@ __global__ __launch_bounds__(kUvThreads) void merge_split_uv_kernel(
     const int row_start = s_pref[pv_seq];
     int w_first, nseg;
     plan_row_splits(plan, pv_seq, row_start, nbb, s_wpref, w_first, nseg);
-    if (nseg > 1) {  // pieces hold 16 heads each
+    if (nseg > 1) {  // pieces hold hp heads each
       n = nseg;
-      const size_t slot0 = (size_t)(w_first + pv_seq) * 16 + h16;
+      const size_t slot0 = (size_t)(w_first + pv_seq) * hp + h16;
       pieces = p.part_out + slot0 * p.Dv;
       lsrc = p.part_lse + slot0;
-      sstride = (size_t)16 * p.Dv;
-      lstride = 16;
+      sstride = (size_t)hp * p.Dv;
+      lstride = hp;
     }
   }
   // The merging threads' piece columns are requested with the lse values.
@@ -439,11 +440,12 @@ extern "C" int ws_merge_split(const int32_t* gpu_len, int B, int rows_per_seq, i
     return set_error(WS_EINVAL, "ws_merge_split: null input pointer");
   if (!out_bf16 && !out_f32)
     return set_error(WS_EINVAL, "ws_merge_split: no output");
-  // an absorbed-MLA step with H = 16 ng heads planned (sequence, head group) pairs
-  const int ng = (Dv == 512 && rows_per_seq == 1 && heads > 16 && heads % 16 == 0)
-                     ? heads / 16 : 1;
+  // an absorbed-MLA step with H = 16 ng heads planned (sequence, head group)
+  // pairs, unless its layout is wide (ws_reduce.h mla_layout)
+  const bool mla = Dv == 512 && rows_per_seq == 1 && heads > 16 && heads % 16 == 0;
+  const int ng = mla ? mla_layout(B, heads).ng : 1;
   if (B < 0 || (long long)B * ng > kMaxSeqs || rows_per_seq <= 0 || heads <= 0 ||
-      (heads > 16 && ng == 1) || Dv <= 0 || Dv % 4 || Dv > 512 || page_capacity <= 0 ||
+      (heads > 16 && !mla) || Dv <= 0 || Dv % 4 || Dv > 512 || page_capacity <= 0 ||
       n_workgroups <= 0)
     return set_error(WS_EINVAL, "ws_merge_split: bad sizes");
   const int Bp = B * ng;      // plan sequences
@@ -566,8 +568,9 @@ extern "C" int ws_mla_merge_split_uv(const int32_t* gpu_len, int B, int heads,
       page_capacity <= 0 || n_workgroups <= 0 || Dout <= 0 || Dout % 32 || Dout > 512)
     return set_error(WS_EINVAL, "ws_mla_merge_split_uv: bad sizes B=%d heads=%d Dout=%d", B,
                      heads, Dout);
-  const int ng = heads / 16;
-  const int Bp = B * ng;  // plan sequences (sequence, 16-head group)
+  const MlaLayout lay = mla_layout(B, heads);
+  const int ng = lay.ng;
+  const int Bp = lay.plan_seqs;  // plan sequences (sequence, head group)
   if (b_out && (!b_aux0 || (fmt_has_sum(fmt_b) && !b_aux1)))
     return set_error(WS_EINVAL, "ws_mla_merge_split_uv: host partial without its lse / max / sum");
   if (b_out && !fmt_known(fmt_b))
@@ -579,12 +582,13 @@ extern "C" int ws_mla_merge_split_uv(const int32_t* gpu_len, int B, int heads,
                                          (uintptr_t)w_uv) & 15u ||
       ((uintptr_t)out_latent & 7u) || ((uintptr_t)out_v & 1u))
     return set_error(WS_EINVAL, "ws_mla_merge_split_uv: misaligned buffer");
-  const size_t need = ws::workspace_bytes(Bp, 16, Dv, n_workgroups);
+  const size_t need = ws::workspace_bytes(Bp, lay.piece_heads, Dv, n_workgroups);
   if (workspace_bytes < need)
     return set_error(WS_EWORKSPACE, "ws_mla_merge_split_uv: workspace %zu < %zu bytes",
                      workspace_bytes, need);
   if (B == 0) return WS_OK;
-  const SplitWorkspace w = carve_workspace((void*)workspace, Bp, 16, n_workgroups);
+  const SplitWorkspace w =
+      carve_workspace((void*)workspace, Bp, lay.piece_heads, n_workgroups);
   MergeSplitParams prm;
   prm.gpu_len = gpu_len;
   prm.B = Bp;

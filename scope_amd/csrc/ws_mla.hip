@@ -52,7 +52,9 @@ struct MlaParams {
   float* part_lse;     // [slot][16]
   // B: plan sequences v = b * ng + g, one per (sequence b, 16-head group g);
   // rows of q / out are v * 16 + h, i.e. b * H + 16 g + h with H = 16 ng.
+  // The wide kernel plans sequences (ng = 1) with 128-head rows.
   int B, ng, page_size, max_pages, num_pages, cap;
+  int hp;  // heads of a piece (and of a plan sequence's rows): 16, or 128 (wide)
   float scale_log2;
 };
 
@@ -348,6 +350,12 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
   }
 }
 
+}  // namespace ws
+
+#include "ws_mla_wide.h"
+
+namespace ws {
+
 // Combines the partials of sequences held by several workgroups: one 64-lane
 // workgroup per (head row, 256-column chunk).  Recomputes the decode's plan
 // to find the sequence's workgroups (slots w + b for w in its owner range).
@@ -358,11 +366,11 @@ __global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int g
   __shared__ int s_wpref[kSeqPlanMax + 1];
   __shared__ int s_scan[2];
   __shared__ float s_w[kReduceMaxWeights];
-  const int hrow = blockIdx.x;  // b * 16 + h
+  const int hrow = blockIdx.x;  // b * hp + h
   const int chunk = blockIdx.y;
   const int t = threadIdx.x;
-  const int b = hrow / kMlaH;
-  const int h = hrow - b * kMlaH;
+  const int b = hrow / p.hp;
+  const int h = hrow - b * p.hp;
   const int add = p.c_new ? 1 : 0;
   const Plan plan = plan_build<64>(p.len_in, add, p.cap, p.B, 1, grid, s_pref, s_scan, nullptr,
                                    s_wpref, -1, p.ng);
@@ -371,14 +379,14 @@ __global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int g
   int w_first, n;
   plan_row_splits(plan, b, row_start, row_end - row_start, s_wpref, w_first, n);
   if (n == 1) return;
-  const size_t slot0 = (size_t)(w_first + b) * kMlaH + h;  // partial row of split 0
+  const size_t slot0 = (size_t)(w_first + b) * p.hp + h;  // partial row of split 0
   const int c = chunk * 64 + t;  // float4 column
   // the pieces' columns are requested with their lse values
   uint2 pv[8];
-  if (n <= 8) preload_pieces(p.part_out + slot0 * kMlaC + 4 * c, (size_t)kMlaH * kMlaC, n, pv);
+  if (n <= 8) preload_pieces(p.part_out + slot0 * kMlaC + 4 * c, (size_t)p.hp * kMlaC, n, pv);
   float mx = neg_inf();
   for (int s = t; s < n; s += 64) {
-    const float v = p.part_lse[slot0 + (size_t)s * kMlaH];
+    const float v = p.part_lse[slot0 + (size_t)s * p.hp];
     s_w[s] = v;
     mx = max_nan(mx, v);
   }
@@ -396,7 +404,7 @@ __global__ __launch_bounds__(64) void mla_reduce_kernel(const MlaParams p, int g
   if (n <= 8)
     accum_preloaded(pv, n, s_w, a);
   else
-    accum_pieces(p.part_out + slot0 * kMlaC + 4 * c, (size_t)kMlaH * kMlaC, n, s_w, a);
+    accum_pieces(p.part_out + slot0 * kMlaC + 4 * c, (size_t)p.hp * kMlaC, n, s_w, a);
   const float inv = 1.f / sum;
   ((float4*)(p.out + (size_t)hrow * kMlaC))[c] =
       make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
@@ -429,7 +437,10 @@ static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
     return set_error(WS_EINVAL,
                      "%s: B=%d H=%d unsupported (H a multiple of 16, B * H / 16 <= %d)", name, B,
                      H, kMaxSeqs);
-  const int ng = H / kMlaH;
+  // 128 heads over at most 64 sequences: the wide kernel, one plan sequence
+  // per sequence and 128-head pieces (ws_reduce.h mla_layout)
+  const MlaLayout lay = mla_layout(B, H);
+  const int ng = lay.ng;
   if (page_size <= 0 || max_pages <= 0 || num_pages <= 0 || max_len < 0 ||
       (page_size % 32 && max_pages != 1) ||
       (long long)max_len > (long long)page_size * max_pages)
@@ -448,18 +459,19 @@ static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
   if (len_out && len_out == len_in)
     return set_error(WS_EINVAL, "%s: len_out must not alias len_in", name);
   if (B == 0) return WS_OK;
-  const int Bv = B * ng;  // plan sequences (sequence, head group)
+  const int Bv = lay.plan_seqs;  // plan sequences (sequence, head group)
+  const int hp = lay.piece_heads;
   if ((long long)Bv * ((max_len + 32) / 32) * 4096 >= (1LL << 31))
     return set_error(WS_EINVAL, "%s: %d sequences of %d tokens exceed the block index range",
                      name, Bv, max_len);
   const int n = mla_workgroups(n_workgroups, Bv, max_len);
-  const size_t need = ws::workspace_bytes(Bv, kMlaH, kMlaC, n);
+  const size_t need = ws::workspace_bytes(Bv, hp, kMlaC, n);
   if (!workspace || workspace_bytes < need)
     return set_error(WS_EWORKSPACE, "%s: workspace %zu < %zu bytes", name, workspace_bytes,
                      need);
   if (((uintptr_t)workspace & 255u) != 0)
     return set_error(WS_EINVAL, "%s: workspace must be 256-byte aligned", name);
-  const SplitWorkspace w = carve_workspace(workspace, Bv, kMlaH, n);
+  const SplitWorkspace w = carve_workspace(workspace, Bv, hp, n);
   MlaParams prm;
   prm.q_nope = q_nope;
   prm.q_pe = q_pe;
@@ -478,20 +490,26 @@ static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
   prm.part_lse = w.part_lse;
   prm.B = Bv;
   prm.ng = ng;
+  prm.hp = hp;
   prm.page_size = page_size;
   prm.max_pages = max_pages;
   prm.num_pages = num_pages;
   prm.cap = (int)std::min<long long>((long long)page_size * max_pages, 1LL << 30);
   prm.scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  if (c_new)
+  if (lay.wide) {
+    if (c_new)
+      hipLaunchKernelGGL(mla_wide_kernel<true>, dim3(n), dim3(256), 0, s, prm);
+    else
+      hipLaunchKernelGGL(mla_wide_kernel<false>, dim3(n), dim3(256), 0, s, prm);
+  } else if (c_new) {
     hipLaunchKernelGGL(mla_decode_kernel<true>, dim3(n), dim3(256), 0, s, prm);
-  else
+  } else {
     hipLaunchKernelGGL(mla_decode_kernel<false>, dim3(n), dim3(256), 0, s, prm);
+  }
   int rc = check_launch(name);
   if (rc || n == 1 || !combine) return rc;
-  hipLaunchKernelGGL(mla_reduce_kernel, dim3(Bv * kMlaH, kMlaC / 256), dim3(64), 0, s, prm,
-                     n);
+  hipLaunchKernelGGL(mla_reduce_kernel, dim3(Bv * hp, kMlaC / 256), dim3(64), 0, s, prm, n);
   return check_launch(name);
 }
 

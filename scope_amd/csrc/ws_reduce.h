@@ -49,6 +49,29 @@ __host__ __device__ inline SplitWorkspace carve_workspace(void* base, int rows_k
   return w;
 }
 
+// Layout of an absorbed-MLA call with B sequences of H heads (H a multiple
+// of 16).  H = 128 over at most 64 sequences (DeepSeek-V2) runs the wide
+// kernel (ws_mla_wide.h): its plan sequences are the sequences and a piece
+// holds all 128 heads.  Other head counts plan (sequence, 16-head group)
+// pairs with 16-head pieces.  The step, the merges and the workspace query of
+// a call all take their layout from here, so they agree.
+constexpr int kWideHeads = 128;
+constexpr int kWideMaxSeqs = 64;
+struct MlaLayout {
+  bool wide;
+  int ng;           // plan sequences per sequence
+  int piece_heads;  // heads of one piece
+  int plan_seqs;    // B * ng
+};
+__host__ __device__ inline MlaLayout mla_layout(int B, int H) {
+  MlaLayout l;
+  l.wide = H == kWideHeads && B >= 1 && B <= kWideMaxSeqs;
+  l.ng = l.wide ? 1 : H / 16;
+  l.piece_heads = l.wide ? H : 16;
+  l.plan_seqs = B * l.ng;
+  return l;
+}
+
 // Workgroups of a decode call: n_workgroups, or the library's choice (0):
 // `per_cu` resident workgroups on every CU of the current device, but no more
 // than the call's 32-token blocks can feed with `min_blocks` each.

@@ -125,3 +125,83 @@ def test_paged_mla_cache_128_heads():
         want, wl = _want(qn, qp, [x[:, :512] for x in lat[l]], [x[:, 512:] for x in lat[l]], H)
         assert_close(out.float().cpu().numpy(), want, OUT_ATOL, OUT_RTOL, f"layer {l}")
         assert_close(lse.cpu().numpy(), wl, LSE_ATOL, LSE_RTOL, f"layer {l} lse")
+
+
+@pytest.mark.parametrize("append", [False, True])
+def test_mla_128_heads_scores_climbing_past_the_first_block(append):
+    """128 heads: the rope keys (k_pe, the 64 score-only columns) of every
+    token after each sequence's first 32 are scaled up 1024-fold, so scores
+    climb far above the first block's maximum (by a few hundred in log2
+    units, where probabilities against that maximum would overflow fp32):
+    the segment must run again against its true maximum.  The values (c_kv)
+    keep their N(0, 0.5) scale.  Outputs and LSE against fp64, and the same
+    run unscaled (no climb) alongside."""
+    H = 128
+    lens = [40, 700, 97]
+    B = len(lens)
+    _say(f"mla H=128 climbing scores append={append}")
+    for factor in (1.0, 1024.0):
+        lat_all = []
+        for b, L in enumerate(lens):
+            x = bf16_randn((L + 1, 576), 140 + b, 0.5).float()
+            x[32:, 512:] *= factor
+            lat_all.append(x.to(torch.bfloat16))
+        n_gpu = [L + 1 if append else L for L in lens]
+        lat, pt, gl, _, _ = mla_pool([n + 1 for n in n_gpu], PS, seed=145)
+        for b, L in enumerate(lens):
+            t = torch.arange(L, device=DEV)
+            lat[pt[b, t // PS].long(), t % PS] = lat_all[b][:L].to(DEV)
+        gl.copy_(torch.tensor(lens, dtype=torch.int32, device=DEV))
+        qn = bf16_randn((B * H, 512), 146, 0.5).to(DEV)
+        qp = bf16_randn((B * H, 64), 147, 0.5).to(DEV)
+        if append:
+            new = torch.stack([x[-1] for x in lat_all]).to(DEV)[:, None]
+            len_out = torch.zeros_like(gl)
+            out, lse = ops.mla_append_decode_partial(qn, qp, new[..., :512], new[..., 512:], lat,
+                                                     pt, gl, len_out, SCALE, max(lens) + 1)
+            cs = [x[:, :512] for x in lat_all]
+            pes = [x[:, 512:] for x in lat_all]
+        else:
+            out, lse = ops.mla_decode_partial(qn, qp, lat, pt, gl, SCALE, max(lens))
+            cs = [x[:L, :512] for x, L in zip(lat_all, lens)]
+            pes = [x[:L, 512:] for x, L in zip(lat_all, lens)]
+        torch.cuda.synchronize()
+        want, wl = _want(qn, qp, cs, pes, H)
+        assert np.isfinite(out.cpu().numpy()).all()
+        assert_close(out.cpu().numpy(), want, OUT_ATOL, OUT_RTOL, f"factor {factor} out")
+        assert_close(lse.cpu().numpy(), wl, LSE_ATOL, LSE_RTOL, f"factor {factor} lse")
+
+
+def test_mla_128_heads_b4_every_row_against_the_c_restatement():
+    """DeepSeek-V2 shape, 128 heads, B 4 at 8192 tokens per sequence plus the
+    appended one, split step + merge: every row's output and LSE against
+    the oracle's C restatement of fused_cpu_attn_mla_compressed over all
+    tokens, and the appended latents bit-exact in their pages."""
+    from oracle import port
+    H, B, L = 128, 4, 8192
+    _say("mla H=128 B4 L8192 against the C restatement")
+    gen = torch.Generator(device=DEV).manual_seed(150)
+    lat_all = [(torch.randn((L + 1, 576), generator=gen, device=DEV) * 0.5).to(torch.bfloat16)
+               for _ in range(B)]
+    lat, pt, gl, _, _ = mla_pool([L + 1] * B, PS, seed=151)
+    for b in range(B):
+        t = torch.arange(L, device=DEV)
+        lat[pt[b, t // PS].long(), t % PS] = lat_all[b][:L]
+    gl.fill_(L)
+    qn = (torch.randn((B * H, 512), generator=gen, device=DEV) * 0.5).to(torch.bfloat16)
+    qp = (torch.randn((B * H, 64), generator=gen, device=DEV) * 0.5).to(torch.bfloat16)
+    new = torch.stack([x[-1] for x in lat_all])[:, None]
+    len_out = torch.zeros_like(gl)
+    st = ops.mla_append_decode_split(qn, qp, new[..., :512], new[..., 512:], lat, pt, gl, len_out,
+                                     SCALE, L + 1)
+    out, lse = ops.merge_split(st, None, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    full = np.stack([bits(x) for x in lat_all])
+    po, pm, ps = port.cpu_attn_mla_compressed(bits(qn), bits(qp), full[:, :, :512],
+                                              full[:, :, 512:], SCALE, n_threads=16)
+    assert_close(out.cpu().numpy(), po / ps[:, None], OUT_ATOL, OUT_RTOL, "out vs C port")
+    assert_close(lse.cpu().numpy(), pm + np.log(ps), LSE_ATOL, LSE_RTOL, "lse vs C port")
+    assert len_out.cpu().tolist() == [L + 1] * B
+    lb = bits(lat)
+    for b in range(B):
+        assert np.array_equal(lb[int(pt[b, L // PS]), L % PS], bits(lat_all[b][-1])), b
