@@ -38,13 +38,13 @@ __device__ __forceinline__ uint32_t pair_hi(uint32_t lo, uint32_t hi) {
   return __builtin_amdgcn_perm(hi, lo, 0x07060302u);
 }
 
-// Round-to-nearest-even fp32 -> bf16 of two values packed in one dword.
+// Round-to-nearest-even fp32 -> bf16 of two values packed in one dword (a
+// in the low half): one v_cvt_pk_bf16_f32 (converting the values one at a
+// time costs a shift and a merge per pair).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  __bf16 ha = (__bf16)a;
-  __bf16 hb = (__bf16)b;
-  uint16_t ua = __builtin_bit_cast(uint16_t, ha);
-  uint16_t ub = __builtin_bit_cast(uint16_t, hb);
-  return (uint32_t)ua | ((uint32_t)ub << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
 // Round-to-nearest-even fp32 -> bf16 bits.

@@ -14,23 +14,33 @@
 //   softmax  lanes l and l ^ 32 hold 16 tokens each of head l % 32, in the
 //            log2 domain against a reference max that stays fixed for the
 //            segment (below)
-//   PV       O^T[column][head] += V^T P^T: two 16-token k-steps x 16 column
-//            tiles = 32 MFMAs.  P^T is the QK accumulator as it is: the
+//   PV       O^T[column][head] += V^T P^T: two 16-token k-steps x 16 tiles of
+//            32 columns = 32 MFMAs.  P^T is the QK accumulator as it is: the
 //            k-slots follow the accumulator rows (k-slot 8 j + 4 a + c of
 //            k-step s is token 16 s + 8 a + 4 j + c, lane half j).  V^T comes
-//            from 16-byte LDS reads of eight token rows per lane, paired into
-//            dwords by v_perm; column tile (set, e) holds the columns
-//            256 set + 8 m + e, so one read of 8 columns feeds 8 tiles.
+//            straight from LDS with ds_read_b64_tr_b16 (two per MFMA): in each
+//            16-lane group, result lane 4 r + j, element e is element j of the
+//            8 bytes that lane 4 e + r addresses, so lanes 4 e + r pointing at
+//            token row e, columns 4 r .. 4 r + 3 deliver four tokens of one
+//            column per lane.
 // The waves never exchange data: they share the LDS tile and one barrier per
 // block.  Blocks come from HBM straight into LDS (global_load_lds_dwordx4, no
 // register staging): four tiles, block k consumed while k + 1 .. k + 3 are in
-// flight (108 KB per CU).  A tile's rows are 72 16-byte chunks plus one pad
-// chunk (row stride 73 chunks), so the 16 lanes of an LDS read phase hit 16
-// different 4-bank groups both for the QK reads (one chunk of 16 rows:
-// 73 m mod 16 is a permutation) and the PV reads (16 chunks of one row), and
-// every operand read is one per-lane base plus an immediate offset.  A
-// tile's 2336 chunks take 37 load instructions of 64 lanes; each wave issues
-// 10 per block, the last 3 of them into a small sink, so every wave's
+// flight (148 KB per CU), each wave's ten load instructions of a block spread
+// over its MFMAs (a burst stalls the wave while the memory pipeline drains).
+//
+// Tile layout.  gfx950's LDS has 128 banks of 4 bytes; a 64-lane
+// ds_read_b128 is served in two 32-lane passes and ds_read_b64_tr_b16 in one
+// pass.  Row r of a tile (72 chunks of 16 bytes) starts at chunk
+// wide_row_off(r) = 72 r + 5 (r / 8) + 4 ((r / 4) % 2), so that
+//   - the QK reads (32 rows, one chunk each per pass) hit 32 different
+//     chunk slots mod 32: the row offsets are distinct mod 32;
+//   - the PV transposed reads (rows 8 m .. 8 m + 7, 16 bytes of each row per
+//     8 lanes) hit 128 different banks: within each 8-row group the offsets
+//     are one residue class mod 4, spaced by 4 chunks mod 32.
+// Every operand read is one per-lane base plus an immediate offset.  A tile's
+// 2368 chunks (2323 used) take 37 load instructions of 64 lanes; each wave
+// issues 10 per block, the last 3 of them into a small sink, so every wave's
 // outstanding-load count is the same.
 //
 // No rescaling: the output accumulators feed only MFMAs and the final stores,
@@ -51,16 +61,34 @@
 namespace ws {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWideRowChunks = 73;                      // 576 bf16 = 72 x 16 B, + 1 pad
-constexpr int kWideTileChunks = 32 * kWideRowChunks;    // one 32-token block: 2336
-constexpr int kWideTileDma = 37;                        // instructions of 64 chunks per tile
-constexpr int kWideTileAlloc = kWideTileDma * 64;       // 2368 chunks
+constexpr int kWideRowData = 72;  // 576 bf16 = 72 x 16 B
+// LDS chunk offset of row r of a tile.
+__host__ __device__ constexpr int wide_row_off(int r) {
+  return kWideRowData * r + 5 * (r >> 3) + 4 * ((r >> 2) & 1);
+}
+constexpr int kWideTileChunks = wide_row_off(31) + kWideRowData;  // 2323
+constexpr int kWideTileDma = (kWideTileChunks + 63) / 64;         // 37 instructions of 64 chunks
+constexpr int kWideTileAlloc = kWideTileDma * 64;                 // 2368 chunks
 constexpr int kWideTiles = 4;
-constexpr int kWideDmaPerWave = 10;                     // 4 x 10 = 37 + 3 into the sink
+constexpr int kWideDmaPerWave = 10;  // 4 x 10 = 37 + 3 into the sink
 constexpr int kWideSinkDma = 4 * kWideDmaPerWave - kWideTileDma;
 constexpr float kWideHeadroomLog2 = 64.f;
-static_assert(kWideTileAlloc >= kWideTileChunks, "a tile holds its 37 instructions");
+// chunk offsets of rows 16 s + 8 t + q (q < 8) are wide_row_off(q) + 1162 s + 581 t
+constexpr int kWideRowsS = 1162, kWideRowsT = 581;
+static_assert(wide_row_off(16) == kWideRowsS * 1 + 0 && wide_row_off(8) == kWideRowsT &&
+                  wide_row_off(24 + 7) == wide_row_off(7) + kWideRowsS + kWideRowsT,
+              "row offsets split into a row-group part and a per-lane part");
+static_assert(kWideTileDma == 37 && kWideSinkDma == 3, "ten instructions per wave");
+
+// Row of tile chunk c (the pad chunks after a row count as that row's; c past
+// the tile gives row 31).
+__device__ __forceinline__ int wide_row_of(int c) {
+  int r = min(c / 73, 31);  // 72 r <= wide_row_off(r) <= 73 r: the row is r or r + 1
+  if (r < 31 && wide_row_off(r + 1) <= c) ++r;
+  return r;
+}
 
 __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b,
                                                const f32x16& c) {
@@ -76,17 +104,20 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b,
 // (back-to-back accumulation into the same registers needs no wait states),
 // qk_last ends it with the wait states a VALU read of an XDL result needs
 // (19 for a 16-pass MFMA, plus one on gfx950: 21 here), which the compiler's
-// hazard tracking does not know about for inline assembly.
+// hazard tracking does not know about for inline assembly.  The memory
+// clobber keeps LDS reads on the side of each MFMA where the source puts
+// them (the kernel places its reads a few MFMAs ahead of their use).
 __device__ __forceinline__ void qk_first(f32x16& c, const u32x4& a, const u32x4& b) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b) : "memory");
 }
 __device__ __forceinline__ void qk_next(f32x16& c, const u32x4& a, const u32x4& b) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b) : "memory");
 }
 __device__ __forceinline__ void qk_last(f32x16& c, const u32x4& a, const u32x4& b) {
   asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 4"
                : "+v"(c)
-               : "v"(a), "v"(b));
+               : "v"(a), "v"(b)
+               : "memory");
 }
 
 // One 16-byte chunk from global memory into LDS: lane i of the wave writes
@@ -120,6 +151,39 @@ __device__ __forceinline__ void wide_wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
+// Waits for this wave's LDS operations and joins the workgroup barrier.
+__device__ __forceinline__ void wide_lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+}
+// Waits for this wave's LDS operations (its own LDS writes before it reads
+// other lanes' values back).
+__device__ __forceinline__ void wide_lds_wait() {
+  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+}
+
+// Stores 32 staged 1 KB rows (row h at src + 260 h dwords, lane part at
+// src) to dst + h * row_bytes + col_byte, eight rows' LDS reads in flight
+// before their stores.
+__device__ __forceinline__ void wide_store_rows(char* dst, int row_bytes, const uint32_t* src,
+                                                int col_byte) {
+#pragma unroll
+  for (int h0 = 0; h0 < 32; h0 += 8) {
+    u32x4 v[8];
+#pragma unroll
+    for (int h = 0; h < 8; ++h) v[h] = *(const u32x4*)(src + (h0 + h) * 260);
+#pragma unroll
+    for (int h = 0; h < 8; ++h)
+      *(u32x4*)(dst + (size_t)(h0 + h) * row_bytes + col_byte) = v[h];
+  }
+}
+
+// ds_read_b64_tr_b16 at LDS byte address `addr`.
+__device__ __forceinline__ uint2 wide_tr_read(uint32_t addr) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)addr);
+  return __builtin_bit_cast(uint2, v);
+}
+
 template <bool APPEND>
 __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
   constexpr int NT = 256;
@@ -139,9 +203,9 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
   const int n32 = lane & 31;  // head (QK B, PV B, output) or row (A operands)
   const int j2 = lane >> 5;   // k-slot half
   const int head = 32 * wave + n32;
-  // Byte offsets, within a block of 32 consecutive rows, of the chunks this
-  // lane loads with its kWideDmaPerWave instructions (tile chunk c is row
-  // c / 73, chunk c % 73 of the row, i.e. row-major chunk c - c / 73; pad
+  // Byte offsets, within a block of 32 consecutive token rows in HBM, of the
+  // chunks this lane loads with its kWideDmaPerWave instructions (tile chunk
+  // c of row r = wide_row_of(c) is chunk c - wide_row_off(r) of the row; pad
   // chunks and the sink read a chunk of the block), two 16-bit offsets per
   // register.
   uint32_t offp[kWideDmaPerWave / 2];
@@ -151,11 +215,22 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int c = 64 * (kWideDmaPerWave * wave + 2 * j + h) + lane;
-      const int off = min(16 * (c - c / kWideRowChunks), 32 * kMlaL * 2 - 16);
-      v |= (uint32_t)off << (16 * h);
+      const int r = wide_row_of(c);
+      const int x = min(c - wide_row_off(r), kWideRowData - 1);
+      v |= (uint32_t)(r * (kMlaL * 2) + 16 * x) << (16 * h);
     }
     offp[j] = v;
   }
+  // Per-lane part of the PV transposed reads: 16-lane group G = lane / 16
+  // (k-slot half j2 = G / 2, column half ch = G % 2), lane 4 e + r of the
+  // group addresses token row 4 j2 + e, columns 16 ch + 4 r .. + 3.
+  // Recomputed where used (a few VALU operations) rather than kept live.
+  auto v_lane = [&]() __attribute__((always_inline)) {
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    const int G = l >> 4, e = (l >> 2) & 3, r = l & 3;
+    return (uint32_t)(16 * wide_row_off(4 * (G >> 1) + e) + 2 * (16 * (G & 1) + 4 * r));
+  };
 
   if (APPEND && p.len_out && g == 0)
     for (int b = tid; b < p.B; b += NT) p.len_out[b] = step_len_out(p.len_in, b, add, p.cap);
@@ -170,6 +245,7 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
       if (tid < H) p.lse[b * H + tid] = ok ? neg_inf() : qnan();
     }
   }
+  if (tid == 0) s_redo = 0;  // read after the ring's barriers
   if (!plan.has_work) return;
   const int blk_begin = uniform(plan.begin);
   const int blk_end = uniform(plan.end);
@@ -206,21 +282,33 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
     };
     fetch_pids();
     // Q^T of this wave's 32 heads: k-step u holds dims 16 u + 8 j2 .. + 8.
+    // The q_nope rows come through LDS (the tiles are free here): one 1 KB
+    // load instruction per row into a 65-chunk row slot (the read-back of
+    // chunk 2 u + j2 of 32 rows then hits distinct banks), where per-lane
+    // global loads would fetch 32 separate 32-byte pieces per instruction;
+    // the q_pe chunks are loaded straight into registers.
     u32x4 qb[36];
     {
-      const size_t qrow = (size_t)b * H + head;
-#pragma unroll
-      for (int u = 0; u < 32; ++u)
-        qb[u] = ((const u32x4*)(p.q_nope + qrow * kMlaC))[2 * u + j2];
+      const size_t qrow0 = (size_t)b * H + 32 * wave;
+      const uint32_t qst = tile_base0 + (uint32_t)(32 * wave * 65 * 16);
+#pragma unroll 8
+      for (int h = 0; h < 32; ++h)
+        wide_dma16_s(16 * lane, p.q_nope + (qrow0 + h) * kMlaC, qst + (uint32_t)(h * 65 * 16));
 #pragma unroll
       for (int u = 32; u < 36; ++u)
-        qb[u] = ((const u32x4*)(p.q_pe + qrow * 64))[2 * (u - 32) + j2];
+        qb[u] = ((const u32x4*)(p.q_pe + (qrow0 + n32) * 64))[2 * (u - 32) + j2];
+      asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+      const u32x4* qs = &s_tile[0][0] + (32 * wave + n32) * 65 + j2;
+#pragma unroll
+      for (int u = 0; u < 32; ++u) qb[u] = qs[2 * u];
     }
     // The queries are needed from the first block on: have them in registers
-    // before the block loads go out (the compiler's wait for them would
-    // otherwise also wait for every block load in flight).
+    // before the block loads go out (a wait the compiler placed at their
+    // first use would also wait for every block load in flight), and every
+    // wave done reading its rows before the loads overwrite them.
 #pragma unroll
     for (int u = 0; u < 36; ++u) asm volatile("" : : "v"(qb[u]));
+    wide_lds_barrier();
 
     const long long nc_off =
         APPEND ? (const char*)(p.c_new + (size_t)b * p.c_stride) - g0 : 0;
@@ -231,7 +319,11 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
     // the last three of wave 3 into the sink).  Rows past t_end repeat the
     // last valid row (masked in the softmax); a block past the segment's end
     // goes into a tile no later block of the segment uses.
-    auto issue = [&](int k, int slot) __attribute__((always_inline)) {
+    struct Dma {
+      const char* sb;
+      uint32_t dst0, dstep, sink0;
+    };
+    auto issue_begin = [&](int k, int slot) __attribute__((always_inline)) {
       const bool valid = k < nblk;
       const int kc = min(k, nblk - 1);
       if (kc - pid_base >= 64) {
@@ -247,148 +339,234 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
           (long long)((size_t)pid * p.page_size + (t0 - page * p.page_size)) * (kMlaL * 2);
       const int last = min(32, t_end - t0) - 1;
       const int new_r = (APPEND && valid) ? len_old - t0 : -1;
+      Dma d;
       // LDS destinations: scalar, recomputed per block (not hoisted)
-      uint32_t dst0 = tile_base0 + (uint32_t)slot * (kWideTileAlloc * 16) +
-                      1024 * kWideDmaPerWave * wave;
-      uint32_t sink0 = sink_base;
-      asm volatile("" : "+s"(dst0), "+s"(sink0));
-      if (!valid || (last == 31 && (unsigned)new_r >= 32u)) {
-        // all 32 rows are tokens of the segment (or, past the segment's
-        // end, the loads only have to stay in bounds: they read q_nope,
-        // at least 128 KB): a scalar base and the precomputed offsets
-        const char* sb = valid ? g0 + lb : (const char*)p.q_nope;
-#pragma unroll
-        for (int i = 0; i < kWideDmaPerWave; ++i) {
-          const int I = kWideDmaPerWave * wave + i;
-          const uint32_t off = (i & 1) ? offp[i >> 1] >> 16 : offp[i >> 1] & 0xffffu;
-          const uint32_t dst = I < kWideTileDma ? dst0 + 1024 * i
-                                                : sink0 + 1024 * (I - kWideTileDma);
-          wide_dma16_s(off, sb, dst);
-        }
-        return;
-      }
+      d.dst0 = tile_base0 + (uint32_t)slot * (kWideTileAlloc * 16) +
+               1024 * kWideDmaPerWave * wave;
+      d.sink0 = sink_base;
+      asm volatile("" : "+s"(d.dst0), "+s"(d.sink0));
+      // all 32 rows are tokens of the segment (or, past the segment's end,
+      // the loads only have to stay in bounds: they read q_nope, at least
+      // 128 KB): a scalar base and the precomputed offsets, one instruction
+      // at a time (dma_one)
+      d.dstep = 1024;
+      const bool fast = !valid || (last == 31 && (unsigned)new_r >= 32u);
+      d.sb = valid ? g0 + lb : (const char*)p.q_nope;
+      if (fast) return d;
       // the segment's last block when partial or holding the appended
-      // token: instruction I = 10 wave + i loads tile chunks 64 I .. 64 I +
-      // 63 (row c / 73, chunk c % 73; the pad chunks and the sink take any
-      // valid row), rows past t_end repeat the last valid row, the appended
-      // token's row comes from c_new / pe_new
+      // token, all ten instructions now: rows past t_end repeat the last
+      // valid row, the appended token's row comes from c_new / pe_new
       int lane_v = lane;
       asm volatile("" : "+v"(lane_v));
 #pragma unroll
       for (int i = 0; i < kWideDmaPerWave; ++i) {
         const int I = kWideDmaPerWave * wave + i;
         const int c = 64 * I + lane_v;
-        const int r = min(c / kWideRowChunks, 31);
-        const int x = min(c - (c / kWideRowChunks) * kWideRowChunks, 71);
+        const int r = wide_row_of(c);
+        const int x = min(c - wide_row_off(r), kWideRowData - 1);
         const int rr = min(r, last);
         long long off = lb + rr * (kMlaL * 2) + 16 * x;
         if (APPEND && rr == new_r) off = x < 64 ? nc_off + 16 * x : npe_off + 16 * (x - 64);
-        const uint32_t dst = I < kWideTileDma ? dst0 + 1024 * i
-                                              : sink0 + 1024 * (I - kWideTileDma);
+        const uint32_t dst = I < kWideTileDma ? d.dst0 + 1024 * i
+                                              : d.sink0 + 1024 * (I - kWideTileDma);
         wide_dma16(g0 + off, dst);
       }
+      // the ten per-slot instructions still go out (no branch at each
+      // slot), from q_nope into the sink: waits that count ten per block
+      // then wait for more than they need, never less
+      d.sb = (const char*)p.q_nope;
+      d.dst0 = d.sink0;
+      d.dstep = 0;
+      return d;
+    };
+    // Instruction i of a block (for a block issue_begin loaded already, a
+    // load into the sink).
+    auto dma_one = [&](const Dma& d, int i) __attribute__((always_inline)) {
+      const int I = kWideDmaPerWave * wave + i;
+      // unpacked here, at each use (five live registers, not ten)
+      asm volatile("" : "+v"(offp[i >> 1]));
+      const uint32_t off = (i & 1) ? offp[i >> 1] >> 16 : offp[i >> 1] & 0xffffu;
+      // a scalar select (the compiler makes a branch of the conditional)
+      uint32_t dst;
+      asm("s_cmp_lt_i32 %1, %4\n\ts_cselect_b32 %0, %2, %3"
+          : "=s"(dst)
+          : "s"(I), "s"(d.dst0 + d.dstep * i), "s"(d.sink0 + 1024 * (I - kWideTileDma)),
+            "n"(kWideTileDma)
+          : "scc");
+      wide_dma16_s(off, d.sb, dst);
+    };
+    auto issue = [&](int k, int slot) __attribute__((always_inline)) {
+      const Dma d = issue_begin(k, slot);
+#pragma unroll
+      for (int i = 0; i < kWideDmaPerWave; ++i) dma_one(d, i);
     };
 
     f32x16 acc[16];
-    float m_run = neg_inf();  // reference max (m_ref); -inf until the first block
-    float m_max = neg_inf();  // the segment's largest score so far
+    float m_run = neg_inf();  // reference max (m_ref) of the lane's head
+    float m_max = neg_inf();  // the lane's largest score of the segment so far
     float l_run = 0.f;
 
-    // QK of one block into sc, two k-steps at a time (batch g: k-steps
-    // 2 g, 2 g + 1): A = row n32 of the tile, k-step u = chunk 2 u + j2.
-    auto qk_batch = [&](const u32x4* tile, int g, f32x16& sc) __attribute__((always_inline)) {
-      const u32x4* arow = tile + n32 * kWideRowChunks + j2;
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int ku = 2 * g + u;
-        const u32x4 kr = arow[2 * ku];
-        if (ku == 0)
-          qk_first(sc, kr, qb[ku]);
-        else if (ku == 35)
-          qk_last(sc, kr, qb[ku]);
-        else
-          qk_next(sc, kr, qb[ku]);
-      }
+    // Pieces of the ring (block k in tile k % 4):
+    //   QK(k)    36 MFMAs into sc; A = row n32 of the tile, k-step u = chunk
+    //            2 u + j2, each read four MFMAs ahead
+    //   soft_x   log2-domain scores of a block (xa: the first PV k-step's,
+    //            xh: the second's) and the lane's running max, which only
+    //            feeds the headroom check, so no lanes are combined except to
+    //            set m_run at the pass's first block
+    //   soft_p   one dword of a k-step's P^T from its scores (two exp2
+    //            against m_run)
+    //   PV(k)    MFMA m (k-step m / 16, columns 32 (m % 16) ..) into
+    //            accumulator m % 16, its V^T operand from two transposed reads
+    //            (tokens 16 s + 8 t + 4 j2 + e, t = 0, 1) three MFMAs ahead
+    const u32x4* arow0 = &s_tile[0][0] + wide_row_off(n32) + j2;
+    auto qk_read = [&](int tile, int u) __attribute__((always_inline)) {
+      return arow0[tile * kWideTileAlloc + 2 * u];
     };
-    // Softmax of block k from its scores: accumulator i is token
-    // 8 (i / 4) + 4 j2 + i % 4 of head n32 (valid when below nt, the lane's
-    // part moved to the right).  Writes P^T for the two PV k-steps.
-    auto softmax = [&](int k, const f32x16& sc, u32x4 (&pb)[2]) __attribute__((always_inline)) {
-      const int nt = min(32, t_end - (t_begin + 32 * k));
-      const int lim = nt - 4 * j2;
-      float x[16];
-      float bm = neg_inf();
+    auto qk_mfma = [&](f32x16& sc, const u32x4& kr, int u) __attribute__((always_inline)) {
+      if (u == 0)
+        qk_first(sc, kr, qb[0]);
+      else if (u == 35)
+        qk_last(sc, kr, qb[35]);
+      else
+        qk_next(sc, kr, qb[u]);
+    };
+    // lane's V^T base in tile `tile`, opaque to the compiler (which would
+    // otherwise keep a register per read offset instead of using the
+    // instruction's offset field)
+    auto vbase = [&](int tile) __attribute__((always_inline)) {
+      return tile_base0 + (uint32_t)tile * (kWideTileAlloc * 16) + v_lane();
+    };
+    auto vread = [&](uint32_t vt, int m) __attribute__((always_inline)) {
+      const int sv = m >> 4, ct = m & 15;
+      const uint32_t a = vt + 16 * kWideRowsS * sv + 64 * ct;
+      const uint2 lo = wide_tr_read(a);
+      const uint2 hi = wide_tr_read(a + 16 * kWideRowsT);
+      return u32x4{lo.x, lo.y, hi.x, hi.y};
+    };
+    // the memory clobber keeps the operand reads where the source puts them
+    auto pv_mfma = [&](const u32x4& va, const u32x4& pbs, int m) __attribute__((always_inline)) {
+      f32x16& a = acc[m & 15];
+      a = mfma32x32x16(va, pbs, a);
+      asm volatile("" : "+a"(a));
+      asm volatile("" : : : "memory");
+    };
+    // soft_x: the scores of a block as x = q.k * scale_log2 - m_run (xa: the
+    // first PV k-step's, xh: the second's).  For a positive scale (the only
+    // one attention uses) the block's largest score is the scale times the
+    // largest raw score (v_max3 over the accumulator) and x is one FMA per
+    // score; tokens past the end of a partial block are raw -inf.  Any other
+    // scale takes the plain route.
+    auto soft_x = [&](int kb, const f32x16& sc, float (&xa)[8], float (&xh)[8])
+        __attribute__((always_inline)) {
+      const int nt = min(32, t_end - (t_begin + 32 * kb));
+      const float sl = p.scale_log2;
+      f32x16 v = sc;
+      if (nt < 32) {  // accumulator i is token 8 (i / 4) + 4 j2 + i % 4
+        int l = lane;  // recomputed here rather than kept live
+        asm volatile("" : "+v"(l));
+        const int lim = nt - 4 * (l >> 5);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        x[i] = 8 * (i >> 2) + (i & 3) < lim ? sc[i] * p.scale_log2 : neg_inf();
-        bm = fmaxf(bm, x[i]);
+        for (int i = 0; i < 16; ++i) v[i] = 8 * (i >> 2) + (i & 3) < lim ? v[i] : neg_inf();
       }
-      {
+      float bm;
+      if (sl > 0.f) {
+        float r = v[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) r = fmaxf(r, v[i]);
+        bm = r * sl;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = v[i] == neg_inf() ? neg_inf() : v[i] * sl;
+        bm = v[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) bm = fmaxf(bm, v[i]);
+      }
+      m_max = fmaxf(m_max, bm);
+      {  // m_run unset (the pass's first block): the head's largest score
         float lo, hi;
         pair_xor32(bm, lo, hi);
-        bm = fmaxf(lo, hi);
+        m_run = m_run == neg_inf() ? fmaxf(lo, hi) : m_run;
       }
-      m_run = m_run == neg_inf() ? bm : m_run;
-      m_max = fmaxf(m_max, bm);
-      float ps = 0.f;
+      const float nm = -m_run;
+      const float sx = sl > 0.f ? sl : 1.f;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const float pa = __builtin_amdgcn_exp2f(x[8 * s + 2 * d] - m_run);
-          const float pc = __builtin_amdgcn_exp2f(x[8 * s + 2 * d + 1] - m_run);
-          ps += pa + pc;
-          pb[s][d] = pack_bf16x2(pa, pc);
-        }
+      for (int i = 0; i < 8; ++i) {
+        xa[i] = __builtin_fmaf(v[i], sx, nm);
+        xh[i] = __builtin_fmaf(v[8 + i], sx, nm);
       }
-      l_run += ps;
     };
-    // PV group g of a block (k-step s = g / 2, column set g % 2): lane
-    // (n32, j2) reads the 16 bytes of columns 256 set + 8 n32 .. + 8 of tokens
-    // 16 s + 8 (q >> 2) + 4 j2 + (q & 3) (16 lanes of one token read 16
-    // consecutive chunks: no bank conflicts), one read feeding 8 tiles.
-    auto pv_group = [&](const u32x4* tile, int g, const u32x4 (&pb)[2])
-        __attribute__((always_inline)) {
-      const int s = g >> 1, set = g & 1;
-      const u32x4* vrow = tile + 4 * j2 * kWideRowChunks + n32 + 32 * set;
-      u32x4 vr[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) vr[q] = vrow[(16 * s + 8 * (q >> 2) + (q & 3)) * kWideRowChunks];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int w = e >> 1;
-        u32x4 va;
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-          va[d] = (e & 1) ? pair_hi(vr[2 * d][w], vr[2 * d + 1][w])
-                          : pair_lo(vr[2 * d][w], vr[2 * d + 1][w]);
-        acc[8 * set + e] = mfma32x32x16(va, pb[s], acc[8 * set + e]);
-      }
+    // soft_p: one dword of a k-step's P^T (two exp2), its two probabilities
+    // added to the row sum as rounded (the PV MFMAs see the same values)
+    auto soft_p = [&](const float (&xs)[8], u32x4& pbs, int dd) __attribute__((always_inline)) {
+      typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+      const uint32_t pk = pack_bf16x2(__builtin_amdgcn_exp2f(xs[2 * dd]),
+                                      __builtin_amdgcn_exp2f(xs[2 * dd + 1]));
+      pbs[dd] = pk;
+      l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk),
+                                              __builtin_bit_cast(bf16x2_t, 0x3f803f80u), l_run,
+                                              false);
     };
 
-    // Ring over the four tiles (block m in tile m % 4).  Step k: wait for
-    // block k (this wave's loads of blocks k + 1 and k + 2 may still be in
-    // flight), the barrier (every wave's part of block k is in, every wave is
-    // done with block k - 1's tile), block k + 3 into that tile, then block
-    // k's QK, softmax and PV.  The tile of a block is picked at run time (its
-    // LDS address is one scalar add).
-    auto step = [&](int kk) __attribute__((always_inline)) {
-      const int s = kk & (kWideTiles - 1);
-      wide_wait_barrier<2 * kWideDmaPerWave>();
-      // the pass's first barrier: every wave has read the previous decision
-      if (kk == 0 && tid == 0) s_redo = 0;
-      issue(kk + 3, (s + 3) & (kWideTiles - 1));
-      __builtin_amdgcn_sched_barrier(0);
-      const u32x4* tile = s_tile[s];
+    // Step kk of the ring, software-pipelined.  Block kk's scores (xa, xh)
+    // come from the previous step.  The QK chain of block kk + 1 (36
+    // MFMAs) runs with PV(kk) between its links: its first four links beside
+    // the first k-step's probabilities (soft_p from xa), then 24 PV MFMAs,
+    // three to every four links (the XDL unit alternates between the
+    // independent PV MFMAs and the dependent QK chain), the second k-step's
+    // probabilities beside PV's first k-step; soft_x of block kk + 1 runs
+    // beside the last 8 PV MFMAs.  Block kk + 3's ten load instructions go
+    // out over the chain into tile (kk + 3) % 4.  The step waits for block
+    // kk + 1 (block kk + 2 may be in flight) and the barrier (every wave's
+    // part of block kk + 1 is in, every wave is done with step kk - 1 and so
+    // with tile (kk - 1) % 4 = (kk + 3) % 4).
+    auto step = [&](int kk, float (&xa)[8], float (&xh)[8]) __attribute__((always_inline)) {
+      const int tp = kk & (kWideTiles - 1), tq = (kk + 1) & (kWideTiles - 1);
+      wide_wait_barrier<kWideDmaPerWave>();
+      const Dma d = issue_begin(kk + 3, (kk + 3) & (kWideTiles - 1));
       f32x16 sc;
+      u32x4 kr[5], va[4], pb[2];
+      const uint32_t vt = vbase(tp);
 #pragma unroll
-      for (int g = 0; g < 18; ++g) qk_batch(tile, g, sc);
-      __builtin_amdgcn_sched_barrier(0);
-      u32x4 pb[2];
-      softmax(kk, sc, pb);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int u = 0; u < 4; ++u) kr[u] = qk_read(tq, u);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) pv_group(tile, g, pb);
+      for (int m = 0; m < 3; ++m) va[m] = vread(vt, m);
+#pragma unroll
+      for (int u = 0; u < 36; ++u) {
+        if (u + 4 < 36) kr[(u + 4) % 5] = qk_read(tq, u + 4);
+        qk_mfma(sc, kr[u % 5], u);
+        if (u < 4) {
+          soft_p(xa, pb[0], u);
+        } else if ((u - 4) % 4 != 3) {
+          const int m = 3 * ((u - 4) / 4) + (u - 4) % 4;
+          va[(m + 3) & 3] = vread(vt, m + 3);
+          pv_mfma(va[m & 3], pb[m >> 4], m);
+          if (m < 16 && (m & 3) == 1) soft_p(xh, pb[1], m >> 2);
+        }
+        if (u % 4 == 2 && u < 40) dma_one(d, u / 4);  // instructions 0-8
+      }
+      soft_x(kk + 1, sc, xa, xh);
+#pragma unroll
+      for (int m = 24; m < 32; ++m) {
+        if (m + 3 < 32) va[(m + 3) & 3] = vread(vt, m + 3);
+        pv_mfma(va[m & 3], pb[1], m);
+        if (m == 27) dma_one(d, 9);
+      }
+    };
+    // The pass's last block: PV only (its tile is in and synchronised).
+    auto step_last = [&](int kk, const float (&xa)[8], const float (&xh)[8])
+        __attribute__((always_inline)) {
+      const uint32_t vt = vbase(kk & (kWideTiles - 1));
+      u32x4 va[4], pb[2];
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) soft_p(xa, pb[0], dd);
+#pragma unroll
+      for (int m = 0; m < 3; ++m) va[m] = vread(vt, m);
+#pragma unroll
+      for (int m = 0; m < 32; ++m) {
+        if (m + 3 < 32) va[(m + 3) & 3] = vread(vt, m + 3);
+        pv_mfma(va[m & 3], pb[m >> 4], m);
+        if (m < 16 && (m & 3) == 1) soft_p(xh, pb[1], m >> 2);
+      }
     };
     for (int pass = 0;; ++pass) {
 #pragma unroll
@@ -403,18 +581,40 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
       issue(0, 0);
       issue(1, 1);
       issue(2, 2);
-      for (int k = 0; k < nblk; ++k) step(k);
+      float xa[8], xh[8];
+      {  // QK and soft_x of block 0
+        wide_wait_barrier<2 * kWideDmaPerWave>();
+        f32x16 sc;
+        u32x4 kr[5];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) kr[u] = qk_read(0, u);
+#pragma unroll
+        for (int u = 0; u < 36; ++u) {
+          if (u + 4 < 36) kr[(u + 4) % 5] = qk_read(0, u + 4);
+          qk_mfma(sc, kr[u % 5], u);
+        }
+        soft_x(0, sc, xa, xh);
+      }
+#pragma clang loop unroll(disable)
+      for (int k = 0; k + 1 < nblk; ++k) step(k, xa, xh);
+      step_last(nblk - 1, xa, xh);
+      {  // the head's largest score (both lanes of the head)
+        float lo, hi;
+        pair_xor32(m_max, lo, hi);
+        m_max = fmaxf(lo, hi);
+      }
       // every load of the pass has landed and every wave is done with the
       // tiles (a second pass, or the next segment, overwrites them)
       const bool climbed = __builtin_amdgcn_ballot_w64(m_max > m_run + kWideHeadroomLog2) != 0;
       if (climbed && lane == 0) s_redo = 1;
       wide_wait_barrier<0>();
       const bool redo = s_redo != 0;
+      wide_wait_barrier<0>();  // every wave has read s_redo
+      if (tid == 0) s_redo = 0;  // before the next vote, past the ring's barriers
       if (pass > 0 || !redo) break;
       // scores climbed out of the reference's headroom: again, with the
       // segment's maximum as the reference (no score exceeds it)
       m_run = m_max;
-      wide_wait_barrier<0>();  // every wave has read s_redo
     }
 
     // The appended token is its sequence's last, so a segment that holds it
@@ -426,10 +626,10 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
       const int pid = __builtin_amdgcn_readlane(m_pid, nblk - 1 - pid_base);
       const int page = t0 / p.page_size;
       const int r = len_old - t0;
-      if (tid < kWideRowChunks && pid >= 0)  // bit 31: the page id is outside the pool
+      if (tid < kWideRowData && pid >= 0)  // bit 31: the page id is outside the pool
         ((u32x4*)(p.latent_w +
                   ((size_t)pid * p.page_size + (len_old - page * p.page_size)) * kMlaL))[tid] =
-            s_tile[(nblk - 1) % kWideTiles][r * kWideRowChunks + tid];
+            s_tile[(nblk - 1) % kWideTiles][wide_row_off(r) + tid];
     }
 
     float lo, hi;
@@ -438,36 +638,53 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
     const bool bad = seg_bad < 0;  // a bad page id was read (clamped): the piece is NaN
     const float inv_l = bad ? qnan() : 1.f / l_tot;
     const float lse_v = bad ? qnan() : (m_run + __log2f(l_tot)) * kLn2;
-    const size_t orow = (size_t)b * H + head;
-    // accumulator (set, e) value i is column 256 set + 64 (i / 4) + 32 j2 +
-    // 8 (i % 4) + e: eight consecutive columns per (set, i)
-    if (row_start >= blk_begin && row_end <= blk_end) {  // the whole sequence is here
-      float* dst = p.out + orow * kMlaC;
-#pragma unroll
-      for (int set = 0; set < 2; ++set)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float4* o = (float4*)(dst + 256 * set + 64 * (i >> 2) + 32 * j2 + 8 * (i & 3));
-          o[0] = make_float4(acc[8 * set + 0][i] * inv_l, acc[8 * set + 1][i] * inv_l,
-                             acc[8 * set + 2][i] * inv_l, acc[8 * set + 3][i] * inv_l);
-          o[1] = make_float4(acc[8 * set + 4][i] * inv_l, acc[8 * set + 5][i] * inv_l,
-                             acc[8 * set + 6][i] * inv_l, acc[8 * set + 7][i] * inv_l);
-        }
-      if (j2 == 0) p.lse[orow] = lse_v;
-    } else {
-      const size_t prow = (size_t)(g + b) * H + head;
-      uint16_t* dst = p.part_out + prow * kMlaC;
-#pragma unroll
-      for (int set = 0; set < 2; ++set)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          store_piece8(dst + 256 * set + 64 * (i >> 2) + 32 * j2 + 8 * (i & 3),
-                       acc[8 * set + 0][i] * inv_l, acc[8 * set + 1][i] * inv_l,
-                       acc[8 * set + 2][i] * inv_l, acc[8 * set + 3][i] * inv_l,
-                       acc[8 * set + 4][i] * inv_l, acc[8 * set + 5][i] * inv_l,
-                       acc[8 * set + 6][i] * inv_l, acc[8 * set + 7][i] * inv_l);
-      if (j2 == 0) p.part_lse[prow] = lse_v;
+    const bool whole = row_start >= blk_begin && row_end <= blk_end;  // final, fp32
+    if (j2 == 0) {
+      if (whole)
+        p.lse[(size_t)b * H + head] = lse_v;
+      else
+        p.part_lse[(size_t)(g + b) * H + head] = lse_v;
     }
+    // The outputs leave through LDS (the tiles are free: every wave is past
+    // the pass's last barrier, and the append above has read its row), so
+    // that each store instruction writes one contiguous 1 KB row: wave w
+    // stages its 32 rows (row stride 260 dwords: the 64 lanes' writes and
+    // reads hit distinct banks) and stores them itself.  Accumulator ct
+    // value i is column 32 ct + 8 (i / 4) + 4 j2 + i % 4.
+    wide_lds_barrier();  // the append's tile read is done
+    uint32_t* stage = (uint32_t*)&s_tile[0][0] + (size_t)(32 * wave) * 260;
+    if (!whole) {  // bf16 piece: all 512 columns at once
+#pragma unroll
+      for (int ct = 0; ct < 16; ++ct)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *(uint2*)(stage + n32 * 260 + 16 * ct + 4 * q + 2 * j2) =
+              make_uint2(pack_bf16x2(acc[ct][4 * q] * inv_l, acc[ct][4 * q + 1] * inv_l),
+                         pack_bf16x2(acc[ct][4 * q + 2] * inv_l, acc[ct][4 * q + 3] * inv_l));
+      wide_lds_wait();  // this wave's rows are in LDS
+      char* dst = (char*)(p.part_out + ((size_t)(g + b) * H + 32 * wave) * kMlaC);
+      wide_store_rows(dst, kMlaC * 2, stage + 4 * lane, 16 * lane);
+    } else {  // fp32 final: two halves of 256 columns
+      char* dst = (char*)(p.out + ((size_t)b * H + 32 * wave) * kMlaC);
+#pragma unroll
+      for (int hc = 0; hc < 2; ++hc) {
+#pragma unroll
+        for (int c8 = 0; c8 < 8; ++c8)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int ct = 8 * hc + c8;
+            *(float4*)(stage + n32 * 260 + 32 * c8 + 8 * q + 4 * j2) =
+                make_float4(acc[ct][4 * q] * inv_l, acc[ct][4 * q + 1] * inv_l,
+                            acc[ct][4 * q + 2] * inv_l, acc[ct][4 * q + 3] * inv_l);
+          }
+        wide_lds_wait();
+        wide_store_rows(dst, kMlaC * 4, stage + 4 * lane, 1024 * hc + 16 * lane);
+        wide_lds_wait();  // the next half overwrites the rows
+      }
+    }
+    // the next segment's loads overwrite the tiles: every wave's stores
+    // have read their rows
+    wide_lds_barrier();
     blk = seg_end;
   }
 }
