@@ -217,6 +217,12 @@ class _PagedTwoSided:
     # boundaries.
     MOVE_WAIT_FRACTION = 0.25
     _move_rate = 50e9
+    # A move begun under the decode steps may be cut to the pages its copies
+    # can move in this fraction of a step (at _move_rate): its copies then
+    # end within the step that runs beside them, and the next decisions carry
+    # the boundary on.  None (the default): the whole move at once, which
+    # measured faster when the copies do not slow the steps beside them.
+    MOVE_STEP_FRACTION = None
 
     def begin_boundaries(self, targets) -> bool:
         """Start moving every sequence's boundary to targets[b] host tokens
@@ -275,8 +281,7 @@ class _PagedTwoSided:
         up_g = [x for e in m.ups for x in e[4]]
         up_h = [x for e in m.ups for x in e[5]]
         m.pages = len(down_g) + len(up_g)
-        m.bytes = m.pages * sum(p[0, 0].numel() * p.element_size() * p.shape[0]
-                                for p in self._gpu_payload())
+        m.bytes = m.pages * self._page_bytes()
         m.t_begin = time.perf_counter()
         dev = g.device
         side = dev.type == "cuda" and all(hp.is_pinned() for hp in self.host.data)
@@ -545,6 +550,7 @@ class _PagedTwoSided:
 
     controller = None  # a scheduler.ShareController, or None
     _step_end = None  # perf_counter at the end of the last step's bookkeeping
+    _step_t0 = None  # perf_counter at the end of the current step's first layer
 
     async_moves = False  # controller moves: begin_boundaries (True) or set_boundaries
 
@@ -569,6 +575,8 @@ class _PagedTwoSided:
         of a decode step, fold them into the scheduler and move the boundary
         if it chooses to."""
         g = self.gpu
+        if layer == 0:
+            self._step_t0 = time.perf_counter()
         self._layer_log.append((layer, float(g.lens[layer].sum()), float(self.host.lens.sum()),
                                 host_s))
         if layer != self.num_layers - 1:
@@ -588,16 +596,23 @@ class _PagedTwoSided:
             ctl.observe_layer(g_tok * bpt, a.elapsed_time(e) * 1e-3, h_tok * bpt, h_s)
         self._layer_log = []
         now = time.perf_counter()
-        step_s = now - self._step_end if self._step_end is not None else None
+        if self._step_end is not None:
+            step_s = now - self._step_end
+        elif self._step_t0 is not None and self.num_layers > 1:
+            # the first step: from the end of its first layer, scaled to all
+            step_s = (now - self._step_t0) * self.num_layers / (self.num_layers - 1)
+        else:
+            step_s = None
         m = self._move
         if m is not None:
             t0 = now
             done = self.poll_boundaries()
             if not done and step_s is not None:
-                # copies expected to end within a small part of a step: wait
-                # for them rather than run one more step at the old share
+                # wait for the copies when what is left of them is shorter
+                # than what the next step saves at the new boundaries (the
+                # scheduler's prediction), or than a small part of a step
                 left = m.bytes / self._move_rate - (now - m.t_begin)
-                if left < self.MOVE_WAIT_FRACTION * step_s:
+                if left < max(self.MOVE_WAIT_FRACTION * step_s, self._switch_gain(m)):
                     self.finish_boundaries()
                     done = True
             if done and m.info is not None:
@@ -622,6 +637,11 @@ class _PagedTwoSided:
             return
         # the step's outputs are already queued: a move that cannot start is
         # recorded and skipped, never raised out of the step
+        if self.async_moves and self.MOVE_STEP_FRACTION is not None and step_s is not None:
+            cap = int(self.MOVE_STEP_FRACTION * step_s * self._move_rate / self._page_bytes())
+            targets = self.paced_targets(targets, max(1, cap))
+            r1 = ctl.share_of(lens, targets)
+            ctl.amend_last_share(r1)
         try:
             if self.async_moves:
                 t0 = time.perf_counter()
@@ -638,6 +658,47 @@ class _PagedTwoSided:
             return
         pages = sum(abs(t - h) for t, h in zip(targets, host_now)) // self.page_size
         ctl.record_move(r0, r1, pages, time.perf_counter() - t0)
+
+    def _switch_gain(self, m) -> float:
+        """Seconds one decode step is predicted to save at move m's
+        boundaries over the current ones (0 when unknown)."""
+        if m.info is None or self.controller is None:
+            return 0.0
+        ctl = self.controller
+        _, r0, r1, _, _ = m.info
+        layer_bytes = float(sum(self.seq_len(b) for b in range(self.batch))) * ctl.bytes_per_token
+        try:
+            t0 = ctl.sched.predict(r0, layer_bytes)["layer"]
+            t1 = ctl.sched.predict(r1, layer_bytes)["layer"]
+        except ValueError:
+            return 0.0
+        return max(0.0, (t0 - t1) * self.num_layers)
+
+    def _page_bytes(self) -> int:
+        """Bytes one page of a sequence moves: all layers, every payload."""
+        return sum(p[0, 0].numel() * p.element_size() * p.shape[0] for p in self._gpu_payload())
+
+    def paced_targets(self, targets, max_pages: int) -> list:
+        """targets[b] host tokens with the move cut to at most max_pages pages
+        in all: every sequence moves the same fraction of its way (rounded
+        down to pages), and the pages left by the rounding go to the first
+        sequences still short of their targets."""
+        ps = self.page_size
+        cur = [int(x) for x in self.host.lens]
+        want = [abs(int(t) - h) // ps for t, h in zip(targets, cur)]
+        total = sum(want)
+        if total <= max_pages:
+            return [int(t) for t in targets]
+        take = [k * max_pages // total for k in want]
+        left = max_pages - sum(take)
+        for b in range(len(take)):
+            if left <= 0:
+                break
+            if take[b] < want[b]:
+                take[b] += 1
+                left -= 1
+        return [h + (k * ps if int(t) > h else -k * ps)
+                for t, h, k in zip(targets, cur, take)]
 
     def feasible_targets(self, targets, gpu_reserve: int = 0) -> list:
         """targets[b] host tokens, each move cut down to what can start now:

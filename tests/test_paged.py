@@ -4,6 +4,8 @@ directly, and only the bookkeeping and page copies run.  After every move
 the concatenation host tokens ++ GPU tokens must equal the original token
 sequence bit for bit, every page must be accounted for, and both sides'
 lengths and tables must agree."""
+import time
+
 import numpy as np
 import pytest
 import torch
@@ -341,3 +343,50 @@ def test_feasible_targets_respect_capacity_and_host_pool():
     cache.gpu.max_pages = 5
     free = cache.gpu.pool.free
     assert cache.feasible_targets([0, 0], gpu_reserve=free - 1) == [3 * PS, 0]
+
+def test_paced_targets_cut_every_sequence_by_the_same_fraction():
+    layers = 1
+    lens, hosts = [8 * PS, 8 * PS, 4 * PS], [8 * PS, 0, 4 * PS]
+    cache, _ = _mla_cache_with(lens, hosts, layers, 8 * PS, host_pages=30, gpu_pages=30)
+    # sequence 0 wants 8 pages up, sequence 1 4 pages down, sequence 2 stays
+    targets = [0, 4 * PS, 4 * PS]
+    assert cache.paced_targets(targets, 12) == targets  # within the cap: unchanged
+    assert cache.paced_targets(targets, 100) == targets
+    # 6 of 12 pages: half of each way
+    assert cache.paced_targets(targets, 6) == [4 * PS, 2 * PS, 4 * PS]
+    # 5 of 12: 8*5//12 = 3 and 4*5//12 = 1, the leftover page to the first
+    assert cache.paced_targets(targets, 5) == [4 * PS, PS, 4 * PS]
+    # one page
+    assert cache.paced_targets(targets, 1) == [7 * PS, 0, 4 * PS]
+    # every result is a feasible boundary and moves no more than the cap
+    for cap in range(1, 13):
+        out = cache.paced_targets(targets, cap)
+        moved = sum(abs(o - h) // PS for o, h in zip(out, hosts))
+        assert moved == min(cap, 12)
+        assert all(o % PS == 0 and 0 <= o <= L for o, L in zip(out, lens))
+        # each sequence moves toward its target and not past it
+        for o, h, t in zip(out, hosts, targets):
+            assert min(h, t) <= o <= max(h, t)
+
+
+def test_async_controller_paces_a_move_to_the_step_time():
+    """With pacing on, an async controller whose copies could move only a
+    few pages within half a step starts a move of that many pages."""
+    layers = 2
+    lens, hosts = [6 * PS, 6 * PS], [6 * PS, 6 * PS]
+    cache, data = _mla_cache_with(lens, hosts, layers, 6 * PS, gpu_pages=40)
+    ctl = _controlled(cache)
+    cache.async_moves = True
+    cache.MOVE_STEP_FRACTION = 0.5
+    # copies of 4 pages per step, so half a step moves 2
+    step_s = 1.0
+    cache._move_rate = 4 * cache._page_bytes() / step_s
+    cache._step_end = time.perf_counter() - step_s
+    cache._step_done()
+    assert cache.moving  # the move is in flight
+    m = cache._move
+    assert m.pages == 2
+    cache.finish_boundaries()
+    assert sum(hosts) - sum(cache.host_tokens(b) for b in range(2)) == 2 * PS
+    _check_accounting(cache)
+    _check_tokens(cache, data)
