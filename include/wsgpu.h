@@ -432,7 +432,10 @@ int ws_lse_merge(const float* out_g, const float* lse_g,
  * held until the process ends.  A call whose plan needs more returns
  * WS_EWORKSPACE before launching anything.  The call allocates nothing (no
  * hipMalloc, no library allocation); its first call on a device looks up the
- * array's address there.  Every call on one GPU shares that GPU's array:
+ * array's address there (hipGetSymbolAddress, which is not a capturable
+ * operation), so that first call must come before any graph capture on the
+ * device; later calls capture as plain kernel nodes.  Every call on one GPU
+ * shares that GPU's array:
  * calls that overlap on one GPU (other streams, unordered threads) race;
  * calls ordered on one stream do not.  The array needs no initial contents.
  */

@@ -305,3 +305,56 @@ def test_paged_mla_step_with_more_sequences_than_one_wave_plans():
         want, _ = O.mla_attention_fp64(bits(qn[hh]), bits(qp[hh]), full[None, :, :512],
                                        full[None, :, 512:], scale)
         assert_close(got[hh], want, OUT_ATOL, OUT_RTOL, f"b={b} (L={lens[b]}, host={hosts[b]})")
+
+
+def test_paged_mla_steps_overlap_a_large_begun_move():
+    """A move large enough to outlast a decode step (16 layers x 4 sequences
+    x 4096 tokens, host -> HBM, 302 MB): the steps are launched without
+    synchronising between layers, whether the copies were still in flight
+    when each step started is recorded (cache._move.event), and the first
+    step must have started under them.  Sampled layers of every step match
+    fp64 attention over the whole sequence."""
+    B, H, layers, L = 4, 16, 16, 4096
+    scale = 192 ** -0.5
+    steps = 3
+    cache = PagedMlaCache(layers, B, max_tokens=L + steps + PS, page_size=PS,
+                          host_pages=B * (L // PS + 2), gpu_pages=B * (L // PS + 4), device=DEV)
+    lat = {}
+    for layer in range(layers):
+        for b in range(B):
+            lat[layer, b] = bf16_randn((L + steps, 576), 2000 + 10 * layer + b, 0.5)
+            x = lat[layer, b]
+            cache.load(layer, b, x[:L, :512].contiguous(), x[:L, 512:].contiguous(), L)
+    torch.cuda.synchronize()
+    assert cache.begin_boundaries([0] * B)
+    under_copies = []
+    outs = {}
+    for s in range(steps):
+        m = cache._move
+        under_copies.append(m is not None and m.event is not None and not m.event.query())
+        _say(f"large move: step {s} starts with the copies in flight: {under_copies[-1]} "
+             f"host={[cache.host_tokens(b) for b in range(B)]}")
+        for layer in range(layers):
+            pos = [L + s] * B
+            new = torch.stack([lat[layer, b][pos[b]] for b in range(B)]).view(B, 1, 576)
+            qn = bf16_randn((B * H, 512), 3000 + 100 * s + layer, 0.5)
+            qp = bf16_randn((B * H, 64), 3500 + 100 * s + layer, 0.5)
+            out = cache.step(layer, qn.to(DEV), qp.to(DEV), new[..., :512].contiguous().to(DEV),
+                             new[..., 512:].contiguous().to(DEV), scale, host_threads=8)
+            if layer in (0, layers - 1):
+                outs[s, layer] = (out, qn, qp)
+        if s == 1:
+            cache.finish_boundaries()
+    torch.cuda.synchronize()
+    assert under_copies[0], "the first step finished queueing after the copies ended"
+    assert [cache.host_tokens(b) for b in range(B)] == [0] * B
+    for (s, layer), (out, qn, qp) in outs.items():
+        got = out.float().cpu().numpy()
+        for b in (0, B - 1):
+            full = bits(lat[layer, b][:L + s + 1])
+            hh = slice(b * H, (b + 1) * H)
+            want, _ = O.mla_attention_fp64(bits(qn[hh]), bits(qp[hh]), full[None, :, :512],
+                                           full[None, :, 512:], scale)
+            assert_close(got[hh], want, OUT_ATOL, OUT_RTOL, f"step {s} layer {layer} b={b}")
+    for b in range(B):
+        assert cache.seq_len(b) == L + steps

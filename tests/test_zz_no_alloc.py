@@ -34,6 +34,32 @@ def _p(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _setup(L, lens, Hkv, G, seed, n_splits):
+    """A fresh seeded pool and the no-alloc step over it: returns (call,
+    tensors), call(stream) making the call on `stream` (a ctypes handle)."""
+    D, PS = 128, 64
+    B = len(lens)
+    k_pages, v_pages, table, gpu_len, _, _ = gqa_pool([L_ + 1 for L_ in lens], Hkv, D, PS, seed)
+    gpu_len.copy_(torch.tensor(lens, dtype=torch.int32, device=DEV))
+    g = torch.Generator(device="cpu").manual_seed(seed + 7)
+    q = (torch.randn((B, Hkv * G, D), generator=g)).to(torch.bfloat16).to(DEV)
+    k_new = (torch.randn((B, Hkv, 1, D), generator=g)).to(torch.bfloat16).to(DEV)
+    v_new = (torch.randn((B, Hkv, 1, D), generator=g)).to(torch.bfloat16).to(DEV)
+    out = torch.full((B, Hkv * G, D), float("nan"), dtype=torch.float32, device=DEV)
+    lse = torch.full((B, Hkv * G), float("nan"), dtype=torch.float32, device=DEV)
+    len_out = torch.zeros(B, dtype=torch.int32, device=DEV)
+    t = dict(q=q, k_new=k_new, v_new=v_new, k_pages=k_pages, v_pages=v_pages, table=table,
+             gpu_len=gpu_len, out=out, lse=lse, len_out=len_out)
+
+    def call(stream):
+        return L.ws_gqa_append_decode_partial_noalloc(
+            _p(q), _p(k_new), _p(v_new), _p(k_pages), _p(v_pages), _p(table), _p(gpu_len),
+            _p(len_out), B, Hkv * G, Hkv, D, PS, table.shape[1], k_pages.shape[0],
+            max(lens) + 1, n_splits, ctypes.c_float(D ** -0.5), _p(out), _p(lse), stream)
+
+    return call, t
+
+
 def _step(L, use_noalloc, lens, Hkv, G, seed, n_splits):
     """One fused step over a fresh seeded pool; returns (out, lse, len_out,
     k_pages, v_pages) after the call."""
@@ -101,3 +127,48 @@ def test_noalloc_refuses_plans_beyond_its_scratch():
         ctypes.c_float(0.1), p, p, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == -3  # WS_EWORKSPACE
     assert b"static" in L.ws_last_error()
+
+
+def test_noalloc_captured_in_a_graph_replays_bit_for_bit():
+    """The entry point under HIP graph capture (torch.cuda.graph): after an
+    eager call on the device (its first call there looks up the scratch
+    address, which must not happen during a capture), a captured call
+    replays three times, with the state restored and the test's own eager
+    work between replays, each time bit for bit what the eager call gave."""
+    L = _lib()
+    lens, Hkv, G, seed = [900, 17, 300, 64], 4, 8, 41
+    call, t = _setup(L, lens, Hkv, G, seed, 0)
+    keep = {k: v.clone() for k, v in t.items()}
+    torch.cuda.synchronize()
+    rc = call(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, L.ws_last_error().decode()
+    torch.cuda.synchronize()
+    names = ("out", "lse", "len_out", "k_pages", "v_pages")
+    want = {k: t[k].clone() for k in names}
+
+    def restore():
+        for k, v in keep.items():
+            t[k].copy_(v)
+        torch.cuda.synchronize()
+
+    restore()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = call(ctypes.c_void_p(side.cuda_stream))
+    assert rc == 0, L.ws_last_error().decode()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        print(f"noalloc graph replay {rep}", flush=True)
+        restore()
+        graph.replay()
+        torch.cuda.synchronize()
+        for k in names:
+            a, b = t[k].cpu(), want[k].cpu()
+            assert torch.equal(a.view(torch.uint8) if a.dtype != torch.int32 else a,
+                               b.view(torch.uint8) if b.dtype != torch.int32 else b), \
+                f"replay {rep}: {k} differs from the eager call"
+    assert t["len_out"].cpu().tolist() == [x + 1 for x in lens]
