@@ -29,19 +29,23 @@
 // flight (148 KB per CU), each wave's ten load instructions of a block spread
 // over its MFMAs (a burst stalls the wave while the memory pipeline drains).
 //
-// Tile layout.  gfx950's LDS has 128 banks of 4 bytes; a 64-lane
-// ds_read_b128 is served in two 32-lane passes and ds_read_b64_tr_b16 in one
-// pass.  Row r of a tile (72 chunks of 16 bytes) starts at chunk
-// wide_row_off(r) = 72 r + 5 (r / 8) + 4 ((r / 4) % 2), so that
-//   - the QK reads (32 rows, one chunk each per pass) hit 32 different
-//     chunk slots mod 32: the row offsets are distinct mod 32;
-//   - the PV transposed reads (rows 8 m .. 8 m + 7, 16 bytes of each row per
-//     8 lanes) hit 128 different banks: within each 8-row group the offsets
-//     are one residue class mod 4, spaced by 4 chunks mod 32.
+// Tile layout.  gfx950's LDS serves 256 bytes per pass, 64 banks of 4 bytes
+// (as the bank-conflict counter measures it): a 64-lane ds_read_b128 takes
+// four passes of 16 lanes, ds_read_b64_tr_b16 two passes of 32 lanes, and a
+// pass whose lanes hit one bank twice takes a cycle more per repeat.  Row r
+// of a tile (72 chunks of 16 bytes) starts at chunk
+// wide_row_off(r) = 72 r + 5 (r / 4) + 4 ((r / 2) % 2), so that
+//   - the QK reads (16 rows, one chunk each per pass) hit 16 different
+//     chunk slots mod 16: the offsets of rows 0 .. 15, and of 16 .. 31, are
+//     distinct mod 16;
+//   - the PV transposed reads (rows 4 a .. 4 a + 3, 64 bytes of each row per
+//     pass) hit 64 different banks: within each aligned 4-row group the
+//     offsets are c, c + 4, c + 8, c + 12 mod 16.
 // Every operand read is one per-lane base plus an immediate offset.  A tile's
-// 2368 chunks (2323 used) take 37 load instructions of 64 lanes; each wave
-// issues 10 per block, the last 3 of them into a small sink, so every wave's
-// outstanding-load count is the same.
+// 2368 chunks (2343 used) take 37 load instructions of 64 lanes: instruction
+// i of wave w fills chunks 64 I .. 64 I + 63, I = w + 4 i, and the waves
+// other than wave 0 send their tenth (I = 37 .. 39) into a 1 KB sink, so
+// every wave's outstanding-load count is the same (ten per block).
 //
 // No rescaling: the output accumulators feed only MFMAs and the final stores,
 // so they stay in AGPRs (a VALU rescale merged back into them makes the
@@ -66,26 +70,26 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 constexpr int kWideRowData = 72;  // 576 bf16 = 72 x 16 B
 // LDS chunk offset of row r of a tile.
 __host__ __device__ constexpr int wide_row_off(int r) {
-  return kWideRowData * r + 5 * (r >> 3) + 4 * ((r >> 2) & 1);
+  return kWideRowData * r + 5 * (r >> 2) + 4 * ((r >> 1) & 1);
 }
-constexpr int kWideTileChunks = wide_row_off(31) + kWideRowData;  // 2323
+constexpr int kWideTileChunks = wide_row_off(31) + kWideRowData;  // 2343
 constexpr int kWideTileDma = (kWideTileChunks + 63) / 64;         // 37 instructions of 64 chunks
 constexpr int kWideTileAlloc = kWideTileDma * 64;                 // 2368 chunks
 constexpr int kWideTiles = 4;
 constexpr int kWideDmaPerWave = 10;  // 4 x 10 = 37 + 3 into the sink
-constexpr int kWideSinkDma = 4 * kWideDmaPerWave - kWideTileDma;
 constexpr float kWideHeadroomLog2 = 64.f;
-// chunk offsets of rows 16 s + 8 t + q (q < 8) are wide_row_off(q) + 1162 s + 581 t
-constexpr int kWideRowsS = 1162, kWideRowsT = 581;
+// chunk offsets of rows 16 s + 8 t + q (q < 8) are wide_row_off(q) + 1172 s + 586 t
+constexpr int kWideRowsS = 1172, kWideRowsT = 586;
 static_assert(wide_row_off(16) == kWideRowsS * 1 + 0 && wide_row_off(8) == kWideRowsT &&
                   wide_row_off(24 + 7) == wide_row_off(7) + kWideRowsS + kWideRowsT,
               "row offsets split into a row-group part and a per-lane part");
-static_assert(kWideTileDma == 37 && kWideSinkDma == 3, "ten instructions per wave");
+static_assert(kWideTileDma == 37 && 4 * (kWideDmaPerWave - 1) == kWideTileDma - 1,
+              "instructions 0-8 of every wave and instruction 9 of wave 0 fill the tile");
 
 // Row of tile chunk c (the pad chunks after a row count as that row's; c past
 // the tile gives row 31).
 __device__ __forceinline__ int wide_row_of(int c) {
-  int r = min(c / 73, 31);  // 72 r <= wide_row_off(r) <= 73 r: the row is r or r + 1
+  int r = min(c / 74, 31);  // 72 r <= wide_row_off(r) <= 74 r: the row is r or r + 1
   if (r < 31 && wide_row_off(r + 1) <= c) ++r;
   return r;
 }
@@ -144,6 +148,16 @@ __device__ __forceinline__ void wide_dma16_s(uint32_t off, const void* sbase,
                : "memory");
 }
 
+// The same with the LDS destination lds_base + imm, imm a constant once the
+// caller's loop is unrolled (one scalar add into M0).
+__device__ __forceinline__ void wide_dma16_add(uint32_t off, const void* sbase,
+                                               uint32_t lds_base, int imm) {
+  asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off), "s"(sbase), "s"(lds_base), "i"(imm)
+               : "memory", "scc");
+}
+
 // Waits until at most N vector memory operations of this wave are in flight
 // and its LDS reads are done, then joins the workgroup barrier.
 template <int N>
@@ -190,7 +204,7 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
   constexpr int H = kWideHeads;
   constexpr int add = APPEND ? 1 : 0;
   __shared__ u32x4 s_tile[kWideTiles][kWideTileAlloc];
-  __shared__ u32x4 s_sink[kWideSinkDma * 64];
+  __shared__ u32x4 s_sink[64];
   __shared__ int s_pref[kWideMaxSeqs + 1];
   __shared__ int s_len[kWideMaxSeqs];
   __shared__ int s_wpref[kSeqPlanMax + 1];
@@ -207,14 +221,14 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
   // chunks this lane loads with its kWideDmaPerWave instructions (tile chunk
   // c of row r = wide_row_of(c) is chunk c - wide_row_off(r) of the row; pad
   // chunks and the sink read a chunk of the block), two 16-bit offsets per
-  // register.
+  // register (the largest is 31 * 1152 + 1136).
   uint32_t offp[kWideDmaPerWave / 2];
 #pragma unroll
   for (int j = 0; j < kWideDmaPerWave / 2; ++j) {
     uint32_t v = 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int c = 64 * (kWideDmaPerWave * wave + 2 * j + h) + lane;
+      const int c = 64 * min(wave + 4 * (2 * j + h), kWideTileDma - 1) + lane;
       const int r = wide_row_of(c);
       const int x = min(c - wide_row_off(r), kWideRowData - 1);
       v |= (uint32_t)(r * (kMlaL * 2) + 16 * x) << (16 * h);
@@ -224,13 +238,10 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
   // Per-lane part of the PV transposed reads: 16-lane group G = lane / 16
   // (k-slot half j2 = G / 2, column half ch = G % 2), lane 4 e + r of the
   // group addresses token row 4 j2 + e, columns 16 ch + 4 r .. + 3.
-  // Recomputed where used (a few VALU operations) rather than kept live.
-  auto v_lane = [&]() __attribute__((always_inline)) {
-    int l = lane;
-    asm volatile("" : "+v"(l));
-    const int G = l >> 4, e = (l >> 2) & 3, r = l & 3;
+  const uint32_t v_lane = [&] {
+    const int G = lane >> 4, e = (lane >> 2) & 3, r = lane & 3;
     return (uint32_t)(16 * wide_row_off(4 * (G >> 1) + e) + 2 * (16 * (G & 1) + 4 * r));
-  };
+  }();
 
   if (APPEND && p.len_out && g == 0)
     for (int b = tid; b < p.B; b += NT) p.len_out[b] = step_len_out(p.len_in, b, add, p.cap);
@@ -247,6 +258,12 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
   }
   if (tid == 0) s_redo = 0;  // read after the ring's barriers
   if (!plan.has_work) return;
+  // The scores enter the softmax as q.k * sx with sx > 0: a negative scale
+  // negates the queries instead (exact in bf16), and a zero scale becomes the
+  // smallest normal float, whose products round every finite score to the
+  // same probability while masked tokens stay -inf.
+  const bool q_neg = p.scale_log2 < 0.f;
+  const float sx = q_neg ? -p.scale_log2 : p.scale_log2 > 0.f ? p.scale_log2 : 1.17549435e-38f;
   const int blk_begin = uniform(plan.begin);
   const int blk_end = uniform(plan.end);
   int blk = blk_begin;
@@ -267,20 +284,38 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
     const int nblk = seg_end - blk;
     const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
 
-    // Page ids of the segment's blocks, 64 at a time (lane l: block
-    // pid_base + l), read with readlane; an id outside the pool is kept
-    // clamped with bit 31 set (the loads read the clamped page, the piece is
-    // NaN and the append skips it).
+    // Pool token index of the first row of each of the segment's blocks, 64
+    // at a time (lane l: block pid_base + l), read with readlane; a page id
+    // outside the pool is clamped and marks the index with bit 31 (the loads
+    // read the clamped page and the piece is NaN).
     int pid_base = 0;
-    int m_pid = 0;
+    int m_tok = 0;
     int seg_bad = 0;
     auto fetch_pids = [&]() __attribute__((always_inline)) {
       const int t0 = t_begin + 32 * min(pid_base + lane, nblk - 1);
-      const int raw = pt[t0 / p.page_size];
+      const int page = t0 / p.page_size;
+      const int raw = pt[page];
       const int pid = clamp_page(raw, p.num_pages);
-      m_pid = pid | (raw == pid ? 0 : (int)0x80000000u);
+      m_tok = (pid * p.page_size + (t0 - page * p.page_size)) |
+              (raw == pid ? 0 : (int)0x80000000u);
     };
     fetch_pids();
+    // The appended token is its sequence's last, so one segment holds it: that
+    // segment's workgroup writes its row (c_new, pe_new) into the token's page
+    // slot first, and every block then loads from the pool alike.
+    const bool owner = APPEND && len_old >= t_begin && len_old < t_end;
+    u32x4 new_chunk = {0u, 0u, 0u, 0u};
+    int new_dst = -1;  // the row's pool token index, -1: not written here
+    if (owner && tid < kWideRowData) {
+      const int page = len_old / p.page_size;
+      const int raw = pt[page];
+      new_dst = clamp_page(raw, p.num_pages) == raw
+                    ? raw * p.page_size + (len_old - page * p.page_size)
+                    : -1;
+      new_chunk = tid < kMlaC / 8
+                      ? ((const u32x4*)(p.c_new + (size_t)b * p.c_stride))[tid]
+                      : ((const u32x4*)(p.pe_new + (size_t)b * p.pe_stride))[tid - kMlaC / 8];
+    }
     // Q^T of this wave's 32 heads: k-step u holds dims 16 u + 8 j2 .. + 8.
     // The q_nope rows come through LDS (the tiles are free here): one 1 KB
     // load instruction per row into a 65-chunk row slot (the read-back of
@@ -298,9 +333,14 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
       for (int u = 32; u < 36; ++u)
         qb[u] = ((const u32x4*)(p.q_pe + (qrow0 + n32) * 64))[2 * (u - 32) + j2];
       asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+      if (new_dst >= 0) ((u32x4*)(p.latent_w + (size_t)new_dst * kMlaL))[tid] = new_chunk;
       const u32x4* qs = &s_tile[0][0] + (32 * wave + n32) * 65 + j2;
 #pragma unroll
       for (int u = 0; u < 32; ++u) qb[u] = qs[2 * u];
+      if (q_neg) {
+#pragma unroll
+        for (int u = 0; u < 36; ++u) qb[u] ^= 0x80008000u;
+      }
     }
     // The queries are needed from the first block on: have them in registers
     // before the block loads go out (a wait the compiler placed at their
@@ -308,20 +348,21 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
     // wave done reading its rows before the loads overwrite them.
 #pragma unroll
     for (int u = 0; u < 36; ++u) asm volatile("" : : "v"(qb[u]));
+    // the appended row is in its page before any wave's loads of the block
+    // go out (this wave's store done, then the barrier)
+    if (owner) asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
     wide_lds_barrier();
 
-    const long long nc_off =
-        APPEND ? (const char*)(p.c_new + (size_t)b * p.c_stride) - g0 : 0;
-    const long long npe_off =
-        APPEND ? (const char*)(p.pe_new + (size_t)b * p.pe_stride) - g0 : 0;
     // Block k of the segment into tile `slot`: this wave's 10 instructions
-    // of 64 chunks (chunks 64 I .. 64 I + 63 of the tile, I = 10 wave + i,
-    // the last three of wave 3 into the sink).  Rows past t_end repeat the
-    // last valid row (masked in the softmax); a block past the segment's end
-    // goes into a tile no later block of the segment uses.
+    // of 64 chunks.  Rows past t_end read the last valid row's last chunk
+    // (each lane's offset clamped: finite values whose probabilities are 0);
+    // a block past the segment's end reads q_nope (at least 128 KB) into a
+    // tile no later block of the segment uses.
     struct Dma {
-      const char* sb;
-      uint32_t dst0, dstep, sink0;
+      const char* sb;   // the block's first row
+      uint32_t wbase;   // this wave's part of the tile (LDS bytes)
+      uint32_t d9;      // instruction 9's destination (tile or sink)
+      uint32_t lim;     // offset clamp
     };
     auto issue_begin = [&](int k, int slot) __attribute__((always_inline)) {
       const bool valid = k < nblk;
@@ -330,75 +371,48 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
         pid_base += 64;
         fetch_pids();
       }
-      const int t0 = t_begin + 32 * kc;
-      const int page = t0 / p.page_size;
-      const int pid_raw = __builtin_amdgcn_readlane(m_pid, kc - pid_base);
-      seg_bad |= pid_raw;
-      const int pid = pid_raw & 0x7fffffff;
-      const long long lb =
-          (long long)((size_t)pid * p.page_size + (t0 - page * p.page_size)) * (kMlaL * 2);
-      const int last = min(32, t_end - t0) - 1;
-      const int new_r = (APPEND && valid) ? len_old - t0 : -1;
+      const int tok_raw = __builtin_amdgcn_readlane(m_tok, kc - pid_base);
+      seg_bad |= tok_raw;
+      const uint32_t tok = (uint32_t)tok_raw & 0x7fffffffu;
+      const int nt = t_end - (t_begin + 32 * kc);
+      const uint32_t lim =
+          nt >= 32 ? 0xffffu : (uint32_t)((nt - 1) * (kMlaL * 2) + 16 * (kWideRowData - 1));
       Dma d;
-      // LDS destinations: scalar, recomputed per block (not hoisted)
-      d.dst0 = tile_base0 + (uint32_t)slot * (kWideTileAlloc * 16) +
-               1024 * kWideDmaPerWave * wave;
-      d.sink0 = sink_base;
-      asm volatile("" : "+s"(d.dst0), "+s"(d.sink0));
-      // all 32 rows are tokens of the segment (or, past the segment's end,
-      // the loads only have to stay in bounds: they read q_nope, at least
-      // 128 KB): a scalar base and the precomputed offsets, one instruction
-      // at a time (dma_one)
-      d.dstep = 1024;
-      const bool fast = !valid || (last == 31 && (unsigned)new_r >= 32u);
-      d.sb = valid ? g0 + lb : (const char*)p.q_nope;
-      if (fast) return d;
-      // the segment's last block when partial or holding the appended
-      // token, all ten instructions now: rows past t_end repeat the last
-      // valid row, the appended token's row comes from c_new / pe_new
-      int lane_v = lane;
-      asm volatile("" : "+v"(lane_v));
-#pragma unroll
-      for (int i = 0; i < kWideDmaPerWave; ++i) {
-        const int I = kWideDmaPerWave * wave + i;
-        const int c = 64 * I + lane_v;
-        const int r = wide_row_of(c);
-        const int x = min(c - wide_row_off(r), kWideRowData - 1);
-        const int rr = min(r, last);
-        long long off = lb + rr * (kMlaL * 2) + 16 * x;
-        if (APPEND && rr == new_r) off = x < 64 ? nc_off + 16 * x : npe_off + 16 * (x - 64);
-        const uint32_t dst = I < kWideTileDma ? d.dst0 + 1024 * i
-                                              : d.sink0 + 1024 * (I - kWideTileDma);
-        wide_dma16(g0 + off, dst);
-      }
-      // the ten per-slot instructions still go out (no branch at each
-      // slot), from q_nope into the sink: waits that count ten per block
-      // then wait for more than they need, never less
-      d.sb = (const char*)p.q_nope;
-      d.dst0 = d.sink0;
-      d.dstep = 0;
+      d.sb = valid ? g0 + (size_t)tok * (kMlaL * 2) : (const char*)p.q_nope;
+      d.lim = lim;
+      const uint32_t tb = tile_base0 + (uint32_t)slot * (kWideTileAlloc * 16);
+      d.wbase = tb + 1024 * wave;
+      // a scalar select (the compiler makes a branch of the conditional)
+      asm("s_cmp_eq_u32 %1, 0\n\ts_cselect_b32 %0, %2, %3"
+          : "=s"(d.d9)
+          : "s"(wave), "s"(tb + 1024 * (kWideTileDma - 1)), "s"(sink_base)
+          : "scc");
+      // recomputed per block (not hoisted)
+      asm volatile("" : "+s"(d.wbase), "+s"(d.d9));
       return d;
     };
-    // Instruction i of a block (for a block issue_begin loaded already, a
-    // load into the sink).
-    auto dma_one = [&](const Dma& d, int i) __attribute__((always_inline)) {
-      const int I = kWideDmaPerWave * wave + i;
-      // unpacked here, at each use (five live registers, not ten)
-      asm volatile("" : "+v"(offp[i >> 1]));
-      const uint32_t off = (i & 1) ? offp[i >> 1] >> 16 : offp[i >> 1] & 0xffffu;
-      // a scalar select (the compiler makes a branch of the conditional)
-      uint32_t dst;
-      asm("s_cmp_lt_i32 %1, %4\n\ts_cselect_b32 %0, %2, %3"
-          : "=s"(dst)
-          : "s"(I), "s"(d.dst0 + d.dstep * i), "s"(d.sink0 + 1024 * (I - kWideTileDma)),
-            "n"(kWideTileDma)
-          : "scc");
-      wide_dma16_s(off, d.sb, dst);
+    // The offset pair of instructions 2 j and 2 j + 1 (offp[j]).
+    auto dma_pair = [&](const Dma& d, int j) __attribute__((always_inline)) {
+      asm volatile("" : "+v"(offp[j]));  // unpacked at each use: five live registers
+      return offp[j];
+    };
+    // Instruction i of a block (i a constant after unrolling), pr =
+    // dma_pair(d, i / 2), its offset clamped.
+    auto dma_one = [&](const Dma& d, uint32_t pr, int i) __attribute__((always_inline)) {
+      const uint32_t off = min((i & 1) ? pr >> 16 : pr & 0xffffu, d.lim);
+      if (i < kWideDmaPerWave - 1)
+        wide_dma16_add(off, d.sb, d.wbase, 4 * 1024 * i);
+      else
+        wide_dma16_s(off, d.sb, d.d9);
     };
     auto issue = [&](int k, int slot) __attribute__((always_inline)) {
       const Dma d = issue_begin(k, slot);
+      uint32_t pr = 0;
 #pragma unroll
-      for (int i = 0; i < kWideDmaPerWave; ++i) dma_one(d, i);
+      for (int i = 0; i < kWideDmaPerWave; ++i) {
+        if ((i & 1) == 0) pr = dma_pair(d, i >> 1);
+        dma_one(d, pr, i);
+      }
     };
 
     f32x16 acc[16];
@@ -434,7 +448,9 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
     // otherwise keep a register per read offset instead of using the
     // instruction's offset field)
     auto vbase = [&](int tile) __attribute__((always_inline)) {
-      return tile_base0 + (uint32_t)tile * (kWideTileAlloc * 16) + v_lane();
+      uint32_t vl = v_lane;
+      asm volatile("" : "+v"(vl));
+      return tile_base0 + (uint32_t)tile * (kWideTileAlloc * 16) + vl;
     };
     auto vread = [&](uint32_t vt, int m) __attribute__((always_inline)) {
       const int sv = m >> 4, ct = m & 15;
@@ -450,16 +466,13 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
       asm volatile("" : "+a"(a));
       asm volatile("" : : : "memory");
     };
-    // soft_x: the scores of a block as x = q.k * scale_log2 - m_run (xa: the
-    // first PV k-step's, xh: the second's).  For a positive scale (the only
-    // one attention uses) the block's largest score is the scale times the
-    // largest raw score (v_max3 over the accumulator) and x is one FMA per
-    // score; tokens past the end of a partial block are raw -inf.  Any other
-    // scale takes the plain route.
-    auto soft_x = [&](int kb, const f32x16& sc, float (&xa)[8], float (&xh)[8])
+    // soft_x: the scores of a block as x = q.k * sx - m_run (xa: the first PV
+    // k-step's, xh: the second's).  With sx > 0 the block's largest score is
+    // sx times the largest raw score (v_max3 over the accumulator) and x is
+    // one FMA per score; tokens past the end of a partial block are raw -inf.
+    auto soft_x = [&](int kb, const f32x16& sc, float (&xa)[8], float (&xh)[8], bool first)
         __attribute__((always_inline)) {
       const int nt = min(32, t_end - (t_begin + 32 * kb));
-      const float sl = p.scale_log2;
       f32x16 v = sc;
       if (nt < 32) {  // accumulator i is token 8 (i / 4) + 4 j2 + i % 4
         int l = lane;  // recomputed here rather than kept live
@@ -468,27 +481,17 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = 8 * (i >> 2) + (i & 3) < lim ? v[i] : neg_inf();
       }
-      float bm;
-      if (sl > 0.f) {
-        float r = v[0];
+      float r = v[0];
 #pragma unroll
-        for (int i = 1; i < 16; ++i) r = fmaxf(r, v[i]);
-        bm = r * sl;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = v[i] == neg_inf() ? neg_inf() : v[i] * sl;
-        bm = v[0];
-#pragma unroll
-        for (int i = 1; i < 16; ++i) bm = fmaxf(bm, v[i]);
-      }
+      for (int i = 1; i < 16; ++i) r = fmaxf(r, v[i]);
+      const float bm = r * sx;
       m_max = fmaxf(m_max, bm);
-      {  // m_run unset (the pass's first block): the head's largest score
+      if (first) {  // m_run unset (the first pass): the head's largest score
         float lo, hi;
         pair_xor32(bm, lo, hi);
         m_run = m_run == neg_inf() ? fmaxf(lo, hi) : m_run;
       }
       const float nm = -m_run;
-      const float sx = sl > 0.f ? sl : 1.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         xa[i] = __builtin_fmaf(v[i], sx, nm);
@@ -525,6 +528,7 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
       const Dma d = issue_begin(kk + 3, (kk + 3) & (kWideTiles - 1));
       f32x16 sc;
       u32x4 kr[5], va[4], pb[2];
+      uint32_t pr = 0;
       const uint32_t vt = vbase(tp);
 #pragma unroll
       for (int u = 0; u < 4; ++u) kr[u] = qk_read(tq, u);
@@ -542,14 +546,17 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
           pv_mfma(va[m & 3], pb[m >> 4], m);
           if (m < 16 && (m & 3) == 1) soft_p(xh, pb[1], m >> 2);
         }
-        if (u % 4 == 2 && u < 40) dma_one(d, u / 4);  // instructions 0-8
+        if (u % 4 == 2) {  // instructions 0-8
+          if ((u / 4) % 2 == 0) pr = dma_pair(d, u / 8);
+          dma_one(d, pr, u / 4);
+        }
       }
-      soft_x(kk + 1, sc, xa, xh);
+      soft_x(kk + 1, sc, xa, xh, false);
 #pragma unroll
       for (int m = 24; m < 32; ++m) {
         if (m + 3 < 32) va[(m + 3) & 3] = vread(vt, m + 3);
         pv_mfma(va[m & 3], pb[1], m);
-        if (m == 27) dma_one(d, 9);
+        if (m == 27) dma_one(d, pr, 9);
       }
     };
     // The pass's last block: PV only (its tile is in and synchronised).
@@ -593,7 +600,7 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
           if (u + 4 < 36) kr[(u + 4) % 5] = qk_read(0, u + 4);
           qk_mfma(sc, kr[u % 5], u);
         }
-        soft_x(0, sc, xa, xh);
+        soft_x(0, sc, xa, xh, true);
       }
 #pragma clang loop unroll(disable)
       for (int k = 0; k + 1 < nblk; ++k) step(k, xa, xh);
@@ -617,21 +624,6 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
       m_run = m_max;
     }
 
-    // The appended token is its sequence's last, so a segment that holds it
-    // ends with its block, whose tile is intact: row len_old - t0 of tile
-    // (nblk - 1) % 4 holds its 72 chunks (read from c_new / pe_new), which go
-    // into the token's page slot.
-    if (APPEND && len_old >= t_begin && len_old < t_end) {
-      const int t0 = t_begin + 32 * (nblk - 1);
-      const int pid = __builtin_amdgcn_readlane(m_pid, nblk - 1 - pid_base);
-      const int page = t0 / p.page_size;
-      const int r = len_old - t0;
-      if (tid < kWideRowData && pid >= 0)  // bit 31: the page id is outside the pool
-        ((u32x4*)(p.latent_w +
-                  ((size_t)pid * p.page_size + (len_old - page * p.page_size)) * kMlaL))[tid] =
-            s_tile[(nblk - 1) % kWideTiles][wide_row_off(r) + tid];
-    }
-
     float lo, hi;
     pair_xor32(l_run, lo, hi);
     const float l_tot = lo + hi;
@@ -646,12 +638,11 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
         p.part_lse[(size_t)(g + b) * H + head] = lse_v;
     }
     // The outputs leave through LDS (the tiles are free: every wave is past
-    // the pass's last barrier, and the append above has read its row), so
-    // that each store instruction writes one contiguous 1 KB row: wave w
-    // stages its 32 rows (row stride 260 dwords: the 64 lanes' writes and
-    // reads hit distinct banks) and stores them itself.  Accumulator ct
-    // value i is column 32 ct + 8 (i / 4) + 4 j2 + i % 4.
-    wide_lds_barrier();  // the append's tile read is done
+    // the pass's last barrier), so that each store instruction writes one
+    // contiguous 1 KB row: wave w stages its 32 rows (row stride 260 dwords:
+    // the row reads and the fp32 writes hit distinct banks, the bf16 writes
+    // two lanes per bank pair) and stores them itself.  Accumulator ct value
+    // i is column 32 ct + 8 (i / 4) + 4 j2 + i % 4.
     uint32_t* stage = (uint32_t*)&s_tile[0][0] + (size_t)(32 * wave) * 260;
     if (!whole) {  // bf16 piece: all 512 columns at once
 #pragma unroll

@@ -52,6 +52,34 @@ def test_mla_partial_many_heads(H, wg):
     assert_close(lse.cpu().numpy(), wl, LSE_ATOL, LSE_RTOL, f"H={H} lse")
 
 
+@pytest.mark.parametrize("scale", [-SCALE, 0.0])
+def test_mla_128_heads_non_positive_scale(scale):
+    """A negative scale (the kernel negates the queries and uses |scale|) and
+    a zero scale (every score equal: uniform weights, lse = ln n), partial
+    blocks and an empty sequence included, against fp64 at that scale."""
+    H = 128
+    lens = [0, 70, 1500, 4097]
+    _say(f"mla H=128 scale={scale} lens={lens}")
+    lat, pt, gl, cs, pes = mla_pool(lens, PS, seed=141)
+    B = len(lens)
+    qn = bf16_randn((B * H, 512), 142, 0.5).to(DEV)
+    qp = bf16_randn((B * H, 64), 143, 0.5).to(DEV)
+    out, lse = ops.mla_decode_partial(qn, qp, lat, pt, gl, scale, max(lens))
+    torch.cuda.synchronize()
+    outs, lses = [], []
+    for b in range(B):
+        rows = slice(b * H, (b + 1) * H)
+        o, l = O.mla_attention_fp64(bits(qn[rows]), bits(qp[rows]), bits(cs[b])[None],
+                                    bits(pes[b])[None], scale)
+        outs.append(o)
+        lses.append(l)
+    want, wl = np.concatenate(outs), np.concatenate(lses)
+    assert_close(out.cpu().numpy(), want, OUT_ATOL, OUT_RTOL, f"scale={scale} out")
+    assert_close(lse.cpu().numpy(), wl, LSE_ATOL, LSE_RTOL, f"scale={scale} lse")
+    if scale == 0.0:
+        assert np.allclose(lse.cpu().numpy()[H:2 * H], np.log(70), atol=1e-5)
+
+
 def test_mla_split_step_128_heads_with_host_partial_and_uv():
     H, Dout = 128, 128
     lens = [333, 2000, 64]
