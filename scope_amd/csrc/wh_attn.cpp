@@ -61,12 +61,10 @@ void state_init(float* base, int H, int Dv) {
   std::memset(base + H, 0, sizeof(float) * (size_t)H * (Dv + 1));
 }
 
-// Folds the states of `cnt` slots into dst (same layout); `oh(i)` is the head
-// of o element i.
-template <class HeadOf>
-void state_combine(const float* const* src, int cnt, int H, int Dv, float* dst, HeadOf oh) {
+// Per-head weights 2^(m_s - M) of `cnt` slot states (w[s*H + h]) and the
+// combined m, l into dst.
+void state_weights(const float* const* src, int cnt, int H, float* dst, float* w) {
   StateView d = view(dst, H);
-  std::vector<float> w((size_t)cnt * H);
   for (int h = 0; h < H; ++h) {
     float M = -INFINITY;
     for (int s = 0; s < cnt; ++s) M = std::max(M, src[s][h]);
@@ -80,6 +78,15 @@ void state_combine(const float* const* src, int cnt, int H, int Dv, float* dst, 
     d.m[h] = M;
     d.l[h] = L;
   }
+}
+
+// Folds the states of `cnt` slots into dst (same layout); `oh(i)` is the head
+// of o element i.
+template <class HeadOf>
+void state_combine(const float* const* src, int cnt, int H, int Dv, float* dst, HeadOf oh) {
+  StateView d = view(dst, H);
+  std::vector<float> w((size_t)cnt * H);
+  state_weights(src, cnt, H, dst, w.data());
   const size_t no = (size_t)H * Dv;
   for (size_t i = 0; i < no; ++i) {
     const int h = oh(i);
@@ -105,9 +112,9 @@ int resolve_threads(int n_threads, int64_t T) {
 // Runs the plan.  seg(row, tok0, tok1, state) fills a state; fin(row, state)
 // writes a row's output; empty(row) writes the empty result.  Slots hold
 // states of rows split across threads.
-template <class Seg, class Fin, class Empty, class HeadOf>
+template <class Seg, class Fin, class Empty, class Comb>
 void run_plan(const Plan& P, int R, int H, int Dv, int n_req, const int32_t* row_len, Seg seg,
-              Fin fin, Empty empty, HeadOf oh) {
+              Fin fin, Empty empty, Comb comb) {
   const size_t ssz = (size_t)H * (Dv + 2);
   if (P.T == 0) {
     for (int r = 0; r < R; ++r) empty(r);
@@ -148,7 +155,7 @@ void run_plan(const Plan& P, int R, int H, int Dv, int n_req, const int32_t* row
       if (o0 == o1) continue;  // written by its only thread
       src.clear();
       for (int o = o0; o <= o1; ++o) src.push_back(slots.get() + (size_t)(o + row) * ssz);
-      state_combine(src.data(), (int)src.size(), H, Dv, st.get(), oh);
+      comb(src.data(), (int)src.size(), st.get());
       fin(row, st.get());
     }
   }
@@ -320,7 +327,9 @@ int attn_partial(const char* fn, const InT* q, const InT* k_pages, const InT* v_
   };
   auto empty = [&](int r) { write_empty(sink, (size_t)r * G, G, D); };
   run_plan(P, R, G, D, n_threads, row_len.data(), seg, fin, empty,
-           [D](size_t i) { return (int)(i / D); });
+           [G, D](const float* const* src, int cnt, float* dst) {
+             state_combine(src, cnt, G, D, dst, [D](size_t i) { return (int)(i / D); });
+           });
   return WH_OK;
 }
 
@@ -372,13 +381,41 @@ int mla_partial(const char* fn, const uint16_t* q_nope, const uint16_t* q_pe,
                            s.o, vs);
               });
   };
+  // the 16 rows of a group, 16 heads at a time (AVX-512; the values and
+  // rounding of write_final)
   auto fin = [&](int v, const float* st) {
-    write_final<OutT>(st, Hg, Dv, sink, (size_t)v * Hg,
-                      [&](int h, int s) { return st[2 * Hg + s * Hg + h]; });
+    const size_t row0 = (size_t)v * Hg;
+    float inv[kMlaHeads];
+    for (int h = 0; h < Hg; ++h) {
+      const float l = st[Hg + h];
+      inv[h] = (sink.lse || sink.normalize) ? 1.f / l : 1.f;
+    }
+    if constexpr (std::is_same_v<OutT, uint16_t>)
+      mla_final_bf16(st + 2 * Hg, inv, sink.out + row0 * Dv, (size_t)Dv);
+    else
+      mla_final_f32(st + 2 * Hg, inv, sink.out + row0 * Dv, (size_t)Dv);
+    for (int h = 0; h < Hg; ++h) {
+      const size_t r = row0 + h;
+      const float l = st[Hg + h];
+      if (!(l > 0.f)) {
+        write_empty(sink, r, 1, Dv);
+      } else if (sink.lse) {
+        sink.lse[r] = (st[h] + std::log2(l)) * kLn2;
+      } else {
+        sink.mx[r] = st[h] * kLn2;
+        sink.sm[r] = l;
+      }
+    }
   };
   auto empty = [&](int v) { write_empty(sink, (size_t)v * Hg, Hg, Dv); };
   run_plan(P, R, Hg, Dv, n_threads, row_len.data(), seg, fin, empty,
-           [](size_t i) { return (int)(i % kMlaHeads); });
+           [](const float* const* src, int cnt, float* dst) {
+             std::vector<float> w((size_t)cnt * kMlaHeads);
+             std::vector<const float*> so((size_t)cnt);
+             for (int s = 0; s < cnt; ++s) so[s] = src[s] + 2 * kMlaHeads;  // the o parts
+             state_weights(src, cnt, kMlaHeads, dst, w.data());
+             mla_combine_o(so.data(), w.data(), cnt, dst + 2 * kMlaHeads);
+           });
   return WH_OK;
 }
 

@@ -470,6 +470,111 @@ double sum_lines(const double* p, size_t words) {
   return _mm512_reduce_add_pd(_mm512_add_pd(a0, a1));
 }
 
+namespace {
+
+// In-register transpose of a 16 x 16 float tile: r[i] element j becomes r[j]
+// element i (unpack pairs, then 128-bit lane shuffles).
+inline void transpose16(__m512 (&r)[16]) {
+  __m512 t[16];
+  for (int i = 0; i < 16; i += 2) {
+    t[i] = _mm512_unpacklo_ps(r[i], r[i + 1]);
+    t[i + 1] = _mm512_unpackhi_ps(r[i], r[i + 1]);
+  }
+  for (int i = 0; i < 16; i += 4) {
+    const __m512d a0 = _mm512_castps_pd(t[i]), a1 = _mm512_castps_pd(t[i + 1]);
+    const __m512d b0 = _mm512_castps_pd(t[i + 2]), b1 = _mm512_castps_pd(t[i + 3]);
+    r[i] = _mm512_castpd_ps(_mm512_unpacklo_pd(a0, b0));
+    r[i + 1] = _mm512_castpd_ps(_mm512_unpackhi_pd(a0, b0));
+    r[i + 2] = _mm512_castpd_ps(_mm512_unpacklo_pd(a1, b1));
+    r[i + 3] = _mm512_castpd_ps(_mm512_unpackhi_pd(a1, b1));
+  }
+  // r[4g + k] now holds, in 128-bit lane L, row 4L + (k's pair) elements of
+  // column block g; gather the lanes
+  for (int i = 0; i < 4; ++i) {
+    const __m512 a = r[i], b = r[4 + i], c = r[8 + i], d = r[12 + i];
+    const __m512 ab0 = _mm512_shuffle_f32x4(a, b, 0x44), ab1 = _mm512_shuffle_f32x4(a, b, 0xee);
+    const __m512 cd0 = _mm512_shuffle_f32x4(c, d, 0x44), cd1 = _mm512_shuffle_f32x4(c, d, 0xee);
+    r[i] = _mm512_shuffle_f32x4(ab0, cd0, 0x88);
+    r[4 + i] = _mm512_shuffle_f32x4(ab0, cd0, 0xdd);
+    r[8 + i] = _mm512_shuffle_f32x4(ab1, cd1, 0x88);
+    r[12 + i] = _mm512_shuffle_f32x4(ab1, cd1, 0xdd);
+  }
+}
+
+// bf16 of 16 floats, nearest even, a NaN made quiet (the scalar to_out).
+inline __m256i to_bf16(__m512 v) {
+  const __m512i u = _mm512_castps_si512(v);
+  const __m512i abs = _mm512_and_si512(u, _mm512_set1_epi32(0x7fffffff));
+  const __mmask16 nan = _mm512_cmpgt_epu32_mask(abs, _mm512_set1_epi32(0x7f800000));
+  const __m512i lsb = _mm512_and_si512(_mm512_srli_epi32(u, 16), _mm512_set1_epi32(1));
+  const __m512i rnd = _mm512_add_epi32(_mm512_add_epi32(u, _mm512_set1_epi32(0x7fff)), lsb);
+  __m512i r = _mm512_srli_epi32(rnd, 16);
+  r = _mm512_mask_or_epi32(r, nan, _mm512_srli_epi32(u, 16), _mm512_set1_epi32(0x40));
+  return _mm512_cvtepi32_epi16(r);
+}
+
+// The 32 staged slots of chunk c of every head, scaled: h0[h] holds slots
+// 32c .. 32c+15 of head h, h1[h] slots 32c+16 .. 32c+31.
+inline void mla_chunk(const float* o, __m512 vinv, int c, __m512 (&h0)[16], __m512 (&h1)[16]) {
+  for (int k = 0; k < 16; ++k) {
+    h0[k] = _mm512_mul_ps(_mm512_loadu_ps(o + (size_t)(32 * c + k) * 16), vinv);
+    h1[k] = _mm512_mul_ps(_mm512_loadu_ps(o + (size_t)(32 * c + 16 + k) * 16), vinv);
+  }
+  transpose16(h0);
+  transpose16(h1);
+}
+
+}  // namespace
+
+// Slot 16*half + 4a + b of a chunk is column 8a + 4*half + b: the column
+// order interleaves 4-column pieces of the two halves.
+void mla_final_f32(const float* o, const float* inv, float* out, size_t out_stride) {
+  const __m512 vinv = _mm512_loadu_ps(inv);
+  const __m512i lo = _mm512_setr_epi32(0, 1, 2, 3, 16, 17, 18, 19, 4, 5, 6, 7, 20, 21, 22, 23);
+  const __m512i hi = _mm512_setr_epi32(8, 9, 10, 11, 24, 25, 26, 27, 12, 13, 14, 15, 28, 29, 30,
+                                       31);
+  for (int c = 0; c < kMlaC / 32; ++c) {
+    __m512 h0[16], h1[16];
+    mla_chunk(o, vinv, c, h0, h1);
+    for (int h = 0; h < 16; ++h) {
+      float* dst = out + (size_t)h * out_stride + 32 * c;
+      _mm512_storeu_ps(dst, _mm512_permutex2var_ps(h0[h], lo, h1[h]));
+      _mm512_storeu_ps(dst + 16, _mm512_permutex2var_ps(h0[h], hi, h1[h]));
+    }
+  }
+}
+
+void mla_final_bf16(const float* o, const float* inv, uint16_t* out, size_t out_stride) {
+  const __m512 vinv = _mm512_loadu_ps(inv);
+  const __m512i idx = _mm512_setr_epi64(0, 8, 1, 9, 2, 10, 3, 11);
+  for (int c = 0; c < kMlaC / 32; ++c) {
+    __m512 h0[16], h1[16];
+    mla_chunk(o, vinv, c, h0, h1);
+    for (int h = 0; h < 16; ++h) {
+      const __m512i a = _mm512_castsi256_si512(to_bf16(h0[h]));
+      const __m512i b = _mm512_castsi256_si512(to_bf16(h1[h]));
+      _mm512_storeu_si512(out + (size_t)h * out_stride + 32 * c,
+                          _mm512_permutex2var_epi64(a, idx, b));
+    }
+  }
+}
+
+// Separate multiplies and adds (no contraction into FMAs), as the scalar
+// combine computes them.
+#pragma GCC push_options
+#pragma GCC optimize("fp-contract=off")
+void mla_combine_o(const float* const* src, const float* w, int cnt, float* dst) {
+  constexpr int kH = kMlaHeads;
+  for (int i = 0; i < kMlaC * kH; i += kH) {
+    __m512 acc = _mm512_setzero_ps();
+    for (int s = 0; s < cnt; ++s)
+      acc = _mm512_add_ps(acc, _mm512_mul_ps(_mm512_loadu_ps(w + s * kH),
+                                             _mm512_loadu_ps(src[s] + i)));
+    _mm512_storeu_ps(dst + i, acc);
+  }
+}
+#pragma GCC pop_options
+
 void mla_attend(const uint32_t* qt, const uint16_t* c, size_t c_tok, const uint16_t* pe,
                 size_t pe_tok, int t0, int t1, float sl2, float* m, float* l, float* o,
                 uint32_t* vst) {

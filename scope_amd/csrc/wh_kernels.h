@@ -60,6 +60,18 @@ void mla_attend(const uint32_t* qt, const uint16_t* c, size_t c_tok, const uint1
                 size_t pe_tok, int t0, int t1, float scale_log2, float* m, float* l, float* o,
                 uint32_t* vst);
 
+// Final rows of an MLA state (16 heads): row h of out (row stride
+// out_stride elements) gets o[s*16 + h] * inv[h] in column order, as fp32 or
+// as bf16 rounded to nearest even (a NaN stays a quiet NaN) -- the values
+// and rounding of the scalar write, 16 heads at a time.
+void mla_final_f32(const float* o, const float* inv, float* out, size_t out_stride);
+void mla_final_bf16(const float* o, const float* inv, uint16_t* out, size_t out_stride);
+
+// o part of an MLA state combine: dst[i] = sum over s < cnt of
+// w[s*16 + i%16] * src[s][i] for the 512*16 slot-major values (multiplies
+// and adds, in source order, as the scalar combine).
+void mla_combine_o(const float* const* src, const float* w, int cnt, float* dst);
+
 // Sum of `words` doubles (a multiple of 8) streamed with 512-bit loads: the
 // reading side of the host bandwidth probe.
 double sum_lines(const double* p, size_t words);
