@@ -80,6 +80,39 @@ def test_mla_128_heads_non_positive_scale(scale):
         assert np.allclose(lse.cpu().numpy()[H:2 * H], np.log(70), atol=1e-5)
 
 
+@pytest.mark.parametrize("wg", [3, 7])
+def test_mla_128_heads_append_in_long_segments(wg):
+    """Fused append with few workgroups: segments of hundreds of blocks, so
+    the block holding the appended token (written into its page before the
+    segment's loads) goes out late in the load ring, and each sequence's last
+    block is partial.  Against fp64 over the old tokens plus the new one, and
+    the appended latents bit-exact in their pages."""
+    H = 128
+    lens = [3000, 1500, 64]
+    B = len(lens)
+    _say(f"mla H=128 append, {wg} workgroups, lens={lens}")
+    lat_all = [bf16_randn((L + 1, 576), 160 + b, 0.5) for b, L in enumerate(lens)]
+    lat, pt, gl, _, _ = mla_pool([L + 1 for L in lens], PS, seed=170)
+    for b, L in enumerate(lens):
+        t = torch.arange(L, device=DEV)
+        lat[pt[b, t // PS].long(), t % PS] = lat_all[b][:L].to(DEV)
+    gl.copy_(torch.tensor(lens, dtype=torch.int32, device=DEV))
+    qn = bf16_randn((B * H, 512), 171, 0.5).to(DEV)
+    qp = bf16_randn((B * H, 64), 172, 0.5).to(DEV)
+    new = torch.stack([x[-1] for x in lat_all]).to(DEV)[:, None]
+    len_out = torch.zeros_like(gl)
+    out, lse = ops.mla_append_decode_partial(qn, qp, new[..., :512], new[..., 512:], lat, pt, gl,
+                                             len_out, SCALE, max(lens) + 1, n_workgroups=wg)
+    torch.cuda.synchronize()
+    want, wl = _want(qn, qp, [x[:, :512] for x in lat_all], [x[:, 512:] for x in lat_all], H)
+    assert_close(out.cpu().numpy(), want, OUT_ATOL, OUT_RTOL, f"wg={wg} out")
+    assert_close(lse.cpu().numpy(), wl, LSE_ATOL, LSE_RTOL, f"wg={wg} lse")
+    assert len_out.cpu().tolist() == [L + 1 for L in lens]
+    lb = bits(lat)
+    for b, L in enumerate(lens):
+        assert np.array_equal(lb[int(pt[b, L // PS]), L % PS], bits(lat_all[b][-1])), b
+
+
 def test_mla_split_step_128_heads_with_host_partial_and_uv():
     H, Dout = 128, 128
     lens = [333, 2000, 64]
