@@ -101,14 +101,22 @@ def test_gqa_length_without_room_is_poisoned_not_clamped():
     assert np.isfinite(out2.cpu().numpy()[1]).all()
 
 
-def test_mla_bad_page_and_length_are_poisoned():
+@pytest.mark.parametrize("H,bad_new_page", [(16, False), (128, False), (128, True)])
+def test_mla_bad_page_and_length_are_poisoned(H, bad_new_page):
+    """A page id outside the pool poisons its sequence (NaN), an invalid
+    length its own; the other sequence is exact.  128 heads run the one-pass
+    kernel; with bad_new_page the appended token's own page id is bad, and
+    nothing is written where the clamped id points."""
     lens = [500, 200, 90]
-    _say("mla bad page id + bad length")
+    _say(f"mla bad page id + bad length, H={H}, bad_new_page={bad_new_page}")
     lat, pt, gl, cs, pes = mla_pool([L + 1 for L in lens], PS, seed=43)
     gl.copy_(torch.tensor(lens, dtype=torch.int32, device=DEV))
     pt[0, 3] = -3
+    if bad_new_page:
+        pt[0, lens[0] // PS] = -5  # clamped to pool page 0
+    before = bits(lat[0, lens[0] % PS])
     gl[2] = 10 ** 6
-    B, H = 3, 16
+    B = 3
     qn = bf16_randn((B * H, 512), 44, 0.5).to(DEV)
     qp = bf16_randn((B * H, 64), 45, 0.5).to(DEV)
     c_new = torch.stack([c[-1:] for c in cs]).to(DEV)
@@ -128,6 +136,8 @@ def test_mla_bad_page_and_length_are_poisoned():
     want, _ = O.mla_attention_fp64(bits(qn[H:2 * H]), bits(qp[H:2 * H]), full[None, :, :512],
                                    full[None, :, 512:], 192 ** -0.5)
     assert_close(o[H:2 * H], want, OUT_ATOL, OUT_RTOL, "b=1")
+    if bad_new_page:  # the clamped page's slot kept its contents
+        assert np.array_equal(bits(lat[0, lens[0] % PS]), before)
 
 
 @pytest.mark.parametrize("n_new", [1, 40])  # 40 tokens: three chunks + the length kernel
