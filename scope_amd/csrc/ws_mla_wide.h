@@ -124,22 +124,15 @@ __device__ __forceinline__ void qk_last(f32x16& c, const u32x4& a, const u32x4& 
                : "memory");
 }
 
-// One 16-byte chunk from global memory into LDS: lane i of the wave writes
-// lds_base + 16 i (lds_base wave-uniform, in bytes).  Written as inline
-// assembly: the compiler then does not see an LDS write whose completion it
-// would wait for (vmcnt(0)) before every later LDS read, which would drain
-// the blocks in flight; the kernel waits for completion itself
-// (wide_wait_barrier).  Vector memory loads complete in issue order, so the
-// waits the compiler computes for its own loads stay sufficient.
-__device__ __forceinline__ void wide_dma16(const void* gptr, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(gptr), "s"(lds_base)
-               : "memory");
-}
-
-// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
-// byte offset (no per-lane 64-bit address arithmetic).
+// One 16-byte chunk per lane from global memory into LDS, from the
+// wave-uniform 64-bit base `sbase` (SGPRs) plus the lane's 32-bit byte offset:
+// lane i of the wave writes lds_base + 16 i (lds_base wave-uniform, in
+// bytes).  Written as inline assembly: the compiler then does not see an LDS
+// write whose completion it would wait for (vmcnt(0)) before every later LDS
+// read, which would drain the blocks in flight; the kernel waits for
+// completion itself (wide_wait_barrier).  Vector memory loads complete in
+// issue order, so the waits the compiler computes for its own loads stay
+// sufficient.
 __device__ __forceinline__ void wide_dma16_s(uint32_t off, const void* sbase,
                                              uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
@@ -486,7 +479,11 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
       for (int i = 1; i < 16; ++i) r = fmaxf(r, v[i]);
       const float bm = r * sx;
       m_max = fmaxf(m_max, bm);
-      if (first) {  // m_run unset (the first pass): the head's largest score
+      // The pass's first block (first): m_run, unless a second pass set it,
+      // becomes the head's largest score.  That block holds at least one
+      // token, so for finite inputs m_run is finite from then on and later
+      // blocks need not look.
+      if (first) {
         float lo, hi;
         pair_xor32(bm, lo, hi);
         m_run = m_run == neg_inf() ? fmaxf(lo, hi) : m_run;
