@@ -81,9 +81,12 @@ __device__ __forceinline__ void store_cols_piece(uint16_t* __restrict__ dst,
 }
 
 // LDS tile of one 32-token block: row-major latent rows of 72 16-byte chunks
-// plus one pad chunk, so the 16 rows a QK operand read touches start in
-// different banks.
-constexpr int kRowChunks = 73;
+// plus four pad chunks.  Measured with the LDS bank-conflict counters on the
+// two read patterns below: a row stride of 76 chunks leaves the PV reads
+// (8 rows x 16 consecutive chunks per instruction) conflict-free and the QK
+// reads (16 rows x 4 chunks) 2-way; 73 leaves both 2-way, and no stride or
+// per-row offset table tried frees both.
+constexpr int kRowChunks = 76;
 constexpr int kTileChunks = 32 * kRowChunks;
 // Blocks in flight in registers while one is consumed from LDS.
 constexpr int kMlaDepth = 3;
