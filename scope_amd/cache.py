@@ -255,7 +255,7 @@ class GqaGpuPartition(_PagedBase):
         B, Hkv, D = self.batch, self.num_kv_heads, self.head_dim
         self._reserve_next(layer, 1)
         max_len = self.max_len(layer) + 1
-        nwg, wsb = ops.decode_plan(0, B * Hkv, Hq // Hkv, max_len, n_workgroups)
+        nwg, wsb = ops.gqa_plan(B * Hkv, Hq // Hkv, D, D, max_len, n_workgroups)
         ws = self._split_workspace_bytes(wsb)
         out, lse = self._partial_bufs(B * Hq, D)
         return max_len, nwg, ws, out, lse

@@ -85,18 +85,21 @@ __device__ __forceinline__ u32x4 softmax_block(const f32x4& s0, const f32x4& s1,
   return pb;
 }
 
-// PV update of 8 output tiles from the 8 V vectors vr[i] (token pv_token(i,j),
-// 8 columns starting at 8*n16 of the lane's 128-column slice).  Tile e covers
-// columns 8*m + e of the slice.  The accumulators are scaled by alpha first
-// when the softmax moved its reference max.
-__device__ __forceinline__ void pv_block(f32x4 (&acc)[8], const u32x4 (&vr)[8],
-                                         const u32x4& pb, float alpha, bool rescale) {
+// PV update of C output tiles from the 8 V vectors vr[i] (token pv_token(i,j),
+// C columns starting at C*n16 of the lane's 16*C-column slice, as C / 2
+// dwords of bf16 pairs).  Tile e covers columns C*m + e of the slice.  The
+// accumulators are scaled by alpha first when the softmax moved its
+// reference max.
+template <int C, class VT>
+__device__ __forceinline__ void pv_block(f32x4 (&acc)[C], const VT (&vr)[8], const u32x4& pb,
+                                         float alpha, bool rescale) {
+  static_assert(C % 2 == 0, "columns per lane come in bf16 pairs");
   if (rescale) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = acc[e] * alpha;
+    for (int e = 0; e < C; ++e) acc[e] = acc[e] * alpha;
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < C; ++e) {
     const int w = e >> 1;
     u32x4 va;
     if (e & 1) {
@@ -112,12 +115,6 @@ __device__ __forceinline__ void pv_block(f32x4 (&acc)[8], const u32x4 (&vr)[8],
     }
     acc[e] = mfma16x16x32(va, pb, acc[e]);
   }
-}
-
-// Column (within the lane's 128-column slice) of accumulator value acc[e][i]
-// of lane group j.
-__device__ __forceinline__ int acc_col(int j, int i, int e) {
-  return 32 * j + 8 * i + e;
 }
 
 }  // namespace ws

@@ -39,9 +39,28 @@ namespace ws {
 
 constexpr int kGqaD = 128;   // value width (and key width of the Dk == Dv calls)
 constexpr int kGqaDk192 = 192;  // key width of the decompressed DeepSeek-V2 layout
+constexpr int kGqaMaxD = 256;   // widest key / value rows
 constexpr int kGqaWaves = 2;        // waves per workgroup, each its own split
 constexpr int kGqaStages = 2;       // register stages of a wave's load ring
 constexpr int kGqaSplitsPerCu = 2;  // default splits (waves) per CU
+
+// Register stages of the ring: two 256-wide K and V stages (256 VGPRs) do
+// not fit beside the accumulators and q even in the 512 registers of one wave
+// per SIMD (the compiler spilled 730 bytes per lane), so 256-wide values
+// stream one block per wave at a time.
+__host__ __device__ constexpr int gqa_stages(int DV) { return DV > kGqaD ? 1 : kGqaStages; }
+// Waves per SIMD the kernel is compiled for (its register budget): rings
+// wider than 128 need the 512 registers of one wave per SIMD.
+__host__ __device__ constexpr int gqa_waves_per_simd(int DK, int DV) {
+  return DK <= kGqaD && DV <= kGqaD ? 2 : 1;
+}
+
+// N dwords of a lane's V columns (DV / 16 bf16 values): 8, 16 or 32 bytes,
+// one or two dwordx4 loads.
+template <int N> struct VVec;
+template <> struct VVec<2> { typedef uint32_t type __attribute__((ext_vector_type(2))); };
+template <> struct VVec<4> { typedef u32x4 type; };
+template <> struct VVec<8> { typedef uint32_t type __attribute__((ext_vector_type(8))); };
 
 // Calls f(integral_constant<int, I>) ... f(integral_constant<int, N - 1>).
 template <int I, int N, class F>
@@ -61,7 +80,7 @@ struct GqaParams {
   const int32_t* page_table;
   const int32_t* len_in;
   int32_t* len_out;
-  const uint16_t* k_new;  // [B][Hkv][1][DK] or nullptr (v_new [B][Hkv][1][D])
+  const uint16_t* k_new;  // [B][Hkv][1][DK] or nullptr (v_new [B][Hkv][1][DV])
   const uint16_t* v_new;
   float* out;
   float* lse;
@@ -83,14 +102,20 @@ constexpr int kFirst = 64;
 constexpr int kLast = 128;
 constexpr int kBadPage = 256;
 
-// (The 192-wide key ring needs more than the 256 registers of two waves per
-// SIMD; the grid holds one workgroup per CU, so one wave per SIMD costs no
-// occupancy the launch would use.)
-template <int G, int DK, bool APPEND>
-__global__ __launch_bounds__(64 * kGqaWaves, (kGqaStages <= 2 && DK == kGqaD) ? 2 : 1) void
+// Key width DK (a multiple of 32), value width DV (64, 128 or 256).  Lane
+// (n16, j) holds DV / 16 value columns of 8 tokens per block, and DV / 16
+// accumulator tiles.  (A key or value ring wider than 128 needs more than the
+// 256 registers of two waves per SIMD; the grid holds one workgroup per CU,
+// so one wave per SIMD costs no occupancy the launch would use.)
+template <int G, int DK, int DV, bool APPEND>
+__global__ __launch_bounds__(64 * kGqaWaves, gqa_waves_per_simd(DK, DV)) void
 gqa_decode_kernel(
     const GqaParams p) {
-  constexpr int D = kGqaD;     // value width
+  static_assert(DK % 32 == 0 && DK <= kGqaMaxD, "key width: a multiple of 32 up to 256");
+  static_assert(DV == 64 || DV == 128 || DV == 256, "value width: 64, 128 or 256");
+  constexpr int D = DV;
+  constexpr int C = DV / 16;   // value columns (and accumulator tiles) per lane
+  using VT = typename VVec<C / 2>::type;
   constexpr int KS = DK / 32;  // QK k-steps (32 key columns each)
   constexpr int W = kGqaWaves;
   constexpr int NT = 64 * W;
@@ -169,7 +194,7 @@ gqa_decode_kernel(
   // block) every lane reads the first row of q instead: same instructions
   // and registers, a cache hit, no HBM traffic.
   auto load_block = [&](const GqaBlock& m, bool valid, u32x4 (&ka)[2][KS],
-                        u32x4 (&vr)[8]) __attribute__((always_inline)) {
+                        VT (&vr)[8]) __attribute__((always_inline)) {
     const uint16_t* kb = valid ? p.k_pages + (size_t)m.tok * DK : p.q;
     const uint16_t* vb = valid ? p.v_pages + (size_t)m.tok * D : p.q;
     const int last = valid ? (m.nt & kNtMask) - 1 : 0;
@@ -187,7 +212,7 @@ gqa_decode_kernel(
       const int r = min(pv_token(i, j), last);
       const uint16_t* vrow =
           (APPEND && r == new_r) ? p.v_new + (size_t)m.row * D : vb + (size_t)r * D;
-      vr[i] = ld_stream(vrow + 8 * n16);
+      vr[i] = __builtin_nontemporal_load((const VT*)(vrow + C * n16));
     }
   };
   // The q rows of kv row `row` as the QK B operand.  Lanes of padding head
@@ -200,14 +225,14 @@ gqa_decode_kernel(
     for (int s = 0; s < KS; ++s) qb[s] = qp[4 * s + j];
   };
 
-  f32x4 acc[8];
+  f32x4 acc[C];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int e = 0; e < C; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = neg_inf();
   float l_run = 0.f;
 
   auto compute_block = [&](const GqaBlock& m, const u32x4 (&ka)[2][KS],
-                           const u32x4 (&vr)[8]) __attribute__((always_inline)) {
+                           const VT (&vr)[8]) __attribute__((always_inline)) {
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -221,7 +246,7 @@ gqa_decode_kernel(
     pv_block(acc, vr, pb, alpha, rescale);
     // Fused append: the new token's K row sits in lanes n16 == nr % 16 of
     // ka[nr / 16] (16 bytes per (lane, s)), its V row in vr[4 (nr / 16) +
-    // nr % 4] of the lanes j == (nr % 16) / 4 (8 columns each).
+    // nr % 4] of the lanes j == (nr % 16) / 4 (C columns each).
     if (APPEND && m.nr >= 0 && m.nr < 32 && !(m.nt & kBadPage)) {
       const size_t dst = ((size_t)m.tok + m.nr) * D;
       const size_t dst_k = ((size_t)m.tok + m.nr) * DK;
@@ -238,7 +263,7 @@ gqa_decode_kernel(
         const int isel = 4 * tt + (m.nr & 3);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          if (i == isel) ((u32x4*)(p.v_pages_w + dst))[n16] = vr[i];
+          if (i == isel) ((VT*)(p.v_pages_w + dst))[n16] = vr[i];
       }
     }
   };
@@ -254,24 +279,34 @@ gqa_decode_kernel(
     if (head_ok) {
       const float inv = bad ? qnan() : 1.f / l_tot;
       const float lse_v = bad ? qnan() : (m_run + __log2f(l_tot)) * kLn2;
+      // acc[e][i] of lane group j is output column C * (4 j + i) + e.
       if (whole) {
-        float* o = p.out + ((size_t)row * G + n16) * D + 32 * j;
+        float* o = p.out + ((size_t)row * G + n16) * D + 4 * C * j;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          ((float4*)(o + 8 * i))[0] =
-              make_float4(acc[0][i] * inv, acc[1][i] * inv, acc[2][i] * inv, acc[3][i] * inv);
-          ((float4*)(o + 8 * i))[1] =
-              make_float4(acc[4][i] * inv, acc[5][i] * inv, acc[6][i] * inv, acc[7][i] * inv);
-        }
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int e = 0; e < C; e += 4)
+            ((float4*)(o + C * i + e))[0] = make_float4(acc[e][i] * inv, acc[e + 1][i] * inv,
+                                                        acc[e + 2][i] * inv, acc[e + 3][i] * inv);
         if (j == 0) p.lse[(size_t)row * G + n16] = lse_v;
       } else {
         const size_t slot = (size_t)(split + row) * G + n16;
-        uint16_t* o = p.ws.part_out + slot * D + 32 * j;
+        uint16_t* o = p.ws.part_out + slot * D + 4 * C * j;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          store_piece8(o + 8 * i, acc[0][i] * inv, acc[1][i] * inv, acc[2][i] * inv,
-                       acc[3][i] * inv, acc[4][i] * inv, acc[5][i] * inv, acc[6][i] * inv,
-                       acc[7][i] * inv);
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (C == 4) {
+            uint2 v;
+            v.x = pack_bf16x2(acc[0][i] * inv, acc[1][i] * inv);
+            v.y = pack_bf16x2(acc[2][i] * inv, acc[3][i] * inv);
+            *(uint2*)(o + C * i) = v;
+          } else {
+#pragma unroll
+            for (int e = 0; e < C; e += 8)
+              store_piece8(o + C * i + e, acc[e][i] * inv, acc[e + 1][i] * inv,
+                           acc[e + 2][i] * inv, acc[e + 3][i] * inv, acc[e + 4][i] * inv,
+                           acc[e + 5][i] * inv, acc[e + 6][i] * inv, acc[e + 7][i] * inv);
+          }
+        }
         if (j == 0) p.ws.part_lse[slot] = lse_v;
       }
     }
@@ -289,11 +324,12 @@ gqa_decode_kernel(
   // early exit (the last nblk % S blocks run after it): a path around one
   // step would make the compiler assume that step's loads are still in
   // flight when the ring comes back to it, and wait.
-  constexpr int S = kGqaStages;
+  constexpr int S = gqa_stages(DV);
   int xb = x_begin;
   fetch_meta(xb);
   GqaBlock mq[S];
-  u32x4 ka[S][2][KS], vr[S][8];
+  u32x4 ka[S][2][KS];
+  VT vr[S][8];
   mq[0] = read_meta(0);
   int run_row = mq[0].row;
   bool run_first = (mq[0].nt & kFirst) != 0;  // the running row's first block was ours
@@ -316,7 +352,9 @@ gqa_decode_kernel(
       fetch_meta(xb);
     }
     if (S > 1) mq[ld] = valid ? read_meta(x_begin + k + S - 1 - xb) : mq[st];
+    else mq[0] = read_meta(x_begin + k - xb);  // (one stage: block k itself, always valid)
     load_block(mq[ld], valid, ka[ld], vr[ld]);
+    if (S == 1) load_q(mq[0].row);
     __builtin_amdgcn_sched_barrier(0);
     const GqaBlock& cur = mq[st];
     if (cur.row != run_row) {
@@ -327,13 +365,15 @@ gqa_decode_kernel(
       m_run = neg_inf();
       l_run = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int e = 0; e < C; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     run_last = (cur.nt & kLast) != 0;
     run_bad |= (cur.nt & kBadPage) != 0;
     compute_block(cur, ka[st], vr[st]);
     __builtin_amdgcn_sched_barrier(0);
-    load_q(mq[nx].row);
+    // (One stage: block k + 1's row is not known yet; its step requests q
+    // right after its block.)
+    if (S > 1) load_q(mq[nx].row);
   };
   int base = 0;
   for (; base + S <= nblk; base += S)
@@ -348,6 +388,13 @@ gqa_decode_kernel(
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Key / value widths with a kernel: equal widths of 64, 128 or 256, and 192
+// keys with 128 values (group size 1).
+static bool gqa_widths_ok(int Dk, int Dv) {
+  if (Dk == kGqaDk192) return Dv == kGqaD;
+  return Dk == Dv && (Dv == 64 || Dv == kGqaD || Dv == kGqaMaxD);
+}
+
 }  // namespace ws
 
 using namespace ws;
@@ -360,11 +407,14 @@ using namespace ws;
 // step + merge, r = 1, us per layer): B1 Hkv4 L4096 (516 blocks) 14.4 at 8
 // blocks per split (71 splits), 12.5-12.8 at 2 (258); B1 Hkv8 L4096 16.2 ->
 // 11.9; B4 Hkv4 L4096 16.3 -> 13.3; one block per split makes the merge's
-// rows longer (128 pieces) and was slower again (14.0).
-static int gqa_splits(int n_splits, int rows_kv, int max_len) {
+// rows longer (128 pieces) and was slower again (14.0).  Other widths (B16
+// Hkv8 G4 L16384): 64-wide blocks (8 KB per wave) need four waves per CU in
+// flight (88 us against 104 at two, 92 at six); the one-stage 256-wide ring
+// is fastest at two as well (363 us against 382 at four, 476 at three).
+static int gqa_splits(int n_splits, int rows_kv, int max_len, int Dv) {
   if (n_splits > 0) return n_splits;
   const long long max_blocks = (long long)rows_kv * ((max_len + 31) / 32);
-  return choose_workgroups(0, kGqaSplitsPerCu, max_blocks, 2);
+  return choose_workgroups(0, Dv == 64 ? 4 : kGqaSplitsPerCu, max_blocks, 2);
 }
 
 static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
@@ -382,8 +432,9 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   const int G = Hq / Hkv;
   if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16)
     return set_error(WS_EINVAL, "%s: group size %d unsupported (1,2,4,8,16)", name, G);
-  if (D != kGqaD || (Dk != kGqaD && Dk != kGqaDk192))
-    return set_error(WS_EINVAL, "%s: head_dim Dk=%d Dv=%d unsupported (128/128, 192/128)",
+  if (!gqa_widths_ok(Dk, D))
+    return set_error(WS_EINVAL,
+                     "%s: head_dim Dk=%d Dv=%d unsupported (64/64, 128/128, 256/256, 192/128)",
                      name, Dk, D);
   if (Dk == kGqaDk192 && G != 1)
     return set_error(WS_EINVAL, "%s: Dk=192 takes group size 1 (got %d)", name, G);
@@ -409,7 +460,7 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
     return set_error(WS_EINVAL, "%s: %lld kv rows of %d tokens exceed the block index range",
                      name, (long long)B * Hkv, max_len);
   const int rows_kv = B * Hkv;
-  const int n = gqa_splits(n_splits, rows_kv, max_len);
+  const int n = gqa_splits(n_splits, rows_kv, max_len, D);
   if (n > kReduceMaxWeights)
     return set_error(WS_EINVAL, "%s: %d splits exceed the merge's %d", name, n,
                      kReduceMaxWeights);
@@ -443,30 +494,38 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   prm.n_splits = n;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((n + kGqaWaves - 1) / kGqaWaves), block(64 * kGqaWaves);
-#define WS_GQA_CASE(GG, DKK)                                                           \
-  case GG:                                                                             \
-    if (k_new)                                                                         \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, DKK, true>), grid, block, 0, s, prm);  \
-    else                                                                               \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, DKK, false>), grid, block, 0, s, prm); \
+#define WS_GQA_CASE(GG, DKK, DVV)                                                           \
+  case GG:                                                                                  \
+    if (k_new)                                                                              \
+      hipLaunchKernelGGL((gqa_decode_kernel<GG, DKK, DVV, true>), grid, block, 0, s, prm);  \
+    else                                                                                    \
+      hipLaunchKernelGGL((gqa_decode_kernel<GG, DKK, DVV, false>), grid, block, 0, s, prm); \
     break;
-  if (Dk == kGqaD) {
-    switch (G) {
-      WS_GQA_CASE(1, kGqaD)
-      WS_GQA_CASE(2, kGqaD)
-      WS_GQA_CASE(4, kGqaD)
-      WS_GQA_CASE(8, kGqaD)
-      WS_GQA_CASE(16, kGqaD)
-    }
-  } else {
-    switch (G) { WS_GQA_CASE(1, kGqaDk192) }
+#define WS_GQA_GROUPS(DD)     \
+  switch (G) {                \
+    WS_GQA_CASE(1, DD, DD)    \
+    WS_GQA_CASE(2, DD, DD)    \
+    WS_GQA_CASE(4, DD, DD)    \
+    WS_GQA_CASE(8, DD, DD)    \
+    WS_GQA_CASE(16, DD, DD)   \
   }
+  if (Dk == kGqaDk192) {
+    switch (G) { WS_GQA_CASE(1, kGqaDk192, kGqaD) }
+  } else if (D == 64) {
+    WS_GQA_GROUPS(64)
+  } else if (D == kGqaMaxD) {
+    WS_GQA_GROUPS(kGqaMaxD)
+  } else {
+    WS_GQA_GROUPS(kGqaD)
+  }
+#undef WS_GQA_GROUPS
 #undef WS_GQA_CASE
   int rc = check_launch(name);
   if (rc != WS_OK || !combine) return rc;
   // One-launch entry points: the rows held by several waves are combined by
-  // the split merge on the same stream, in place (D = 128: one column chunk
-  // per row, so each element is read and written by the same thread).
+  // the split merge on the same stream, in place (each element is read and
+  // written by the same thread; the merge workgroups of a row's column chunks
+  // all write its unchanged lse when one wave held it).
   rc = merge_split_pieces(len_in, k_new ? 1 : 0, B, Hkv, G, D, prm.cap, n, out, lse, prm.ws,
                           out, lse, out_bf16, s);
   return rc != WS_OK ? rc : check_launch(name);
@@ -481,7 +540,7 @@ extern "C" int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
   int n;
   size_t bytes;
   if (kind == 0) {
-    n = gqa_splits(n_workgroups, rows_kv, max_len);
+    n = gqa_splits(n_workgroups, rows_kv, max_len, kGqaD);
     bytes = ws::workspace_bytes(rows_kv, heads, kGqaD, n);
   } else {  // one plan sequence per (sequence, 16-head group), or per sequence (wide)
     const MlaLayout lay = mla_layout(rows_kv, heads);
@@ -490,6 +549,21 @@ extern "C" int ws_decode_plan(int kind, int rows_kv, int heads, int max_len,
   }
   if (n_workgroups_out) *n_workgroups_out = n;
   if (workspace_bytes_out) *workspace_bytes_out = bytes;
+  return WS_OK;
+}
+
+extern "C" int ws_attn_decode_plan(int rows_kv, int heads, int Dk, int Dv, int max_len,
+                                   int n_splits, int* n_splits_out,
+                                   size_t* workspace_bytes_out) {
+  if (!gqa_widths_ok(Dk, Dv))
+    return set_error(WS_EINVAL,
+                     "ws_attn_decode_plan: head_dim Dk=%d Dv=%d unsupported (64/64, 128/128, "
+                     "256/256, 192/128)", Dk, Dv);
+  if (rows_kv < 0 || max_len < 0 || n_splits < 0 || heads <= 0 || heads > 16)
+    return set_error(WS_EINVAL, "ws_attn_decode_plan: bad arguments");
+  const int n = gqa_splits(n_splits, rows_kv, max_len, Dv);
+  if (n_splits_out) *n_splits_out = n;
+  if (workspace_bytes_out) *workspace_bytes_out = ws::workspace_bytes(rows_kv, heads, Dv, n);
   return WS_OK;
 }
 

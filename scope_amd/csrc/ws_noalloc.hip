@@ -65,7 +65,7 @@ extern "C" int ws_gqa_append_decode_partial_noalloc(
     return set_error(WS_EINVAL, "%s: bad batch/heads B=%d Hq=%d Hkv=%d", name, B, Hq, Hkv);
   int n = 0;
   size_t need = 0;
-  int rc = ws_decode_plan(0, B * Hkv, Hq / Hkv, max_len, n_workgroups, &n, &need);
+  int rc = ws_attn_decode_plan(B * Hkv, Hq / Hkv, D, D, max_len, n_workgroups, &n, &need);
   if (rc != WS_OK) return rc;
   if (need > kNoAllocScratchBytes)
     return set_error(WS_EWORKSPACE,

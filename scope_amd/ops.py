@@ -29,6 +29,7 @@ EXPORTS = (
     "ws_kv_append",
     "ws_latent_append",
     "ws_decode_plan",
+    "ws_attn_decode_plan",
     "ws_gqa_decode_partial",
     "ws_gqa_append_decode_partial",
     "ws_mla_decode_partial",
@@ -92,6 +93,9 @@ def lib() -> ctypes.CDLL:
         L.ws_decode_plan.restype = i32
         L.ws_decode_plan.argtypes = [i32, i32, i32, i32, i32,
                                      ctypes.POINTER(i32), ctypes.POINTER(sz)]
+        L.ws_attn_decode_plan.restype = i32
+        L.ws_attn_decode_plan.argtypes = [i32, i32, i32, i32, i32, i32,
+                                          ctypes.POINTER(i32), ctypes.POINTER(sz)]
         L.ws_gqa_decode_partial.restype = i32
         L.ws_gqa_decode_partial.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32,
                                             i32, i32, i32, i32, i32, i32, f32,
@@ -218,6 +222,27 @@ def decode_plan(kind: int, rows_kv: int, heads: int, max_len: int,
     n, wsb = ctypes.c_int(0), ctypes.c_size_t(0)
     _check(lib().ws_decode_plan(kind, rows_kv, heads, max_len, n_workgroups,
                                 ctypes.byref(n), ctypes.byref(wsb)), "ws_decode_plan")
+    if len(_plans) > 4096:
+        _plans.clear()
+    _plans[key] = (n.value, wsb.value)
+    return n.value, wsb.value
+
+
+def gqa_plan(rows_kv: int, heads: int, Dk: int, Dv: int, max_len: int,
+             n_workgroups: int = 0):
+    """decode_plan kind 0 at key width Dk and value width Dv
+    (ws_attn_decode_plan; kind 0 itself sizes the workspace for 128)."""
+    if Dk == 128 and Dv == 128:
+        return decode_plan(0, rows_kv, heads, max_len, n_workgroups)
+    key = ("attn", rows_kv, heads, Dk, Dv, max_len, n_workgroups,
+           torch.cuda.current_device() if torch.cuda.is_initialized() else -1)
+    hit = _plans.get(key)
+    if hit is not None:
+        return hit
+    n, wsb = ctypes.c_int(0), ctypes.c_size_t(0)
+    _check(lib().ws_attn_decode_plan(rows_kv, heads, Dk, Dv, max_len, n_workgroups,
+                                     ctypes.byref(n), ctypes.byref(wsb)),
+           "ws_attn_decode_plan")
     if len(_plans) > 4096:
         _plans.clear()
     _plans[key] = (n.value, wsb.value)
@@ -371,7 +396,7 @@ def gqa_decode_partial(q, k_pages, v_pages, page_table, gpu_len, scale, max_len,
         lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
     _require(out, "out", torch.float32, dev, 3)
     _require(lse, "lse", torch.float32, dev, 2)
-    nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
+    nwg, wsb = gqa_plan(B * Hkv, Hq // Hkv, D, D, int(max_len), int(n_workgroups))
     ws = _workspace(dev, wsb)
     _check(lib().ws_gqa_decode_partial(
         _ptr(q), _ptr(k_pages), _ptr(v_pages), _ptr(page_table), _ptr(gpu_len),
@@ -387,8 +412,9 @@ def attn_decode_partial(q, k_pages, v_pages, page_table, gpu_len, scale, max_len
     or ws_attn_append_decode_partial with k_new / v_new): q [B, Hq, Dk],
     k_pages [P, Hkv, PS, Dk], v_pages [P, Hkv, PS, Dv] bf16 ->
     (out [B, Hq, Dv] fp32 normalised, lse [B, Hq] fp32).  (Dk, Dv) is
-    (128, 128) or (192, 128) with one query head per KV head.  With k_new
-    [B, Hkv, 1, Dk] / v_new [B, Hkv, 1, Dv], token gpu_len[b] is appended
+    (64, 64), (128, 128), (256, 256), or (192, 128) with one query head
+    per KV head.  With k_new [B, Hkv, 1, Dk] / v_new [B, Hkv, 1, Dv], token
+    gpu_len[b] is appended
     first (fused step; len_out gets the new lengths, max_len must bound
     gpu_len + 1)."""
     dev = k_pages.device
@@ -411,7 +437,7 @@ def attn_decode_partial(q, k_pages, v_pages, page_table, gpu_len, scale, max_len
         lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
     _require(out, "out", torch.float32, dev, 3)
     _require(lse, "lse", torch.float32, dev, 2)
-    nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
+    nwg, wsb = gqa_plan(B * Hkv, Hq // Hkv, Dk, Dv, int(max_len), int(n_workgroups))
     ws = _workspace(dev, wsb)
     tail = (B, Hq, Hkv, Dk, Dv, PS, page_table.shape[1], P, int(max_len), nwg, float(scale),
             _ptr(out), _ptr(lse), _ptr(ws), wsb, _stream(dev))
@@ -503,7 +529,7 @@ def gqa_append_decode_partial(q, k_new, v_new, k_pages, v_pages, page_table, len
         lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
     _require(out, "out", torch.float32, dev, 3)
     _require(lse, "lse", torch.float32, dev, 2)
-    nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
+    nwg, wsb = gqa_plan(B * Hkv, Hq // Hkv, D, D, int(max_len), int(n_workgroups))
     ws = _workspace(dev, wsb)
     _check(lib().ws_gqa_append_decode_partial(
         _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
@@ -553,7 +579,7 @@ def gqa_append_decode_full(q, k_new, v_new, k_pages, v_pages, page_table, len_in
     _require(lse, "lse", torch.float32, dev, 2)
     if out_bf16.shape != q.shape or out.shape != q.shape or lse.shape != (B, Hq):
         raise ValueError("out_bf16/out must be [B, Hq, D] and lse [B, Hq]")
-    nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
+    nwg, wsb = gqa_plan(B * Hkv, Hq // Hkv, D, D, int(max_len), int(n_workgroups))
     ws = _workspace(dev, wsb)
     _check(lib().ws_gqa_append_decode_full(
         _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
@@ -686,7 +712,7 @@ def gqa_append_decode_split(q, k_new, v_new, k_pages, v_pages, page_table, len_i
         raise ValueError("len_out must be a separate [B] int32 tensor")
     out = torch.empty((B, Hq, D), dtype=torch.float32, device=dev)
     lse = torch.empty((B, Hq), dtype=torch.float32, device=dev)
-    nwg, wsb = decode_plan(0, B * Hkv, Hq // Hkv, int(max_len), int(n_workgroups))
+    nwg, wsb = gqa_plan(B * Hkv, Hq // Hkv, D, D, int(max_len), int(n_workgroups))
     if workspace is None:
         workspace = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
     elif workspace.numel() * workspace.element_size() < wsb:

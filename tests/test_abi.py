@@ -54,6 +54,21 @@ def test_version_and_plan():
         ops.decode_plan(0, 16, 8, 100, -1)
 
 
+def test_width_plan():
+    """The plan at other head widths: the piece slots scale with the value
+    width, 128/128 matches kind 0, and widths without a kernel are refused."""
+    pad = lambda n: -(-n // 256) * 256
+    for Dk, Dv in ((64, 64), (128, 128), (256, 256), (192, 128)):
+        n, wsb = ops.gqa_plan(16, 8 if Dk != 192 else 1, Dk, Dv, 32768, 100)
+        G = 8 if Dk != 192 else 1
+        assert n == 100 and wsb == pad((100 + 16) * G * 4) + (100 + 16) * G * Dv * 2
+    n_w, wsb_w = ops.gqa_plan(16, 8, 128, 128, 32768, 100)
+    assert (n_w, wsb_w) == ops.decode_plan(0, 16, 8, 32768, 100)
+    for Dk, Dv in ((96, 96), (80, 80), (128, 64), (256, 128), (192, 192)):
+        with pytest.raises(ops.WsError, match="unsupported"):
+            ops.gqa_plan(16, 1, Dk, Dv, 100, 10)
+
+
 def test_host_side_argument_checks():
     L = ops.lib()
     rc = L.ws_kv_append(None, None, None, None, None, None, 1, 1, 128, 1, 64, 1, 1, 1, None)
