@@ -175,10 +175,10 @@ int ws_attn_decode_plan(int rows_kv, int heads, int Dk, int Dv, int max_len,
 
 /*
  * Split-KV GQA decode attention over the pooled tokens of every sequence.
- * q: [B][Hq][D] bf16, Hq = Hkv * G, G in {1,2,4,8,16}, D in {64, 128, 256}
- * (the reference's bmm takes any width; its CPU kernel any multiple of 16,
- * kernel/cpu_attn.cpp:583).  Workspace: ws_decode_plan kind 0 for D = 128,
- * ws_attn_decode_plan for any D.
+ * q: [B][Hq][D] bf16, Hq = Hkv * G, G from 1 to 16, D a multiple of 16 up
+ * to 256 (the reference's bmm takes any width; its CPU kernel any multiple of
+ * 16, kernel/cpu_attn.cpp:583).  Workspace: ws_decode_plan kind 0 for
+ * D = 128, ws_attn_decode_plan for any D.
  * n_splits: waves of the plan (0 = choose, see ws_decode_plan); max_len:
  * upper bound of gpu_len[] (must be >= every gpu_len[b]).  Rows held by one
  * wave are written final by the streaming launch; rows spread over several
@@ -268,10 +268,10 @@ int ws_gqa_append_decode_split(const uint16_t* q, const uint16_t* k_new,
  * ws_gqa_decode_partial / ws_gqa_append_decode_partial with separate key and
  * value widths: k_pages [num_pages][Hkv][page_size][Dk], v_pages
  * [num_pages][Hkv][page_size][Dv], q [B][Hq][Dk], k_new [B][Hkv][1][Dk],
- * v_new [B][Hkv][1][Dv], out [B][Hq][Dv].  (Dk, Dv) = (64, 64), (128, 128)
- * or (256, 256) is the GQA call; (192, 128) with group size 1 is the
- * decompressed DeepSeek-V2 attention (128 nope + 64 rope key columns, 128
- * value columns, 16 heads).  Workspace from ws_attn_decode_plan.
+ * v_new [B][Hkv][1][Dv], out [B][Hq][Dv].  Dk == Dv, a multiple of 16 up
+ * to 256, is the GQA call; (192, 128) with group size 1 is the decompressed
+ * DeepSeek-V2 attention (128 nope + 64 rope key columns, 128 value columns,
+ * 16 heads).  Workspace from ws_attn_decode_plan.
  * Replaces _local_bmm_softmax / _resident_layer with the reference's ds2
  * model entry, QHD 192 / VHD 128 / GROUPS 1 (roofline/bench_resident_kv.py:10,
  * 150-157, 261-271), the GPU side of the fused_cpu_attn_mla split

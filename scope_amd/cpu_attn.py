@@ -20,9 +20,9 @@ wh_mla_triple.
 
 Differences from the reference: an empty sequence (S == 0) gives out = 0,
 max = -inf, sum = 0 (the merge identity) where the reference divides by zero;
-bf16 head widths are multiples of 32 up to 256 or 192 / 128 (float32: multiples
-of 16), where the reference takes any multiple of 16; at most 16 query heads
-share a KV row (G <= 16), and absorbed MLA takes H a multiple of 16.
+head widths are multiples of 16 up to 256, or 192 / 128, where the reference
+takes any multiple of 16; at most 16 query heads share a KV row (G <= 16), and
+absorbed MLA takes H a multiple of 16.
 """
 from __future__ import annotations
 

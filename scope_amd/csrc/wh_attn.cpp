@@ -226,7 +226,7 @@ void write_final(const float* base, int H, int Dv, const Sink<OutT>& k, size_t r
     }
     const float inv = (k.lse || k.normalize) ? 1.f / l : 1.f;
     for (int s = 0; s < Dv; ++s)
-      dst[kStaged ? wh::stage_col(s) : s] = to_out(o_at(h, s) * inv, dst);
+      dst[kStaged ? wh::stage_col(s, Dv) : s] = to_out(o_at(h, s) * inv, dst);
     if (k.lse) {
       k.lse[r] = (base[h] + std::log2(l)) * kLn2;
     } else {
@@ -295,9 +295,9 @@ int attn_partial(const char* fn, const InT* q, const InT* k_pages, const InT* v_
   if (G > 16) return fail(WH_EINVAL, "%s: group size %d > 16", fn, G);
   if (kF32 ? !wh::gqa_f32_dims_supported(Dk, D) : !wh::gqa_dims_supported(Dk, D))
     return fail(WH_EINVAL,
-                "%s: head_dim Dk=%d Dv=%d unsupported (equal multiples of %d in [%d, 256], "
+                "%s: head_dim Dk=%d Dv=%d unsupported (equal multiples of 16 in [16, 256], "
                 "or 192 / 128)",
-                fn, Dk, D, kF32 ? 16 : 32, kF32 ? 16 : 32);
+                fn, Dk, D);
   if (B == 0) return WH_OK;
   if (!q || !k_pages || !v_pages || !page_table || !lens || !sink.ok())
     return fail(WH_EINVAL, "%s: null pointer", fn);

@@ -81,8 +81,12 @@ inline __m512bh bcast_pair(const void* p) {
   return (__m512bh)_mm512_set1_epi32(w);
 }
 
+// The 16 bf16 values at p in the low half of a zmm, zeros above (no read
+// past them).
+inline __m512i ld16(const void* p) { return _mm512_maskz_loadu_epi16(0xFFFFu, p); }
+
 // Interleaves the value rows of tokens (a, b) as bf16 pairs into dst (D words,
-// staging order).
+// staging order; a last 16-column chunk in column order).
 template <int D>
 inline void stage_pair(const uint16_t* a, const uint16_t* b, uint32_t* dst) {
 #pragma GCC unroll 8
@@ -90,6 +94,16 @@ inline void stage_pair(const uint16_t* a, const uint16_t* b, uint32_t* dst) {
     const __m512i x = _mm512_loadu_si512(a + 32 * c), y = _mm512_loadu_si512(b + 32 * c);
     _mm512_store_si512(dst + 32 * c, _mm512_unpacklo_epi16(x, y));
     _mm512_store_si512(dst + 32 * c + 16, _mm512_unpackhi_epi16(x, y));
+  }
+  if constexpr (D % 32 != 0) {
+    constexpr int c = D / 32;
+    const __m512i x = ld16(a + 32 * c), y = ld16(b + 32 * c);
+    // 128-bit lanes 0, 1 of unpacklo hold the pairs of columns 0-3, 8-11; of
+    // unpackhi 4-7, 12-15
+    const __m512i idx = _mm512_setr_epi64(0, 1, 8, 9, 2, 3, 10, 11);
+    _mm512_store_si512(dst + 32 * c, _mm512_permutex2var_epi64(_mm512_unpacklo_epi16(x, y),
+                                                               idx,
+                                                               _mm512_unpackhi_epi16(x, y)));
   }
 }
 
@@ -107,6 +121,13 @@ inline __m512 gqa_scores16(const uint16_t* qg, const uint16_t* k) {
     const __m512bh qv = ld_bh(qg + 32 * c);
 #pragma GCC unroll 16
     for (int j = 0; j < 16; ++j) acc[j] = _mm512_dpbf16_ps(acc[j], qv, ld_bh(k + j * D + 32 * c));
+  }
+  if constexpr (D % 32 != 0) {  // a last 16-column chunk, zeros in the upper half
+    constexpr int c = D / 32;
+    const __m512bh qv = (__m512bh)ld16(qg + 32 * c);
+#pragma GCC unroll 16
+    for (int j = 0; j < 16; ++j)
+      acc[j] = _mm512_dpbf16_ps(acc[j], qv, (__m512bh)ld16(k + j * D + 32 * c));
   }
   return reduce16(acc);
 }
@@ -182,9 +203,7 @@ void gqa_attend_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G
       const __m512 cv = _mm512_set1_ps(corr);
       int z = 0;
       for (; z + 8 <= NZ; z += 8) gqa_pv<8, D>(og + 16 * z, vst + 16 * z, pw, np, cv);
-      if constexpr (NZ % 8 == 2) gqa_pv<2, D>(og + 16 * z, vst + 16 * z, pw, np, cv);
-      if constexpr (NZ % 8 == 4) gqa_pv<4, D>(og + 16 * z, vst + 16 * z, pw, np, cv);
-      if constexpr (NZ % 8 == 6) gqa_pv<6, D>(og + 16 * z, vst + 16 * z, pw, np, cv);
+      if constexpr (NZ % 8 != 0) gqa_pv<NZ % 8, D>(og + 16 * z, vst + 16 * z, pw, np, cv);
     }
   }
 }
@@ -192,7 +211,7 @@ void gqa_attend_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G
 }  // namespace
 
 bool gqa_dims_supported(int Dk, int Dv) {
-  return (Dk == Dv && Dk >= 32 && Dk <= 256 && Dk % 32 == 0) || (Dk == 192 && Dv == 128);
+  return (Dk == Dv && Dk >= 16 && Dk <= 256 && Dk % 16 == 0) || (Dk == 192 && Dv == 128);
 }
 
 void gqa_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G, int Dk,
@@ -200,14 +219,14 @@ void gqa_attend(const uint16_t* q, const uint16_t* k, const uint16_t* v, int G, 
   if (Dk == 192 && Dv == 128) return gqa_attend_d<192, 128>(q, k, v, G, t0, t1, sl2, m, l, o);
   if (Dk != Dv) return;  // rejected by the caller
   switch (Dk) {
-    case 32: return gqa_attend_d<32, 32>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 64: return gqa_attend_d<64, 64>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 96: return gqa_attend_d<96, 96>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 128: return gqa_attend_d<128, 128>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 160: return gqa_attend_d<160, 160>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 192: return gqa_attend_d<192, 192>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 224: return gqa_attend_d<224, 224>(q, k, v, G, t0, t1, sl2, m, l, o);
-    case 256: return gqa_attend_d<256, 256>(q, k, v, G, t0, t1, sl2, m, l, o);
+#define WH_BF16_CASE(DD) \
+  case DD:               \
+    return gqa_attend_d<DD, DD>(q, k, v, G, t0, t1, sl2, m, l, o);
+    WH_BF16_CASE(16) WH_BF16_CASE(32) WH_BF16_CASE(48) WH_BF16_CASE(64)
+    WH_BF16_CASE(80) WH_BF16_CASE(96) WH_BF16_CASE(112) WH_BF16_CASE(128)
+    WH_BF16_CASE(144) WH_BF16_CASE(160) WH_BF16_CASE(176) WH_BF16_CASE(192)
+    WH_BF16_CASE(208) WH_BF16_CASE(224) WH_BF16_CASE(240) WH_BF16_CASE(256)
+#undef WH_BF16_CASE
     default: return;  // rejected by the caller
   }
 }

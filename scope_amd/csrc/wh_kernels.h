@@ -8,7 +8,9 @@
 // Staging order: the value columns come out of the bf16 pair interleave
 // (vpunpck{l,h}wd of two tokens' rows) permuted inside each 32-column chunk;
 // column d of chunk c sits at slot stage_slot(d) below.  Callers keep o in
-// staging order until the final write, which un-permutes it.
+// staging order until the final write, which un-permutes it.  A width that
+// is not a multiple of 32 ends with a 16-column chunk, staged in column
+// order.
 #pragma once
 
 #include <cstddef>
@@ -16,9 +18,11 @@
 
 namespace wh {
 
-// Slot of value column d in staging order (and its inverse): inside a
-// 32-column chunk, slot 16*half + i holds column 8*(i/4) + 4*half + i%4.
-inline int stage_col(int s) {
+// Column held by slot s of a D-column row in staging order: inside a
+// 32-column chunk, slot 16*half + i holds column 8*(i/4) + 4*half + i%4; the
+// slots of a last 16-column chunk hold their own columns.
+inline int stage_col(int s, int D) {
+  if (s >= (D & ~31)) return s;
   const int c = s >> 5, half = (s >> 4) & 1, i = s & 15;
   return 32 * c + 8 * (i >> 2) + 4 * half + (i & 3);
 }
@@ -28,7 +32,7 @@ inline int stage_col(int s) {
 extern const uint16_t kZeroRow[1024];
 
 // GQA: q holds G rows of Dk bf16 (the query heads sharing one KV head); token
-// t of the row is k + t*Dk / v + t*Dv.  (Dk, Dv): Dk == Dv a multiple of 32
+// t of the row is k + t*Dk / v + t*Dv.  (Dk, Dv): Dk == Dv a multiple of 16
 // up to 256, or (192, 128) (gqa_dims_supported); G at most 16.  m, l: G
 // floats; o: G*Dv floats (staging order).  scale_log2 = softmax scale *
 // log2(e).

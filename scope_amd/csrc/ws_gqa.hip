@@ -50,17 +50,49 @@ constexpr int kGqaSplitsPerCu = 2;  // default splits (waves) per CU
 // stream one block per wave at a time.
 __host__ __device__ constexpr int gqa_stages(int DV) { return DV > kGqaD ? 1 : kGqaStages; }
 // Waves per SIMD the kernel is compiled for (its register budget): rings
-// wider than 128 need the 512 registers of one wave per SIMD.
-__host__ __device__ constexpr int gqa_waves_per_simd(int DK, int DV) {
-  return DK <= kGqaD && DV <= kGqaD ? 2 : 1;
+// wider than 128 need the 512 registers of one wave per SIMD, and so does the
+// 128-wide ring with the group size read at run time (G = 0: it spilled in
+// 256).  The grid never places more than one wave per SIMD, so this costs no
+// occupancy the launch uses.
+__host__ __device__ constexpr int gqa_waves_per_simd(int G, int DK, int DV) {
+  return G > 0 && DK <= kGqaD && DV <= kGqaD ? 2 : 1;
 }
 
-// N dwords of a lane's V columns (DV / 16 bf16 values): 8, 16 or 32 bytes,
-// one or two dwordx4 loads.
-template <int N> struct VVec;
+// Value columns per lane of a DV-wide row: the smallest even count >= DV / 16
+// that divides DV (64: 4, 128: 8, 256: 16; 80: 8).  Lanes n16 < DV / C hold
+// columns; the other lanes read the row's first columns, and the MFMA rows
+// they feed give output columns that are never stored.
+__host__ __device__ constexpr int gqa_lane_cols(int DV) {
+  int c = (DV / 16 + 1) & ~1;
+  while (DV % c) c += 2;
+  return c;
+}
+
+// N dwords of a lane's V columns: 8, 16 or 32 bytes as vector loads, other
+// sizes as dword arrays (4, 12, 20, 24 or 28 bytes: 4-byte aligned only).
+template <int N> struct DwVec {
+  uint32_t w[N];
+  __device__ __forceinline__ uint32_t operator[](int i) const { return w[i]; }
+};
+template <int N> struct VVec { typedef DwVec<N> type; };
 template <> struct VVec<2> { typedef uint32_t type __attribute__((ext_vector_type(2))); };
 template <> struct VVec<4> { typedef u32x4 type; };
 template <> struct VVec<8> { typedef uint32_t type __attribute__((ext_vector_type(8))); };
+
+template <class VT> __device__ __forceinline__ VT ld_v(const uint16_t* p) {
+  return __builtin_nontemporal_load((const VT*)p);
+}
+template <class VT, int N = sizeof(VT) / 4>
+__device__ __forceinline__ VT ld_dw(const uint16_t* p) {
+  VT v;
+#pragma unroll
+  for (int d = 0; d < N; ++d) v.w[d] = __builtin_nontemporal_load((const uint32_t*)p + d);
+  return v;
+}
+template <class VT> __device__ __forceinline__ VT ld_lane(const uint16_t* p) {
+  if constexpr (sizeof(VT) == 8 || sizeof(VT) == 16 || sizeof(VT) == 32) return ld_v<VT>(p);
+  else return ld_dw<VT>(p);
+}
 
 // Calls f(integral_constant<int, I>) ... f(integral_constant<int, N - 1>).
 template <int I, int N, class F>
@@ -85,7 +117,7 @@ struct GqaParams {
   float* out;
   float* lse;
   SplitWorkspace ws;
-  int B, Hkv, page_size, max_pages, num_pages, cap, n_splits;
+  int B, Hkv, G, page_size, max_pages, num_pages, cap, n_splits;
   float scale_log2;
 };
 
@@ -102,21 +134,29 @@ constexpr int kFirst = 64;
 constexpr int kLast = 128;
 constexpr int kBadPage = 256;
 
-// Key width DK (a multiple of 32), value width DV (64, 128 or 256).  Lane
-// (n16, j) holds DV / 16 value columns of 8 tokens per block, and DV / 16
-// accumulator tiles.  (A key or value ring wider than 128 needs more than the
-// 256 registers of two waves per SIMD; the grid holds one workgroup per CU,
-// so one wave per SIMD costs no occupancy the launch would use.)
+// Key width DK and value width DV, multiples of 16 up to 256.  Lane (n16, j)
+// holds C = gqa_lane_cols(DV) value columns of 8 tokens per block, and C
+// accumulator tiles.  A key width that is not a multiple of 32 ends with a
+// half k-step: its upper 16 columns are zero in both MFMA operands.  G: the
+// group size, or 0 to take it from p.G.  (A key or value ring wider than 128
+// needs more than the 256 registers of two waves per SIMD; the grid holds one
+// workgroup per CU, so one wave per SIMD costs no occupancy the launch would
+// use.)
 template <int G, int DK, int DV, bool APPEND>
-__global__ __launch_bounds__(64 * kGqaWaves, gqa_waves_per_simd(DK, DV)) void
+__global__ __launch_bounds__(64 * kGqaWaves, gqa_waves_per_simd(G, DK, DV)) void
 gqa_decode_kernel(
     const GqaParams p) {
-  static_assert(DK % 32 == 0 && DK <= kGqaMaxD, "key width: a multiple of 32 up to 256");
-  static_assert(DV == 64 || DV == 128 || DV == 256, "value width: 64, 128 or 256");
+  static_assert(DK % 16 == 0 && DK <= kGqaMaxD, "key width: a multiple of 16 up to 256");
+  static_assert(DV % 16 == 0 && DV <= kGqaMaxD, "value width: a multiple of 16 up to 256");
   constexpr int D = DV;
-  constexpr int C = DV / 16;   // value columns (and accumulator tiles) per lane
+  constexpr int C = gqa_lane_cols(DV);  // value columns (and accumulator tiles) per lane
+  constexpr int LV = DV / C;            // lanes n16 that hold value columns
   using VT = typename VVec<C / 2>::type;
-  constexpr int KS = DK / 32;  // QK k-steps (32 key columns each)
+  constexpr int KS = (DK + 31) / 32;    // QK k-steps (32 key columns each)
+  constexpr bool KPAD = DK % 32 != 0;   // the last k-step has 16 columns
+  // Key column of (k-step s, lane group j); the padding of a half step reads
+  // column 0 (its values are zeroed before the MFMA).
+  auto kcol = [](int s, int jj) { return (KPAD && s == KS - 1 && jj >= 2) ? 0 : 8 * (4 * s + jj); };
   constexpr int W = kGqaWaves;
   constexpr int NT = 64 * W;
   constexpr int add = APPEND ? 1 : 0;
@@ -129,7 +169,8 @@ gqa_decode_kernel(
   const int lane = tid & 63;
   const int n16 = lane & 15;
   const int j = lane >> 4;
-  const bool head_ok = n16 < G;
+  const int GG = G > 0 ? G : p.G;
+  const bool head_ok = n16 < GG;
 
   // Lengths (len_in clamped to what the page table row holds) and the plan.
   if (APPEND && p.len_out && blockIdx.x == 0)
@@ -141,9 +182,9 @@ gqa_decode_kernel(
     for (int b = 0; b < p.B; ++b) {  // or NaN for an invalid length
       if (s_pref[b + 1] != s_pref[b]) continue;
       const bool ok = len_ok(p.len_in[b], add, p.cap);
-      const size_t q0 = (size_t)b * p.Hkv * G;
-      for (int idx = tid; idx < p.Hkv * G * D; idx += NT) p.out[q0 * D + idx] = ok ? 0.f : qnan();
-      for (int idx = tid; idx < p.Hkv * G; idx += NT) p.lse[q0 + idx] = ok ? neg_inf() : qnan();
+      const size_t q0 = (size_t)b * p.Hkv * GG;
+      for (int idx = tid; idx < p.Hkv * GG * D; idx += NT) p.out[q0 * D + idx] = ok ? 0.f : qnan();
+      for (int idx = tid; idx < p.Hkv * GG; idx += NT) p.lse[q0 + idx] = ok ? neg_inf() : qnan();
     }
   }
   const int split = uniform(blockIdx.x * W + (tid >> 6));
@@ -205,14 +246,14 @@ gqa_decode_kernel(
       const uint16_t* kr =
           (APPEND && r == new_r) ? p.k_new + (size_t)m.row * DK : kb + (size_t)r * DK;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) ka[tt][s] = ld_stream(kr + 8 * (4 * s + j));
+      for (int s = 0; s < KS; ++s) ka[tt][s] = ld_stream(kr + kcol(s, j));
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = min(pv_token(i, j), last);
       const uint16_t* vrow =
           (APPEND && r == new_r) ? p.v_new + (size_t)m.row * D : vb + (size_t)r * D;
-      vr[i] = __builtin_nontemporal_load((const VT*)(vrow + C * n16));
+      vr[i] = ld_lane<VT>(vrow + ((LV == 16 || n16 < LV) ? C * n16 : 0));
     }
   };
   // The q rows of kv row `row` as the QK B operand.  Lanes of padding head
@@ -220,9 +261,9 @@ gqa_decode_kernel(
   // those columns are never written.
   u32x4 qb[KS];
   auto load_q = [&](int row) __attribute__((always_inline)) {
-    const u32x4* qp = (const u32x4*)(p.q + (size_t)(row * G + min(n16, G - 1)) * DK);
+    const u32x4* qp = (const u32x4*)(p.q + (size_t)(row * GG + min(n16, GG - 1)) * DK);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qb[s] = qp[4 * s + j];
+    for (int s = 0; s < KS; ++s) qb[s] = qp[(KPAD && s == KS - 1 && j >= 2) ? 0 : 4 * s + j];
   };
 
   f32x4 acc[C];
@@ -236,8 +277,16 @@ gqa_decode_kernel(
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      s0 = mfma16x16x32(ka[0][s], qb[s], s0);
-      s1 = mfma16x16x32(ka[1][s], qb[s], s1);
+      if (KPAD && s == KS - 1) {  // the half step's upper 16 columns are zero
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        const bool lo = j < 2;
+        const u32x4 qs = lo ? qb[s] : z;
+        s0 = mfma16x16x32(lo ? ka[0][s] : z, qs, s0);
+        s1 = mfma16x16x32(lo ? ka[1][s] : z, qs, s1);
+      } else {
+        s0 = mfma16x16x32(ka[0][s], qb[s], s0);
+        s1 = mfma16x16x32(ka[1][s], qb[s], s1);
+      }
     }
     float alpha;
     bool rescale;
@@ -256,14 +305,28 @@ gqa_decode_kernel(
         for (int t2 = 0; t2 < 2; ++t2)
           if (t2 == tt) {
 #pragma unroll
-            for (int s = 0; s < KS; ++s) ((u32x4*)(p.k_pages_w + dst_k))[4 * s + j] = ka[t2][s];
+            for (int s = 0; s < KS; ++s)
+              if (!(KPAD && s == KS - 1 && j >= 2))
+                *(u32x4*)(p.k_pages_w + dst_k + 8 * (4 * s + j)) = ka[t2][s];
           }
       }
-      if (j == ((m.nr & 15) >> 2)) {
+      if (j == ((m.nr & 15) >> 2) && (LV == 16 || n16 < LV)) {
         const int isel = 4 * tt + (m.nr & 3);
+        if constexpr (sizeof(VT) == 8 || sizeof(VT) == 16 || sizeof(VT) == 32) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (i == isel) ((VT*)(p.v_pages_w + dst))[n16] = vr[i];
+          for (int i = 0; i < 8; ++i)
+            if (i == isel) ((VT*)(p.v_pages_w + dst))[n16] = vr[i];
+        } else {  // dword rows: a select chain per dword (indexing the row array by
+                  // isel put it in scratch)
+          uint32_t* vd = (uint32_t*)(p.v_pages_w + dst + C * n16);
+#pragma unroll
+          for (int d = 0; d < C / 2; ++d) {
+            uint32_t x = vr[0][d];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) x = i == isel ? vr[i][d] : x;
+            vd[d] = x;
+          }
+        }
       }
     }
   };
@@ -279,32 +342,46 @@ gqa_decode_kernel(
     if (head_ok) {
       const float inv = bad ? qnan() : 1.f / l_tot;
       const float lse_v = bad ? qnan() : (m_run + __log2f(l_tot)) * kLn2;
-      // acc[e][i] of lane group j is output column C * (4 j + i) + e.
+      // acc[e][i] of lane group j is output column C * (4 j + i) + e; rows
+      // 4 j + i >= LV are padding (nothing stored).
       if (whole) {
-        float* o = p.out + ((size_t)row * G + n16) * D + 4 * C * j;
+        float* o = p.out + ((size_t)row * GG + n16) * D + 4 * C * j;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+          if (LV < 16 && 4 * j + i >= LV) continue;
+          if constexpr (C % 4 == 0) {
 #pragma unroll
-          for (int e = 0; e < C; e += 4)
-            ((float4*)(o + C * i + e))[0] = make_float4(acc[e][i] * inv, acc[e + 1][i] * inv,
-                                                        acc[e + 2][i] * inv, acc[e + 3][i] * inv);
-        if (j == 0) p.lse[(size_t)row * G + n16] = lse_v;
+            for (int e = 0; e < C; e += 4)
+              ((float4*)(o + C * i + e))[0] = make_float4(acc[e][i] * inv, acc[e + 1][i] * inv,
+                                                          acc[e + 2][i] * inv, acc[e + 3][i] * inv);
+          } else {
+#pragma unroll
+            for (int e = 0; e < C; e += 2)
+              ((float2*)(o + C * i + e))[0] = make_float2(acc[e][i] * inv, acc[e + 1][i] * inv);
+          }
+        }
+        if (j == 0) p.lse[(size_t)row * GG + n16] = lse_v;
       } else {
-        const size_t slot = (size_t)(split + row) * G + n16;
+        const size_t slot = (size_t)(split + row) * GG + n16;
         uint16_t* o = p.ws.part_out + slot * D + 4 * C * j;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if constexpr (C == 4) {
+          if (LV < 16 && 4 * j + i >= LV) continue;
+          if constexpr (C % 8 == 0) {
+#pragma unroll
+            for (int e = 0; e < C; e += 8)
+              store_piece8(o + C * i + e, acc[e][i] * inv, acc[e + 1][i] * inv,
+                           acc[e + 2][i] * inv, acc[e + 3][i] * inv, acc[e + 4][i] * inv,
+                           acc[e + 5][i] * inv, acc[e + 6][i] * inv, acc[e + 7][i] * inv);
+          } else if constexpr (C == 4) {
             uint2 v;
             v.x = pack_bf16x2(acc[0][i] * inv, acc[1][i] * inv);
             v.y = pack_bf16x2(acc[2][i] * inv, acc[3][i] * inv);
             *(uint2*)(o + C * i) = v;
           } else {
 #pragma unroll
-            for (int e = 0; e < C; e += 8)
-              store_piece8(o + C * i + e, acc[e][i] * inv, acc[e + 1][i] * inv,
-                           acc[e + 2][i] * inv, acc[e + 3][i] * inv, acc[e + 4][i] * inv,
-                           acc[e + 5][i] * inv, acc[e + 6][i] * inv, acc[e + 7][i] * inv);
+            for (int e = 0; e < C; e += 2)
+              *(uint32_t*)(o + C * i + e) = pack_bf16x2(acc[e][i] * inv, acc[e + 1][i] * inv);
           }
         }
         if (j == 0) p.ws.part_lse[slot] = lse_v;
@@ -388,11 +465,11 @@ gqa_decode_kernel(
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Key / value widths with a kernel: equal widths of 64, 128 or 256, and 192
+// Key / value widths with a kernel: equal multiples of 16 up to 256, and 192
 // keys with 128 values (group size 1).
 static bool gqa_widths_ok(int Dk, int Dv) {
-  if (Dk == kGqaDk192) return Dv == kGqaD;
-  return Dk == Dv && (Dv == 64 || Dv == kGqaD || Dv == kGqaMaxD);
+  if (Dk == kGqaDk192 && Dv == kGqaD) return true;
+  return Dk == Dv && Dv >= 16 && Dv <= kGqaMaxD && Dv % 16 == 0;
 }
 
 }  // namespace ws
@@ -414,7 +491,7 @@ using namespace ws;
 static int gqa_splits(int n_splits, int rows_kv, int max_len, int Dv) {
   if (n_splits > 0) return n_splits;
   const long long max_blocks = (long long)rows_kv * ((max_len + 31) / 32);
-  return choose_workgroups(0, Dv == 64 ? 4 : kGqaSplitsPerCu, max_blocks, 2);
+  return choose_workgroups(0, Dv <= 64 ? 4 : kGqaSplitsPerCu, max_blocks, 2);
 }
 
 static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
@@ -430,13 +507,14 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
     return set_error(WS_EINVAL, "%s: bad batch/heads B=%d Hq=%d Hkv=%d (B <= %d)", name,
                      B, Hq, Hkv, kMaxSeqs);
   const int G = Hq / Hkv;
-  if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16)
-    return set_error(WS_EINVAL, "%s: group size %d unsupported (1,2,4,8,16)", name, G);
+  if (G < 1 || G > 16)
+    return set_error(WS_EINVAL, "%s: group size %d unsupported (1 to 16)", name, G);
   if (!gqa_widths_ok(Dk, D))
     return set_error(WS_EINVAL,
-                     "%s: head_dim Dk=%d Dv=%d unsupported (64/64, 128/128, 256/256, 192/128)",
+                     "%s: head_dim Dk=%d Dv=%d unsupported (equal multiples of 16 up to 256, "
+                     "192/128)",
                      name, Dk, D);
-  if (Dk == kGqaDk192 && G != 1)
+  if (Dk == kGqaDk192 && D == kGqaD && G != 1)
     return set_error(WS_EINVAL, "%s: Dk=192 takes group size 1 (got %d)", name, G);
   if (page_size <= 0 || max_pages <= 0 || num_pages <= 0 || max_len < 0 ||
       (page_size % 32 && max_pages != 1) ||
@@ -486,6 +564,7 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   prm.ws = carve_workspace(workspace, rows_kv, G, n);
   prm.B = B;
   prm.Hkv = Hkv;
+  prm.G = G;
   prm.page_size = page_size;
   prm.max_pages = max_pages;
   prm.num_pages = num_pages;
@@ -494,32 +573,52 @@ static int gqa_launch(const uint16_t* q, const uint16_t* k_new, const uint16_t* 
   prm.n_splits = n;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((n + kGqaWaves - 1) / kGqaWaves), block(64 * kGqaWaves);
-#define WS_GQA_CASE(GG, DKK, DVV)                                                           \
-  case GG:                                                                                  \
-    if (k_new)                                                                              \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, DKK, DVV, true>), grid, block, 0, s, prm);  \
-    else                                                                                    \
-      hipLaunchKernelGGL((gqa_decode_kernel<GG, DKK, DVV, false>), grid, block, 0, s, prm); \
+#define WS_GQA_LAUNCH(GG, DKK, DVV)                                                         \
+  if (k_new)                                                                                \
+    hipLaunchKernelGGL((gqa_decode_kernel<GG, DKK, DVV, true>), grid, block, 0, s, prm);    \
+  else                                                                                      \
+    hipLaunchKernelGGL((gqa_decode_kernel<GG, DKK, DVV, false>), grid, block, 0, s, prm);
+#define WS_GQA_CASE(GG, DKK, DVV) \
+  case GG:                        \
+    WS_GQA_LAUNCH(GG, DKK, DVV)   \
     break;
-#define WS_GQA_GROUPS(DD)     \
-  switch (G) {                \
-    WS_GQA_CASE(1, DD, DD)    \
-    WS_GQA_CASE(2, DD, DD)    \
-    WS_GQA_CASE(4, DD, DD)    \
-    WS_GQA_CASE(8, DD, DD)    \
-    WS_GQA_CASE(16, DD, DD)   \
+#define WS_GQA_GROUPS(DD)        \
+  switch (G) {                   \
+    WS_GQA_CASE(1, DD, DD)       \
+    WS_GQA_CASE(2, DD, DD)       \
+    WS_GQA_CASE(4, DD, DD)       \
+    WS_GQA_CASE(8, DD, DD)       \
+    WS_GQA_CASE(16, DD, DD)      \
+    default:                     \
+      WS_GQA_LAUNCH(0, DD, DD)   \
+      break;                     \
   }
-  if (Dk == kGqaDk192) {
+  // 64, 128 and 256 (and the ds2 pair) are instantiated per power-of-two
+  // group size; other group sizes and the other widths take it at run time
+  // (prm.G).
+#define WS_GQA_ANY(DD)        \
+  case DD:                    \
+    WS_GQA_LAUNCH(0, DD, DD)  \
+    break;
+  if (Dk == kGqaDk192 && D == kGqaD) {
     switch (G) { WS_GQA_CASE(1, kGqaDk192, kGqaD) }
   } else if (D == 64) {
     WS_GQA_GROUPS(64)
   } else if (D == kGqaMaxD) {
     WS_GQA_GROUPS(kGqaMaxD)
-  } else {
+  } else if (D == kGqaD) {
     WS_GQA_GROUPS(kGqaD)
+  } else {
+    switch (D) {
+      WS_GQA_ANY(16) WS_GQA_ANY(32) WS_GQA_ANY(48) WS_GQA_ANY(80) WS_GQA_ANY(96)
+      WS_GQA_ANY(112) WS_GQA_ANY(144) WS_GQA_ANY(160) WS_GQA_ANY(176) WS_GQA_ANY(192)
+      WS_GQA_ANY(208) WS_GQA_ANY(224) WS_GQA_ANY(240)
+    }
   }
+#undef WS_GQA_ANY
 #undef WS_GQA_GROUPS
 #undef WS_GQA_CASE
+#undef WS_GQA_LAUNCH
   int rc = check_launch(name);
   if (rc != WS_OK || !combine) return rc;
   // One-launch entry points: the rows held by several waves are combined by
@@ -557,8 +656,8 @@ extern "C" int ws_attn_decode_plan(int rows_kv, int heads, int Dk, int Dv, int m
                                    size_t* workspace_bytes_out) {
   if (!gqa_widths_ok(Dk, Dv))
     return set_error(WS_EINVAL,
-                     "ws_attn_decode_plan: head_dim Dk=%d Dv=%d unsupported (64/64, 128/128, "
-                     "256/256, 192/128)", Dk, Dv);
+                     "ws_attn_decode_plan: head_dim Dk=%d Dv=%d unsupported (equal multiples "
+                     "of 16 up to 256, 192/128)", Dk, Dv);
   if (rows_kv < 0 || max_len < 0 || n_splits < 0 || heads <= 0 || heads > 16)
     return set_error(WS_EINVAL, "ws_attn_decode_plan: bad arguments");
   const int n = gqa_splits(n_splits, rows_kv, max_len, Dv);

@@ -58,13 +58,14 @@ def test_width_plan():
     """The plan at other head widths: the piece slots scale with the value
     width, 128/128 matches kind 0, and widths without a kernel are refused."""
     pad = lambda n: -(-n // 256) * 256
-    for Dk, Dv in ((64, 64), (128, 128), (256, 256), (192, 128)):
+    for Dk, Dv in ((64, 64), (128, 128), (256, 256), (192, 128), (16, 16), (80, 80),
+                   (192, 192), (240, 240)):
         n, wsb = ops.gqa_plan(16, 8 if Dk != 192 else 1, Dk, Dv, 32768, 100)
         G = 8 if Dk != 192 else 1
         assert n == 100 and wsb == pad((100 + 16) * G * 4) + (100 + 16) * G * Dv * 2
     n_w, wsb_w = ops.gqa_plan(16, 8, 128, 128, 32768, 100)
     assert (n_w, wsb_w) == ops.decode_plan(0, 16, 8, 32768, 100)
-    for Dk, Dv in ((96, 96), (80, 80), (128, 64), (256, 128), (192, 192)):
+    for Dk, Dv in ((40, 40), (8, 8), (272, 272), (128, 64), (256, 128)):
         with pytest.raises(ops.WsError, match="unsupported"):
             ops.gqa_plan(16, 1, Dk, Dv, 100, 10)
 
@@ -74,10 +75,10 @@ def test_host_side_argument_checks():
     rc = L.ws_kv_append(None, None, None, None, None, None, 1, 1, 128, 1, 64, 1, 1, 1, None)
     assert rc == -1 and b"null" in L.ws_last_error()
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: rejected before launch
-    rc = L.ws_gqa_decode_partial(fake, fake, fake, fake, fake, 1, 24, 8, 128, 64, 4, 4,
+    rc = L.ws_gqa_decode_partial(fake, fake, fake, fake, fake, 1, 136, 8, 128, 64, 4, 4,
                                  100, 0, 1.0, fake, fake, None, 0, None)
     assert rc == -1 and b"group size" in L.ws_last_error()
-    rc = L.ws_gqa_decode_partial(fake, fake, fake, fake, fake, 1, 32, 8, 96, 64, 4, 4,
+    rc = L.ws_gqa_decode_partial(fake, fake, fake, fake, fake, 1, 32, 8, 40, 64, 4, 4,
                                  100, 0, 1.0, fake, fake, None, 0, None)
     assert rc == -1 and b"head_dim" in L.ws_last_error()
     rc = L.ws_gqa_decode_partial(fake, fake, fake, fake, fake, 1, 32, 8, 128, 48, 4, 4,

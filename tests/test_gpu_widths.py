@@ -1,8 +1,8 @@
-"""GPU parity of the GQA decode path at head widths other than 128 (64 and
-256; the reference's GPU partial is a torch bmm of any width,
-roofline/bench_resident_kv.py:150-157, and its CPU kernel takes any multiple
-of 16, kernel/cpu_attn.cpp:583), through the C-ABI, against fp64 attention
-and the oracle's C restatement of the reference CPU kernel.
+"""GPU parity of the GQA decode path at head widths other than 128 (every
+multiple of 16 up to 256; the reference's GPU partial is a torch bmm of any
+width, roofline/bench_resident_kv.py:150-157, and its CPU kernel takes any
+multiple of 16, kernel/cpu_attn.cpp:583), through the C-ABI, against fp64
+attention and the oracle's C restatement of the reference CPU kernel.
 
 Bar: appends bit-exact; outputs within 2e-2 abs/rel; fp32 LSE within 1e-3.
 """
@@ -23,6 +23,10 @@ from tests.helpers import (LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, assert_close,
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 WIDTHS = [64, 256]
+# widths whose kernels take the group size at run time; 16-column key tails
+# (48, 80, 112, ...) and value rows split over fewer than 16 lanes (80: 10
+# lanes of 8 columns, 176: 11 of 16)
+OTHER_WIDTHS = [16, 32, 48, 80, 96, 112, 144, 160, 176, 192, 208, 224, 240]
 
 
 def _say(msg):
@@ -68,7 +72,51 @@ def test_gqa_width_partial(D, G, wg):
     assert torch.equal(o2.cpu(), out.cpu()) and torch.equal(l2.cpu(), lse.cpu())
 
 
-@pytest.mark.parametrize("D", WIDTHS)
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("G", [3, 7, 12])
+def test_gqa_group_sizes_without_a_kernel_of_their_own(D, G):
+    """Group sizes that are not powers of two (Qwen2-7B: 28 query heads over
+    4 KV heads) run the width's kernel with the group size read at run time;
+    the fused append step over the same inputs agrees bit for bit with the
+    unfused call."""
+    lens = [0, 5, 64, 700]
+    Hkv = 2
+    _say(f"gqa group size G={G} D={D}")
+    total = [L + 1 for L in lens]
+    k_pages, v_pages, pt, gl, ks, vs = gqa_pool(total, Hkv, D, 64, seed=G + D, device=DEV)
+    q = bf16_randn((len(lens), Hkv * G, D), 3 * G + D).to(DEV)
+    scale = D ** -0.5
+    k_new = torch.stack([k[:, L:L + 1] for k, L in zip(ks, lens)]).to(DEV).contiguous()
+    v_new = torch.stack([v[:, L:L + 1] for v, L in zip(vs, lens)]).to(DEV).contiguous()
+    len_in = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    len_out = torch.zeros_like(len_in)
+    out, lse = ops.gqa_append_decode_partial(q, k_new, v_new, k_pages, v_pages, pt, len_in,
+                                             len_out, scale, max(total), 5)
+    o2, l2 = ops.gqa_decode_partial(q, k_pages, v_pages, pt, len_out, scale, max(total), 5)
+    torch.cuda.synchronize()
+    assert torch.equal(o2.cpu(), out.cpu()) and torch.equal(l2.cpu(), lse.cpu())
+    _check_rows(out, lse, q.cpu(), ks, vs, total, Hkv, G, D, scale, f"G={G} D={D}",
+                port_check=True)
+
+
+@pytest.mark.parametrize("D", OTHER_WIDTHS)
+@pytest.mark.parametrize("G,wg", [(1, 0), (6, 5)])
+def test_gqa_other_widths_partial(D, G, wg):
+    """Every other multiple of 16, group sizes 1 and 6 (a size without a
+    kernel of its own), against fp64 and the C port."""
+    lens = [0, 1, 33, 300, 1100]
+    Hkv = 2
+    _say(f"gqa width D={D} G={G} wg={wg}")
+    k_pages, v_pages, pt, gl, ks, vs = gqa_pool(lens, Hkv, D, 64, seed=D + 3 * G, device=DEV)
+    q = bf16_randn((len(lens), Hkv * G, D), 7 * D + G)
+    scale = D ** -0.5
+    out, lse = ops.attn_decode_partial(q.to(DEV), k_pages, v_pages, pt, gl, scale, max(lens),
+                                       n_workgroups=wg)
+    torch.cuda.synchronize()
+    _check_rows(out, lse, q, ks, vs, lens, Hkv, G, D, scale, f"D={D}", port_check=True)
+
+
+@pytest.mark.parametrize("D", WIDTHS + [48, 80, 96, 176, 240])
 def test_gqa_width_fused_steps_append_bit_exact(D):
     """Three fused append + attend steps with page size 32: outputs against
     fp64, the unfused call over the written pages bit-identical, and every
@@ -112,7 +160,7 @@ def test_gqa_width_fused_steps_append_bit_exact(D):
             assert np.array_equal(gv[b], bits(vs[b][h])), (b, h)
 
 
-@pytest.mark.parametrize("D", WIDTHS)
+@pytest.mark.parametrize("D", WIDTHS + [80, 144])
 def test_gqa_width_full_step_bf16(D):
     """The whole-step entry point: bf16 output is the fp32 output rounded to
     nearest even, the fp32 output bit-identical to the partial step's."""
@@ -137,7 +185,7 @@ def test_gqa_width_full_step_bf16(D):
     _check_rows(ob.float(), lse, q.cpu(), ks, vs, total, Hkv, G, D, scale, f"full D={D}")
 
 
-@pytest.mark.parametrize("D", WIDTHS)
+@pytest.mark.parametrize("D", WIDTHS + [112, 208])
 @pytest.mark.parametrize("fmt", [ops.PARTIAL_LSE_F32, ops.TRIPLE_NORM_BF16])
 def test_gqa_width_split_step_and_host_merge(D, fmt):
     """Deferred-combine step + merge with a host partial in two of the
@@ -173,7 +221,7 @@ def test_gqa_width_split_step_and_host_merge(D, fmt):
         assert_close(gls[b], wl, LSE_ATOL, LSE_RTOL, f"merged lse D={D} b={b}")
 
 
-@pytest.mark.parametrize("D", WIDTHS)
+@pytest.mark.parametrize("D", WIDTHS + [80])
 def test_gqa_width_noalloc_matches_workspace_call(D):
     """The no-allocation entry point at another width: bit-identical to the
     workspace entry point, on two calls in a row, the second smaller."""
@@ -200,11 +248,11 @@ def test_gqa_width_noalloc_matches_workspace_call(D):
         assert torch.equal(kp.cpu(), kp2.cpu()) and torch.equal(vp.cpu(), vp2.cpu())
 
 
-@pytest.mark.parametrize("D", WIDTHS)
+@pytest.mark.parametrize("D", WIDTHS + [80, 112])
 def test_partitioned_gqa_step_with_native_host_partial(D):
     """One two-sided decode step through the partitioned cache: GPU split
     step with the append, this package's host partial over the host tokens
-    (bf16, any multiple of 32 up to 256), merge; against fp64 attention over
+    (bf16, any multiple of 16 up to 256), merge; against fp64 attention over
     the whole sequence."""
     B, Hkv, G = 3, 4, 4
     rng = np.random.default_rng(D)
@@ -236,7 +284,7 @@ def test_partitioned_gqa_step_with_native_host_partial(D):
     assert cache.gpu.lens[0].tolist() == [gg + 1 for gg in g]
 
 
-@pytest.mark.parametrize("Dk,Dv", [(96, 96), (80, 80), (128, 64), (256, 128)])
+@pytest.mark.parametrize("Dk,Dv", [(40, 40), (8, 8), (272, 272), (128, 64), (256, 128)])
 def test_unsupported_widths_are_rejected(Dk, Dv):
     B, Hkv, PS = 1, 1, 64
     q = torch.zeros((B, Hkv, Dk), dtype=torch.bfloat16, device=DEV)

@@ -68,6 +68,12 @@ GQA_CASES = [
     (1, 1, 2, 192, [48], 64, 1),
     (1, 1, 2, 224, [129], 129, 4),
     (3, 1, 8, 128, [0, 0, 0], 16, 4),       # all empty
+    # widths with a last 16-column chunk (the reference takes any multiple of 16)
+    (1, 1, 1, 16, [40], 40, 1),
+    (2, 2, 4, 48, [33, 100], 100, 3),
+    (2, 1, 8, 80, [257, 5], 257, 4),
+    (1, 2, 2, 112, [64], 64, 2),
+    (1, 1, 16, 240, [90], 96, 3),
 ]
 
 
@@ -144,8 +150,8 @@ def test_argument_errors():
     with pytest.raises(host.WhError, match="group size"):
         host.gqa_partial_dense(bf16_randn((1, 17, 128), 0), k, k, [4], 0.1)
     with pytest.raises(host.WhError, match="head_dim"):
-        host.gqa_partial_dense(bf16_randn((1, 4, 48), 0), bf16_randn((1, 8, 48), 1),
-                         bf16_randn((1, 8, 48), 2), [4], 0.1)
+        host.gqa_partial_dense(bf16_randn((1, 4, 40), 0), bf16_randn((1, 8, 40), 1),
+                         bf16_randn((1, 8, 40), 2), [4], 0.1)
     with pytest.raises(ValueError):
         host.gqa_partial_dense(q.float(), k, k, [4], 0.1)  # dtype
     with pytest.raises(ValueError):
@@ -288,6 +294,7 @@ def test_prepared_call_reads_its_buffers_at_call_time():
     (16, 1, 192, 128, 64, 7),   # decompressed DeepSeek-V2: 16 heads, 192-wide keys
     (2, 4, 192, 128, 32, 3),
     (3, 2, 96, 96, 64, 4),      # Dk == Dv through the same entry point
+    (2, 4, 80, 80, 32, 3),      # a last 16-column chunk
 ])
 def test_attn_partial_separate_key_value_widths(Hkv, G, Dk, Dv, page_size, threads):
     """wh_attn_partial (the fused_cpu_attn_mla contract with Dk != Dv,
