@@ -62,7 +62,7 @@ int wh_isa_supported(void);
  *              page_table[b][t / page_size] at offset t % page_size
  *   lens       [B] int32 host tokens, 0 <= lens[b] <= max_pages * page_size
  *   out        [B, Hq, D] fp32 normalised partial; lse [B, Hq] fp32
- * D: a multiple of 32 up to 256; G: 1..16.  n_threads <= 0: the OpenMP
+ * D: a multiple of 16 up to 256; G: 1..16.  n_threads <= 0: the OpenMP
  * default.  Returns WH_OK or a negative WH_E* code. */
 int wh_gqa_partial(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
                    const int32_t* page_table, const int32_t* lens, int B, int Hq, int Hkv,
@@ -81,7 +81,7 @@ int wh_gqa_partial_bf16(const uint16_t* q, const uint16_t* k_pages, const uint16
 
 /* wh_gqa_partial with separate key and value widths: q [B, Hq, Dk],
  * k_pages [num_pages, Hkv, page_size, Dk], v_pages [num_pages, Hkv,
- * page_size, Dv], out [B, Hq, Dv].  (Dk, Dv): equal multiples of 32 up to 256,
+ * page_size, Dv], out [B, Hq, Dv].  (Dk, Dv): equal multiples of 16 up to 256,
  * or (192, 128), the decompressed DeepSeek-V2 layout (128 nope + 64 rope key
  * columns, 128 value columns; the reference's ds2 model entry,
  * roofline/bench_resident_kv.py:10).
