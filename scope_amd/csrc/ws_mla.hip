@@ -148,23 +148,27 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     const int sb = uniform(seq_of(b, p.ng));  // the sequence whose latent it reads
     const int32_t* pt = p.page_table + (size_t)sb * p.max_pages;
 
-    // Page ids of the segment's blocks, 64 at a time (lane l: block
-    // pid_base + l), read with readlane: the ring issues no load whose
-    // address waits on another load (a page-table read per block would make
-    // every block wait for all loads in flight).  They are requested first:
-    // the first KV requests wait for them.  An id outside the pool
-    // is kept clamped with bit 31 set: the loads read the clamped page, the
-    // append skips it.  (The clamp also keeps the wait for the page-table
-    // load inside the refill branch: the raw value flowing out of it would
-    // make the compiler wait for every load in flight on each block.)
+    // Pool token index of the first row of each of the segment's blocks, 64
+    // at a time (lane l: block pid_base + l), read with readlane: the ring
+    // issues no load whose address waits on another load (a page-table read
+    // per block would make every block wait for all loads in flight).  They
+    // are requested first: the first KV requests wait for them.  A page id
+    // outside the pool is kept clamped and marks the index with bit 31: the
+    // loads read the clamped page, the append skips it.  (The clamp also
+    // keeps the wait for the page-table load inside the refill branch: the
+    // raw value flowing out of it would make the compiler wait for every
+    // load in flight on each block.)  A block never crosses a page (page
+    // sizes are multiples of 32, or the pool has one page per sequence).
     int pid_base = 0;
-    int m_pid = 0;
+    int m_tok = 0;
     int seg_bad = 0;  // bit 31: a block of the segment had a page id outside the pool
     auto fetch_pids = [&]() {
       const int t0 = t_begin + 32 * min(pid_base + lane, nblk - 1);
-      const int raw = pt[t0 / p.page_size];
+      const int page = t0 / p.page_size;
+      const int raw = pt[page];
       const int pid = clamp_page(raw, p.num_pages);
-      m_pid = pid | (raw == pid ? 0 : (int)0x80000000u);
+      m_tok = (pid * p.page_size + (t0 - page * p.page_size)) |
+              (raw == pid ? 0 : (int)0x80000000u);
     };
     fetch_pids();
 
@@ -205,6 +209,10 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     const long long dummy_off = (const char*)dummy - g0;
     const int pe_row = tid >> 3;
     const int pe_col = kMlaC / 8 + (tid & 7);
+    // Byte offsets of a thread's chunks inside a block: chunk u at row
+    // 4 u + wave, column `lane` (vo_row + u * 4 rows); chunk 8 at vo_pe.
+    const uint32_t vo_row = (uint32_t)(wave * (kMlaL * 2) + 16 * lane);
+    const uint32_t vo_pe = (uint32_t)(pe_row * (kMlaL * 2) + 16 * pe_col);
     auto gload = [&](int k, u32x4 (&dst)[kChunksPerThread]) {
       const bool valid = k < nblk;
       const int kc = min(k, nblk - 1);
@@ -213,14 +221,20 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
         fetch_pids();
       }
       const int t0 = t_begin + 32 * kc;
-      const int page = t0 / p.page_size;
-      const int pid_raw = __builtin_amdgcn_readlane(m_pid, kc - pid_base);
-      seg_bad |= pid_raw;
-      const int pid = pid_raw & 0x7fffffff;
-      const long long lb =
-          (long long)((size_t)pid * p.page_size + (t0 - page * p.page_size)) * (kMlaL * 2);
+      const int tok_raw = __builtin_amdgcn_readlane(m_tok, kc - pid_base);
+      seg_bad |= tok_raw;
+      const long long lb = (long long)(uint32_t)(tok_raw & 0x7fffffff) * (kMlaL * 2);
       const int last = min(32, t_end - t0) - 1;
       const int new_r = (APPEND && valid) ? len_old - t0 : -1;
+      if (valid && last == 31 && (unsigned)new_r > 31u) {
+        // A full block without the appended token (all but a segment's last
+        // few requests): one scalar base, fixed per-lane offsets.
+        const char* bp = g0 + lb;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) dst[u] = ld_stream(bp + u * (4 * kMlaL * 2) + vo_row);
+        dst[8] = ld_stream(bp + vo_pe);
+        return;
+      }
       // Chunks 0..7 of a thread: row 4 u + wave, 16-byte column `lane` of
       // the row's c_kv part (each load reads whole rows, so its row, clamp
       // and new-token test are uniform); chunk 8: row tid / 8, k_pe column
@@ -329,11 +343,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     // 0 of the sequence writes it.)
     if (APPEND && len_old >= t_begin && len_old < t_end && b == sb * p.ng) {
       const int t0 = t_begin + 32 * (nblk - 1);
-      const int pid = __builtin_amdgcn_readlane(m_pid, nblk - 1 - pid_base);
-      const int page = t0 / p.page_size;
-      if (tid < kMlaL / 8 && pid >= 0)  // bit 31: the page id is outside the pool
-        ((u32x4*)(p.latent_w +
-                  ((size_t)pid * p.page_size + (len_old - page * p.page_size)) * kMlaL))[tid] =
+      const int tok = __builtin_amdgcn_readlane(m_tok, nblk - 1 - pid_base);
+      if (tid < kMlaL / 8 && tok >= 0)  // bit 31: the page id is outside the pool
+        ((u32x4*)(p.latent_w + ((size_t)tok + (len_old - t0)) * kMlaL))[tid] =
             s_lat[(nblk - 1) % 3][(len_old - t0) * kRowChunks + tid];
     }
 
@@ -467,6 +479,9 @@ static int mla_launch(const uint16_t* q_nope, const uint16_t* q_pe,
   if ((long long)Bv * ((max_len + 32) / 32) * 4096 >= (1LL << 31))
     return set_error(WS_EINVAL, "%s: %d sequences of %d tokens exceed the block index range",
                      name, Bv, max_len);
+  if ((long long)num_pages * page_size >= (1LL << 31))  // bit 31 marks bad page ids
+    return set_error(WS_EINVAL, "%s: pools of %lld tokens exceed the 31-bit token index", name,
+                     (long long)num_pages * page_size);
   const int n = mla_workgroups(n_workgroups, Bv, max_len);
   const size_t need = ws::workspace_bytes(Bv, hp, kMlaC, n);
   if (!workspace || workspace_bytes < need)
