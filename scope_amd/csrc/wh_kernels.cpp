@@ -74,11 +74,12 @@ inline __m512 reduce16(const __m512* a) {
 
 inline __m512bh ld_bh(const void* p) { return (__m512bh)_mm512_loadu_si512(p); }
 
-// Broadcast of the bf16 pair at p (two adjacent 16-bit values).
-inline __m512bh bcast_pair(const void* p) {
-  int w;
-  std::memcpy(&w, p, 4);
-  return (__m512bh)_mm512_set1_epi32(w);
+// acc + vdpbf16ps(a, the bf16 pair at p in every lane), with the pair as the
+// instruction's {1to16} memory operand: one instruction, where the intrinsic
+// over a broadcast compiles to a separate vpbroadcastd load per product.
+inline __m512 dp_pair(__m512 acc, __m512bh a, const void* p) {
+  asm("vdpbf16ps %2%{1to16%}, %1, %0" : "+v"(acc) : "v"(a), "m"(*(const int32_t*)p));
+  return acc;
 }
 
 // The 16 bf16 values at p in the low half of a zmm, zeros above (no read
@@ -370,14 +371,14 @@ inline void mla_scores16(const uint32_t* qt, const uint16_t* c, const uint16_t* 
     const __m512bh qv = (__m512bh)_mm512_loadu_si512(qt + 16 * p);
 #pragma GCC unroll 16
     for (int j = 0; j < 16; ++j)
-      acc[j] = _mm512_dpbf16_ps(acc[j], qv, bcast_pair(c + j * CT + 2 * p));
+      acc[j] = dp_pair(acc[j], qv, c + j * CT + 2 * p);
   }
   for (int p = 0; p < kMlaPe / 2; ++p) {
     if (pf_pe) _mm_prefetch(pf_pe + 64 * p, _MM_HINT_T0);
     const __m512bh qv = (__m512bh)_mm512_loadu_si512(qt + 16 * (kMlaC / 2 + p));
 #pragma GCC unroll 16
     for (int j = 0; j < 16; ++j)
-      acc[j] = _mm512_dpbf16_ps(acc[j], qv, bcast_pair(pe + j * PT + 2 * p));
+      acc[j] = dp_pair(acc[j], qv, pe + j * PT + 2 * p);
   }
 }
 
@@ -466,7 +467,7 @@ void mla_attend_t(const uint32_t* qt, const uint16_t* c, size_t c_tok, const uin
         const __m512bh pv = (__m512bh)_mm512_load_si512(p2[kq]);
         const uint32_t* src = vst + (size_t)kq * kMlaC + s0;
 #pragma GCC unroll 16
-        for (int i = 0; i < 16; ++i) acc[i] = _mm512_dpbf16_ps(acc[i], pv, bcast_pair(src + i));
+        for (int i = 0; i < 16; ++i) acc[i] = dp_pair(acc[i], pv, src + i);
       }
 #pragma GCC unroll 16
       for (int i = 0; i < 16; ++i) _mm512_storeu_ps(o + 16 * (s0 + i), acc[i]);
