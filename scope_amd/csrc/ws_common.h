@@ -59,6 +59,16 @@ __device__ __forceinline__ u32x4 ld_stream(const void* p) {
   return __builtin_nontemporal_load((const u32x4*)p);
 }
 
+// ds_read_b64_tr_b16 at LDS byte address `addr`.  In each 16-lane group,
+// result lane 4 r + j, element e is element j of the four 16-bit values lane
+// 4 e + r addresses (measured with an in-bounds probe on gfx950).
+__device__ __forceinline__ uint2 lds_read_tr_b64(uint32_t addr) {
+  typedef short i16x4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+  const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(uintptr_t)addr);
+  return __builtin_bit_cast(uint2, v);
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __builtin_bit_cast(float, (uint32_t)h << 16);
 }

@@ -58,35 +58,37 @@ struct MlaParams {
   float scale_log2;
 };
 
+// A wave's 128 output columns of head n16 from its accumulators: acc[e][i] of
+// lane group j is column 16 e + 4 j + i.
 __device__ __forceinline__ void store_cols(float* __restrict__ dst, const f32x4 (&acc)[8],
                                            int j, float inv_l) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float4* o = (float4*)(dst + 32 * j + 8 * i);
-    o[0] = make_float4(acc[0][i] * inv_l, acc[1][i] * inv_l, acc[2][i] * inv_l,
-                       acc[3][i] * inv_l);
-    o[1] = make_float4(acc[4][i] * inv_l, acc[5][i] * inv_l, acc[6][i] * inv_l,
-                       acc[7][i] * inv_l);
-  }
+  for (int e = 0; e < 8; ++e)
+    *(float4*)(dst + 16 * e + 4 * j) = make_float4(acc[e][0] * inv_l, acc[e][1] * inv_l,
+                                                   acc[e][2] * inv_l, acc[e][3] * inv_l);
 }
 
 // The same columns as a bf16 piece.
 __device__ __forceinline__ void store_cols_piece(uint16_t* __restrict__ dst,
                                                  const f32x4 (&acc)[8], int j, float inv_l) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    store_piece8(dst + 32 * j + 8 * i, acc[0][i] * inv_l, acc[1][i] * inv_l, acc[2][i] * inv_l,
-                 acc[3][i] * inv_l, acc[4][i] * inv_l, acc[5][i] * inv_l, acc[6][i] * inv_l,
-                 acc[7][i] * inv_l);
+  for (int e = 0; e < 8; ++e) {
+    uint2 v;
+    v.x = pack_bf16x2(acc[e][0] * inv_l, acc[e][1] * inv_l);
+    v.y = pack_bf16x2(acc[e][2] * inv_l, acc[e][3] * inv_l);
+    *(uint2*)(dst + 16 * e + 4 * j) = v;
+  }
 }
 
 // LDS tile of one 32-token block: row-major latent rows of 72 16-byte chunks
-// plus four pad chunks.  Measured with the LDS bank-conflict counters on the
-// two read patterns below: a row stride of 76 chunks leaves the PV reads
-// (8 rows x 16 consecutive chunks per instruction) conflict-free and the QK
-// reads (16 rows x 4 chunks) 2-way; 73 leaves both 2-way, and no stride or
-// per-row offset table tried frees both.
-constexpr int kRowChunks = 76;
+// plus two pad chunks.  A row stride of 74 chunks leaves the QK reads (16
+// rows x 4 chunks per ds_read_b128) conflict-free, measured with the LDS
+// bank-conflict counters on an in-bounds probe of that pattern (73 and 76:
+// 2-way).  The PV reads (ds_read_b64_tr_b16: per 32-lane pass, rows 4 a ..
+// 4 a + 7, 32 bytes of each) hit 64 different banks at this stride: rows
+// 74 chunks apart fall in different 64-byte quarters of a 256-byte bank
+// cycle, and the second four rows fill the other half of each quarter.
+constexpr int kRowChunks = 74;
 constexpr int kTileChunks = 32 * kRowChunks;
 // Blocks in flight in registers while one is consumed from LDS.
 constexpr int kMlaDepth = 3;
@@ -112,6 +114,10 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
   const int tt = wave & 1;
   const int kh = wave >> 1;
   const int col0 = 128 * wave;
+  // byte offset in a tile of this lane's V^T reads (token row 4 j + n16 / 4,
+  // columns col0 + 4 (n16 % 4) ..): the PV reads add 32 e and 16 rows
+  const uint32_t v_lane =
+      (uint32_t)(((4 * j + (n16 >> 2)) * kRowChunks) * 16 + 2 * col0 + 8 * (n16 & 3));
 
   if (APPEND && p.len_out && g == 0)
     for (int b = tid; b < p.B / p.ng; b += NT)
@@ -284,10 +290,26 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
       bool rescale;
       const u32x4 pb =
           softmax_block(s0, s1, j, nt, p.scale_log2, m_run, l_run, alpha, rescale);
-      u32x4 vr[8];
+      // V^T straight from LDS: for output tile e, lanes 4 e' + r of lane
+      // group j address token rows 4 j + e' and 16 + 4 j + e' (the k-slots of
+      // pb, pv_token) at columns col0 + 16 e + 4 r, so result lane m holds
+      // four tokens of column col0 + 16 e + m (lds_read_tr_b64).
+      if (rescale) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) vr[i] = tile[pv_token(i, j) * kRowChunks + (col0 >> 3) + n16];
-      pv_block(acc, vr, pb, alpha, rescale);
+        for (int e = 0; e < 8; ++e) acc[e] = acc[e] * alpha;
+      }
+      // (All sixteen reads go out before the first MFMA, as in the QK.)
+      const uint32_t vt = (uint32_t)(uintptr_t)tile + v_lane;
+      uint2 lo[8], hi[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        lo[e] = lds_read_tr_b64(vt + 32 * e);
+        hi[e] = lds_read_tr_b64(vt + 32 * e + 16 * 16 * kRowChunks);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        acc[e] = mfma16x16x32(u32x4{lo[e].x, lo[e].y, hi[e].x, hi[e].y}, pb, acc[e]);
     };
 
     // Pipeline over three LDS tiles (block m in tile m % 3) and three

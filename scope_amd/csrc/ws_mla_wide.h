@@ -65,7 +65,6 @@
 namespace ws {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWideRowData = 72;  // 576 bf16 = 72 x 16 B
 // LDS chunk offset of row r of a tile.
@@ -182,13 +181,6 @@ __device__ __forceinline__ void wide_store_rows(char* dst, int row_bytes, const 
     for (int h = 0; h < 8; ++h)
       *(u32x4*)(dst + (size_t)(h0 + h) * row_bytes + col_byte) = v[h];
   }
-}
-
-// ds_read_b64_tr_b16 at LDS byte address `addr`.
-__device__ __forceinline__ uint2 wide_tr_read(uint32_t addr) {
-  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)addr);
-  return __builtin_bit_cast(uint2, v);
 }
 
 template <bool APPEND>
@@ -448,8 +440,8 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
     auto vread = [&](uint32_t vt, int m) __attribute__((always_inline)) {
       const int sv = m >> 4, ct = m & 15;
       const uint32_t a = vt + 16 * kWideRowsS * sv + 64 * ct;
-      const uint2 lo = wide_tr_read(a);
-      const uint2 hi = wide_tr_read(a + 16 * kWideRowsT);
+      const uint2 lo = lds_read_tr_b64(a);
+      const uint2 hi = lds_read_tr_b64(a + 16 * kWideRowsT);
       return u32x4{lo.x, lo.y, hi.x, hi.y};
     };
     // the memory clobber keeps the operand reads where the source puts them
