@@ -267,25 +267,32 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
     };
     // QK partial of block k from its LDS tile: token tile tt over latent
     // half kh, into score buffer `par`.
-    auto qk = [&](const u32x4* tile, int par) {
+    // All nine operand reads go out before the first MFMA (the MFMA chain
+    // is serial; read by read, each would wait a full LDS round trip).
+    auto qk_read = [&](const u32x4* tile, u32x4 (&kr)[9]) {
       const u32x4* krow = tile + (16 * tt + n16) * kRowChunks + j;
-      // All nine operand reads go out before the first MFMA (the MFMA chain
-      // is serial; read by read, each would wait a full LDS round trip).
-      u32x4 kr[9];
 #pragma unroll
       for (int u = 0; u < 9; ++u) kr[u] = krow[4 * (9 * kh + u)];
-      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto qk_mfma = [&](const u32x4 (&kr)[9], int par) {
       f32x4 sp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < 9; ++u) sp = mfma16x16x32(kr[u], qb[u], sp);
       sbuf[par][kh][tt][lane] = sp;
     };
-    // Softmax of block k from the four score partials in buffer `par`, then
-    // PV of this wave's 128 output columns from the block's tile.
-    auto finish = [&](int k, const u32x4* tile, int par) {
+    auto qk = [&](const u32x4* tile, int par) {
+      u32x4 kr[9];
+      qk_read(tile, kr);
+      __builtin_amdgcn_sched_barrier(0);
+      qk_mfma(kr, par);
+    };
+    // Softmax of block k from its scores (s0, s1: the sums of the four score
+    // partials of buffer `par`, token tiles 0 and 1), then PV of this wave's
+    // 128 output columns from the block's tile.
+    auto finish = [&](int k, const u32x4* tile, const f32x4 (&sp)[4]) {
       const int nt = min(32, t_end - (t_begin + 32 * k));
-      const f32x4 s0 = sbuf[par][0][0][lane] + sbuf[par][1][0][lane];
-      const f32x4 s1 = sbuf[par][0][1][lane] + sbuf[par][1][1][lane];
+      const f32x4 s0 = sp[0] + sp[1];
+      const f32x4 s1 = sp[2] + sp[3];
       float alpha;
       bool rescale;
       const u32x4 pb =
@@ -341,8 +348,19 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
       constexpr int s = decltype(slot)::value;  // kk % 3
       if (kk + 2 < nblk) lwrite(s_lat[(s + 2) % 3], st[(s + 2) % 3]);
       gload(kk + 5, st[(s + 2) % 3]);
-      finish(kk, s_lat[s], kk & 1);
-      if (kk + 1 < nblk) qk(s_lat[(s + 1) % 3], (kk + 1) & 1);
+      // block k's scores, then block k + 1's QK operands, requested before
+      // block k's softmax, which does not need them (LDS reads complete in
+      // order; past the segment's last block the QK reads see a stale tile
+      // and go unused)
+      const int par = kk & 1;
+      const f32x4 sp[4] = {sbuf[par][0][0][lane], sbuf[par][1][0][lane], sbuf[par][0][1][lane],
+                           sbuf[par][1][1][lane]};
+      __builtin_amdgcn_sched_barrier(0);
+      u32x4 kr[9];
+      qk_read(s_lat[(s + 1) % 3], kr);
+      __builtin_amdgcn_sched_barrier(0);
+      finish(kk, s_lat[s], sp);
+      if (kk + 1 < nblk) qk_mfma(kr, (kk + 1) & 1);
       __syncthreads();
     };
     using S0 = std::integral_constant<int, 0>;
