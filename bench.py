@@ -1029,7 +1029,7 @@ WORKLOADS = ("shares", "qwen3", "single", "mla", "mla_sweep", "mla128", "host", 
 EXTRA_WORKLOADS = ("mla32k",)
 
 # The kernel the headline roofline is measured on (its rocprofv3 name).
-HEAD_KERNEL = "ws::gqa_decode_kernel<4, 128, true>"
+HEAD_KERNEL = "ws::gqa_decode_kernel<4, 128, 128, true>"
 
 
 MLA_KERNEL = "ws::mla_decode_kernel<true>"
