@@ -115,7 +115,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
   const int kh = wave >> 1;
   const int col0 = 128 * wave;
   // byte offset in a tile of this lane's V^T reads (token row 4 j + n16 / 4,
-  // columns col0 + 4 (n16 % 4) ..): the PV reads add 32 e and 16 rows
+  // columns col0 + 4 (n16 % 4) ..); the read of output tile e adds 32 e bytes
+  // (16 columns), the second read of a tile 16 rows
   const uint32_t v_lane =
       (uint32_t)(((4 * j + (n16 >> 2)) * kRowChunks) * 16 + 2 * col0 + 8 * (n16 & 3));
 
@@ -286,9 +287,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(const MlaParams p) {
       __builtin_amdgcn_sched_barrier(0);
       qk_mfma(kr, par);
     };
-    // Softmax of block k from its scores (s0, s1: the sums of the four score
-    // partials of buffer `par`, token tiles 0 and 1), then PV of this wave's
-    // 128 output columns from the block's tile.
+    // Softmax of block k from its four score partials sp (latent halves 0 and
+    // 1 of token tile 0, then of token tile 1), then PV of this wave's 128
+    // output columns from the block's tile.
     auto finish = [&](int k, const u32x4* tile, const f32x4 (&sp)[4]) {
       const int nt = min(32, t_end - (t_begin + 32 * k));
       const f32x4 s0 = sp[0] + sp[1];
