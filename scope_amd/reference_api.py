@@ -29,8 +29,8 @@ def local_bmm_softmax(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: 
 
     q [N, G, Dk], k [N, S, Dk], v [N, S, Dv] bf16 contiguous on the GPU ->
     (o [N, G, Dv] fp32, max [N, G, 1] fp32, sum [N, G, 1] fp32), equivalent
-    triple.  Dk == Dv == 128 for the GQA model entries (64 and 256 also have
-    kernels); Dk 192 / Dv 128 with G = 1 for the ds2 entry
+    triple.  Dk == Dv == 128 for the GQA model entries (any multiple of 16 up
+    to 256 has a kernel); Dk 192 / Dv 128 with G = 1 for the ds2 entry
     (roofline/bench_resident_kv.py:10).
     """
     N, G, Dk = q.shape

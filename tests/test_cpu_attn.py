@@ -72,6 +72,24 @@ def test_fused_cpu_attn_matches_the_c_restatement():
     assert_close(_lse(m, s), pm + np.log(ps), BF16_LSE_TOL, BF16_LSE_TOL, "lse vs C port")
 
 
+@pytest.mark.parametrize("D", [16, 48, 80, 112, 240])
+def test_fused_cpu_attn_any_multiple_of_16_width(D):
+    """Head widths with a last 16-column chunk (the reference kernel takes any
+    multiple of 16, kernel/cpu_attn.cpp:583), bf16 inputs, against fp64 and
+    the oracle's C restatement."""
+    from oracle import port
+    N, G, S = 3, 4, 149
+    q, k, v = bf16_randn((N, G, D), 10 + D), bf16_randn((N, S, D), 11 + D), bf16_randn((N, S, D), 12 + D)
+    scale = D ** -0.5
+    o, m, s = X.fused_cpu_attn(q, k, v, scale)
+    assert tuple(o.shape) == (N, G, D)
+    ow, lw = O.gqa_attention_fp64(bits(q), bits(k), bits(v), scale)
+    assert_close(o.float().numpy(), ow, OUT_ATOL, OUT_RTOL, f"out D={D}")
+    assert_close(_lse(m, s)[..., 0], lw, BF16_LSE_TOL, BF16_LSE_TOL, f"max + log(sum) D={D}")
+    po, pm, ps = port.cpu_attn(bits(q), bits(k), bits(v), scale, normalize=True, n_threads=2)
+    assert_close(o.float().numpy(), po, OUT_ATOL, OUT_RTOL, f"out vs C port D={D}")
+
+
 def test_fused_cpu_attn_mla_separate_widths_unnormalised():
     N, G, Dk, Dv, S = 16, 1, 192, 128, 257
     q, k, v = bf16_randn((N, G, Dk), 7), bf16_randn((N, S, Dk), 8), bf16_randn((N, S, Dv), 9)

@@ -284,6 +284,24 @@ def test_partitioned_gqa_step_with_native_host_partial(D):
     assert cache.gpu.lens[0].tolist() == [gg + 1 for gg in g]
 
 
+@pytest.mark.parametrize("D", [64, 80, 96, 256])
+def test_reference_api_local_bmm_softmax_widths(D):
+    """The reference-signature GPU partial (_local_bmm_softmax,
+    roofline/bench_resident_kv.py:150-157) at other head widths: its
+    (o, max, sum) triple against fp64 attention."""
+    from scope_amd import reference_api
+    N, G, S = 6, 4, 700
+    q, k, v = (bf16_randn((N, G, D), 20 + D), bf16_randn((N, S, D), 21 + D),
+               bf16_randn((N, S, D), 22 + D))
+    scale = D ** -0.5
+    o, m, s = reference_api.local_bmm_softmax(q.to(DEV), k.to(DEV), v.to(DEV), scale)
+    torch.cuda.synchronize()
+    ow, lw = O.gqa_attention_fp64(bits(q), bits(k), bits(v), scale)
+    assert_close(o.cpu().numpy(), ow, OUT_ATOL, OUT_RTOL, f"o D={D}")
+    lse = (m + torch.log(s)).cpu().numpy()[..., 0]
+    assert_close(lse, lw, LSE_ATOL, LSE_RTOL, f"max + log(sum) D={D}")
+
+
 @pytest.mark.parametrize("Dk,Dv", [(40, 40), (8, 8), (272, 272), (128, 64), (256, 128)])
 def test_unsupported_widths_are_rejected(Dk, Dv):
     B, Hkv, PS = 1, 1, 64
