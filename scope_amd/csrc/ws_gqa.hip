@@ -660,6 +660,9 @@ extern "C" int ws_attn_decode_plan(int rows_kv, int heads, int Dk, int Dv, int m
                      "of 16 up to 256, 192/128)", Dk, Dv);
   if (rows_kv < 0 || max_len < 0 || n_splits < 0 || heads <= 0 || heads > 16)
     return set_error(WS_EINVAL, "ws_attn_decode_plan: bad arguments");
+  if (Dk == kGqaDk192 && Dv == kGqaD && heads != 1)
+    return set_error(WS_EINVAL, "ws_attn_decode_plan: Dk=192 takes group size 1 (got %d)",
+                     heads);
   const int n = gqa_splits(n_splits, rows_kv, max_len, Dv);
   if (n_splits_out) *n_splits_out = n;
   if (workspace_bytes_out) *workspace_bytes_out = ws::workspace_bytes(rows_kv, heads, Dv, n);

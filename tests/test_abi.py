@@ -68,6 +68,9 @@ def test_width_plan():
     for Dk, Dv in ((40, 40), (8, 8), (272, 272), (128, 64), (256, 128)):
         with pytest.raises(ops.WsError, match="unsupported"):
             ops.gqa_plan(16, 1, Dk, Dv, 100, 10)
+    # the 192/128 kernel exists for group size 1 only, as the launch checks
+    with pytest.raises(ops.WsError, match="group size 1"):
+        ops.gqa_plan(16, 8, 192, 128, 100, 10)
 
 
 def test_host_side_argument_checks():
