@@ -266,3 +266,42 @@ def test_mla_128_heads_b4_every_row_against_the_c_restatement():
     lb = bits(lat)
     for b in range(B):
         assert np.array_equal(lb[int(pt[b, L // PS]), L % PS], bits(lat_all[b][-1])), b
+
+
+def test_mla_128_heads_b4_full_size_against_the_c_restatement():
+    """DeepSeek-V2 shape at the size the step is timed on: 128 heads, B 4 at
+    32768 tokens per sequence plus the appended one, split step + merge.
+    Sequences 0 and 3 (every head) against the oracle's C restatement over
+    all their tokens; all four appended latents bit-exact in their pages."""
+    from oracle import port
+    H, B, L = 128, 4, 32768
+    _say("mla H=128 B4 L32768 against the C restatement (sequences 0, 3)")
+    gen = torch.Generator(device=DEV).manual_seed(160)
+    lat_all = [(torch.randn((L + 1, 576), generator=gen, device=DEV) * 0.5).to(torch.bfloat16)
+               for _ in range(B)]
+    lat, pt, gl, _, _ = mla_pool([L + 1] * B, PS, seed=161)
+    for b in range(B):
+        t = torch.arange(L, device=DEV)
+        lat[pt[b, t // PS].long(), t % PS] = lat_all[b][:L]
+    gl.fill_(L)
+    qn = (torch.randn((B * H, 512), generator=gen, device=DEV) * 0.5).to(torch.bfloat16)
+    qp = (torch.randn((B * H, 64), generator=gen, device=DEV) * 0.5).to(torch.bfloat16)
+    new = torch.stack([x[-1] for x in lat_all])[:, None]
+    len_out = torch.zeros_like(gl)
+    st = ops.mla_append_decode_split(qn, qp, new[..., :512], new[..., 512:], lat, pt, gl, len_out,
+                                     SCALE, L + 1)
+    out, lse = ops.merge_split(st, None, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    out, lse = out.cpu().numpy(), lse.cpu().numpy()
+    assert len_out.cpu().tolist() == [L + 1] * B
+    lb = bits(lat)
+    for b in range(B):
+        assert np.array_equal(lb[int(pt[b, L // PS]), L % PS], bits(lat_all[b][-1])), b
+    for b in (0, 3):
+        rows = slice(b * H, (b + 1) * H)
+        full = bits(lat_all[b])[None]
+        po, pm, ps = port.cpu_attn_mla_compressed(bits(qn[rows]), bits(qp[rows]),
+                                                  full[:, :, :512], full[:, :, 512:], SCALE,
+                                                  n_threads=16)
+        assert_close(out[rows], po / ps[:, None], OUT_ATOL, OUT_RTOL, f"out b={b} vs C port")
+        assert_close(lse[rows], pm + np.log(ps), LSE_ATOL, LSE_RTOL, f"lse b={b} vs C port")
