@@ -145,3 +145,48 @@ def test_dsv2lite_mla_b8_full_size_share_invariance():
         for r in outs:
             assert_close(outs[r][rows], want, OUT_ATOL, OUT_RTOL, f"r={r} b={b}")
             assert_close(lses[r][rows], wl, LSE_ATOL, LSE_RTOL, f"r={r} b={b} lse")
+
+
+@pytest.mark.parametrize("L", [32768, 131072])
+def test_dsv2lite_mla_b8_length_sweep_all_in_hbm(L):
+    """The MLA length sweep's shapes (16 heads, B=8, r = 1): the fused append
+    + split step + merge over L tokens per sequence plus the appended one.
+    Every head of sequences 0 and 7 against the C restatement over all their
+    tokens; every appended latent bit-exact in its page."""
+    from gpu_pool import page_layout
+    H, B = 16, 8
+    _say(f"mla B8 H16 L={L} r=1 against the C restatement (sequences 0, 7)")
+    gen = torch.Generator(device=DEV).manual_seed(170 + L % 97)
+    table, num_pages = page_layout([L + 1] * B, PS, seed=171)
+    pt = torch.from_numpy(table).to(DEV)
+    lat = torch.zeros((num_pages, PS, 576), dtype=torch.bfloat16, device=DEV)
+    t = torch.arange(L, device=DEV)
+    keep, new = {}, []
+    for b in range(B):
+        x = _randn_bf16((L + 1, 576), gen, 0.5)
+        lat[pt[b, t // PS].long(), t % PS] = x[:L]
+        new.append(x[-1])
+        if b in (0, 7):
+            keep[b] = bits(x)
+        del x
+    gl = torch.full((B,), L, dtype=torch.int32, device=DEV)
+    qn = _randn_bf16((B * H, 512), gen, 0.5)
+    qp = _randn_bf16((B * H, 64), gen, 0.5)
+    new = torch.stack(new)[:, None]
+    len_out = torch.zeros_like(gl)
+    scale = 192 ** -0.5
+    st = ops.mla_append_decode_split(qn, qp, new[..., :512], new[..., 512:], lat, pt, gl,
+                                     len_out, scale, L + 1)
+    out, lse = ops.merge_split(st, None, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    out, lse = out.cpu().numpy(), lse.cpu().numpy()
+    assert len_out.cpu().tolist() == [L + 1] * B
+    slots = lat[pt[:, L // PS].long(), L % PS]
+    assert torch.equal(slots, new[:, 0]), "appended latents"
+    for b, full in keep.items():
+        rows = slice(b * H, (b + 1) * H)
+        po, pm, ps = port.cpu_attn_mla_compressed(bits(qn[rows]), bits(qp[rows]),
+                                                  full[None, :, :512], full[None, :, 512:],
+                                                  scale, n_threads=16)
+        assert_close(out[rows], po / ps[:, None], OUT_ATOL, OUT_RTOL, f"L={L} out b={b}")
+        assert_close(lse[rows], pm + np.log(ps), LSE_ATOL, LSE_RTOL, f"L={L} lse b={b}")
