@@ -6,7 +6,6 @@ cache, and the cache moves its pages between steps.  Starting host-heavy
 hold it; every step's merged output matches fp64 attention over all tokens,
 before and after the moves.
 """
-import numpy as np
 import pytest
 import torch
 

@@ -2,7 +2,6 @@
 the fp32 / C restatements vs the fp64 closed forms, merge invariants, and the
 reference's own checks (kernel/build.py:28-64 self-test shape,
 roofline/bench_resident_kv.py:410-459 split/merge check)."""
-import itertools
 import math
 
 import numpy as np
