@@ -377,12 +377,12 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
       return d;
     };
     // The offset pair of instructions 2 j and 2 j + 1 (offp[j]).
-    auto dma_pair = [&](const Dma& d, int j) __attribute__((always_inline)) {
+    auto dma_pair = [&](int j) __attribute__((always_inline)) {
       asm volatile("" : "+v"(offp[j]));  // unpacked at each use: five live registers
       return offp[j];
     };
     // Instruction i of a block (i a constant after unrolling), pr =
-    // dma_pair(d, i / 2), its offset clamped.
+    // dma_pair(i / 2), its offset clamped.
     auto dma_one = [&](const Dma& d, uint32_t pr, int i) __attribute__((always_inline)) {
       const uint32_t off = min((i & 1) ? pr >> 16 : pr & 0xffffu, d.lim);
       if (i < kWideDmaPerWave - 1)
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
       uint32_t pr = 0;
 #pragma unroll
       for (int i = 0; i < kWideDmaPerWave; ++i) {
-        if ((i & 1) == 0) pr = dma_pair(d, i >> 1);
+        if ((i & 1) == 0) pr = dma_pair(i >> 1);
         dma_one(d, pr, i);
       }
     };
@@ -536,7 +536,7 @@ __global__ __launch_bounds__(256) void mla_wide_kernel(const MlaParams p) {
           if (m < 16 && (m & 3) == 1) soft_p(xh, pb[1], m >> 2);
         }
         if (u % 4 == 2) {  // instructions 0-8
-          if ((u / 4) % 2 == 0) pr = dma_pair(d, u / 8);
+          if ((u / 4) % 2 == 0) pr = dma_pair(u / 8);
           dma_one(d, pr, u / 4);
         }
       }
